@@ -1,0 +1,137 @@
+"""The oracle: the CPU restatement of TurboEmbed's CPU encoder (oracle.cpp).
+
+Test infrastructure only. Tests, the smoke check and the benchmark's CPU
+baseline call it as the checker; no product code imports it.
+"""
+import ctypes as C
+import json
+import os
+import subprocess
+
+import numpy as np
+
+from turboembed_amd import seam as S
+from turboembed_amd.model import ModelDesc
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+GOLDEN = os.path.join(os.path.dirname(HERE), "tests", "golden")
+
+_lib = None
+
+
+def build():
+    """Compile oracle.cpp into liboracle.so (a few seconds)."""
+    subprocess.check_call(["make", "-s", "-C", HERE, "-B"])
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        _lib = C.CDLL(LIB)
+        _lib.oracle_encode.restype = C.c_int32
+        _lib.oracle_encode.argtypes = [C.POINTER(S.turbo_backend_model), C.POINTER(S.turbo_backend_embed_rows),
+                                       C.POINTER(S.turbo_token_range), C.c_uint32, C.c_uint32, C.c_void_p,
+                                       C.c_void_p, C.c_char_p, C.c_uint32]
+        _lib.oracle_pack.restype = C.c_uint32
+        _lib.oracle_pack.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(S.turbo_token_range),
+                                     C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p]
+        for f in ("oracle_exp", "oracle_gelu", "oracle_silu"):
+            getattr(_lib, f).restype = C.c_float
+            getattr(_lib, f).argtypes = [C.c_float]
+        _lib.oracle_layer_norm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_float]
+    return _lib
+
+
+def rows_struct(ids, mask, types, pooling, normalize, output_dim):
+    r = S.turbo_backend_embed_rows()
+    r.struct_size = C.sizeof(S.turbo_backend_embed_rows)
+    r.batch, r.seq = ids.shape
+    r.row_stride = ids.shape[1]
+    r.ids = ids.ctypes.data_as(C.POINTER(C.c_int32))
+    r.mask = mask.ctypes.data_as(C.POINTER(C.c_int32))
+    r.types = types.ctypes.data_as(C.POINTER(C.c_int32)) if types is not None else None
+    r.pooling, r.normalize, r.output_dim = pooling, normalize, output_dim
+    r.head, r.taps, r.tap_alone = 0, 1, 0
+    return r
+
+
+def ranges_array(ranges):
+    arr = (S.turbo_token_range * max(1, len(ranges)))()
+    for i, (row, start, end) in enumerate(ranges):
+        arr[i].row, arr[i].start, arr[i].end = row, start, end
+    return arr
+
+
+def encode(desc: ModelDesc, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN, normalize=S.TURBO_NORMALIZE_L2,
+           output_dim=None, ranges=None, threads=0, hidden=False):
+    """The oracle's vectors for the rows (and ranges); with hidden=True also
+    the final hidden states of the packed tokens."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    mask = np.ascontiguousarray(mask, dtype=np.int32)
+    types = None if types is None else np.ascontiguousarray(types, dtype=np.int32)
+    od = output_dim or desc.hidden
+    r = rows_struct(ids, mask, types, pooling, normalize, od)
+    ranges = list(ranges or [])
+    rr = ranges_array(ranges)
+    n_out = len(ranges) if ranges else ids.shape[0]
+    out = np.zeros((n_out, od), dtype=np.float32)
+    hid = np.zeros((ids.shape[0] * ids.shape[1], desc.hidden), dtype=np.float32) if hidden else None
+    why = C.create_string_buffer(512)
+    rc = lib().oracle_encode(C.byref(desc.struct()), C.byref(r), rr, len(ranges), threads, out.ctypes.data,
+                             None if hid is None else hid.ctypes.data, why, 512)
+    if rc != 0:
+        raise RuntimeError(f"oracle: {S.STATUS_NAMES.get(rc, rc)}: {why.value.decode()}")
+    if hidden:
+        _, ln, _ = pack(mask, ranges)
+        return out, hid[: int(ln.sum())]
+    return out
+
+
+def pack(mask, ranges=()):
+    """(start, len, at) of the oracle's packing for `mask` [batch, seq]."""
+    mask = np.ascontiguousarray(mask, dtype=np.int32)
+    b, s = mask.shape
+    start = np.zeros(b, np.uint32)
+    ln = np.zeros(b, np.uint32)
+    at = np.zeros(b * s, np.uint32)
+    rr = ranges_array(list(ranges))
+    t = lib().oracle_pack(mask.ctypes.data, b, s, s, rr, len(ranges), start.ctypes.data, ln.ctypes.data, at.ctypes.data)
+    return start, ln, at[:t]
+
+
+# ---- The reference's sealed tiny bundles (tests/golden/) --------------------
+
+_FAMILIES = {"FAMILY_BERT": S.TURBO_FAMILY_BERT, "FAMILY_MODERNBERT": S.TURBO_FAMILY_MODERNBERT,
+             "FAMILY_NOMIC_BERT": S.TURBO_FAMILY_NOMIC_BERT}
+
+
+def fixture(name):
+    """(ModelDesc, ids, lengths, vectors, info) of a golden fixture: the
+    reference bundle's weights and its upstream fp32 reference cases."""
+    from safetensors.numpy import load_file
+    t = load_file(os.path.join(GOLDEN, name + ".safetensors"))
+    info = json.load(open(os.path.join(GOLDEN, name + ".json")))
+    a = info["architecture"]
+    family = _FAMILIES[info["family"]]
+    tensors = [t[k] if k else None for k in info["order"]]
+    kw = {}
+    if family == S.TURBO_FAMILY_MODERNBERT:
+        kw = dict(rope=(a["rope"]["global_theta"], a["rope"]["local_theta"]), attention_window=a["attention"]["window"],
+                  global_every=a["attention"]["global_every"], mlp=S.TURBO_MLP_GATED,
+                  activation=S.TURBO_ACTIVATION_GELU_ERF, norm=S.TURBO_NORM_LAYER_NO_BIAS)
+    elif family == S.TURBO_FAMILY_NOMIC_BERT:
+        g = a["rope"]["global_theta"]
+        kw = dict(rope=(g, g), mlp=S.TURBO_MLP_GATED, activation=S.TURBO_ACTIVATION_SILU, norm=S.TURBO_NORM_LAYER)
+    desc = ModelDesc(family, a["layers"], a["hidden"], a["heads"], a["intermediate"], info["vocab_rows_kept"],
+                     a["max_positions"], max(1, a["token_types"]), a["layer_norm_eps"], tensors,
+                     names=[k or "absent" for k in info["order"]], **kw)
+    return desc, t["case.ids"], t["case.lengths"], t["case.vectors"], info
+
+
+def fixture_rows(ids, lengths):
+    """The reference cases as rows: each case's ids, mask 1 through its length."""
+    mask = (np.arange(ids.shape[1])[None, :] < lengths[:, None]).astype(np.int32)
+    return np.ascontiguousarray(ids, dtype=np.int32), mask

@@ -1,0 +1,46 @@
+/* The oracle: a CPU restatement of TurboEmbed's CPU encoder (the reference's
+ * core/src/cpu/), used only as the checker of the rocm backend's results and
+ * as the CPU baseline the benchmark times beside it. It is test
+ * infrastructure: no product code links, loads or calls it.
+ *
+ * It takes the same seam structs a backend does (turbo_backend_model,
+ * turbo_backend_embed_rows, turbo_token_range), so a test hands the same
+ * description to the oracle and to the backend.
+ */
+#ifndef TURBO_ORACLE_H
+#define TURBO_ORACLE_H
+
+#include "turbo/turbo_seam.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One run: rows (and, when count > 0, ranges pooled by the mean) through the
+ * encoder `m` describes, into out: [batch, output_dim] or [count, output_dim]
+ * F32. `hidden`, when not NULL, receives the final hidden states of the
+ * packed tokens, [tokens, hidden] F32 (room for batch * seq rows).
+ * `threads` 0 is one per processor. Returns TURBO_OK or a status; `why`
+ * (may be NULL) receives a message of up to why_len bytes. */
+int32_t oracle_encode(const turbo_backend_model *m, const turbo_backend_embed_rows *rows,
+                      const turbo_token_range *ranges, uint32_t count, uint32_t threads,
+                      float *out, float *hidden, char *why, uint32_t why_len);
+
+/* The packing alone (reference core/src/cpu/encoder/mod.rs:379-424): for each
+ * row its first packed token and its packed length, and for each packed
+ * token its place r * seq + p in the rows. Returns the packed tokens. */
+uint32_t oracle_pack(const int32_t *mask, uint32_t batch, uint32_t seq, uint32_t row_stride,
+                     const turbo_token_range *ranges, uint32_t count,
+                     uint32_t *start, uint32_t *len, uint32_t *at);
+
+/* The scalar functions the encoder uses, for their own tests. */
+float oracle_exp(float x);
+float oracle_gelu(float x);
+float oracle_silu(float x);
+void  oracle_layer_norm(float *y, const float *w, const float *b, uint32_t n, float eps);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
