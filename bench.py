@@ -1,0 +1,156 @@
+"""Throughput of the rocm backend's encoder forward pass on one MI355X.
+
+Default workload: the BERT-base-shaped encoder (12 layers, hidden 768, 12
+heads, FFN 3072, vocab 30522), weights stored F32 and run in the FASTEST
+tier (F16 operands, F32 sums), 64 rows x 512 tokens all live, CLS pooling +
+L2. A step is one session run over the batch (pack, embeddings, 12 layers,
+pool), with the rows already resident on the device. Prints one JSON line.
+
+The CPU baseline is the oracle (this repository's C++ restatement of the
+reference's CPU encoder) on a bounded sample of the same rows, on the host's
+cores; the same sample gives the cosine of the GPU's vectors against it.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import turboembed_amd as T  # noqa: E402
+from turboembed_amd import seam as S  # noqa: E402
+from turboembed_amd import workloads as W  # noqa: E402
+
+PEAK = {"f16": 2.5e15, "bf16": 2.5e15, "f32": 157.3e12}   # dense MFMA, MI355X
+HBM_PEAK = 8.0e12
+
+
+def kernel_flops(shape, tokens, lengths):
+    """Algorithmic FLOPs of one launch of each kernel, by the names the
+    session's timing hook reports."""
+    H, I = shape.hidden, shape.intermediate
+    gated = shape.family == S.TURBO_FAMILY_MODERNBERT
+    f = {
+        "gemm_qkv": 2.0 * tokens * 3 * H * H,
+        "gemm_out": 2.0 * tokens * H * H,
+        "gemm_ffn_in": 2.0 * tokens * (2 * I if gated else I) * H,
+        "gemm_ffn_out": 2.0 * tokens * H * I,
+        "attention": W.attention_flops(shape, lengths) / shape.layers,
+    }
+    return f
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="bert-base", choices=sorted(W.SHAPES))
+    ap.add_argument("--lengths", default="default", help="'default', 'full', or lo,hi")
+    ap.add_argument("--cpu-rows", type=int, default=4, help="rows of the CPU baseline's sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run (each row's encoder is "
+              "independent, so more GPUs would shard rows with no exchange)", file=sys.stderr)
+        sys.exit(2)
+
+    shape = W.SHAPES[args.workload]
+    lengths = {"default": "default", "full": None}.get(args.lengths)
+    if lengths is None and args.lengths not in ("default", "full"):
+        lengths = tuple(int(v) for v in args.lengths.split(","))
+    t0 = time.time()
+    desc = W.model(shape)
+    ids, mask, types = W.rows(shape, lengths=lengths)
+    print(f"# model and rows ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+
+    rt = T.Runtime()
+    assert rt.device_count() >= 1, "no gfx950 device"
+    ctx = rt.context(0)
+    model = ctx.load(desc)
+    sess = model.session(shape.batch, shape.seq, shape.precision)
+    dtype = {S.TURBO_DTYPE_F16: "f16", S.TURBO_DTYPE_BF16: "bf16", S.TURBO_DTYPE_F32: "f32"}[sess.compute_dtype]
+    sess.write_tokens(ids, mask, types, pooling=shape.pooling, normalize=shape.normalize)
+    sess.run()
+    gpu_vecs = sess.read()
+    print(f"# loaded, first run done in {time.time() - t0:.1f}s; choices {sess.choices()}", file=sys.stderr,
+          flush=True)
+
+    sess.replay(args.warmup)
+    start = time.perf_counter()
+    sess.replay(args.steps)
+    elapsed = time.perf_counter() - start
+    ms = elapsed / args.steps * 1e3
+    lens = mask.sum(1)
+    tokens = int(lens.sum())
+    seq_per_s = shape.batch / (ms / 1e3)
+
+    # Per-kernel times from HIP events on the session's stream, one run.
+    sess.set_timing(True)
+    sess.replay(1)
+    times = sess.times()
+    sess.set_timing(False)
+    per = kernel_flops(shape, tokens, lens)
+    gemm_names = [k for k in times if k.startswith("gemm_")]
+    gemm_ms = sum(times[k] for k in gemm_names)
+    gemm_flops = sum(per[k] for k in gemm_names) * shape.layers
+    launches = {k: shape.layers for k in per}
+    total_flops = W.gemm_flops_per_token(shape) * tokens + W.attention_flops(shape, lens)
+    # The dominant kernel: the GEMM kernel (every linear layer's launches),
+    # or attention when it takes longer.
+    if times.get("attention", 0.0) > gemm_ms:
+        dom, dom_ms, dom_flops, dom_launches = "attention", times["attention"], per["attention"] * shape.layers, \
+            launches["attention"]
+    else:
+        dom, dom_ms, dom_flops, dom_launches = "gemm", gemm_ms, gemm_flops, len(gemm_names) * shape.layers
+    achieved = dom_flops / (dom_ms / 1e3)
+    roofline = {"kernel": dom, "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[dtype] / 1e12,
+                "unit": "TFLOP/s", "frac": achieved / PEAK[dtype], "traffic": None,
+                "launches_per_step": dom_launches, "avg_launch_us": dom_ms / dom_launches * 1e3,
+                "flops_per_launch": dom_flops / dom_launches}
+
+    cpu = None
+    min_cos = None
+    if not args.no_cpu:
+        import oracle
+        n = min(args.cpu_rows, shape.batch)
+        threads = min(16, os.cpu_count() or 1)
+        c0 = time.perf_counter()
+        want = oracle.encode(desc, ids[:n], mask[:n], types[:n], pooling=shape.pooling, normalize=shape.normalize,
+                             threads=threads)
+        cpu_s = time.perf_counter() - c0
+        cos = (gpu_vecs[:n] * want).sum(1) / np.linalg.norm(gpu_vecs[:n], axis=1) / np.linalg.norm(want, axis=1)
+        min_cos = float(cos.min())
+        cpu = {"value": n / cpu_s, "unit": "sequences/s", "cores": threads, "kind": "port",
+               "sample": f"{n} of the {shape.batch} rows ({int(lens[:n].sum())} tokens), all {shape.layers} layers, "
+                         f"one pass, {cpu_s:.1f} s on {threads} threads"}
+
+    line = {
+        "metric": f"sequences/s ({args.workload}, {dtype}, {shape.batch}x{shape.seq})",
+        "value": seq_per_s, "unit": "sequences/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: {shape.layers} layers, hidden {shape.hidden}, {shape.heads} heads, "
+                               f"FFN {shape.intermediate}, {shape.batch} rows x {shape.seq}, "
+                               f"{'all live' if lengths is None else 'lengths ' + str(shape.lengths if lengths == 'default' else lengths)}",
+                   "global_batch": shape.batch, "seq_len": shape.seq, "live_tokens": tokens, "parallelism": "none"},
+        "tokens_per_s": tokens / (ms / 1e3),
+        "mfma_util_pct": 100.0 * total_flops / (ms / 1e3) / PEAK[dtype],
+        "algorithmic_tflop_per_step": total_flops / 1e12,
+        "min_cosine_vs_cpu": min_cos,
+        "kernel_ms": {k: round(v, 4) for k, v in times.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    sess.close()
+    model.close()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,90 @@
+/* SPDX-License-Identifier: Apache-2.0
+ *
+ * The rocm backend's C ABI: libturbo_rocm.so.
+ *
+ * The drop-in boundary is one symbol, the backend's function table, which
+ * the TurboEmbed core lists beside its other backends. Everything else here
+ * is the host-side checking the core does before it calls a backend (so a
+ * harness without the Rust core checks rows as the core does) and hooks for
+ * tests and measurement, which the core never calls.
+ */
+#ifndef TURBO_ROCM_H
+#define TURBO_ROCM_H
+
+#include "turbo/turbo_seam.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The backend's table, name "rocm". Replaces, for AMD gfx950 GPUs, the
+ * reference's turbo_cuda_backend (core/cuda/backend.cpp:3776-3809), and is
+ * linked into the core's LINKED list the same way
+ * (core/src/backend/mod.rs:338-360, extern static as core/src/cuda.rs:8-17).
+ * Every function follows include/turbo/turbo_backend.h:455-627. */
+extern const turbo_backend turbo_rocm_backend;
+
+/* The numeric class of BF16 operands with F32 sums: this backend's BF16 tier.
+ * The reference defines classes 1, 2, 4 and 8 (turbo_backend.h:226-229); this
+ * is the next free bit, which the core's NUMERICS_ALLOWED table
+ * (core/src/tuning.rs:32-41) needs for a BF16-stored model. */
+#define TURBO_ROCM_NUMERIC_BF16_F32ACC 16u
+
+/* ---- The core's checks of a write (core/src/session/tokens.rs:274-384) ----
+ *
+ * turbo_rocm_check_tokens: the rows' shape within max_batch x max_seq, each id
+ * under vocab, each type under types (types may be NULL), each mask entry 0
+ * or 1 with a 1 in every row, and, when max_tokens is not 0, each row's
+ * length through its last live token at most max_tokens. row_stride 0 is seq.
+ * Returns TURBO_OK or the status the core returns, with its message. */
+int32_t turbo_rocm_check_tokens(uint32_t batch, uint32_t seq, uint32_t row_stride, const int32_t *ids,
+                                const int32_t *mask, const int32_t *types, uint32_t max_batch, uint32_t max_seq,
+                                uint32_t vocab, uint32_t token_types, uint32_t max_tokens, turbo_error *err);
+
+/* turbo_rocm_check_ranges: count ranges of the rows above (the core's
+ * check_ranges, core/src/session/tokens.rs:274-306, for a backend that does
+ * not compute mask-0 columns): count 1 to max_ranges, each row under batch,
+ * start under end, end at most seq, and a live token inside. */
+int32_t turbo_rocm_check_ranges(uint32_t batch, uint32_t seq, uint32_t row_stride, const int32_t *mask,
+                                const turbo_token_range *ranges, uint32_t count, uint32_t max_ranges,
+                                turbo_error *err);
+
+/* ---- Test and measurement hooks (no counterpart in the reference's seam; the
+ * reference's CUDA backend keeps similar ones, core/src/cuda.rs:177-499) ---- */
+
+/* The last run's packing, read back from the device: each row's first packed
+ * token and length ([batch] each), each packed token's r * seq + p ([tokens]),
+ * and the packed token count. */
+int32_t turbo_rocm_session_packing(void *session, int32_t *start, int32_t *len, int32_t *at, uint32_t *tokens,
+                                   turbo_error *err);
+
+/* The last run's final hidden states, [tokens, hidden] F32. */
+int32_t turbo_rocm_session_hidden(void *session, float *out, uint64_t floats, turbo_error *err);
+
+/* Times every kernel of the session's later runs with HIP events on the
+ * context's stream; turbo_rocm_session_times then writes "<kernel> <ms>"
+ * lines, the milliseconds summed over the last run's launches of that
+ * kernel. */
+int32_t turbo_rocm_session_timing(void *session, uint32_t on, turbo_error *err);
+int32_t turbo_rocm_session_times(void *session, char *out, uint32_t len, turbo_error *err);
+
+/* Runs the last written rows `runs` more times, back to back on the
+ * context's stream, then waits: the rows stay resident on the device, so
+ * this is the device's throughput on them, for measurement. */
+int32_t turbo_rocm_session_replay(void *session, uint32_t runs, turbo_error *err);
+
+/* The session's kernel choices, as TURBO_ROCM_CHOICES takes them. */
+int32_t turbo_rocm_session_choices(void *session, char *out, uint32_t len, turbo_error *err);
+
+/* One GEMM, out [M, N] = A [M, K] W [N, K]^T + bias (bias may be NULL), with
+ * the operands narrowed on the device to dtype (TURBO_DTYPE_F32, F16 or
+ * BF16) and block shape `tile` (0 = the default choice). Allocates its own
+ * device memory; for kernel tests. */
+int32_t turbo_rocm_gemm_check(uint32_t ordinal, uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, const float *A,
+                              const float *W, const float *bias, float *out, uint32_t tile, turbo_error *err);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TURBO_ROCM_H */

@@ -1,0 +1,198 @@
+"""The HIP path against the oracle and the reference's sealed vectors, on an
+MI355X, through the C ABI.
+
+Tolerances are the reference's conformance floors
+(core/src/record/mod.rs:341-348): F32 cosine >= 0.9999 and max abs diff
+<= 1e-4; F16 and BF16 cosine >= 0.999. Bookkeeping (packing) is held bit
+for bit, and so is the reference's whole-row range rule.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import turboembed_amd as T
+from turboembed_amd import seam as S
+from turboembed_amd import workloads as W
+
+import small
+
+pytestmark = pytest.mark.gpu
+
+FLOOR = {S.TURBO_DTYPE_F32: 0.9999, S.TURBO_DTYPE_F16: 0.999, S.TURBO_DTYPE_BF16: 0.999}
+
+
+def assert_close(got, want, compute_dtype):
+    cos = small.cosine_rows(got, want)
+    assert cos.min() >= FLOOR[compute_dtype], f"min cosine {cos.min()} (dtype {compute_dtype})"
+    if compute_dtype == S.TURBO_DTYPE_F32:
+        assert np.abs(got - want).max() <= 1e-4, np.abs(got - want).max()
+
+
+# ---- The GEMM kernel alone ------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [S.TURBO_DTYPE_F32, S.TURBO_DTYPE_F16, S.TURBO_DTYPE_BF16])
+@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 200, 96), (33, 96, 32), (1000, 768, 768)])
+def test_gemm_matches_numpy(runtime, dtype, tile, mnk):
+    m, n, k = mnk
+    g = np.random.Generator(np.random.PCG64(m * 7 + n + k))
+    a = g.standard_normal((m, k)).astype(np.float32)
+    w = g.standard_normal((n, k)).astype(np.float32)
+    b = g.standard_normal(n).astype(np.float32)
+    got = T.gemm_check(a, w, b, dtype=dtype, tile=tile)
+    if dtype == S.TURBO_DTYPE_F16:
+        a, w = a.astype(np.float16).astype(np.float64), w.astype(np.float16).astype(np.float64)
+    elif dtype == S.TURBO_DTYPE_BF16:
+        from turboembed_amd.model import to_bf16_bits
+        f = lambda x: (to_bf16_bits(x).astype(np.uint32) << 16).view(np.float32).astype(np.float64)  # noqa: E731
+        a, w = f(a), f(w)
+    want = a.astype(np.float64) @ w.astype(np.float64).T + b
+    err = np.abs(got - want).max() / np.sqrt(k)
+    assert err < 1e-4, err
+
+
+# ---- The sealed tiny bundles ---------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["tiny_bert", "tiny_modernbert", "tiny_nomic"])
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+def test_tiny_bundles_meet_the_upstream_vectors(context, name, precision):
+    desc, ids, lengths, vectors, info = oracle.fixture(name)
+    ids, mask = oracle.fixture_rows(ids, lengths)
+    norm = S.TURBO_NORMALIZE_L2 if info["embed"]["normalize"] == "NORMALIZE_L2" else S.TURBO_NORMALIZE_NONE
+    model = context.load(desc)
+    s = model.session(ids.shape[0], ids.shape[1], precision)
+    got = s.embed(ids, mask, normalize=norm)
+    assert_close(got, vectors, s.compute_dtype)
+    want = oracle.encode(desc, ids, mask, normalize=norm)
+    assert_close(got, want, s.compute_dtype)
+    # One row at a time gives the batch's vectors within the bound.
+    for r in (0, 7):
+        one = s.embed(ids[r:r + 1], mask[r:r + 1], normalize=norm)
+        assert_close(one, got[r:r + 1], s.compute_dtype)
+    s.close()
+    model.close()
+
+
+# ---- Small models of every family, ragged rows ------------------------------------------
+
+MODELS = {"bert": small.bert, "modernbert": small.modernbert, "nomic": small.nomic}
+
+
+@pytest.mark.parametrize("family", ["bert", "modernbert", "nomic"])
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+def test_ragged_rows_meet_the_oracle(context, family, precision):
+    desc = MODELS[family](seed=11)
+    ids, mask, types = small.ragged_rows(11, 7, 48, desc.vocab_size)
+    if family == "modernbert":
+        types = None
+    model = context.load(desc)
+    s = model.session(8, 64, precision)
+    for pooling in (S.TURBO_POOLING_MEAN, S.TURBO_POOLING_CLS, S.TURBO_POOLING_LAST):
+        got = s.embed(ids, mask, types, pooling=pooling, output_dim=40)
+        want = oracle.encode(desc, ids, mask, types, pooling=pooling, output_dim=40)
+        assert_close(got, want, s.compute_dtype)
+    s.close()
+    model.close()
+
+
+def test_packing_is_the_oracle_s_bit_for_bit(context):
+    desc = small.bert(seed=12)
+    ids, mask, types = small.ragged_rows(12, 9, 40, desc.vocab_size)
+    model = context.load(desc)
+    s = model.session(16, 64, S.TURBO_PRECISION_EXACT)
+    s.embed(ids, mask, types)
+    start, ln, at = s.packing()
+    o_start, o_len, o_at = oracle.pack(mask)
+    assert np.array_equal(start, o_start.astype(np.int32))
+    assert np.array_equal(ln, o_len.astype(np.int32))
+    assert np.array_equal(at, o_at.astype(np.int32))
+    s.close()
+    model.close()
+
+
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+def test_ranges(context, precision):
+    desc = small.bert(seed=13)
+    ids, mask, types = small.ragged_rows(13, 6, 48, desc.vocab_size)
+    model = context.load(desc)
+    s = model.session(8, 64, precision, max_ranges=64)
+    rows = s.embed(ids, mask, types)
+    # Whole-row ranges give the rows' vectors bit for bit
+    # (core/tests/ranges/whole_row.rs:8-28).
+    s.write_ranges(ids, mask, [(r, 0, 48) for r in range(6)], types)
+    s.run()
+    assert np.array_equal(s.read(), rows)
+    g = np.random.Generator(np.random.PCG64(5))
+    ranges = []
+    while len(ranges) < 40:
+        r = int(g.integers(0, 6))
+        a = int(g.integers(0, 47))
+        b = int(g.integers(a + 1, 49))
+        if mask[r, a:b].any():
+            ranges.append((r, a, b))
+    s.write_ranges(ids, mask, ranges, types)
+    s.run()
+    got = s.read()
+    want = oracle.encode(desc, ids, mask, types, ranges=ranges)
+    assert_close(got, want, s.compute_dtype)
+    s.close()
+    model.close()
+
+
+def test_same_rows_same_bits(context):
+    desc = small.bert(seed=14)
+    ids, mask, types = small.ragged_rows(14, 8, 64, desc.vocab_size)
+    model = context.load(desc)
+    s = model.session(8, 64, S.TURBO_PRECISION_FASTEST)
+    a = s.embed(ids, mask, types)
+    b = s.embed(ids, mask, types)
+    assert np.array_equal(a, b)
+    info = s.run_info
+    assert info.device_allocs == 0 and info.host_allocs == 0
+    assert info.stage[S.TURBO_STAGE_MAX - 16 + 3] == S.TURBO_STAGE_DEVICE
+    s.close()
+    model.close()
+
+
+def test_run_before_write_is_invalid_state(context):
+    desc = small.bert(seed=15)
+    model = context.load(desc)
+    s = model.session(2, 16, S.TURBO_PRECISION_EXACT)
+    with pytest.raises(T.TurboError) as e:
+        s.run()
+    assert e.value.code == S.TURBO_E_INVALID_STATE
+    s.close()
+    model.close()
+
+
+# ---- The workloads at their real widths -------------------------------------------------
+
+def test_minilm_exact_meets_the_oracle(context):
+    sh = W.SHAPES["minilm"]
+    desc = W.model(sh)
+    ids, mask, types = W.rows(sh)
+    model = context.load(desc)
+    s = model.session(sh.batch, sh.seq, sh.precision)
+    assert s.compute_dtype == S.TURBO_DTYPE_F32
+    got = s.embed(ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
+    want = oracle.encode(desc, ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
+    assert_close(got, want, s.compute_dtype)
+    s.close()
+    model.close()
+
+
+@pytest.mark.parametrize("lengths", [None, (64, 512)])
+def test_bert_base_fastest_meets_the_oracle(context, lengths):
+    # Full width and sequence; 2 of the 12 layers and 6 of the 64 rows keep
+    # the oracle's share to seconds. The full model runs in the benchmark.
+    sh = W.SHAPES["bert-base"]
+    desc = W.model(sh, layers=2)
+    ids, mask, types = W.rows(sh, batch=6, lengths=lengths)
+    model = context.load(desc)
+    s = model.session(64, 512, sh.precision)
+    assert s.compute_dtype == S.TURBO_DTYPE_F16
+    got = s.embed(ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
+    want = oracle.encode(desc, ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
+    assert_close(got, want, s.compute_dtype)
+    s.close()
+    model.close()

@@ -1,0 +1,304 @@
+"""turboembed_amd: TurboEmbed's encoder forward pass as an MI355X-native `rocm` backend.
+
+The product is libturbo_rocm.so (built from csrc/ by build.py): the
+`turbo_rocm_backend` function table behind the reference's backend seam, and
+its gfx950 kernels. This module is the host side above that C ABI, playing
+the TurboEmbed core's part for this path: it loads a model description,
+opens sessions, checks rows and ranges as the core does before it calls a
+backend, and reads results back. It mirrors the core's session flow
+(reference core/src/session/create.rs:56-281, tokens.rs:9-152,
+result.rs:8-63) and raises `TurboError` with the status the core would
+return.
+
+There is no fallback: without the built library every call raises.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import seam as S
+from .model import ModelDesc  # noqa: F401  (re-exported)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libturbo_rocm.so")
+
+_lib = None
+
+
+class TurboError(RuntimeError):
+    def __init__(self, code, field, message):
+        self.code, self.field, self.message = code, field, message
+        super().__init__(f"{S.STATUS_NAMES.get(code, code)}"
+                         f"{' (field ' + str(field) + ')' if field else ''}: {message}")
+
+
+def library():
+    """The loaded libturbo_rocm.so, with the hook prototypes set. Raises when
+    it has not been built: this package has no other path."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run turboembed_amd/build.py (or __graft_entry__.build())")
+    lib = C.CDLL(LIB_PATH)
+    E = C.POINTER(S.turbo_error)
+    P = C.c_void_p
+    u32 = C.c_uint32
+    i32p = C.POINTER(C.c_int32)
+    protos = {
+        "turbo_rocm_check_tokens": [u32, u32, u32, i32p, i32p, i32p, u32, u32, u32, u32, u32, E],
+        "turbo_rocm_check_ranges": [u32, u32, u32, i32p, C.POINTER(S.turbo_token_range), u32, u32, E],
+        "turbo_rocm_session_packing": [P, P, P, P, C.POINTER(u32), E],
+        "turbo_rocm_session_hidden": [P, P, C.c_uint64, E],
+        "turbo_rocm_session_timing": [P, u32, E],
+        "turbo_rocm_session_times": [P, C.c_char_p, u32, E],
+        "turbo_rocm_session_choices": [P, C.c_char_p, u32, E],
+        "turbo_rocm_session_replay": [P, u32, E],
+        "turbo_rocm_gemm_check": [u32, u32, u32, u32, u32, P, P, P, P, u32, E],
+    }
+    for name, args in protos.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = C.c_int32
+    _lib = lib
+    return lib
+
+
+def table():
+    """The backend's turbo_backend table."""
+    return S.turbo_backend.in_dll(library(), "turbo_rocm_backend")
+
+
+def _ok(rc, err):
+    if rc != S.TURBO_OK:
+        raise TurboError(rc, err.field, err.message.decode(errors="replace"))
+
+
+def _i32(a):
+    return a.ctypes.data_as(C.POINTER(C.c_int32))
+
+
+class Runtime:
+    """The backend's devices (the core's runtime, restricted to this backend)."""
+
+    def __init__(self):
+        self.t = table()
+        self._log = S.turbo_log_fn(lambda ud, level, text: None)
+
+    def device_count(self):
+        n = C.c_uint32()
+        err = S.new_error()
+        _ok(self.t.device_count(C.byref(n), C.byref(err)), err)
+        return n.value
+
+    def device_info(self, ordinal=0):
+        info = S.turbo_device_info()
+        info.struct_size = C.sizeof(info)
+        err = S.new_error()
+        _ok(self.t.device_info(ordinal, C.byref(info), C.byref(err)), err)
+        return info
+
+    def capability(self, ordinal, task, precision):
+        st, dt, hon = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        reason = C.create_string_buffer(160)
+        err = S.new_error()
+        _ok(self.t.capability(ordinal, task, precision, C.byref(st), C.byref(dt), C.byref(hon), reason, 160,
+                              C.byref(err)), err)
+        return st.value, dt.value, hon.value, reason.value.decode()
+
+    def context(self, ordinal=0):
+        return Context(self, ordinal)
+
+
+class Context:
+    def __init__(self, rt, ordinal):
+        self.rt, self.t = rt, rt.t
+        h = C.c_void_p()
+        err = S.new_error()
+        _ok(self.t.context_create(ordinal, rt._log, None, C.byref(h), C.byref(err)), err)
+        self.h = h
+
+    def load(self, desc: ModelDesc):
+        return Model(self, desc)
+
+    def close(self):
+        if self.h:
+            self.t.context_release(self.h)
+            self.h = None
+
+
+class Model:
+    def __init__(self, ctx, desc):
+        self.ctx, self.t, self.desc = ctx, ctx.t, desc
+        h = C.c_void_p()
+        err = S.new_error()
+        _ok(self.t.model_load(ctx.h, C.byref(desc.struct()), C.byref(h), C.byref(err)), err)
+        self.h = h
+
+    def session(self, max_batch, max_seq, precision=S.TURBO_PRECISION_MODEL, max_ranges=0, task=S.TURBO_TASK_EMBED,
+                numerics_allowed=0):
+        return Session(self, max_batch, max_seq, precision, max_ranges, task, numerics_allowed)
+
+    def close(self):
+        if self.h:
+            self.t.model_release(self.h)
+            self.h = None
+
+
+class Session:
+    """A session opened through session_open, as the core opens one
+    (core/src/session/create.rs:151-180)."""
+
+    def __init__(self, model, max_batch, max_seq, precision, max_ranges, task, numerics_allowed):
+        self.model, self.t, self.lib = model, model.t, library()
+        d = S.turbo_backend_session_desc()
+        d.struct_size = C.sizeof(d)
+        d.task, d.max_batch, d.max_seq, d.precision = task, max_batch, max_seq, precision
+        d.max_ranges = max_ranges or max_batch
+        self.max_batch, self.max_seq, self.max_ranges = max_batch, max_seq, d.max_ranges
+        tun = S.turbo_backend_tuning()
+        tun.struct_size = C.sizeof(tun)
+        tun.mode = S.TURBO_AUTOTUNE_OFF
+        tun.numerics_allowed = numerics_allowed
+        self.tuning = tun
+        cd = C.c_uint32()
+        h = C.c_void_p()
+        err = S.new_error()
+        _ok(self.t.session_open(model.h, C.byref(d), C.byref(tun), C.byref(cd), C.byref(h), C.byref(err)), err)
+        self.h, self.compute_dtype = h, cd.value
+        self.run_info = None
+        self.n_out = 0
+        self.od = 0
+
+    # -- writes ---------------------------------------------------------------
+    def _rows(self, ids, mask, types, pooling, normalize, output_dim):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        mask = np.ascontiguousarray(mask, dtype=np.int32)
+        types = None if types is None else np.ascontiguousarray(types, dtype=np.int32)
+        desc = self.model.desc
+        err = S.new_error()
+        b, s = ids.shape
+        _ok(self.lib.turbo_rocm_check_tokens(b, s, s, _i32(ids), _i32(mask), None if types is None else _i32(types),
+                                             self.max_batch, self.max_seq, desc.vocab_size, desc.token_types, 0,
+                                             C.byref(err)), err)
+        od = output_dim or desc.hidden
+        if not 1 <= od <= desc.hidden:
+            raise TurboError(S.TURBO_E_INVALID_ARGUMENT, 6, f"output_dim {od} is not 1 to {desc.hidden}")
+        r = S.turbo_backend_embed_rows()
+        r.struct_size = C.sizeof(r)
+        r.batch, r.seq, r.row_stride = b, s, s
+        r.ids, r.mask = _i32(ids), _i32(mask)
+        r.types = None if types is None else _i32(types)
+        r.pooling, r.normalize, r.output_dim = pooling, normalize, od
+        r.head, r.taps, r.tap_alone = 0, 1, 0
+        self._keep = (ids, mask, types)
+        return r
+
+    def write_tokens(self, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN, normalize=S.TURBO_NORMALIZE_L2,
+                     output_dim=0):
+        r = self._rows(ids, mask, types, pooling, normalize, output_dim)
+        err = S.new_error()
+        _ok(self.t.embed_write(self.h, C.byref(r), C.byref(err)), err)
+        self.n_out, self.od = r.batch, r.output_dim
+
+    def write_ranges(self, ids, mask, ranges, types=None, normalize=S.TURBO_NORMALIZE_L2, output_dim=0):
+        """Ranges are (row, start, end) triples; pooled by the mean, as the
+        core forces for a range write (core/src/session/tokens.rs:132-146)."""
+        r = self._rows(ids, mask, types, S.TURBO_POOLING_MEAN, normalize, output_dim)
+        ranges = list(ranges)
+        arr = (S.turbo_token_range * max(1, len(ranges)))()
+        for i, (row, start, end) in enumerate(ranges):
+            arr[i].row, arr[i].start, arr[i].end = row, start, end
+        err = S.new_error()
+        mask = self._keep[1]
+        _ok(self.lib.turbo_rocm_check_ranges(r.batch, r.seq, r.seq, _i32(mask), arr, len(ranges), self.max_ranges,
+                                             C.byref(err)), err)
+        _ok(self.t.embed_write_ranges(self.h, C.byref(r), arr, len(ranges), C.byref(err)), err)
+        self.n_out, self.od = len(ranges), r.output_dim
+
+    # -- run and read -----------------------------------------------------------
+    def run(self):
+        out = S.turbo_backend_run()
+        out.struct_size = C.sizeof(out)
+        err = S.new_error()
+        _ok(self.t.session_run(self.h, C.byref(out), C.byref(err)), err)
+        self.run_info = out
+        return out
+
+    def read(self):
+        """The last run's vectors, [n, output_dim] F32, via buffer_read."""
+        v = np.empty((self.n_out, self.od), dtype=np.float32)
+        err = S.new_error()
+        _ok(self.t.buffer_read(self.run_info.output, v.ctypes.data, v.nbytes, C.byref(err)), err)
+        return v
+
+    def embed(self, ids, mask, types=None, **kw):
+        self.write_tokens(ids, mask, types, **kw)
+        self.run()
+        return self.read()
+
+    # -- hooks ---------------------------------------------------------------------
+    def packing(self):
+        b = self._keep[0].shape[0]
+        start = np.zeros(b, np.int32)
+        ln = np.zeros(b, np.int32)
+        at = np.zeros(self._keep[0].size, np.int32)
+        t = C.c_uint32()
+        err = S.new_error()
+        _ok(self.lib.turbo_rocm_session_packing(self.h, start.ctypes.data, ln.ctypes.data, at.ctypes.data,
+                                                C.byref(t), C.byref(err)), err)
+        return start, ln, at[: t.value]
+
+    def hidden(self):
+        _, ln, _ = self.packing()
+        n = int(ln.sum())
+        out = np.empty((n, self.model.desc.hidden), np.float32)
+        err = S.new_error()
+        _ok(self.lib.turbo_rocm_session_hidden(self.h, out.ctypes.data, out.size, C.byref(err)), err)
+        return out
+
+    def set_timing(self, on=True):
+        err = S.new_error()
+        _ok(self.lib.turbo_rocm_session_timing(self.h, 1 if on else 0, C.byref(err)), err)
+
+    def times(self):
+        buf = C.create_string_buffer(8192)
+        err = S.new_error()
+        _ok(self.lib.turbo_rocm_session_times(self.h, buf, 8192, C.byref(err)), err)
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, ms = line.split()
+            out[name] = float(ms)
+        return out
+
+    def replay(self, runs):
+        """Run the written rows `runs` more times on the device, then wait."""
+        err = S.new_error()
+        _ok(self.lib.turbo_rocm_session_replay(self.h, runs, C.byref(err)), err)
+
+    def choices(self):
+        buf = C.create_string_buffer(1024)
+        err = S.new_error()
+        _ok(self.lib.turbo_rocm_session_choices(self.h, buf, 1024, C.byref(err)), err)
+        return buf.value.decode()
+
+    def close(self):
+        if self.h:
+            self.t.session_release(self.h)
+            self.h = None
+
+
+def gemm_check(a, w, bias=None, dtype=S.TURBO_DTYPE_F32, tile=0, ordinal=0):
+    """out = a w^T + bias on the device, through the GEMM kernel alone."""
+    a = np.ascontiguousarray(a, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    m, k = a.shape
+    n = w.shape[0]
+    out = np.empty((m, n), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    err = S.new_error()
+    _ok(library().turbo_rocm_gemm_check(ordinal, dtype, m, n, k, a.ctypes.data, w.ctypes.data,
+                                        None if b is None else b.ctypes.data, out.ctypes.data, tile, C.byref(err)),
+        err)
+    return out

@@ -1,0 +1,430 @@
+// The rocm backend's host side: the turbo_backend table TurboEmbed's core
+// calls (reference include/turbo/turbo_backend.h:455-627), over HIP on
+// MI355X (gfx950) devices.
+//
+// Ownership follows the seam: a context owns a HIP stream; a model owns its
+// weights on the device (F32, plus the narrowed copies a session's precision
+// needs, made on first need and shared); a session owns every byte a run
+// touches, allocated at creation, so a run allocates nothing. A run is one
+// pass of kernels on the context's stream, then one synchronization.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "turbo/turbo_seam.h"
+#include "turbo_rocm.h"
+#include "kernels.h"
+#include "session.h"
+
+using namespace rocm;
+
+namespace rocm {
+
+// ---- Errors ---------------------------------------------------------------------
+
+[[noreturn]] void fail(int32_t code, const std::string &m, uint32_t field) { throw Failure{code, field, m}; }
+
+void check(hipError_t e, const char *what) {
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        fail(TURBO_E_RUNTIME, std::string("rocm: ") + what + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+    }
+}
+
+void fill(turbo_error *err, int32_t code, uint32_t field, const std::string &m) {
+    if (!err) return;
+    err->code = code;
+    err->field = field;
+    std::snprintf(err->message, sizeof err->message, "%s", m.c_str());
+}
+
+std::atomic<uint64_t> device_allocs{0};
+std::atomic<uint64_t> host_allocs{0};
+
+void *dev_alloc(size_t bytes, const char *what) {
+    void *p = nullptr;
+    if (bytes == 0) bytes = 256;
+    const hipError_t e = hipMalloc(&p, bytes);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) {
+        (void)hipGetLastError();
+        fail(TURBO_E_OUT_OF_MEMORY,
+             std::string("rocm: ") + what + ": " + std::to_string(bytes) + " bytes of device memory");
+    }
+    check(e, what);
+    ++device_allocs;
+    return p;
+}
+
+// Never throws: the release functions use it too. A device that cannot be
+// made current fails the next HIP call instead.
+OnDevice::OnDevice(int ordinal) {
+    if (hipGetDevice(&prev) != hipSuccess) {
+        (void)hipGetLastError();
+        prev = -1;
+    }
+    if (prev != ordinal && hipSetDevice(ordinal) != hipSuccess) (void)hipGetLastError();
+}
+OnDevice::~OnDevice() {
+    int now = -1;
+    if (prev >= 0 && hipGetDevice(&now) == hipSuccess && now != prev) (void)hipSetDevice(prev);
+}
+
+// Only gfx950 devices are listed: the kernels are built for that alone.
+const std::vector<int> &devices() {
+    static std::vector<int> list;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        for (int i = 0; i < n; ++i) {
+            hipDeviceProp_t p;
+            if (hipGetDeviceProperties(&p, i) != hipSuccess) {
+                (void)hipGetLastError();
+                continue;
+            }
+            if (std::strncmp(p.gcnArchName, "gfx950", 6) == 0) list.push_back(i);
+        }
+    });
+    return list;
+}
+
+void Context::say(uint32_t level, const std::string &m) const {
+    if (!log) return;
+    turbo_text t{m.c_str(), m.size()};
+    log(log_user_data, level, t);
+}
+
+}  // namespace rocm
+
+namespace {
+
+#define ROCM_STR2(x) #x
+#define ROCM_STR(x) ROCM_STR2(x)
+// The HIP runtime this build compiled against.
+constexpr const char *RUNTIME_VERSION =
+    "HIP " ROCM_STR(HIP_VERSION_MAJOR) "." ROCM_STR(HIP_VERSION_MINOR) "." ROCM_STR(HIP_VERSION_PATCH);
+const char *runtime_version_string() { return RUNTIME_VERSION; }
+
+// ---- Devices and capability ---------------------------------------------------------
+
+int32_t device_count(uint32_t *out, turbo_error *err) {
+    return guarded(err, [&] {
+        *out = (uint32_t)devices().size();
+        return TURBO_OK;
+    });
+}
+
+int32_t device_info(uint32_t ordinal, turbo_device_info *out, turbo_error *err) {
+    return guarded(err, [&] {
+        if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device " + std::to_string(ordinal));
+        const int dev = devices()[ordinal];
+        hipDeviceProp_t p;
+        check(hipGetDeviceProperties(&p, dev), "hipGetDeviceProperties");
+        OnDevice on(dev);
+        size_t free_b = 0, total_b = 0;
+        check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+        int driver = 0;
+        (void)hipDriverGetVersion(&driver);
+        out->kind = TURBO_DEVICE_GPU;
+        out->ordinal = ordinal;
+        out->unified_memory = 0;
+        out->memory_total = total_b;
+        out->memory_free = free_b;
+        std::snprintf(out->arch, sizeof out->arch, "%s", "mi355x");
+        std::snprintf(out->name, sizeof out->name, "%s (%s)", p.name, p.gcnArchName);
+        std::snprintf(out->vendor, sizeof out->vendor, "%s", "AMD");
+        std::snprintf(out->runtime_version, sizeof out->runtime_version, "%s", runtime_version_string());
+        std::snprintf(out->driver_version, sizeof out->driver_version, "%d", driver);
+        return TURBO_OK;
+    });
+}
+
+// Fields of turbo_embed_options a run honors: normalize (4), pooling (5)
+// and output_dim (6), every value of each.
+constexpr uint32_t EMBED_HONORED = (1u << 3) | (1u << 4) | (1u << 5);
+
+int32_t capability(uint32_t ordinal, uint32_t task, uint32_t precision, uint32_t *status, uint32_t *dtype,
+                   uint32_t *options_honored, char *reason, uint32_t reason_len, turbo_error *err) {
+    return guarded(err, [&] {
+        if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device " + std::to_string(ordinal));
+        if (task != TURBO_TASK_EMBED && task != TURBO_TASK_RERANK) {
+            *status = TURBO_CAP_UNSUPPORTED;
+            *dtype = 0;
+            *options_honored = 0;
+            if (reason_len) std::snprintf(reason, reason_len, "the rocm backend runs the embed and rerank encoders alone");
+            return TURBO_OK;
+        }
+        *status = TURBO_CAP_EXPERIMENTAL;
+        *dtype = precision == TURBO_PRECISION_FASTEST ? TURBO_DTYPE_F16 : TURBO_DTYPE_F32;
+        *options_honored = EMBED_HONORED;
+        if (reason_len) reason[0] = 0;
+        return TURBO_OK;
+    });
+}
+
+// ---- Contexts and buffers ---------------------------------------------------------------
+
+int32_t context_create(uint32_t ordinal, turbo_log_fn log, void *ud, void **out, turbo_error *err) {
+    return guarded(err, [&] {
+        if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device " + std::to_string(ordinal));
+        auto c = std::make_unique<Context>();
+        c->ordinal = devices()[ordinal];
+        c->log = log;
+        c->log_user_data = ud;
+        OnDevice on(c->ordinal);
+        // Default priority: the one stream priority every run uses.
+        check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+        *out = c.release();
+        return TURBO_OK;
+    });
+}
+
+void context_release(void *ctx) {
+    if (!ctx) return;
+    Context *c = static_cast<Context *>(ctx);
+    {
+        OnDevice on(c->ordinal);
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipStreamDestroy(c->stream);
+    }
+    delete c;
+}
+
+uint64_t desc_bytes(const turbo_buffer_desc *d) {
+    if (d->bytes) return d->bytes;
+    uint64_t el = 0;
+    switch (d->dtype) {
+    case TURBO_DTYPE_I8:
+    case TURBO_DTYPE_U8: el = 1; break;
+    case TURBO_DTYPE_F16:
+    case TURBO_DTYPE_BF16: el = 2; break;
+    case TURBO_DTYPE_I32:
+    case TURBO_DTYPE_F32: el = 4; break;
+    default: el = 8;
+    }
+    uint64_t n = d->shape[0];
+    if (d->ndim == 2) n *= d->shape[1];
+    return n * el;
+}
+
+int32_t buffer_alloc(void *ctx, const turbo_buffer_desc *desc, void **out, void **host, turbo_error *err) {
+    return guarded(err, [&] {
+        Context *c = static_cast<Context *>(ctx);
+        OnDevice on(c->ordinal);
+        auto b = std::make_unique<Buffer>();
+        b->ctx = c;
+        b->placement = desc->placement;
+        b->bytes = desc_bytes(desc);
+        b->owned = true;
+        switch (desc->placement) {
+        case TURBO_PLACE_DEVICE: b->dev = dev_alloc(b->bytes, "buffer_alloc"); break;
+        case TURBO_PLACE_PINNED:
+            check(hipHostMalloc(&b->host, b->bytes, hipHostMallocDefault), "hipHostMalloc");
+            b->dev = b->host;
+            break;
+        case TURBO_PLACE_SHARED:
+            check(hipMallocManaged(&b->dev, b->bytes, hipMemAttachGlobal), "hipMallocManaged");
+            b->host = b->dev;
+            break;
+        case TURBO_PLACE_HOST:
+            b->host = std::malloc(b->bytes ? b->bytes : 1);
+            if (!b->host) fail(TURBO_E_OUT_OF_MEMORY, "rocm: host buffer");
+            break;
+        default: fail(TURBO_E_INVALID_ENUM, "rocm: placement " + std::to_string(desc->placement));
+        }
+        *host = b->placement == TURBO_PLACE_DEVICE ? nullptr : b->host;
+        *out = b.release();
+        return TURBO_OK;
+    });
+}
+
+int32_t buffer_import(void *ctx, const turbo_buffer_desc *desc, const turbo_native_handle *handle, void **out,
+                      void **host, turbo_error *err) {
+    return guarded(err, [&] {
+        Context *c = static_cast<Context *>(ctx);
+        auto b = std::make_unique<Buffer>();
+        b->ctx = c;
+        b->placement = desc->placement;
+        b->bytes = desc_bytes(desc);
+        b->owned = false;
+        char *p = reinterpret_cast<char *>(handle->handle) + handle->offset;
+        if (handle->kind == TURBO_HANDLE_CUDA_PTR && desc->placement == TURBO_PLACE_DEVICE) {
+            b->dev = p;
+        } else if (handle->kind == TURBO_HANDLE_HOST_PTR && desc->placement != TURBO_PLACE_DEVICE) {
+            b->host = p;
+            b->dev = p;
+        } else {
+            fail(TURBO_E_UNSUPPORTED, "rocm: handle kind " + std::to_string(handle->kind) + " for placement " +
+                                          std::to_string(desc->placement));
+        }
+        *host = desc->placement == TURBO_PLACE_DEVICE ? nullptr : b->host;
+        *out = b.release();
+        return TURBO_OK;
+    });
+}
+
+void buffer_release(void *buf) {
+    if (!buf) return;
+    Buffer *b = static_cast<Buffer *>(buf);
+    if (b->owned) {
+        OnDevice on(b->ctx->ordinal);
+        switch (b->placement) {
+        case TURBO_PLACE_DEVICE:
+        case TURBO_PLACE_SHARED: (void)hipFree(b->dev); break;
+        case TURBO_PLACE_PINNED: (void)hipHostFree(b->host); break;
+        case TURBO_PLACE_HOST: std::free(b->host); break;
+        }
+    }
+    delete b;
+}
+
+int32_t buffer_export(void *buf, uint32_t kind, turbo_native_handle *out, turbo_error *err) {
+    return guarded(err, [&] {
+        Buffer *b = static_cast<Buffer *>(buf);
+        if (kind == TURBO_HANDLE_CUDA_PTR && b->dev) {
+            out->kind = kind;
+            out->handle = reinterpret_cast<uint64_t>(b->dev);
+            out->aux = (uint64_t)b->ctx->ordinal;
+            out->offset = 0;
+            return TURBO_OK;
+        }
+        if (kind == TURBO_HANDLE_HOST_PTR && b->host) {
+            out->kind = kind;
+            out->handle = reinterpret_cast<uint64_t>(b->host);
+            out->aux = 0;
+            out->offset = 0;
+            return TURBO_OK;
+        }
+        fail(TURBO_E_UNSUPPORTED, "rocm: this buffer has no handle of kind " + std::to_string(kind));
+    });
+}
+
+int32_t buffer_read(void *buf, void *dst, uint64_t bytes, turbo_error *err) {
+    return guarded(err, [&] {
+        Buffer *b = static_cast<Buffer *>(buf);
+        if (bytes > b->bytes) fail(TURBO_E_INVALID_ARGUMENT, "rocm: read of " + std::to_string(bytes) +
+                                                                 " bytes from a buffer of " + std::to_string(b->bytes));
+        std::lock_guard<std::mutex> g(b->ctx->lock);
+        OnDevice on(b->ctx->ordinal);
+        check(hipMemcpyAsync(dst, b->dev ? b->dev : b->host, bytes, hipMemcpyDefault, b->ctx->stream), "buffer_read");
+        check(hipStreamSynchronize(b->ctx->stream), "buffer_read");
+        return TURBO_OK;
+    });
+}
+
+// ---- Models ------------------------------------------------------------------------
+
+int32_t model_load_fn(void *ctx, const turbo_backend_model *desc, void **out, turbo_error *err) {
+    return guarded(err, [&] {
+        *out = model_load(static_cast<Context *>(ctx), desc);
+        return TURBO_OK;
+    });
+}
+
+void model_release_fn(void *model) { model_release(static_cast<Model *>(model)); }
+
+// ---- Sessions ------------------------------------------------------------------------
+
+int32_t session_open_fn(void *model, const turbo_backend_session_desc *desc, turbo_backend_tuning *tuning,
+                        uint32_t *compute_dtype, void **out, turbo_error *err) {
+    return guarded(err, [&] {
+        Session *s = session_open(static_cast<Model *>(model), desc, tuning);
+        *compute_dtype = s->compute_dtype;
+        *out = s;
+        return TURBO_OK;
+    });
+}
+
+int32_t session_create_tuned_fn(void *model, uint32_t task, uint32_t max_batch, uint32_t max_seq, uint32_t precision,
+                                 turbo_backend_tuning *tuning, uint32_t *compute_dtype, void **out, turbo_error *err) {
+    turbo_backend_session_desc d{};
+    d.struct_size = sizeof d;
+    d.task = task;
+    d.max_batch = max_batch;
+    d.max_seq = max_seq;
+    d.precision = precision;
+    d.max_ranges = max_batch;
+    return session_open_fn(model, &d, tuning, compute_dtype, out, err);
+}
+
+int32_t session_create_fn(void *model, uint32_t task, uint32_t max_batch, uint32_t max_seq, uint32_t precision,
+                          uint32_t *compute_dtype, void **out, turbo_error *err) {
+    return session_create_tuned_fn(model, task, max_batch, max_seq, precision, nullptr, compute_dtype, out, err);
+}
+
+void session_release_fn(void *session) { session_release(static_cast<Session *>(session)); }
+
+int32_t embed_write_fn(void *session, const turbo_backend_embed_rows *rows, turbo_error *err) {
+    return guarded(err, [&] {
+        session_write(static_cast<Session *>(session), rows, nullptr, 0);
+        return TURBO_OK;
+    });
+}
+
+int32_t embed_write_ranges_fn(void *session, const turbo_backend_embed_rows *rows, const turbo_token_range *ranges,
+                              uint32_t count, turbo_error *err) {
+    return guarded(err, [&] {
+        if (count == 0) fail(TURBO_E_INVALID_ARGUMENT, "rocm: a range write needs at least one range");
+        session_write(static_cast<Session *>(session), rows, ranges, count);
+        return TURBO_OK;
+    });
+}
+
+int32_t session_run_fn(void *session, turbo_backend_run *out, turbo_error *err) {
+    return guarded(err, [&] {
+        session_run(static_cast<Session *>(session), out);
+        return TURBO_OK;
+    });
+}
+
+}  // namespace
+
+extern "C" {
+
+const turbo_backend turbo_rocm_backend = {
+    sizeof(turbo_backend),
+    0,
+    "rocm",
+    RUNTIME_VERSION,
+    device_count,
+    device_info,
+    capability,
+    context_create,
+    context_release,
+    buffer_alloc,
+    buffer_import,
+    buffer_release,
+    buffer_export,
+    model_load_fn,
+    model_release_fn,
+    session_create_fn,
+    session_release_fn,
+    embed_write_fn,
+    session_run_fn,
+    buffer_read,
+    TURBO_FORMAT_BIT(TURBO_FORMAT_SAFETENSORS),
+    0,
+    session_create_tuned_fn,
+    session_open_fn,
+    embed_write_ranges_fn,
+    0,
+    0,
+    nullptr,
+};
+
+}  // extern "C"

@@ -1,0 +1,89 @@
+// Launchers of the rocm backend's gfx950 kernels. Every launcher enqueues on
+// the given stream and returns the launch's error; none allocates or syncs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rocm {
+
+// The arithmetic type of a session's GEMM operands and activations.
+enum class Dt : int { F32 = 0, F16 = 1, BF16 = 2 };
+
+inline size_t dt_bytes(Dt d) { return d == Dt::F32 ? 4 : 2; }
+
+// Where each packed token of a run sits, written on the device by pack_rows
+// (reference core/src/cpu/encoder/mod.rs:379-424; core/cuda/kernels.h:56-77).
+// A row's tokens are its columns 0 .. len - 1 (len = last live column + 1),
+// one after another, rows in order.
+struct Packing {
+    int32_t *start;     // [max_batch] first packed token of each row
+    int32_t *len;       // [max_batch] packed tokens of each row
+    int32_t *at;        // [tcap] r * seq + p of each packed token
+    int32_t *row;       // [tcap] the row of each packed token
+    int32_t *tokens;    // [1] packed tokens of the run
+};
+
+hipError_t pack_rows(hipStream_t s, const int32_t *mask, int batch, int seq, Packing p);
+
+// x[t] = LN(word[id] + pos[p + offset] + type[ty]) (BERT, RoBERTa), or, with
+// pos NULL, LN(word[id] (+ type[ty] when type is not NULL)) (rotary
+// families); ln_b NULL is no bias. Writes x (F32) and, when xh is not NULL,
+// its copy in `dt`.
+hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
+                    const Packing &p, int seq, int position_offset, const float *word, const float *pos,
+                    const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt);
+
+// out = LN(in) row by row over `tokens` rows of `hidden`; out_f32 and out_h
+// (in `dt`) may each be NULL, and out_f32 may be in (in place). ln_b NULL is
+// no bias.
+hipError_t layer_norm(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
+                      float eps, float *out_f32, void *out_h, Dt dt);
+
+// What a GEMM does with each output once its sum is done.
+enum class Epi : int {
+    Plain = 0,     // outf[m, n] = acc + bias (F32 out; kernel tests)
+    Qkv = 1,       // head-major [3][heads][tcap][d] in the operand type: acc + bias
+    Gelu = 2,      // out[m, n] = gelu(acc + bias) in the operand type
+    Residual = 3,  // x[m, n] += acc + bias (F32)
+    QkvRope = 4,   // as Qkv, Q and K rotated by their tokens' positions (pair-adjacent columns)
+    Gated = 5,     // out[m, n / 2] = act(acc_n + b_n) * (acc_{n+1} + b_{n+1}) in the operand type
+};
+
+struct EpiArgs {
+    Epi kind = Epi::Plain;
+    const float *bias = nullptr;   // [n] or NULL
+    void *out = nullptr;           // Plain (F32), Qkv, Gelu, Gated: the output
+    int ldo = 0;                   // row stride of out (elements)
+    float *x = nullptr;            // Residual: [m, ldo] F32
+    int tcap = 0, heads = 0, d = 0, hidden = 0;   // Qkv scatter
+    const float *cos = nullptr, *sin = nullptr;   // QkvRope: [positions][d / 2]
+    const int32_t *at = nullptr;   // QkvRope: each token's r * seq + p
+    int seq = 0;
+    int silu = 0;                  // Gated: SiLU instead of GELU
+};
+
+// C[m, n] = sum_k A[m, k] W[n, k] over m < M (rows of A, ld lda), n < N, k < K,
+// operands in `dt`, F32 accumulation on MFMA, then the epilogue. `tile`
+// picks the block shape (0 = the launcher's choice for the shape).
+hipError_t gemm(hipStream_t s, Dt dt, int M, int N, int K, const void *A, int lda, const void *W,
+                const EpiArgs &e, int tile = 0);
+int gemm_tiles();   // how many block shapes `tile` may name (1..n)
+
+// Softmax attention within each row and head over head-major Q, K, V
+// ([3][heads][tcap][d] in `dt`), into ctx [tokens, heads * d] in `dt`.
+// window: keys within `window` of the query (|i - j| <= window), or INT32_MAX.
+hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
+                     const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx);
+
+// One vector per row (mode 0: MEAN/CLS/LAST as pooling says) or per range
+// (mode 1: the mean over the range's live tokens), cut to output_dim, L2
+// normalized when l2, into out [count, output_dim] F32.
+hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
+                int count, const uint32_t *ranges, int pooling, int output_dim, int l2, float *out);
+
+// F32 -> F16 (round to nearest even) or BF16 copies of weights; `overflow`
+// (device int, may be NULL) is set to 1 when an F16 value overflows.
+hipError_t narrow(hipStream_t s, const float *src, void *dst, size_t n, Dt dt, int32_t *overflow);
+
+}  // namespace rocm

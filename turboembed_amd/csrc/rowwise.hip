@@ -1,0 +1,340 @@
+// Row-wise kernels of the encoder: packing, embedding + LayerNorm, LayerNorm,
+// pooling (rows and ranges) with the cut and L2, and weight narrowing.
+// All are HBM-bound; each reads its input once, coalesced, with wave64
+// shuffle reductions and no atomics on floats.
+#include "kernels.h"
+#include "devmath.h"
+
+namespace rocm {
+
+// ---- Packing ------------------------------------------------------------------
+//
+// One workgroup. Each row's packed length is its last live column + 1
+// (reference core/src/cpu/encoder/mod.rs:395-405; core/cuda/kernels.cu:290-381):
+// integer maxima in LDS, then an exclusive scan in row order, then each
+// token's place. Integer work only, so the result is exact.
+__global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restrict__ mask, int batch, int seq,
+                                                         Packing p) {
+    extern __shared__ int32_t lens[];
+    for (int r = threadIdx.x; r < batch; r += blockDim.x) lens[r] = 0;
+    __syncthreads();
+    const int n = batch * seq;
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
+        if (mask[i] != 0) atomicMax(&lens[i / seq], i % seq + 1);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int t = 0;
+        for (int r = 0; r < batch; ++r) {
+            const int l = lens[r];
+            p.start[r] = t;
+            p.len[r] = l;
+            lens[r] = t;   // now each row's start
+            t += l;
+        }
+        p.tokens[0] = t;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int r = i / seq, c = i % seq;
+        if (c < p.len[r]) {
+            p.at[lens[r] + c] = i;
+            p.row[lens[r] + c] = r;
+        }
+    }
+}
+
+hipError_t pack_rows(hipStream_t s, const int32_t *mask, int batch, int seq, Packing p) {
+    hipLaunchKernelGGL(pack_rows_kernel, dim3(1), dim3(1024), batch * sizeof(int32_t), s, mask, batch, seq, p);
+    return hipGetLastError();
+}
+
+// ---- LayerNorm over one token per wave ------------------------------------------
+//
+// Each lane holds V values of the row, columns lane + 64 * v. The mean and
+// the biased variance are summed in F32 across the wave, the variance about
+// the mean (two passes over registers).
+template <int V>
+__device__ __forceinline__ void ln_wave(float (&v)[V], int hidden, const float *__restrict__ w,
+                                        const float *__restrict__ b, float eps) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+        if (lane + 64 * i < hidden) s += v[i];
+    const float mean = wave_sum(s) / (float)hidden;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+        if (lane + 64 * i < hidden) {
+            const float c = v[i] - mean;
+            q = fmaf(c, c, q);
+        }
+    const float var = wave_sum(q) / (float)hidden;
+    const float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = lane + 64 * i;
+        if (c < hidden) v[i] = (v[i] - mean) * inv * w[c] + (b ? b[c] : 0.0f);
+    }
+}
+
+template <int V, typename H>
+__device__ __forceinline__ void store_row(const float (&v)[V], int hidden, float *xf, H *xh) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = lane + 64 * i;
+        if (c < hidden) {
+            if (xf) xf[c] = v[i];
+            if (xh) xh[c] = from_f32<H>(v[i]);
+        }
+    }
+}
+
+template <int V, typename H>
+__global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, const int32_t *__restrict__ ids,
+                                                       const int32_t *__restrict__ types, Packing p, int seq,
+                                                       int offset, const float *__restrict__ word,
+                                                       const float *__restrict__ pos, const float *__restrict__ type,
+                                                       const float *__restrict__ ln_w, const float *__restrict__ ln_b,
+                                                       float eps, float *__restrict__ x, H *__restrict__ xh) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    const int lane = threadIdx.x & 63;
+    const int at = p.at[t];
+    const int id = ids[at];
+    const int ty = types ? types[at] : 0;
+    const float *wr = word + (size_t)id * hidden;
+    const float *pr = pos ? pos + (size_t)(at % seq + offset) * hidden : nullptr;
+    const float *tr = type ? type + (size_t)ty * hidden : nullptr;
+    float v[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = lane + 64 * i;
+        float a = 0.0f;
+        if (c < hidden) {
+            a = wr[c];
+            if (pr) a = a + pr[c];
+            if (tr) a = a + tr[c];
+        }
+        v[i] = a;
+    }
+    ln_wave<V>(v, hidden, ln_w, ln_b, eps);
+    store_row<V, H>(v, hidden, x + (size_t)t * hidden, xh ? xh + (size_t)t * hidden : nullptr);
+}
+
+template <int V, typename H>
+__global__ void __launch_bounds__(256) layer_norm_kernel(int tokens, int hidden, const float *__restrict__ in,
+                                                         const float *__restrict__ ln_w,
+                                                         const float *__restrict__ ln_b, float eps, float *out_f32,
+                                                         H *__restrict__ out_h) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    const int lane = threadIdx.x & 63;
+    const float *row = in + (size_t)t * hidden;
+    float v[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = lane + 64 * i;
+        v[i] = c < hidden ? row[c] : 0.0f;
+    }
+    ln_wave<V>(v, hidden, ln_w, ln_b, eps);
+    store_row<V, H>(v, hidden, out_f32 ? out_f32 + (size_t)t * hidden : nullptr,
+                    out_h ? out_h + (size_t)t * hidden : nullptr);
+}
+
+template <typename H, int V>
+static hipError_t embed_ln_v(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
+                             const Packing &p, int seq, int offset, const float *word, const float *pos,
+                             const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh) {
+    hipLaunchKernelGGL((embed_ln_kernel<V, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, ids, types, p,
+                       seq, offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh);
+    return hipGetLastError();
+}
+
+template <typename H, int V>
+static hipError_t ln_v(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
+                       float eps, float *out_f32, void *out_h) {
+    hipLaunchKernelGGL((layer_norm_kernel<V, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, in, ln_w,
+                       ln_b, eps, out_f32, (H *)out_h);
+    return hipGetLastError();
+}
+
+// The lane count V = ceil(hidden / 64), up to hidden 2048.
+#define ROWWISE_DISPATCH(FN, ...)                                                              \
+    {                                                                                          \
+        const int v = (hidden + 63) / 64;                                                      \
+        if (v <= 1) return FN<H, 1>(__VA_ARGS__);                                              \
+        if (v <= 2) return FN<H, 2>(__VA_ARGS__);                                              \
+        if (v <= 4) return FN<H, 4>(__VA_ARGS__);                                              \
+        if (v <= 6) return FN<H, 6>(__VA_ARGS__);                                              \
+        if (v <= 8) return FN<H, 8>(__VA_ARGS__);                                              \
+        if (v <= 12) return FN<H, 12>(__VA_ARGS__);                                            \
+        if (v <= 16) return FN<H, 16>(__VA_ARGS__);                                            \
+        if (v <= 32) return FN<H, 32>(__VA_ARGS__);                                            \
+        return hipErrorInvalidValue;                                                           \
+    }
+
+template <typename H>
+static hipError_t embed_ln_t(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
+                             const Packing &p, int seq, int offset, const float *word, const float *pos,
+                             const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh) {
+    ROWWISE_DISPATCH(embed_ln_v, s, tokens, hidden, ids, types, p, seq, offset, word, pos, type, ln_w, ln_b, eps, x, xh)
+}
+
+template <typename H>
+static hipError_t ln_t(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
+                       float eps, float *out_f32, void *out_h) {
+    ROWWISE_DISPATCH(ln_v, s, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h)
+}
+
+hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
+                    const Packing &p, int seq, int position_offset, const float *word, const float *pos,
+                    const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt) {
+    if (tokens <= 0) return hipSuccess;
+    switch (dt) {
+    case Dt::F16:
+        return embed_ln_t<_Float16>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w,
+                                    ln_b, eps, x, xh);
+    case Dt::BF16:
+        return embed_ln_t<__bf16>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w, ln_b,
+                                  eps, x, xh);
+    default:
+        return embed_ln_t<float>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w, ln_b,
+                                 eps, x, xh);
+    }
+}
+
+hipError_t layer_norm(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
+                      float eps, float *out_f32, void *out_h, Dt dt) {
+    if (tokens <= 0) return hipSuccess;
+    switch (dt) {
+    case Dt::F16: return ln_t<_Float16>(s, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h);
+    case Dt::BF16: return ln_t<__bf16>(s, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h);
+    default: return ln_t<float>(s, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h);
+    }
+}
+
+// ---- Pooling ----------------------------------------------------------------------
+//
+// One workgroup per output vector. Mode 0 pools row i as `pooling` says;
+// mode 1 pools range i, (row, start, end) in `ranges`. A mean is the F32 sum
+// of the live tokens' states in column order, times one over their count
+// (reference core/src/cpu/encoder/mod.rs:443-468); a row's mean is the range
+// (row, 0, len) through the same code, so a whole-row range gives the row's
+// vector bit for bit. The cut to output_dim comes before the L2 norm, summed
+// in F64 and floored at 1e-12 (mod.rs:470-482).
+constexpr int POOL_THREADS = 256;
+
+__global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const float *__restrict__ x, int hidden, Packing p,
+                                                            const int32_t *__restrict__ mask, int seq, int mode,
+                                                            const uint32_t *__restrict__ ranges, int pooling, int od,
+                                                            int l2, float *__restrict__ out) {
+    __shared__ double part[POOL_THREADS / 64];
+    __shared__ int flag;
+    const int i = blockIdx.x;
+    int r, c0, c1;
+    if (mode == 0) {
+        r = i;
+        c0 = 0;
+        c1 = p.len[r];
+    } else {
+        r = (int)ranges[3 * i];
+        c0 = (int)ranges[3 * i + 1];
+        c1 = min((int)ranges[3 * i + 2], p.len[r]);
+    }
+    const int start = p.start[r];
+    const int32_t *mk = mask + (size_t)r * seq;
+    constexpr int MAXV = 8;   // output_dim up to 2048
+    float acc[MAXV];
+#pragma unroll
+    for (int v = 0; v < MAXV; ++v) acc[v] = 0.0f;
+    if (mode == 0 && pooling != 1) {
+        const int tok = pooling == 2 ? start : start + p.len[r] - 1;   // CLS: column 0; LAST: last live
+#pragma unroll
+        for (int v = 0; v < MAXV; ++v) {
+            const int c = threadIdx.x + POOL_THREADS * v;
+            if (c < od) acc[v] = x[(size_t)tok * hidden + c];
+        }
+    } else {
+        if (threadIdx.x == 0) {
+            int any = 0;
+            for (int q = c0; q < c1 && !any; ++q) any = mk[q] != 0;
+            flag = any;
+        }
+        __syncthreads();
+        const bool live_only = flag != 0;
+        int n = 0;
+        for (int q = c0; q < c1; ++q) {
+            if (live_only && mk[q] == 0) continue;
+            const float *row = x + (size_t)(start + q) * hidden;
+#pragma unroll
+            for (int v = 0; v < MAXV; ++v) {
+                const int c = threadIdx.x + POOL_THREADS * v;
+                if (c < od) acc[v] = __fadd_rn(acc[v], row[c]);
+            }
+            ++n;
+        }
+        const float inv = __fdiv_rn(1.0f, (float)n);
+#pragma unroll
+        for (int v = 0; v < MAXV; ++v) acc[v] = __fmul_rn(acc[v], inv);
+    }
+    if (l2) {
+        double s = 0.0;
+#pragma unroll
+        for (int v = 0; v < MAXV; ++v) {
+            const int c = threadIdx.x + POOL_THREADS * v;
+            if (c < od) s += (double)acc[v] * (double)acc[v];
+        }
+        s = wave_sum(s);
+        if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+        __syncthreads();
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < POOL_THREADS / 64; ++w) tot += part[w];
+        const double norm = fmax(sqrt(tot), 1e-12);
+        const float inv = (float)(1.0 / norm);
+#pragma unroll
+        for (int v = 0; v < MAXV; ++v) acc[v] = __fmul_rn(acc[v], inv);
+    }
+#pragma unroll
+    for (int v = 0; v < MAXV; ++v) {
+        const int c = threadIdx.x + POOL_THREADS * v;
+        if (c < od) out[(size_t)i * od + c] = acc[v];
+    }
+}
+
+hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq, int count,
+                const uint32_t *ranges, int pooling, int output_dim, int l2, float *out) {
+    if (output_dim > 8 * POOL_THREADS) return hipErrorInvalidValue;
+    if (count <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pool_kernel, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq,
+                       ranges ? 1 : 0, ranges, pooling, output_dim, l2, out);
+    return hipGetLastError();
+}
+
+// ---- Weight narrowing ------------------------------------------------------------------
+
+template <typename H>
+__global__ void narrow_kernel(const float *__restrict__ src, H *__restrict__ dst, size_t n, int32_t *overflow) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const float v = src[i];
+        const H h = from_f32<H>(v);
+        if (overflow && isinf(to_f32(h)) && !isinf(v)) *overflow = 1;
+        dst[i] = h;
+    }
+}
+
+hipError_t narrow(hipStream_t s, const float *src, void *dst, size_t n, Dt dt, int32_t *overflow) {
+    const int blocks = (int)std::min<size_t>((n + 255) / 256, 65536);
+    if (n == 0) return hipSuccess;
+    if (dt == Dt::F16)
+        hipLaunchKernelGGL(narrow_kernel<_Float16>, dim3(blocks), dim3(256), 0, s, src, (_Float16 *)dst, n, overflow);
+    else if (dt == Dt::BF16)
+        hipLaunchKernelGGL(narrow_kernel<__bf16>, dim3(blocks), dim3(256), 0, s, src, (__bf16 *)dst, n, overflow);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace rocm

@@ -1,0 +1,832 @@
+// Models and sessions of the rocm backend: weights on the device, the
+// session's memory, rows written, and the run's kernels.
+//
+// A run's kernels, in order (the reference's CPU run, core/src/cpu/encoder/
+// mod.rs:309-374 and rotary/mod.rs:88-175, and the CUDA graph,
+// core/cuda/backend.cpp:2020-2361):
+//   pack_rows -> embed_ln -> per layer { QKV GEMM (+bias, head-major; RoPE on
+//   the rotary families) -> attention -> out GEMM (+bias, residual into x) ->
+//   LayerNorm -> FFN-in GEMM (+bias, GELU; or the gated product) -> FFN-out
+//   GEMM (+bias, residual) -> LayerNorm } -> pool (+cut, +L2).
+// ModernBERT is pre-norm: the norms come before the products they feed and
+// final_norm follows the last layer.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "session.h"
+#include "turbo_rocm.h"
+
+namespace rocm {
+
+// ---- Weights ---------------------------------------------------------------------
+
+namespace {
+
+float half_bits_to_float(uint16_t h) {
+    const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31, m = h & 1023;
+    uint32_t u;
+    if (e == 0) {
+        if (m == 0) {
+            u = s;
+        } else {
+            float f = std::ldexp((float)m, -24);
+            std::memcpy(&u, &f, 4);
+            u |= s;
+        }
+    } else if (e == 31) {
+        u = s | 0x7f800000u | (m << 13);
+    } else {
+        u = s | ((e - 15 + 127) << 23) | (m << 13);
+    }
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// Assembles every tensor the kernels read, in F32, into one host image laid
+// out as the device copy will be; each piece starts on a 256-byte boundary.
+struct Image {
+    std::vector<float> data;
+    size_t add(size_t n) {
+        const size_t at = (data.size() + 63) / 64 * 64;
+        data.resize(at + n, 0.0f);
+        return at;
+    }
+};
+
+const turbo_backend_tensor &tensor_at(const turbo_backend_model *d, uint32_t i) { return d->tensors[i]; }
+
+// Widen tensor i to F32 into dst (n floats), checking its size.
+void widen(const turbo_backend_model *d, uint32_t i, size_t n, float *dst, const char *what) {
+    const turbo_backend_tensor &t = tensor_at(d, i);
+    const size_t el = d->dtype == TURBO_DTYPE_F32 ? 4 : 2;
+    if (!t.data || t.bytes != n * el)
+        fail(TURBO_E_INVALID_ARGUMENT, std::string("rocm: tensor ") + std::to_string(i) + " (" +
+                                           (t.name ? t.name : what) + ") holds " + std::to_string(t.bytes) +
+                                           " bytes, not " + std::to_string(n * el));
+    if (d->dtype == TURBO_DTYPE_F32) {
+        std::memcpy(dst, t.data, n * 4);
+        return;
+    }
+    const uint16_t *src = static_cast<const uint16_t *>(t.data);
+    if (d->dtype == TURBO_DTYPE_F16) {
+        for (size_t k = 0; k < n; ++k) dst[k] = half_bits_to_float(src[k]);
+    } else {
+        for (size_t k = 0; k < n; ++k) {
+            const uint32_t u = (uint32_t)src[k] << 16;
+            std::memcpy(&dst[k], &u, 4);
+        }
+    }
+}
+
+}  // namespace
+
+Model *model_load(Context *c, const turbo_backend_model *d) {
+    if (d->struct_size < offsetof(turbo_backend_model, tensors) + sizeof(void *))
+        fail(TURBO_E_INVALID_STRUCT_SIZE, "rocm: turbo_backend_model of " + std::to_string(d->struct_size) + " bytes");
+    const bool bert = d->family == TURBO_FAMILY_BERT || d->family == TURBO_FAMILY_ROBERTA;
+    const bool modern = d->family == TURBO_FAMILY_MODERNBERT, nomic = d->family == TURBO_FAMILY_NOMIC_BERT;
+    if (!bert && !modern && !nomic)
+        fail(TURBO_E_UNSUPPORTED, "rocm: family " + std::to_string(d->family) +
+                                      ": the rocm backend runs BERT, RoBERTa, ModernBERT and nomic-bert encoders");
+    if (d->format != TURBO_FORMAT_SAFETENSORS) fail(TURBO_E_UNSUPPORTED, "rocm: only raw weights (safetensors) load");
+    if (d->dtype != TURBO_DTYPE_F32 && d->dtype != TURBO_DTYPE_F16 && d->dtype != TURBO_DTYPE_BF16)
+        fail(TURBO_E_UNSUPPORTED, "rocm: weights of dtype " + std::to_string(d->dtype));
+    if (d->lookahead != 0) fail(TURBO_E_UNSUPPORTED, "rocm: a banded (lookahead) model");
+    if (d->heads == 0 || d->hidden % d->heads != 0) fail(TURBO_E_INVALID_ARGUMENT, "rocm: hidden is not heads * d");
+    const uint32_t H = d->hidden, dh = H / d->heads, I = d->intermediate;
+    if (dh != 8 && dh != 16 && dh != 32 && dh != 64 && dh != 128)
+        fail(TURBO_E_UNSUPPORTED, "rocm: head width " + std::to_string(dh) + " (8, 16, 32, 64 or 128)");
+    if (H % 8 != 0 || I % 8 != 0 || H > 2048)
+        fail(TURBO_E_UNSUPPORTED, "rocm: hidden " + std::to_string(H) + " and intermediate " + std::to_string(I) +
+                                      " must be multiples of 8, hidden at most 2048");
+    if (d->head && d->head_out) fail(TURBO_E_UNSUPPORTED, "rocm: a token head on the device");
+
+    auto m = std::make_unique<Model>();
+    m->ctx = c;
+    m->family = d->family;
+    m->dtype = d->dtype;
+    m->layers = d->layers;
+    m->hidden = H;
+    m->heads = d->heads;
+    m->inter = I;
+    m->vocab = d->vocab_size;
+    m->positions = d->max_positions;
+    m->types = d->token_types;
+    m->position_offset = d->position_offset;
+    m->eps = (float)d->layer_norm_eps;
+    m->rotary = modern || nomic;
+    m->modern = modern;
+
+    Image img;
+    struct Off {
+        size_t word = 0, pos = SIZE_MAX, type = SIZE_MAX, emb_w = 0, emb_b = SIZE_MAX, final_w = SIZE_MAX,
+               rope = SIZE_MAX;
+    } off;
+    struct LOff {
+        size_t wqkv, bqkv = SIZE_MAX, wo, bo = SIZE_MAX, ln1_w = SIZE_MAX, ln1_b = SIZE_MAX, w1, b1 = SIZE_MAX, w2,
+                     b2 = SIZE_MAX, ln2_w, ln2_b = SIZE_MAX;
+        size_t n_in;
+    };
+    std::vector<LOff> loff(d->layers);
+    auto put = [&](uint32_t i, size_t n, const char *what) {
+        const size_t at = img.add(n);
+        widen(d, i, n, &img.data[at], what);
+        return at;
+    };
+    if (bert) {
+        if (d->tensor_count != TURBO_BERT_EMBEDDING_TENSORS + d->layers * TURBO_BERT_LAYER_TENSORS)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: tensor_count " + std::to_string(d->tensor_count));
+        off.word = put(TURBO_BERT_WORD_EMBEDDINGS, (size_t)d->vocab_size * H, "word");
+        off.pos = put(TURBO_BERT_POSITION_EMBEDDINGS, (size_t)d->max_positions * H, "position");
+        off.type = put(TURBO_BERT_TOKEN_TYPE_EMBEDDINGS, (size_t)std::max(1u, d->token_types) * H, "type");
+        off.emb_w = put(TURBO_BERT_EMBEDDINGS_LN_WEIGHT, H, "ln");
+        off.emb_b = put(TURBO_BERT_EMBEDDINGS_LN_BIAS, H, "ln");
+        for (uint32_t l = 0; l < d->layers; ++l) {
+            const uint32_t b = TURBO_BERT_EMBEDDING_TENSORS + l * TURBO_BERT_LAYER_TENSORS;
+            LOff &o = loff[l];
+            // Q, K and V back to back: one [3H, H] product.
+            o.wqkv = img.add((size_t)3 * H * H);
+            widen(d, b + TURBO_BERT_Q_WEIGHT, (size_t)H * H, &img.data[o.wqkv], "q");
+            widen(d, b + TURBO_BERT_K_WEIGHT, (size_t)H * H, &img.data[o.wqkv + (size_t)H * H], "k");
+            widen(d, b + TURBO_BERT_V_WEIGHT, (size_t)H * H, &img.data[o.wqkv + (size_t)2 * H * H], "v");
+            o.bqkv = img.add((size_t)3 * H);
+            widen(d, b + TURBO_BERT_Q_BIAS, H, &img.data[o.bqkv], "q bias");
+            widen(d, b + TURBO_BERT_K_BIAS, H, &img.data[o.bqkv + H], "k bias");
+            widen(d, b + TURBO_BERT_V_BIAS, H, &img.data[o.bqkv + 2 * H], "v bias");
+            o.wo = put(b + TURBO_BERT_ATTN_OUT_WEIGHT, (size_t)H * H, "out");
+            o.bo = put(b + TURBO_BERT_ATTN_OUT_BIAS, H, "out bias");
+            o.ln1_w = put(b + TURBO_BERT_ATTN_LN_WEIGHT, H, "attn ln");
+            o.ln1_b = put(b + TURBO_BERT_ATTN_LN_BIAS, H, "attn ln");
+            o.w1 = put(b + TURBO_BERT_FFN_IN_WEIGHT, (size_t)I * H, "ffn in");
+            o.b1 = put(b + TURBO_BERT_FFN_IN_BIAS, I, "ffn in bias");
+            o.w2 = put(b + TURBO_BERT_FFN_OUT_WEIGHT, (size_t)H * I, "ffn out");
+            o.b2 = put(b + TURBO_BERT_FFN_OUT_BIAS, H, "ffn out bias");
+            o.ln2_w = put(b + TURBO_BERT_FFN_LN_WEIGHT, H, "ffn ln");
+            o.ln2_b = put(b + TURBO_BERT_FFN_LN_BIAS, H, "ffn ln");
+            o.n_in = I;
+        }
+    } else {
+        if (d->struct_size < offsetof(turbo_backend_model, global_every) + 4)
+            fail(TURBO_E_INVALID_STRUCT_SIZE, "rocm: a rotary model needs the rotary fields");
+        if (d->mlp != TURBO_MLP_GATED || dh % 2 || d->rope_pairs * 2 != dh || !d->rope_table)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: a rotary model has a gated MLP and a rope table of d/2 pairs");
+        const uint32_t emb = modern ? TURBO_MODERNBERT_EMBEDDING_TENSORS : TURBO_NOMIC_EMBEDDING_TENSORS;
+        const uint32_t per = modern ? TURBO_MODERNBERT_LAYER_TENSORS : TURBO_NOMIC_LAYER_TENSORS;
+        if (d->tensor_count != emb + d->layers * per)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: tensor_count " + std::to_string(d->tensor_count));
+        m->silu = d->activation == TURBO_ACTIVATION_SILU;
+        m->window = d->attention_window / 2;
+        m->global_every = d->global_every;
+        m->pairs = d->rope_pairs;
+        if (modern) {
+            off.word = put(TURBO_MODERNBERT_WORD_EMBEDDINGS, (size_t)d->vocab_size * H, "word");
+            off.emb_w = put(TURBO_MODERNBERT_EMBEDDINGS_LN_WEIGHT, H, "ln");
+            off.final_w = put(TURBO_MODERNBERT_FINAL_NORM_WEIGHT, H, "final norm");
+        } else {
+            off.word = put(TURBO_NOMIC_WORD_EMBEDDINGS, (size_t)d->vocab_size * H, "word");
+            off.type = put(TURBO_NOMIC_TOKEN_TYPE_EMBEDDINGS, (size_t)std::max(1u, d->token_types) * H, "type");
+            off.emb_w = put(TURBO_NOMIC_EMBEDDINGS_LN_WEIGHT, H, "ln");
+            off.emb_b = put(TURBO_NOMIC_EMBEDDINGS_LN_BIAS, H, "ln");
+        }
+        const size_t rope_n = (size_t)4 * d->max_positions * d->rope_pairs;
+        off.rope = img.add(rope_n);
+        std::memcpy(&img.data[off.rope], d->rope_table, rope_n * 4);
+        std::vector<float> tmp;
+        for (uint32_t l = 0; l < d->layers; ++l) {
+            const uint32_t b = emb + l * per;
+            LOff &o = loff[l];
+            // Q and K rows pair-adjacent per head, (c, c + d/2), V as stored
+            // (reference core/src/cpu/kernels/pairs.rs:146-161): the RoPE
+            // epilogue then finds each pair in neighbouring columns.
+            tmp.resize((size_t)3 * H * H);
+            widen(d, b + (modern ? TURBO_MODERNBERT_QKV_WEIGHT : TURBO_NOMIC_QKV_WEIGHT), tmp.size(), tmp.data(),
+                  "qkv");
+            o.wqkv = img.add(tmp.size());
+            size_t row = 0;
+            for (uint32_t third = 0; third < 2; ++third)
+                for (uint32_t head = 0; head < H; head += dh)
+                    for (uint32_t cc = 0; cc < dh / 2; ++cc)
+                        for (uint32_t src : {third * H + head + cc, third * H + head + cc + dh / 2})
+                            std::memcpy(&img.data[o.wqkv + (row++) * H], &tmp[(size_t)src * H], H * 4);
+            std::memcpy(&img.data[o.wqkv + row * H], &tmp[(size_t)2 * H * H], (size_t)H * H * 4);
+            o.wo = put(b + (modern ? TURBO_MODERNBERT_ATTN_OUT_WEIGHT : TURBO_NOMIC_ATTN_OUT_WEIGHT), (size_t)H * H,
+                       "out");
+            // Gate row j then up row j (pairs.rs:163-166).
+            std::vector<float> gate((size_t)I * H), up((size_t)I * H);
+            if (modern) {
+                tmp.resize((size_t)2 * I * H);
+                widen(d, b + TURBO_MODERNBERT_FFN_IN_WEIGHT, tmp.size(), tmp.data(), "ffn in");
+                std::copy(tmp.begin(), tmp.begin() + (size_t)I * H, gate.begin());
+                std::copy(tmp.begin() + (size_t)I * H, tmp.end(), up.begin());
+            } else {
+                widen(d, b + TURBO_NOMIC_FFN_GATE_WEIGHT, gate.size(), gate.data(), "ffn gate");
+                widen(d, b + TURBO_NOMIC_FFN_UP_WEIGHT, up.size(), up.data(), "ffn up");
+            }
+            o.w1 = img.add((size_t)2 * I * H);
+            for (uint32_t j = 0; j < I; ++j) {
+                std::memcpy(&img.data[o.w1 + (size_t)(2 * j) * H], &gate[(size_t)j * H], H * 4);
+                std::memcpy(&img.data[o.w1 + (size_t)(2 * j + 1) * H], &up[(size_t)j * H], H * 4);
+            }
+            o.w2 = put(b + (modern ? TURBO_MODERNBERT_FFN_OUT_WEIGHT : TURBO_NOMIC_FFN_OUT_WEIGHT), (size_t)H * I,
+                       "ffn out");
+            if (modern) {
+                if (l > 0) o.ln1_w = put(b + TURBO_MODERNBERT_ATTN_LN_WEIGHT, H, "attn norm");
+                o.ln2_w = put(b + TURBO_MODERNBERT_FFN_LN_WEIGHT, H, "mlp norm");
+            } else {
+                o.ln1_w = put(b + TURBO_NOMIC_ATTN_LN_WEIGHT, H, "norm1");
+                o.ln1_b = put(b + TURBO_NOMIC_ATTN_LN_BIAS, H, "norm1");
+                o.ln2_w = put(b + TURBO_NOMIC_FFN_LN_WEIGHT, H, "norm2");
+                o.ln2_b = put(b + TURBO_NOMIC_FFN_LN_BIAS, H, "norm2");
+            }
+            o.n_in = (size_t)2 * I;
+        }
+    }
+
+    OnDevice on(c->ordinal);
+    m->f32.reset(dev_alloc(img.data.size() * 4, "model weights"));
+    check(hipMemcpy(m->f32.get(), img.data.data(), img.data.size() * 4, hipMemcpyHostToDevice), "model weights");
+    const float *base = static_cast<const float *>(m->f32.get());
+    auto at = [&](size_t o) -> const float * { return o == SIZE_MAX ? nullptr : base + o; };
+    m->word = at(off.word);
+    m->pos = at(off.pos);
+    m->type = at(off.type);
+    m->emb_w = at(off.emb_w);
+    m->emb_b = at(off.emb_b);
+    m->final_w = at(off.final_w);
+    m->rope = at(off.rope);
+    for (const LOff &o : loff) {
+        Model::Layer L{};
+        L.wqkv = at(o.wqkv);
+        L.bqkv = at(o.bqkv);
+        L.wo = at(o.wo);
+        L.bo = at(o.bo);
+        L.ln1_w = at(o.ln1_w);
+        L.ln1_b = at(o.ln1_b);
+        L.w1 = at(o.w1);
+        L.b1 = at(o.b1);
+        L.w2 = at(o.w2);
+        L.b2 = at(o.b2);
+        L.ln2_w = at(o.ln2_w);
+        L.ln2_b = at(o.ln2_b);
+        L.n_qkv = (size_t)3 * H;
+        L.n_in = o.n_in;
+        m->ls.push_back(L);
+    }
+    // The F32 weights serve the F32 tier as they are.
+    for (const Model::Layer &L : m->ls) m->gemm_w[(int)Dt::F32].push_back({L.wqkv, L.wo, L.w1, L.w2});
+    return m.release();
+}
+
+// The GEMM weights narrowed to `dt`, made on the first session that needs
+// them and kept with the model (reference turbo.h: one resident copy per
+// compute dtype, shared by the model's sessions).
+std::vector<LayerWeights> &Model::weights_in(Dt dt) {
+    std::lock_guard<std::mutex> g(lock);
+    auto &w = gemm_w[(int)dt];
+    if (!w.empty()) return w;
+    const size_t H = hidden;
+    size_t total = 0;
+    for (const Layer &L : ls) total += L.n_qkv * H + H * H + L.n_in * H + H * inter;
+    OnDevice on(ctx->ordinal);
+    narrowed[(int)dt].reset(dev_alloc(total * 2 + 256, "narrowed weights"));
+    char *p = static_cast<char *>(narrowed[(int)dt].get());
+    int32_t *flag = reinterpret_cast<int32_t *>(p + total * 2);
+    check(hipMemsetAsync(flag, 0, 4, ctx->stream), "narrowing weights");
+    std::vector<LayerWeights> out;
+    size_t at = 0;
+    auto one = [&](const float *src, size_t n) {
+        void *dst = p + at * 2;
+        check(narrow(ctx->stream, src, dst, n, dt, flag), "narrowing weights");
+        at += n;
+        return (const void *)dst;
+    };
+    for (const Layer &L : ls) {
+        LayerWeights lw;
+        lw.qkv = one(L.wqkv, L.n_qkv * H);
+        lw.out = one(L.wo, H * H);
+        lw.ffn_in = one(L.w1, L.n_in * H);
+        lw.ffn_out = one(L.w2, H * inter);
+        out.push_back(lw);
+    }
+    int32_t over = 0;
+    check(hipMemcpyAsync(&over, flag, 4, hipMemcpyDeviceToHost, ctx->stream), "narrowing weights");
+    check(hipStreamSynchronize(ctx->stream), "narrowing weights");
+    if (dt == Dt::F16 && over) f16_overflow = true;
+    w = std::move(out);
+    return w;
+}
+
+void model_release(Model *m) {
+    if (!m) return;
+    {
+        OnDevice on(m->ctx->ordinal);
+        (void)hipStreamSynchronize(m->ctx->stream);
+        for (auto &n : m->narrowed) n.reset();
+        m->f32.reset();
+    }
+    delete m;
+}
+
+// ---- Sessions -----------------------------------------------------------------------
+
+namespace {
+
+// The numeric class a dtype's GEMMs compute in. BF16 has none in the
+// reference's header; this backend's is the next free bit.
+uint32_t numeric_of(Dt dt) {
+    switch (dt) {
+    case Dt::F16: return TURBO_NUMERIC_F16_F32ACC;
+    case Dt::BF16: return TURBO_ROCM_NUMERIC_BF16_F32ACC;
+    default: return TURBO_NUMERIC_F32_FMA;
+    }
+}
+
+uint32_t dtype_of(Dt dt) {
+    switch (dt) {
+    case Dt::F16: return TURBO_DTYPE_F16;
+    case Dt::BF16: return TURBO_DTYPE_BF16;
+    default: return TURBO_DTYPE_F32;
+    }
+}
+
+// TURBO_ROCM_CHOICES: "gemm=<tile>" forces the GEMM block shape.
+bool parse_choices(const char *s, int &tile) {
+    if (!s || !*s) return false;
+    const char *g = std::strstr(s, "gemm=");
+    if (!g) return false;
+    tile = std::atoi(g + 5);
+    if (tile < 0 || tile > gemm_tiles()) fail(TURBO_E_INVALID_ARGUMENT, std::string("rocm: TURBO_ROCM_CHOICES ") + s);
+    return true;
+}
+
+}  // namespace
+
+Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_backend_tuning *tuning) {
+    if (desc->task != TURBO_TASK_EMBED && desc->task != TURBO_TASK_RERANK)
+        fail(TURBO_E_UNSUPPORTED_TASK, "rocm: task " + std::to_string(desc->task));
+    if (desc->cpu_threads != 0)
+        fail(TURBO_E_UNSUPPORTED_OPTION, "rocm: cpu_threads applies to a CPU device alone", 6);
+    if (desc->max_batch == 0 || desc->max_seq == 0) fail(TURBO_E_INVALID_SHAPE, "rocm: max_batch and max_seq");
+    // The packing kernel keeps a length per row in LDS.
+    if (desc->max_batch > 16384) fail(TURBO_E_UNSUPPORTED, "rocm: max_batch above 16384");
+    // Every position a row can reach has a table row (BERT's positions from
+    // position_offset; a rotary model's cos/sin table).
+    const uint64_t reach = (uint64_t)desc->max_seq + (m->rotary ? 0 : m->position_offset);
+    if (reach > m->positions)
+        fail(TURBO_E_INVALID_ARGUMENT, "rocm: max_seq " + std::to_string(desc->max_seq) + " reaches past the model's " +
+                                           std::to_string(m->positions) + " positions");
+    Dt dt;
+    switch (desc->precision) {
+    case TURBO_PRECISION_EXACT: dt = Dt::F32; break;
+    case TURBO_PRECISION_MODEL:
+        dt = m->dtype == TURBO_DTYPE_F16 ? Dt::F16 : m->dtype == TURBO_DTYPE_BF16 ? Dt::BF16 : Dt::F32;
+        break;
+    case TURBO_PRECISION_FASTEST: dt = m->dtype == TURBO_DTYPE_BF16 ? Dt::BF16 : Dt::F16; break;
+    default: fail(TURBO_E_INVALID_ENUM, "rocm: precision " + std::to_string(desc->precision), 3);
+    }
+    auto s = std::make_unique<Session>();
+    s->model = m;
+    s->ctx = m->ctx;
+    s->task = desc->task;
+    s->max_batch = desc->max_batch;
+    s->max_seq = desc->max_seq;
+    s->max_ranges = desc->struct_size >= offsetof(turbo_backend_session_desc, max_ranges) + 4 && desc->max_ranges
+                        ? desc->max_ranges
+                        : desc->max_batch;
+    s->precision = desc->precision;
+    if (dt != Dt::F32) {
+        s->w = &m->weights_in(dt);
+        // A GEMM weight past F16's range computes in F32 (as the reference's
+        // CUDA backend does, core/cuda/backend.cpp:1168-1225).
+        if (dt == Dt::F16 && m->f16_overflow) dt = Dt::F32;
+    }
+    if (dt == Dt::F32) s->w = &m->weights_in(Dt::F32);
+    s->dt = dt;
+    s->compute_dtype = dtype_of(dt);
+    if (tuning && tuning->struct_size >= offsetof(turbo_backend_tuning, numerics_used) + 4) {
+        if (tuning->numerics_allowed && !(tuning->numerics_allowed & numeric_of(dt)))
+            fail(TURBO_E_UNSUPPORTED_OPTION,
+                 "rocm: the precision's numeric classes do not include this backend's " +
+                     std::to_string(numeric_of(dt)),
+                 3);
+    }
+    if (parse_choices(std::getenv("TURBO_ROCM_CHOICES"), s->gemm_tile)) {
+        if (tuning) tuning->tuned = TURBO_TUNED_FORCED;
+    }
+    s->choices = "gemm=" + std::to_string(s->gemm_tile) + " attention=simple";
+    if (tuning) {
+        std::snprintf(tuning->choices, sizeof tuning->choices, "%s", s->choices.c_str());
+        if (tuning->struct_size >= offsetof(turbo_backend_tuning, numerics_used) + 4)
+            tuning->numerics_used = tuning->numerics_allowed;
+    }
+
+    const size_t H = m->hidden, I = m->inter, B = s->max_batch, S = s->max_seq;
+    s->tcap = B * S;
+    const size_t el = dt_bytes(dt);
+    OnDevice on(m->ctx->ordinal);
+    auto alloc = [&](size_t bytes, const char *what) {
+        s->owned.emplace_back(dev_alloc(bytes, what));
+        return s->owned.back().get();
+    };
+    // Rows and ranges in one allocation, in the staging buffer's order.
+    s->staging_ints = 3 * B * S + 3 * (size_t)s->max_ranges;
+    int32_t *rows = static_cast<int32_t *>(alloc(s->staging_ints * 4, "session rows"));
+    s->ids = rows;
+    s->mask = rows + B * S;
+    s->types = rows + 2 * B * S;
+    s->ranges = reinterpret_cast<uint32_t *>(rows + 3 * B * S);
+    int32_t *pk = static_cast<int32_t *>(alloc((2 * B + 2 * s->tcap + 64) * 4, "session packing"));
+    s->pk.start = pk;
+    s->pk.len = pk + B;
+    s->pk.at = pk + 2 * B;
+    s->pk.row = pk + 2 * B + s->tcap;
+    s->pk.tokens = pk + 2 * B + 2 * s->tcap;
+    s->x = static_cast<float *>(alloc(s->tcap * H * 4, "session states"));
+    s->xh = alloc(s->tcap * H * 4, "session states");
+    s->qkv = alloc(3 * s->tcap * H * el, "session qkv");
+    s->ctxb = alloc(s->tcap * H * el, "session context");
+    s->ffn = alloc(s->tcap * (m->rotary ? I : I) * el, "session ffn");
+    const size_t outs = std::max<size_t>(B, s->max_ranges);
+    s->out = static_cast<float *>(alloc(outs * H * 4, "session output"));
+    s->output.ctx = m->ctx;
+    s->output.placement = TURBO_PLACE_DEVICE;
+    s->output.dev = s->out;
+    s->output.bytes = outs * H * 4;
+    s->output.owned = false;
+    check(hipHostMalloc((void **)&s->staging, s->staging_ints * 4, hipHostMallocDefault), "session staging");
+    return s.release();
+}
+
+void session_release(Session *s) {
+    if (!s) return;
+    {
+        OnDevice on(s->ctx->ordinal);
+        (void)hipStreamSynchronize(s->ctx->stream);
+        if (s->staging) (void)hipHostFree(s->staging);
+        for (hipEvent_t e : s->ev) (void)hipEventDestroy(e);
+        s->owned.clear();
+    }
+    delete s;
+}
+
+void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_token_range *ranges, uint32_t count) {
+    if (r->batch == 0 || r->seq == 0) fail(TURBO_E_INVALID_SHAPE, "rocm: batch and seq may not be 0");
+    if (r->batch > s->max_batch || r->seq > s->max_seq)
+        fail(TURBO_E_CAPACITY, "rocm: " + std::to_string(r->batch) + " rows of " + std::to_string(r->seq) +
+                                   " over the session's " + std::to_string(s->max_batch) + " of " +
+                                   std::to_string(s->max_seq));
+    if (r->taps > 1) fail(TURBO_E_UNSUPPORTED_OPTION, "rocm: pooling from earlier layers", 9);
+    if (r->head) fail(TURBO_E_UNSUPPORTED, "rocm: a token head on the device");
+    if (r->output_dim == 0 || r->output_dim > s->model->hidden)
+        fail(TURBO_E_INVALID_ARGUMENT, "rocm: output_dim " + std::to_string(r->output_dim));
+    if (count > s->max_ranges) fail(TURBO_E_CAPACITY, "rocm: " + std::to_string(count) + " ranges over max_ranges");
+    const uint32_t B = r->batch, S = r->seq, stride = r->row_stride ? r->row_stride : r->seq;
+    if (stride < S) fail(TURBO_E_INVALID_SHAPE, "rocm: row_stride under seq");
+    // Rows are packed with no stride, in the session's planes of B x S.
+    std::lock_guard<std::mutex> g(s->ctx->lock);
+    OnDevice on(s->ctx->ordinal);
+    // The staging buffer may still feed the last write's copy.
+    check(hipStreamSynchronize(s->ctx->stream), "embed_write");
+    int32_t *ids = s->staging, *mask = ids + (size_t)B * S, *types = mask + (size_t)B * S;
+    uint32_t *rg = reinterpret_cast<uint32_t *>(types + (size_t)B * S);
+    uint32_t tokens = 0, max_len = 0;
+    const Model &m = *s->model;
+    const int32_t ntypes = (int32_t)std::max(1u, m.types);
+    for (uint32_t row = 0; row < B; ++row) {
+        const size_t src = (size_t)row * stride, dst = (size_t)row * S;
+        std::memcpy(ids + dst, r->ids + src, S * 4);
+        std::memcpy(mask + dst, r->mask + src, S * 4);
+        if (r->types) std::memcpy(types + dst, r->types + src, S * 4);
+        else std::memset(types + dst, 0, S * 4);
+        // The core has checked these; the device reads tables by them, so
+        // they are held to their ranges here too.
+        for (uint32_t p = 0; p < S; ++p)
+            if (ids[dst + p] < 0 || (uint32_t)ids[dst + p] >= m.vocab || types[dst + p] < 0 ||
+                types[dst + p] >= ntypes)
+                fail(TURBO_E_INVALID_ARGUMENT, "rocm: row " + std::to_string(row) + " column " + std::to_string(p) +
+                                                   ": an id or type outside the model's");
+        uint32_t len = 0;
+        for (uint32_t p = S; p > 0; --p)
+            if (mask[dst + p - 1] != 0) {
+                len = p;
+                break;
+            }
+        if (len == 0) fail(TURBO_E_INVALID_ARGUMENT, "rocm: row " + std::to_string(row) + " has no live token");
+        tokens += len;
+        max_len = std::max(max_len, len);
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        const turbo_token_range &g2 = ranges[i];
+        if (g2.row >= B || g2.start >= g2.end || g2.end > S)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: ranges[" + std::to_string(i) + "]");
+        rg[3 * i] = g2.row;
+        rg[3 * i + 1] = g2.start;
+        rg[3 * i + 2] = g2.end;
+    }
+    const size_t plane = (size_t)s->max_batch * s->max_seq;
+    // Planes are B*S long here but the device keeps them max_batch*max_seq
+    // apart: three copies, plus the ranges.
+    const size_t n = (size_t)B * S * 4;
+    check(hipMemcpyAsync(s->ids, ids, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+    check(hipMemcpyAsync(s->mask, mask, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+    check(hipMemcpyAsync(s->types, types, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+    if (count) check(hipMemcpyAsync(s->ranges, rg, (size_t)count * 12, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+    (void)plane;
+    s->h2d = 3 * n + (size_t)count * 12;
+    s->batch = B;
+    s->seq = S;
+    s->pooling = r->pooling;
+    s->normalize = r->normalize;
+    s->output_dim = r->output_dim;
+    s->count = count;
+    s->tokens = tokens;
+    s->max_len = max_len;
+    s->has_types = r->types != nullptr;
+    s->written = true;
+}
+
+// Records an event pair around each launch when the session times its runs.
+struct Timer {
+    Session &s;
+    explicit Timer(Session &ss) : s(ss) { s.ev_used = 0; }
+    void begin(const char *name) {
+        if (!s.timing || s.ev_used + 2 > s.ev.size()) return;
+        s.ev_name[s.ev_used / 2] = name;
+        (void)hipEventRecord(s.ev[s.ev_used], s.ctx->stream);
+    }
+    void end() {
+        if (!s.timing || s.ev_used + 2 > s.ev.size()) return;
+        (void)hipEventRecord(s.ev[s.ev_used + 1], s.ctx->stream);
+        s.ev_used += 2;
+    }
+};
+
+void encode(Session &s) {
+    Model &m = *s.model;
+    hipStream_t st = s.ctx->stream;
+    const int T = (int)s.tokens, H = (int)m.hidden, I = (int)m.inter, heads = (int)m.heads, dh = H / heads;
+    const Dt dt = s.dt;
+    const bool f32 = dt == Dt::F32;
+    Timer tm(s);
+    auto run = [&](const char *name, hipError_t e) {
+        (void)name;
+        check(e, name);
+    };
+#define LAUNCH(NAME, CALL) \
+    do {                   \
+        tm.begin(NAME);    \
+        run(NAME, CALL);   \
+        tm.end();          \
+    } while (0)
+    LAUNCH("pack_rows", pack_rows(st, s.mask, (int)s.batch, (int)s.seq, s.pk));
+    // The GEMM operand copy of x: x itself on the F32 tier.
+    void *xa = f32 ? (void *)s.x : s.xh;
+    LAUNCH("embed_ln", embed_ln(st, T, H, s.ids, s.types, s.pk, (int)s.seq, (int)m.position_offset, m.word, m.pos,
+                                m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
+    for (uint32_t l = 0; l < m.layers; ++l) {
+        const Model::Layer &L = m.ls[l];
+        const LayerWeights &W = (*s.w)[l];
+        EpiArgs q;
+        q.bias = L.bqkv;
+        q.out = s.qkv;
+        q.tcap = (int)s.tcap;
+        q.heads = heads;
+        q.d = dh;
+        q.hidden = H;
+        int window = INT32_MAX;
+        const void *src = xa;
+        if (m.rotary) {
+            const bool global = m.global_every == 0 || l % m.global_every == 0;
+            const size_t half = (size_t)m.positions * m.pairs;
+            q.kind = Epi::QkvRope;
+            q.cos = m.rope + (global ? 0 : 2 * half);
+            q.sin = q.cos + half;
+            q.at = s.pk.at;
+            q.seq = (int)s.seq;
+            if (!global) window = (int)m.window;
+            if (m.modern && l > 0) {
+                // xn = LN(x) into xh (F32 on the F32 tier), x kept.
+                LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln1_w, nullptr, m.eps, f32 ? (float *)s.xh : nullptr,
+                                                f32 ? nullptr : s.xh, dt));
+                src = s.xh;
+            } else if (m.modern) {
+                src = xa;
+            }
+        } else {
+            q.kind = Epi::Qkv;
+        }
+        LAUNCH("gemm_qkv", gemm(st, dt, T, (int)L.n_qkv, H, src, H, W.qkv, q, s.gemm_tile));
+        LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, (int)s.seq, (int)s.batch,
+                                      (int)s.max_len, window, s.ctxb));
+        EpiArgs o;
+        o.kind = Epi::Residual;
+        o.bias = L.bo;
+        o.x = s.x;
+        o.ldo = H;
+        LAUNCH("gemm_out", gemm(st, dt, T, H, H, s.ctxb, H, W.out, o, s.gemm_tile));
+        const void *ffn_src = xa;
+        if (m.modern) {
+            LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln2_w, nullptr, m.eps, f32 ? (float *)s.xh : nullptr,
+                                            f32 ? nullptr : s.xh, dt));
+            ffn_src = s.xh;
+        } else {
+            LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln1_w, L.ln1_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
+        }
+        EpiArgs f;
+        f.out = s.ffn;
+        f.ldo = I;
+        f.bias = L.b1;
+        if (m.rotary) {
+            f.kind = Epi::Gated;
+            f.silu = m.silu ? 1 : 0;
+        } else {
+            f.kind = Epi::Gelu;
+        }
+        LAUNCH("gemm_ffn_in", gemm(st, dt, T, (int)L.n_in, H, ffn_src, H, W.ffn_in, f, s.gemm_tile));
+        EpiArgs f2;
+        f2.kind = Epi::Residual;
+        f2.bias = L.b2;
+        f2.x = s.x;
+        f2.ldo = H;
+        LAUNCH("gemm_ffn_out", gemm(st, dt, T, H, I, s.ffn, I, W.ffn_out, f2, s.gemm_tile));
+        if (!m.modern)
+            LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln2_w, L.ln2_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
+    }
+    if (m.modern) LAUNCH("layer_norm", layer_norm(st, T, H, s.x, m.final_w, nullptr, m.eps, s.x, nullptr, dt));
+    const int n_out = s.count ? (int)s.count : (int)s.batch;
+    LAUNCH("pool", pool(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.count ? s.ranges : nullptr, (int)s.pooling,
+                        (int)s.output_dim, s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0, s.out));
+#undef LAUNCH
+}
+
+void session_run(Session *s, turbo_backend_run *out) {
+    if (!s->written) fail(TURBO_E_INVALID_STATE, "rocm: the session has no rows written since its last run");
+    s->written = false;
+    const uint64_t dev0 = device_allocs.load();
+    {
+        std::lock_guard<std::mutex> g(s->ctx->lock);
+        OnDevice on(s->ctx->ordinal);
+        try {
+            encode(*s);
+        } catch (...) {
+            (void)hipStreamSynchronize(s->ctx->stream);
+            throw;
+        }
+        check(hipStreamSynchronize(s->ctx->stream), "the run");
+        if (s->timing) {
+            std::map<std::string, double> by;
+            std::vector<std::string> order;
+            for (size_t i = 0; i + 1 < s->ev_used; i += 2) {
+                float ms = 0;
+                (void)hipEventElapsedTime(&ms, s->ev[i], s->ev[i + 1]);
+                const std::string &n = s->ev_name[i / 2];
+                if (!by.count(n)) order.push_back(n);
+                by[n] += ms;
+            }
+            s->last_times.clear();
+            for (auto &n : order) s->last_times.emplace_back(n, by[n]);
+        }
+    }
+    const uint32_t n_out = s->count ? s->count : s->batch;
+    s->output.bytes = (uint64_t)n_out * s->output_dim * 4;
+    out->placement = TURBO_PLACE_DEVICE;
+    out->output = &s->output;
+    out->host = nullptr;
+    out->h2d_bytes = s->h2d;
+    out->d2h_bytes = 0;
+    out->host_allocs = 0;
+    out->device_allocs = device_allocs.load() - dev0;
+    uint32_t *st = out->stage;
+    st[TURBO_EMBED_STAGE_UPLOAD] = TURBO_STAGE_DEVICE;
+    st[TURBO_EMBED_STAGE_LOOKUP] = TURBO_STAGE_DEVICE;
+    st[TURBO_EMBED_STAGE_ENCODE] = TURBO_STAGE_DEVICE;
+    st[TURBO_EMBED_STAGE_POOL] = TURBO_STAGE_DEVICE;
+    st[TURBO_EMBED_STAGE_NORMALIZE] = s->normalize == TURBO_NORMALIZE_L2 ? TURBO_STAGE_FUSED : TURBO_STAGE_UNUSED;
+    st[TURBO_EMBED_STAGE_DOWNLOAD] = TURBO_STAGE_UNUSED;
+}
+
+}  // namespace rocm
+
+// ---- Test and measurement hooks ----------------------------------------------------------
+
+using namespace rocm;
+
+extern "C" {
+
+int32_t turbo_rocm_session_packing(void *session, int32_t *start, int32_t *len, int32_t *at, uint32_t *tokens,
+                                   turbo_error *err) {
+    return guarded(err, [&] {
+        Session *s = static_cast<Session *>(session);
+        std::lock_guard<std::mutex> g(s->ctx->lock);
+        OnDevice on(s->ctx->ordinal);
+        int32_t t = 0;
+        check(hipMemcpy(&t, s->pk.tokens, 4, hipMemcpyDeviceToHost), "packing");
+        check(hipMemcpy(start, s->pk.start, (size_t)s->batch * 4, hipMemcpyDeviceToHost), "packing");
+        check(hipMemcpy(len, s->pk.len, (size_t)s->batch * 4, hipMemcpyDeviceToHost), "packing");
+        check(hipMemcpy(at, s->pk.at, (size_t)t * 4, hipMemcpyDeviceToHost), "packing");
+        *tokens = (uint32_t)t;
+        return TURBO_OK;
+    });
+}
+
+int32_t turbo_rocm_session_hidden(void *session, float *out, uint64_t floats, turbo_error *err) {
+    return guarded(err, [&] {
+        Session *s = static_cast<Session *>(session);
+        const uint64_t n = (uint64_t)s->tokens * s->model->hidden;
+        if (floats < n) fail(TURBO_E_INVALID_ARGUMENT, "rocm: the hidden states need " + std::to_string(n) + " floats");
+        std::lock_guard<std::mutex> g(s->ctx->lock);
+        OnDevice on(s->ctx->ordinal);
+        check(hipMemcpy(out, s->x, n * 4, hipMemcpyDeviceToHost), "hidden states");
+        return TURBO_OK;
+    });
+}
+
+int32_t turbo_rocm_session_timing(void *session, uint32_t on_, turbo_error *err) {
+    return guarded(err, [&] {
+        Session *s = static_cast<Session *>(session);
+        OnDevice on(s->ctx->ordinal);
+        if (on_ && s->ev.empty()) {
+            s->ev.resize(2 * (16 + 16 * s->model->layers));
+            for (auto &e : s->ev) check(hipEventCreate(&e), "hipEventCreate");
+            s->ev_name.resize(s->ev.size() / 2);
+        }
+        s->timing = on_ != 0;
+        return TURBO_OK;
+    });
+}
+
+int32_t turbo_rocm_session_times(void *session, char *out, uint32_t len, turbo_error *err) {
+    return guarded(err, [&] {
+        Session *s = static_cast<Session *>(session);
+        std::string t;
+        for (auto &p : s->last_times) {
+            char line[128];
+            std::snprintf(line, sizeof line, "%s %.6f\n", p.first.c_str(), p.second);
+            t += line;
+        }
+        if (len) std::snprintf(out, len, "%s", t.c_str());
+        return TURBO_OK;
+    });
+}
+
+int32_t turbo_rocm_session_replay(void *session, uint32_t runs, turbo_error *err) {
+    return guarded(err, [&] {
+        Session *s = static_cast<Session *>(session);
+        if (s->tokens == 0) fail(TURBO_E_INVALID_STATE, "rocm: the session has no rows written");
+        std::lock_guard<std::mutex> g(s->ctx->lock);
+        OnDevice on(s->ctx->ordinal);
+        for (uint32_t i = 0; i < runs; ++i) encode(*s);
+        check(hipStreamSynchronize(s->ctx->stream), "replay");
+        return TURBO_OK;
+    });
+}
+
+int32_t turbo_rocm_session_choices(void *session, char *out, uint32_t len, turbo_error *err) {
+    return guarded(err, [&] {
+        Session *s = static_cast<Session *>(session);
+        if (len) std::snprintf(out, len, "%s", s->choices.c_str());
+        return TURBO_OK;
+    });
+}
+
+int32_t turbo_rocm_gemm_check(uint32_t ordinal, uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, const float *A,
+                              const float *W, const float *bias, float *out, uint32_t tile, turbo_error *err) {
+    return guarded(err, [&] {
+        if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device");
+        const Dt dt = dtype == TURBO_DTYPE_F16 ? Dt::F16 : dtype == TURBO_DTYPE_BF16 ? Dt::BF16 : Dt::F32;
+        OnDevice on(devices()[ordinal]);
+        const size_t na = (size_t)M * K, nw = (size_t)N * K;
+        DevPtr a32(dev_alloc(na * 4, "gemm check")), w32(dev_alloc(nw * 4, "gemm check"));
+        DevPtr a(dev_alloc(na * 4, "gemm check")), w(dev_alloc(nw * 4, "gemm check"));
+        DevPtr b(dev_alloc((size_t)N * 4, "gemm check")), o(dev_alloc((size_t)M * N * 4, "gemm check"));
+        check(hipMemcpy(a32.get(), A, na * 4, hipMemcpyHostToDevice), "gemm check");
+        check(hipMemcpy(w32.get(), W, nw * 4, hipMemcpyHostToDevice), "gemm check");
+        if (bias) check(hipMemcpy(b.get(), bias, (size_t)N * 4, hipMemcpyHostToDevice), "gemm check");
+        const void *pa = a32.get(), *pw = w32.get();
+        if (dt != Dt::F32) {
+            check(narrow(nullptr, (const float *)a32.get(), a.get(), na, dt, nullptr), "gemm check");
+            check(narrow(nullptr, (const float *)w32.get(), w.get(), nw, dt, nullptr), "gemm check");
+            pa = a.get();
+            pw = w.get();
+        }
+        EpiArgs e;
+        e.kind = Epi::Plain;
+        e.bias = bias ? (const float *)b.get() : nullptr;
+        e.out = o.get();
+        e.ldo = (int)N;
+        check(gemm(nullptr, dt, (int)M, (int)N, (int)K, pa, (int)K, pw, e, (int)tile), "gemm check");
+        check(hipDeviceSynchronize(), "gemm check");
+        check(hipMemcpy(out, o.get(), (size_t)M * N * 4, hipMemcpyDeviceToHost), "gemm check");
+        return TURBO_OK;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,155 @@
+// The rocm backend's handles and their shared helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "turbo/turbo_seam.h"
+#include "kernels.h"
+
+namespace rocm {
+
+struct Failure {
+    int32_t code;
+    uint32_t field;
+    std::string message;
+};
+
+[[noreturn]] void fail(int32_t code, const std::string &m, uint32_t field = 0);
+void check(hipError_t e, const char *what);
+void fill(turbo_error *err, int32_t code, uint32_t field, const std::string &m);
+void *dev_alloc(size_t bytes, const char *what);
+const std::vector<int> &devices();
+
+extern std::atomic<uint64_t> device_allocs;
+extern std::atomic<uint64_t> host_allocs;
+
+// Every entry point: a status, the caller's turbo_error filled, nothing
+// thrown across the boundary (reference include/turbo/turbo_backend.h:10-12).
+template <class F> int32_t guarded(turbo_error *err, F &&f) {
+    try {
+        const int32_t rc = f();
+        if (rc == TURBO_OK) fill(err, 0, 0, "");
+        return rc;
+    } catch (const Failure &e) {
+        fill(err, e.code, e.field, e.message);
+        return e.code;
+    } catch (const std::bad_alloc &) {
+        fill(err, TURBO_E_OUT_OF_MEMORY, 0, "rocm: host memory exhausted");
+        return TURBO_E_OUT_OF_MEMORY;
+    } catch (...) {
+        fill(err, TURBO_E_INTERNAL, 0, "rocm: unexpected exception");
+        return TURBO_E_INTERNAL;
+    }
+}
+
+// Holds a device current for a scope, and gives the caller's back.
+struct OnDevice {
+    int prev = -1;
+    explicit OnDevice(int ordinal);
+    ~OnDevice();
+};
+
+struct DevFree {
+    void operator()(void *p) const {
+        if (p) (void)hipFree(p);
+    }
+};
+using DevPtr = std::unique_ptr<void, DevFree>;
+
+struct Context {
+    int ordinal = 0;                 // the HIP device
+    hipStream_t stream = nullptr;
+    turbo_log_fn log = nullptr;
+    void *log_user_data = nullptr;
+    std::mutex lock;                 // a launch through its sync, and reads
+    void say(uint32_t level, const std::string &m) const;
+};
+
+struct Buffer {
+    Context *ctx = nullptr;
+    uint32_t placement = 0;
+    void *dev = nullptr;    // device address (or the host one for host-visible memory)
+    void *host = nullptr;
+    uint64_t bytes = 0;
+    bool owned = false;
+};
+
+// One layer's GEMM weights in one dtype: [n, k] row-major, as the kernels read them.
+struct LayerWeights {
+    const void *qkv, *out, *ffn_in, *ffn_out;
+};
+
+struct Model {
+    Context *ctx = nullptr;
+    uint32_t family = 0, dtype = 0, layers = 0, hidden = 0, heads = 0, inter = 0, vocab = 0, positions = 0,
+             types = 0, position_offset = 0;
+    float eps = 0;
+    bool rotary = false, modern = false, silu = false;
+    uint32_t window = 0, global_every = 0, pairs = 0;   // window: keys each side, 0 for none
+    DevPtr f32;                                         // every tensor in F32, one allocation
+    // F32 device pointers (NULL where absent).
+    const float *word = nullptr, *pos = nullptr, *type = nullptr, *emb_w = nullptr, *emb_b = nullptr,
+                *final_w = nullptr, *rope = nullptr;
+    struct Layer {
+        const float *wqkv, *bqkv, *wo, *bo, *ln1_w, *ln1_b, *w1, *b1, *w2, *b2, *ln2_w, *ln2_b;
+        size_t n_qkv, n_in;   // output rows of the QKV and FFN-in products
+    };
+    std::vector<Layer> ls;
+    // Narrowed GEMM weights, per dtype (index Dt), made on first need.
+    std::mutex lock;
+    DevPtr narrowed[3];
+    std::vector<LayerWeights> gemm_w[3];
+    bool f16_overflow = false;
+    std::vector<LayerWeights> &weights_in(Dt dt);
+};
+
+struct Session {
+    Model *model = nullptr;
+    Context *ctx = nullptr;
+    uint32_t task = 0, max_batch = 0, max_seq = 0, max_ranges = 0, precision = 0, compute_dtype = 0;
+    Dt dt = Dt::F32;
+    size_t tcap = 0;
+    std::vector<DevPtr> owned;
+    int32_t *ids = nullptr, *mask = nullptr, *types = nullptr;
+    uint32_t *ranges = nullptr;
+    Packing pk{};
+    float *x = nullptr;      // [tcap, H] F32 residual stream
+    void *xh = nullptr;      // [tcap, H] GEMM-operand copy (dt), or the pre-norm rows
+    void *qkv = nullptr;     // [3][heads][tcap][d] (dt)
+    void *ctxb = nullptr;    // [tcap, H] (dt)
+    void *ffn = nullptr;     // [tcap, I] (dt)
+    float *out = nullptr;    // [max(max_batch, max_ranges), H] F32
+    Buffer output;
+    int32_t *staging = nullptr;   // pinned: ids, mask, types planes then ranges
+    size_t staging_ints = 0;
+    // The written run.
+    bool written = false;
+    uint32_t batch = 0, seq = 0, pooling = 0, normalize = 0, output_dim = 0, count = 0, tokens = 0, max_len = 0;
+    bool has_types = false;
+    uint64_t h2d = 0;
+    std::vector<LayerWeights> *w = nullptr;
+    std::string choices;
+    int gemm_tile = 0;
+    // Per-launch timing (a test and benchmark hook): events around each
+    // kernel of a run, by name.
+    bool timing = false;
+    std::vector<hipEvent_t> ev;
+    std::vector<std::string> ev_name;
+    size_t ev_used = 0;
+    std::vector<std::pair<std::string, double>> last_times;
+};
+
+Model *model_load(Context *c, const turbo_backend_model *desc);
+void model_release(Model *m);
+Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_backend_tuning *tuning);
+void session_release(Session *s);
+void session_write(Session *s, const turbo_backend_embed_rows *rows, const turbo_token_range *ranges, uint32_t count);
+void session_run(Session *s, turbo_backend_run *out);
+
+}  // namespace rocm
