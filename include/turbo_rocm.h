@@ -83,6 +83,12 @@ int32_t turbo_rocm_session_choices(void *session, char *out, uint32_t len, turbo
 int32_t turbo_rocm_gemm_check(uint32_t ordinal, uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, const float *A,
                               const float *W, const float *bias, float *out, uint32_t tile, turbo_error *err);
 
+/* The average milliseconds of `iters` back-to-back launches of the GEMM
+ * [M, K] x [N, K]^T with the residual epilogue, block shape `tile`, on
+ * device-resident operands; for tuning sweeps. */
+int32_t turbo_rocm_gemm_time(uint32_t ordinal, uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, uint32_t tile,
+                             uint32_t iters, float *ms, turbo_error *err);
+
 #ifdef __cplusplus
 }
 #endif

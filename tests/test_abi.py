@@ -127,3 +127,9 @@ def _check_ranges(mask, ranges, max_ranges=8):
 def test_range_checks(ranges, code, text):
     rc, msg = _check_ranges([[1, 1, 0, 0], [1, 1, 1, 1]], ranges)
     assert rc == code and text in msg, (rc, msg)
+
+
+def test_the_library_leaves_none_of_its_own_symbols_undefined():
+    import subprocess
+    out = subprocess.run(["nm", "-u", "--demangle", T.LIB_PATH], capture_output=True, text=True).stdout
+    assert "rocm::" not in out, [l for l in out.splitlines() if "rocm::" in l]

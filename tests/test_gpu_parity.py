@@ -31,8 +31,8 @@ def assert_close(got, want, compute_dtype):
 # ---- The GEMM kernel alone ------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [S.TURBO_DTYPE_F32, S.TURBO_DTYPE_F16, S.TURBO_DTYPE_BF16])
-@pytest.mark.parametrize("tile", [1, 2, 3])
-@pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 200, 96), (33, 96, 32), (1000, 768, 768)])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 200, 96), (33, 96, 32), (1000, 768, 768), (517, 2304, 1152)])
 def test_gemm_matches_numpy(runtime, dtype, tile, mnk):
     m, n, k = mnk
     g = np.random.Generator(np.random.PCG64(m * 7 + n + k))
@@ -195,4 +195,31 @@ def test_bert_base_fastest_meets_the_oracle(context, lengths):
     want = oracle.encode(desc, ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
     assert_close(got, want, s.compute_dtype)
     s.close()
+    model.close()
+
+
+# ---- Attention paths ------------------------------------------------------------------
+
+@pytest.mark.parametrize("family", ["bert", "modernbert"])
+@pytest.mark.parametrize("heads", [2, 4])
+def test_matrix_core_attention_meets_the_oracle(context, family, heads, monkeypatch):
+    # Head widths 64 and 32 on long ragged rows (several 128-query blocks and
+    # 64-key blocks), and ModernBERT's sliding windows across block edges.
+    if family == "bert":
+        desc = small.bert(seed=21, hidden=128, heads=heads, inter=256, positions=320, std=0.1)
+    else:
+        desc = small.modernbert(seed=21, hidden=128, heads=heads, inter=192, positions=320, window=32, std=0.1)
+    ids, mask, types = small.ragged_rows(21, 5, 300, desc.vocab_size)
+    if family == "modernbert":
+        types = None
+    want = oracle.encode(desc, ids, mask, types)
+    model = context.load(desc)
+    got = {}
+    for path in ("mfma", "simple"):
+        monkeypatch.setenv("TURBO_ROCM_CHOICES", f"attention={path}")
+        s = model.session(8, 320, S.TURBO_PRECISION_FASTEST)
+        assert f"attention={path}" in s.choices()
+        got[path] = s.embed(ids, mask, types)
+        assert_close(got[path], want, s.compute_dtype)
+        s.close()
     model.close()

@@ -56,6 +56,7 @@ def library():
         "turbo_rocm_session_choices": [P, C.c_char_p, u32, E],
         "turbo_rocm_session_replay": [P, u32, E],
         "turbo_rocm_gemm_check": [u32, u32, u32, u32, u32, P, P, P, P, u32, E],
+        "turbo_rocm_gemm_time": [u32, u32, u32, u32, u32, u32, u32, C.POINTER(C.c_float), E],
     }
     for name, args in protos.items():
         f = getattr(lib, name)
@@ -302,3 +303,11 @@ def gemm_check(a, w, bias=None, dtype=S.TURBO_DTYPE_F32, tile=0, ordinal=0):
                                         None if b is None else b.ctypes.data, out.ctypes.data, tile, C.byref(err)),
         err)
     return out
+
+
+def gemm_time(m, n, k, dtype=S.TURBO_DTYPE_F16, tile=0, iters=20, ordinal=0):
+    """Average milliseconds of one GEMM launch on device-resident operands."""
+    ms = C.c_float()
+    err = S.new_error()
+    _ok(library().turbo_rocm_gemm_time(ordinal, dtype, m, n, k, tile, iters, C.byref(ms), C.byref(err)), err)
+    return ms.value

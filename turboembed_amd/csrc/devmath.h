@@ -55,6 +55,24 @@ __device__ __forceinline__ float dev_gelu(float x) {
     return __fmul_rn(__fmul_rn(0.5f, x), x >= 0.0f ? __fsub_rn(2.0f, r) : r);
 }
 
+// GELU for the 16-bit tiers, whose outputs keep 8 to 11 bits: erf by
+// Abramowitz and Stegun's formula 7.1.26 (absolute error under 1.5e-7), on
+// the hardware's exp2 and reciprocal: a dozen instructions against the
+// erfcc fit's fifty.
+__device__ __forceinline__ float dev_gelu_fast(float x) {
+    const float z = fabsf(x) * 0.70710678118654752440f;
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+    float p = fmaf(1.061405429f, t, -1.453152027f);
+    p = fmaf(p, t, 1.421413741f);
+    p = fmaf(p, t, -0.284496736f);
+    p = fmaf(p, t, 0.254829592f);
+    p *= t;
+    // erfc(z) = p e^{-z^2}, e^{-z^2} = 2^{-z^2 log2 e}; gelu(x) = x/2 (2 - erfc)
+    // for x >= 0 and x/2 erfc(|z|) below, with no cancellation.
+    const float r = p * __builtin_amdgcn_exp2f(-z * z * 1.44269504088896340736f);
+    return 0.5f * x * (x >= 0.0f ? 2.0f - r : r);
+}
+
 __device__ __forceinline__ float dev_silu(float x) {
     return __fdiv_rn(x, __fadd_rn(1.0f, dev_exp(-x)));
 }

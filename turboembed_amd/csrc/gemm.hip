@@ -56,61 +56,69 @@ template <> struct Mma<float> {
     }
 };
 
-// The epilogue of one output element pair-aware: v is acc + bias at (m, n).
-template <typename T>
-__device__ __forceinline__ void epilogue_store(const EpiArgs &e, int M, int N, int m, int n, float acc) {
-    const float v = acc + (e.bias ? e.bias[n] : 0.0f);
-    switch (e.kind) {
-    case Epi::Plain:
-        if (m < M && n < N) ((float *)e.out)[(size_t)m * e.ldo + n] = v;
-        break;
-    case Epi::Gelu:
-        if (m < M && n < N) ((T *)e.out)[(size_t)m * e.ldo + n] = from_f32<T>(dev_gelu(v));
-        break;
-    case Epi::Residual:
-        if (m < M && n < N) {
-            float *x = e.x + (size_t)m * e.ldo + n;
-            *x = *x + v;
+// The epilogue of one 32 x 32 MFMA tile, for this lane's column n and its 16
+// rows m0 + 8 (r / 4) + 4 (lane / 32) + r % 4, v = acc + bias. The kind is a
+// template argument, so each kernel carries one small epilogue, and what
+// depends on the column alone is worked out once per tile.
+template <typename T, Epi KIND>
+__device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, int mt, int n, const floatx16 &acc) {
+    const int lane = threadIdx.x & 63;
+    const int mb = mt + (lane >> 5) * 4;   // row of register r: mb + 8 (r / 4) + r % 4
+    const bool col_ok = n < N;
+    const float bias = (e.bias && col_ok) ? e.bias[n] : 0.0f;
+    if constexpr (KIND == Epi::Plain || KIND == Epi::Gelu || KIND == Epi::Residual) {
+        if (!col_ok) return;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = mb + (r >> 2) * 8 + (r & 3);
+            if (m >= M) continue;
+            const float v = acc[r] + bias;
+            const size_t at = (size_t)m * e.ldo + n;
+            if constexpr (KIND == Epi::Plain) ((float *)e.out)[at] = v;
+            else if constexpr (KIND == Epi::Gelu)
+                ((T *)e.out)[at] = from_f32<T>(sizeof(T) == 2 ? dev_gelu_fast(v) : dev_gelu(v));
+            else e.x[at] = e.x[at] + v;
         }
-        break;
-    case Epi::Qkv: {
-        if (m < M && n < N) {
-            const int which = n / e.hidden, rem = n - which * e.hidden;
-            const int head = rem / e.d, c = rem - head * e.d;
-            ((T *)e.out)[(((size_t)which * e.heads + head) * e.tcap + m) * e.d + c] = from_f32<T>(v);
-        }
-        break;
-    }
-    case Epi::QkvRope: {
-        // Columns come pair-adjacent: the partner of n is n ^ 1, in the
-        // neighbouring lane (the MFMA layout puts column n in lane n % 32).
-        const float w = __shfl_xor(v, 1, 64);
-        if (m < M && n < N) {
-            const int which = n / e.hidden, rem = n - which * e.hidden;
-            const int head = rem / e.d, c = rem - head * e.d;
-            float y = v;
-            if (which < 2) {
-                const int pos = e.at[m] % e.seq, pr = c >> 1;
-                const float cs = e.cos[(size_t)pos * (e.d >> 1) + pr], sn = e.sin[(size_t)pos * (e.d >> 1) + pr];
-                // (x1, x2) -> (x1 cos - x2 sin, x2 cos + x1 sin)
-                y = (c & 1) ? __fadd_rn(__fmul_rn(v, cs), __fmul_rn(w, sn)) : __fsub_rn(__fmul_rn(v, cs), __fmul_rn(w, sn));
+    } else if constexpr (KIND == Epi::Qkv || KIND == Epi::QkvRope) {
+        const int which = n / e.hidden, rem = n - which * e.hidden;
+        const int head = rem / e.d, c = rem - head * e.d;
+        T *out = (T *)e.out + (size_t)which * e.heads * e.tcap * e.d;
+        const int half = e.d >> 1, pr = c >> 1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = mb + (r >> 2) * 8 + (r & 3);
+            float v = acc[r] + bias;
+            if constexpr (KIND == Epi::QkvRope) {
+                // Columns come pair-adjacent: the partner of n is n ^ 1, in
+                // the neighbouring lane (column n sits in lane n % 32).
+                const float w = __shfl_xor(v, 1, 64);
+                if (which < 2 && col_ok && m < M) {
+                    const int pos = e.at[m] % e.seq;
+                    const float cs = e.cos[(size_t)pos * half + pr], sn = e.sin[(size_t)pos * half + pr];
+                    // (x1, x2) -> (x1 cos - x2 sin, x2 cos + x1 sin)
+                    v = (c & 1) ? __fadd_rn(__fmul_rn(v, cs), __fmul_rn(w, sn))
+                                : __fsub_rn(__fmul_rn(v, cs), __fmul_rn(w, sn));
+                }
             }
-            ((T *)e.out)[(((size_t)which * e.heads + head) * e.tcap + m) * e.d + c] = from_f32<T>(y);
+            if (!col_ok || m >= M) continue;
+            // Q and K token-major per head; V transposed per head.
+            const size_t at = which < 2 ? ((size_t)head * e.tcap + m) * e.d + c : ((size_t)head * e.d + c) * e.tcap + m;
+            out[at] = from_f32<T>(v);
         }
-        break;
-    }
-    case Epi::Gated: {
-        const float up = __shfl_xor(v, 1, 64);
-        if (m < M && n < N && (n & 1) == 0) {
-            const float g = e.silu ? dev_silu(v) : dev_gelu(v);
+    } else {   // Gated: out[m, n / 2] = act(gate) * up, gate and up in neighbouring columns
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = mb + (r >> 2) * 8 + (r & 3);
+            const float v = acc[r] + bias;
+            const float up = __shfl_xor(v, 1, 64);
+            if (!col_ok || m >= M || (n & 1)) continue;
+            const float g = e.silu ? dev_silu(v) : sizeof(T) == 2 ? dev_gelu_fast(v) : dev_gelu(v);
             ((T *)e.out)[(size_t)m * e.ldo + (n >> 1)] = from_f32<T>(__fmul_rn(g, up));
         }
-        break;
-    }
     }
 }
 
-template <typename T, int BM, int BN, int BK>
+template <typename T, int BM, int BN, int BK, Epi KIND>
 __global__ void __launch_bounds__(256) gemm_kernel(int M, int N, int K, const T *__restrict__ A, int lda,
                                                    const T *__restrict__ W, EpiArgs e, int grid_n) {
     constexpr int VEC = 16 / sizeof(T);          // elements in 16 bytes
@@ -200,36 +208,365 @@ __global__ void __launch_bounds__(256) gemm_kernel(int M, int N, int K, const T 
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int n = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                epilogue_store<T>(e, M, N, m, n, acc[i][j][r]);
-            }
-        }
+        for (int j = 0; j < TN; ++j)
+            epilogue_tile<T, KIND>(e, M, N, m0 + wm * (BM / 2) + i * 32, n0 + wn * (BN / 2) + j * 32 + (lane & 31),
+                                   acc[i][j]);
+}
+
+template <typename T, int BM, int BN, int BK, Epi KIND>
+static hipError_t launch_k(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W,
+                           const EpiArgs &e) {
+    const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM;
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, BK, KIND>), dim3(gn * gm), dim3(256), 0, s, M, N, K, (const T *)A,
+                       lda, (const T *)W, e, gn);
+    return hipGetLastError();
 }
 
 template <typename T, int BM, int BN, int BK>
 static hipError_t launch(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e) {
+    switch (e.kind) {
+    case Epi::Plain: return launch_k<T, BM, BN, BK, Epi::Plain>(s, M, N, K, A, lda, W, e);
+    case Epi::Qkv: return launch_k<T, BM, BN, BK, Epi::Qkv>(s, M, N, K, A, lda, W, e);
+    case Epi::Gelu: return launch_k<T, BM, BN, BK, Epi::Gelu>(s, M, N, K, A, lda, W, e);
+    case Epi::Residual: return launch_k<T, BM, BN, BK, Epi::Residual>(s, M, N, K, A, lda, W, e);
+    case Epi::QkvRope: return launch_k<T, BM, BN, BK, Epi::QkvRope>(s, M, N, K, A, lda, W, e);
+    case Epi::Gated: return launch_k<T, BM, BN, BK, Epi::Gated>(s, M, N, K, A, lda, W, e);
+    }
+    return hipErrorInvalidValue;
+}
+
+
+// ---- The pipelined kernel (16-bit operands, K a multiple of 64) -------------------
+//
+// The same 2 x 2 waves of 32 x 32 MFMA tiles, fed by a STAGES-deep ring of
+// LDS tiles that the hardware fills directly from global memory
+// (global_load_lds_dwordx4: lane l of a wave writes its 16 bytes at the
+// instruction's LDS base + 16 l), so no registers stage the operands and
+// STAGES - 1 tiles are in flight while one is multiplied. A tile row is 64
+// elements, 128 bytes, as 8 chunks of 16 bytes; chunk c of row r is kept at
+// slot c ^ f(r), f(r) = (r & 7) ^ ((r >> 3) & 1), so the 16-byte fragment
+// reads of 16 consecutive rows at one chunk fall in distinct banks whether
+// the LDS serves 8 or 16 lanes of a 16-byte read per clock. A lane of a
+// load instruction fills slot (lane & 7) of row (lane >> 3) of its 8-row
+// group, so it fetches global chunk (lane & 7) ^ f(row).
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// s_waitcnt vmcnt(N) with the other counters left free (gfx9 encoding).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// The pipelined kernel's epilogue: each wave stages 32 rows of its tile at a
+// time through its own LDS scratch (F32, rows padded by 4 floats), then reads
+// them back along rows (or, for V^T, down columns), so every global access is
+// a 16-byte vector of 8 consecutive outputs: coalesced stores of the outputs,
+// and coalesced reads and writes of x for the residual. The values are the
+// accumulators exactly; only the order of the stores changes.
+template <typename T>
+__device__ __forceinline__ void store8(T *dst, const float (&v)[8]) {
+    typedef uint32_t vec4 __attribute__((ext_vector_type(4)));
+    T tmp[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) tmp[q] = from_f32<T>(v[q]);
+    *(vec4 *)dst = *(const vec4 *)tmp;
+}
+
+template <typename T, Epi KIND, int TM, int TN>
+__device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int mw, int nw, float *scratch,
+                                             const floatx16 (&acc)[TM][TN]) {
+    typedef float float4_t __attribute__((ext_vector_type(4)));
+    constexpr int COLS = TN * 32, SROW = COLS + 4, CH = COLS / 8;   // 8-column chunks per row
+    const int lane = threadIdx.x & 63, h = lane >> 5, ql = lane & 31;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        // Registers to LDS: row 8 (r / 4) + 4 h + r % 4, column 32 j + ql.
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) scratch[((r >> 2) * 8 + h * 4 + (r & 3)) * SROW + j * 32 + ql] = acc[i][j][r];
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+        const int mt = mw + i * 32;
+        if constexpr (KIND == Epi::Qkv || KIND == Epi::QkvRope) {
+            const int which = nw / e.hidden;   // a wave's 64 columns lie in one of Q, K, V
+            if (which == 2) {
+                // V^T: for each column, 8 consecutive tokens a lane.
+#pragma unroll
+                for (int k = 0; k < COLS * 4 / 64; ++k) {
+                    const int u = lane + 64 * k, col = u >> 2, g = (u & 3) * 8;
+                    const int n = nw + col;
+                    if (n >= N) continue;
+                    const int rem = n - 2 * e.hidden, head = rem / e.d, c = rem - head * e.d;
+                    float v[8];
+                    const float bias = e.bias ? e.bias[n] : 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) v[q] = scratch[(g + q) * SROW + col] + bias;
+                    T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + ((size_t)head * e.d + c) * e.tcap;
+                    const int m = mt + g;
+                    if (m + 8 <= M && (e.tcap & 7) == 0) {
+                        store8<T>(out + m, v);
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 8; ++q)
+                            if (m + q < M) out[m + q] = from_f32<T>(v[q]);
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+                continue;
+            }
+        }
+        // Row-wise: 8 consecutive columns of one row a lane; a lane's columns
+        // are the same on every pass (64 is a multiple of the chunks a row has).
+        static_assert(64 % CH == 0, "a lane keeps its columns");
+        const int cc = (lane % CH) * 8, n = nw + cc;
+        float bias[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) bias[q] = (e.bias && n + q < N) ? e.bias[n + q] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32 * CH / 64; ++k) {
+            const int row = (lane + 64 * k) / CH;
+            const int m = mt + row;
+            if (m >= M || n >= N) continue;
+            const bool full = n + 8 <= N;
+            float v[8];
+            const float4_t lo = *(const float4_t *)&scratch[row * SROW + cc];
+            const float4_t hi = *(const float4_t *)&scratch[row * SROW + cc + 4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[q] = lo[q] + bias[q];
+                v[4 + q] = hi[q] + bias[4 + q];
+            }
+            if constexpr (KIND == Epi::Plain) {
+                float *o = (float *)e.out + (size_t)m * e.ldo + n;
+                if (full) {
+                    *(float4_t *)o = float4_t{v[0], v[1], v[2], v[3]};
+                    *(float4_t *)(o + 4) = float4_t{v[4], v[5], v[6], v[7]};
+                } else {
+                    for (int q = 0; n + q < N; ++q) o[q] = v[q];
+                }
+            } else if constexpr (KIND == Epi::Residual) {
+                float *o = e.x + (size_t)m * e.ldo + n;
+                if (full) {
+                    const float4_t a = *(const float4_t *)o, b = *(const float4_t *)(o + 4);
+                    *(float4_t *)o = float4_t{a[0] + v[0], a[1] + v[1], a[2] + v[2], a[3] + v[3]};
+                    *(float4_t *)(o + 4) = float4_t{b[0] + v[4], b[1] + v[5], b[2] + v[6], b[3] + v[7]};
+                } else {
+                    for (int q = 0; n + q < N; ++q) o[q] = o[q] + v[q];
+                }
+            } else if constexpr (KIND == Epi::Gelu) {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) v[q] = sizeof(T) == 2 ? dev_gelu_fast(v[q]) : dev_gelu(v[q]);
+                T *o = (T *)e.out + (size_t)m * e.ldo + n;
+                if (full) store8<T>(o, v);
+                else for (int q = 0; n + q < N; ++q) o[q] = from_f32<T>(v[q]);
+            } else if constexpr (KIND == Epi::Gated) {
+                // Columns (2p, 2p + 1) are gate and up of output column n / 2 + p.
+                T *o = (T *)e.out + (size_t)m * e.ldo + (n >> 1);
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    if (n + 2 * p + 1 >= N) break;
+                    const float g = e.silu ? dev_silu(v[2 * p]) : sizeof(T) == 2 ? dev_gelu_fast(v[2 * p]) : dev_gelu(v[2 * p]);
+                    o[p] = from_f32<T>(__fmul_rn(g, v[2 * p + 1]));
+                }
+            } else {   // Qkv, QkvRope: Q or K, token-major per head
+                const int which = n / e.hidden, rem = n - which * e.hidden;
+                const int head = rem / e.d, c = rem - head * e.d;
+                if constexpr (KIND == Epi::QkvRope) {
+                    const int pos = e.at[m] % e.seq, half = e.d >> 1;
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        const int pr = (c >> 1) + p;
+                        const float cs = e.cos[(size_t)pos * half + pr], sn = e.sin[(size_t)pos * half + pr];
+                        const float x1 = v[2 * p], x2 = v[2 * p + 1];
+                        v[2 * p] = __fsub_rn(__fmul_rn(x1, cs), __fmul_rn(x2, sn));
+                        v[2 * p + 1] = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
+                    }
+                }
+                T *o = (T *)e.out + (size_t)which * e.heads * e.tcap * e.d + ((size_t)head * e.tcap + m) * e.d + c;
+                if (full && (e.d & 7) == 0) store8<T>(o, v);
+                else for (int q = 0; q < 8 && n + q < N; ++q) {
+                    const int nq = n + q, wq = nq / e.hidden, rq = nq - wq * e.hidden, hq = rq / e.d, cq = rq - hq * e.d;
+                    ((T *)e.out)[(size_t)wq * e.heads * e.tcap * e.d + ((size_t)hq * e.tcap + m) * e.d + cq] =
+                        from_f32<T>(v[q]);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, Epi KIND>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *__restrict__ W, EpiArgs e,
+                int grid_n) {
+    constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
+    constexpr int BK = 64, ROWB = 128;
+    constexpr int TILE = (BM + BN) * ROWB;             // bytes of one stage
+    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA tiles per wave
+    constexpr int LA = BM / 8 / WAVES, LB = BN / 8 / WAVES;   // 8-row load instructions per wave per stage
+    constexpr int L = LA + LB;
+    static_assert(LA * 8 * WAVES == BM && LB * 8 * WAVES == BN, "whole 8-row groups per wave");
+    static_assert(STAGES >= 2 && STAGES * TILE <= 160 * 1024, "LDS");
+    static_assert((STAGES - 2) * L < 64, "vmcnt");
+    typedef typename Mma<T>::frag frag;
+    extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+    const int nb = gridDim.x, per = nb / 8;
+    int b = blockIdx.x;
+    if (b < per * 8) b = (b % 8) * per + b / 8;
+    const int tile_n = b % grid_n, tile_m = b / grid_n;
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    // This lane's source in each of its load instructions.
+    const T *src_a[LA];
+    const T *src_b[LB];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+        const int row = (wave * LA + i) * 8 + (lane >> 3);
+        src_a[i] = A + (size_t)min(m0 + row, M - 1) * lda + 8 * ((lane & 7) ^ swz(row));
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+        const int row = (wave * LB + i) * 8 + (lane >> 3);
+        src_b[i] = W + (size_t)min(n0 + row, N - 1) * K + 8 * ((lane & 7) ^ swz(row));
+    }
+    // (The host pass of the compiler sees no LDS address space: the loads
+    // are device code alone.)
+    auto issue = [&](int stage, int k0) {
+#if defined(__HIP_DEVICE_COMPILE__)
+        char *base = smem + stage * TILE;
+#pragma unroll
+        for (int i = 0; i < LA; ++i)
+            __builtin_amdgcn_global_load_lds(src_a[i] + k0,
+                                             (__attribute__((address_space(3))) void *)(base + (wave * LA + i) * 8 * ROWB),
+                                             16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < LB; ++i)
+            __builtin_amdgcn_global_load_lds(
+                src_b[i] + k0, (__attribute__((address_space(3))) void *)(base + BM * ROWB + (wave * LB + i) * 8 * ROWB),
+                16, 0, 0);
+#else
+        (void)stage;
+        (void)k0;
+#endif
+    };
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = floatx16{};
+
+    const int nk = K / BK;
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+        if (st < nk) issue(st, st * BK);
+    const int ra = wm * (BM / WM) + (lane & 31), rb = wn * (BN / WN) + (lane & 31);
+    const int h = lane >> 5;
+    // Each lane's fragment addresses within a stage, for chunk pair (h, s).
+    int off_a[TM], off_b[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) off_a[i] = (ra + i * 32) * ROWB;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) off_b[j] = BM * ROWB + (rb + j * 32) * ROWB;
+    const int sw_a = swz(ra), sw_b = swz(rb);   // rows 32 apart share the swizzle
+    frag fa[2][TM], fb[2][TN];
+    auto fetch = [&](const char *base, int s, int set) {
+        const int c = 2 * s + h;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[set][i] = *(const frag *)(base + off_a[i] + 16 * (c ^ sw_a));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[set][j] = *(const frag *)(base + off_b[j] + 16 * (c ^ sw_b));
+    };
+    for (int kt = 0; kt < nk; ++kt) {
+        // This wave's loads of stage kt have landed once at most the later
+        // stages' are outstanding; then the barrier makes every wave's visible.
+        const int later = min(STAGES - 2, nk - 1 - kt);
+        if (later >= STAGES - 2) wait_vmcnt<(STAGES - 2) * L>();
+        else if (STAGES > 3 && later == 1) wait_vmcnt<L>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+        const char *base = smem + (kt % STAGES) * TILE;
+        // The next k-step's fragments are read while this one's products run.
+        // (sched_barrier keeps the compiler from sinking those reads back
+        // under the products that do not need them.)
+        fetch(base, 0, 0);
+#pragma unroll
+        for (int s = 0; s < BK / 16; ++s) {
+            if (s + 1 < BK / 16) fetch(base, s + 1, (s + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] = Mma<T>::run(fa[s & 1][i], fb[s & 1][j], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // Every wave is done with the stages: their LDS becomes each wave's
+    // staging area for the stores.
+    __syncthreads();
+    static_assert(WAVES * 32 * (TN * 32 + 4) * 4 <= STAGES * TILE, "epilogue staging fits the stages");
+    epilogue_lds<T, KIND, TM, TN>(e, M, N, m0 + wm * (BM / WM), n0 + wn * (BN / WN),
+                                  reinterpret_cast<float *>(smem) + wave * 32 * (TN * 32 + 4), acc);
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, Epi KIND>
+static hipError_t launch_lds_k(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W,
+                               const EpiArgs &e) {
+    constexpr int bytes = STAGES * (BM + BN) * 128;
+    // Dynamic LDS up to the device's 160 KB per workgroup needs no attribute on gfx950.
     const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM;
-    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, BK>), dim3(gn * gm), dim3(256), 0, s, M, N, K, (const T *)A, lda,
-                       (const T *)W, e, gn);
+    hipLaunchKernelGGL((gemm_lds_kernel<T, BM, BN, WM, WN, STAGES, KIND>), dim3(gn * gm), dim3(64 * WM * WN), bytes,
+                       s, M, N, K, (const T *)A, lda, (const T *)W, e, gn);
     return hipGetLastError();
 }
 
-int gemm_tiles() { return 3; }
+template <typename T, int BM, int BN, int WM, int WN, int STAGES>
+static hipError_t launch_lds(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W,
+                             const EpiArgs &e) {
+    switch (e.kind) {
+    case Epi::Plain: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Plain>(s, M, N, K, A, lda, W, e);
+    case Epi::Qkv: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Qkv>(s, M, N, K, A, lda, W, e);
+    case Epi::Gelu: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Gelu>(s, M, N, K, A, lda, W, e);
+    case Epi::Residual: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Residual>(s, M, N, K, A, lda, W, e);
+    case Epi::QkvRope: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::QkvRope>(s, M, N, K, A, lda, W, e);
+    case Epi::Gated: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Gated>(s, M, N, K, A, lda, W, e);
+    }
+    return hipErrorInvalidValue;
+}
 
+int gemm_tiles() { return 8; }
+
+// Block shapes by number: 1-3 stage operands through registers (any K a
+// multiple of 8, and the F32 tier); 4-6 are the pipelined kernel, for 16-bit
+// operands with K a multiple of 64 (every encoder shape here).
 template <typename T, int BK>
 static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
                          int tile) {
-    if (tile == 0) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
+    const bool pipelined = sizeof(T) == 2 && K % 64 == 0 && lda % 8 == 0;
+    if (tile == 0) tile = pipelined ? (M >= 2048 ? 7 : 5) : 1;
+    // A pipelined shape asked of an operand it cannot take runs the staged kernel.
+    if (tile >= 4 && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
     switch (tile) {
     case 1: return launch<T, 128, 128, BK>(s, M, N, K, A, lda, W, e);
     case 2: return launch<T, 256, 128, BK>(s, M, N, K, A, lda, W, e);
     case 3: return launch<T, 64, 128, BK>(s, M, N, K, A, lda, W, e);
-    default: return hipErrorInvalidValue;
     }
+    if constexpr (sizeof(T) == 2) {
+        switch (tile) {
+        case 4: return launch_lds<T, 256, 128, 2, 2, 3>(s, M, N, K, A, lda, W, e);
+        case 5: return launch_lds<T, 128, 128, 2, 2, 4>(s, M, N, K, A, lda, W, e);
+        case 6: return launch_lds<T, 128, 256, 2, 2, 3>(s, M, N, K, A, lda, W, e);
+        case 7: return launch_lds<T, 256, 256, 2, 4, 2>(s, M, N, K, A, lda, W, e);
+        case 8: return launch_lds<T, 128, 128, 2, 2, 2>(s, M, N, K, A, lda, W, e);
+        }
+    }
+    return hipErrorInvalidValue;
 }
 
 hipError_t gemm(hipStream_t s, Dt dt, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,

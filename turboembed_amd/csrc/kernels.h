@@ -70,11 +70,14 @@ hipError_t gemm(hipStream_t s, Dt dt, int M, int N, int K, const void *A, int ld
                 const EpiArgs &e, int tile = 0);
 int gemm_tiles();   // how many block shapes `tile` may name (1..n)
 
-// Softmax attention within each row and head over head-major Q, K, V
-// ([3][heads][tcap][d] in `dt`), into ctx [tokens, heads * d] in `dt`.
-// window: keys within `window` of the query (|i - j| <= window), or INT32_MAX.
+// Softmax attention within each row and head over Q and K ([heads][tcap][d]
+// each) and V transposed ([heads][d][tcap]), in `dt`, one after another in
+// qkv, into ctx [tokens, heads * d] in `dt`. window: keys within `window` of
+// the query (|i - j| <= window), or INT32_MAX. F16 and BF16 run on the matrix
+// cores unless `simple`; F32 runs the scalar path.
 hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
-                     const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx);
+                     const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx,
+                     bool simple = false);
 
 // One vector per row (mode 0: MEAN/CLS/LAST as pooling says) or per range
 // (mode 1: the mean over the range's live tokens), cut to output_dim, L2

@@ -357,14 +357,22 @@ uint32_t dtype_of(Dt dt) {
     }
 }
 
-// TURBO_ROCM_CHOICES: "gemm=<tile>" forces the GEMM block shape.
-bool parse_choices(const char *s, int &tile) {
+// TURBO_ROCM_CHOICES: "gemm=<tile>" forces the GEMM block shape,
+// "attention=simple" the scalar attention path on every tier.
+bool parse_choices(const char *s, int &tile, bool &simple) {
     if (!s || !*s) return false;
-    const char *g = std::strstr(s, "gemm=");
-    if (!g) return false;
-    tile = std::atoi(g + 5);
-    if (tile < 0 || tile > gemm_tiles()) fail(TURBO_E_INVALID_ARGUMENT, std::string("rocm: TURBO_ROCM_CHOICES ") + s);
-    return true;
+    bool any = false;
+    if (const char *g = std::strstr(s, "gemm=")) {
+        tile = std::atoi(g + 5);
+        if (tile < 0 || tile > gemm_tiles())
+            fail(TURBO_E_INVALID_ARGUMENT, std::string("rocm: TURBO_ROCM_CHOICES ") + s);
+        any = true;
+    }
+    if (const char *a = std::strstr(s, "attention=")) {
+        simple = std::strncmp(a + 10, "simple", 6) == 0;
+        any = true;
+    }
+    return any;
 }
 
 }  // namespace
@@ -418,10 +426,11 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
                      std::to_string(numeric_of(dt)),
                  3);
     }
-    if (parse_choices(std::getenv("TURBO_ROCM_CHOICES"), s->gemm_tile)) {
+    if (parse_choices(std::getenv("TURBO_ROCM_CHOICES"), s->gemm_tile, s->simple_attention)) {
         if (tuning) tuning->tuned = TURBO_TUNED_FORCED;
     }
-    s->choices = "gemm=" + std::to_string(s->gemm_tile) + " attention=simple";
+    s->choices = "gemm=" + std::to_string(s->gemm_tile) +
+                 (s->simple_attention || dt == Dt::F32 ? " attention=simple" : " attention=mfma");
     if (tuning) {
         std::snprintf(tuning->choices, sizeof tuning->choices, "%s", s->choices.c_str());
         if (tuning->struct_size >= offsetof(turbo_backend_tuning, numerics_used) + 4)
@@ -625,7 +634,7 @@ void encode(Session &s) {
         }
         LAUNCH("gemm_qkv", gemm(st, dt, T, (int)L.n_qkv, H, src, H, W.qkv, q, s.gemm_tile));
         LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, (int)s.seq, (int)s.batch,
-                                      (int)s.max_len, window, s.ctxb));
+                                      (int)s.max_len, window, s.ctxb, s.simple_attention));
         EpiArgs o;
         o.kind = Epi::Residual;
         o.bias = L.bo;
@@ -667,6 +676,22 @@ void encode(Session &s) {
 #undef LAUNCH
 }
 
+// After a synchronized run: each kernel's milliseconds, summed by name.
+void collect_times(Session &s) {
+    if (!s.timing) return;
+    std::map<std::string, double> by;
+    std::vector<std::string> order;
+    for (size_t i = 0; i + 1 < s.ev_used; i += 2) {
+        float ms = 0;
+        (void)hipEventElapsedTime(&ms, s.ev[i], s.ev[i + 1]);
+        const std::string &n = s.ev_name[i / 2];
+        if (!by.count(n)) order.push_back(n);
+        by[n] += ms;
+    }
+    s.last_times.clear();
+    for (auto &n : order) s.last_times.emplace_back(n, by[n]);
+}
+
 void session_run(Session *s, turbo_backend_run *out) {
     if (!s->written) fail(TURBO_E_INVALID_STATE, "rocm: the session has no rows written since its last run");
     s->written = false;
@@ -681,19 +706,7 @@ void session_run(Session *s, turbo_backend_run *out) {
             throw;
         }
         check(hipStreamSynchronize(s->ctx->stream), "the run");
-        if (s->timing) {
-            std::map<std::string, double> by;
-            std::vector<std::string> order;
-            for (size_t i = 0; i + 1 < s->ev_used; i += 2) {
-                float ms = 0;
-                (void)hipEventElapsedTime(&ms, s->ev[i], s->ev[i + 1]);
-                const std::string &n = s->ev_name[i / 2];
-                if (!by.count(n)) order.push_back(n);
-                by[n] += ms;
-            }
-            s->last_times.clear();
-            for (auto &n : order) s->last_times.emplace_back(n, by[n]);
-        }
+        collect_times(*s);
     }
     const uint32_t n_out = s->count ? s->count : s->batch;
     s->output.bytes = (uint64_t)n_out * s->output_dim * 4;
@@ -785,6 +798,7 @@ int32_t turbo_rocm_session_replay(void *session, uint32_t runs, turbo_error *err
         OnDevice on(s->ctx->ordinal);
         for (uint32_t i = 0; i < runs; ++i) encode(*s);
         check(hipStreamSynchronize(s->ctx->stream), "replay");
+        collect_times(*s);
         return TURBO_OK;
     });
 }
@@ -825,6 +839,44 @@ int32_t turbo_rocm_gemm_check(uint32_t ordinal, uint32_t dtype, uint32_t M, uint
         check(gemm(nullptr, dt, (int)M, (int)N, (int)K, pa, (int)K, pw, e, (int)tile), "gemm check");
         check(hipDeviceSynchronize(), "gemm check");
         check(hipMemcpy(out, o.get(), (size_t)M * N * 4, hipMemcpyDeviceToHost), "gemm check");
+        return TURBO_OK;
+    });
+}
+
+int32_t turbo_rocm_gemm_time(uint32_t ordinal, uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, uint32_t tile,
+                             uint32_t iters, float *ms, turbo_error *err) {
+    return guarded(err, [&] {
+        if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device");
+        if (iters == 0) fail(TURBO_E_INVALID_ARGUMENT, "rocm: iters");
+        const Dt dt = dtype == TURBO_DTYPE_F16 ? Dt::F16 : dtype == TURBO_DTYPE_BF16 ? Dt::BF16 : Dt::F32;
+        OnDevice on(devices()[ordinal]);
+        const size_t el = dt_bytes(dt);
+        DevPtr a(dev_alloc((size_t)M * K * el, "gemm time")), w(dev_alloc((size_t)N * K * el, "gemm time"));
+        DevPtr x(dev_alloc((size_t)M * N * 4, "gemm time")), b(dev_alloc((size_t)N * 4, "gemm time"));
+        // Small finite operands (every 16-bit value 0x1111, about 6.6e-4 in F16).
+        check(hipMemset(a.get(), 0x11, (size_t)M * K * el), "gemm time");
+        check(hipMemset(w.get(), 0x11, (size_t)N * K * el), "gemm time");
+        check(hipMemset(x.get(), 0, (size_t)M * N * 4), "gemm time");
+        check(hipMemset(b.get(), 0, (size_t)N * 4), "gemm time");
+        EpiArgs e;
+        e.kind = Epi::Residual;
+        e.bias = (const float *)b.get();
+        e.x = (float *)x.get();
+        e.ldo = (int)N;
+        hipEvent_t e0, e1;
+        check(hipEventCreate(&e0), "gemm time");
+        check(hipEventCreate(&e1), "gemm time");
+        for (int i = 0; i < 3; ++i) check(gemm(nullptr, dt, (int)M, (int)N, (int)K, a.get(), (int)K, w.get(), e, (int)tile), "gemm time");
+        check(hipEventRecord(e0, nullptr), "gemm time");
+        for (uint32_t i = 0; i < iters; ++i)
+            check(gemm(nullptr, dt, (int)M, (int)N, (int)K, a.get(), (int)K, w.get(), e, (int)tile), "gemm time");
+        check(hipEventRecord(e1, nullptr), "gemm time");
+        check(hipEventSynchronize(e1), "gemm time");
+        float t = 0;
+        check(hipEventElapsedTime(&t, e0, e1), "gemm time");
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        *ms = t / iters;
         return TURBO_OK;
     });
 }

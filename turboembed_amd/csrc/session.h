@@ -136,6 +136,7 @@ struct Session {
     std::vector<LayerWeights> *w = nullptr;
     std::string choices;
     int gemm_tile = 0;
+    bool simple_attention = false;
     // Per-launch timing (a test and benchmark hook): events around each
     // kernel of a run, by name.
     bool timing = false;
