@@ -142,18 +142,38 @@ template <> struct AttnMma<__bf16> {
 
 __device__ __forceinline__ int swap23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
+// LDS rows of 128 bytes (64 keys of V^T, or one key's 64 columns of K) keep
+// 16-byte chunk c at slot c ^ swz(row), as the GEMM's tiles do, so the
+// fragment reads of 16 consecutive rows fall in distinct banks.
+__device__ __forceinline__ int att_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+template <int N> __device__ __forceinline__ void att_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Keys stream through a STAGES-deep LDS ring filled by global_load_lds
+// (lane l of a load instruction writes 16 bytes at its base + 16 l): each
+// 64-key block is K (64 rows of d) and V^T (d rows of 64 keys), 8 rows per
+// instruction. Loads never leave the buffer: a key past the row's end reads a
+// clamped address, and its score is -inf, so it weighs exactly 0 (the
+// session zeroes Q, K and V once, so every value read is finite). Each
+// block's live keys are a 64-bit mask, the same for the whole workgroup.
 template <typename T, int D>
 __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads,
                                                              Packing p, const int32_t *__restrict__ mask, int seq,
                                                              int window, T *__restrict__ ctx) {
-    constexpr int QB = 128, KB = 64;
-    constexpr int KS = D + 8;     // LDS row of K, padded by 16 bytes
-    constexpr int VS = KB + 8;    // LDS row of V^T
+    constexpr int QB = 128, KB = 64, STAGES = 3;
+    constexpr int KBYTES = KB * D * 2, VBYTES = D * KB * 2, SBYTES = KBYTES + VBYTES;
+    constexpr int LK = KB / 8 / 4 * (D / 64 > 0 ? D / 64 : 1);   // K load instructions per wave
+    constexpr int KROW = D * 2;                                   // bytes of one K row
     typedef typename AttnMma<T>::frag frag;
     typedef uint32_t vec4 __attribute__((ext_vector_type(4)));
-    __shared__ __attribute__((aligned(16))) T ks[KB * KS];
-    __shared__ __attribute__((aligned(16))) T vts[D * VS];
-    __shared__ float live[KB];
+    static_assert(D == 64, "the ring kernel is written for 64-wide heads");
+    // The ring is dynamic LDS (STAGES * SBYTES bytes, the launch's), then the
+    // live masks: memory the compiler sees written only through the loads.
+    extern __shared__ __attribute__((aligned(1024))) char ring[];
+    uint64_t *live_bits = reinterpret_cast<uint64_t *>(ring + STAGES * SBYTES);
 
     const int r = blockIdx.z, head = blockIdx.y, q0 = blockIdx.x * QB;
     const int len = p.len[r];
@@ -163,10 +183,9 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
     const int query = q0 + wave * 32 + ql;
     const T *Q = qkv + ((size_t)head * tcap + start) * D;
     const T *K = qkv + ((size_t)(heads + head) * tcap + start) * D;
-    const T *Vt = qkv + (size_t)2 * heads * tcap * D + (size_t)head * D * tcap + start;
+    const T *Vt = qkv + (size_t)2 * heads * tcap * D + (size_t)head * D * tcap;
     const int32_t *mk = mask + (size_t)r * seq;
 
-    // This lane's query as the B operand of S^T, d/16 fragments of 8.
     frag qf[D / 16];
     {
         const T *qrow = Q + (size_t)min(query, len - 1) * D + h * 8;
@@ -176,7 +195,6 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
             qf[s] = *(const frag *)&v;
         }
     }
-    // log2(e) / sqrt(d): scores go straight to base 2.
     const float scale = 1.4426950408889634f / sqrtf((float)D);
     floatx16_t o[D / 32];
 #pragma unroll
@@ -188,55 +206,93 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
         k_lo = max(0, q0 - window) / KB * KB;
         k_hi = min(len, q0 + QB + window);
     }
-    for (int kb = k_lo; kb < k_hi; kb += KB) {
-        __syncthreads();
-        // K rows kb .. kb + 63: 64 x D as 16-byte vectors; rows past len are 0.
+    const int nb = (k_hi - k_lo + KB - 1) / KB;
+    // This lane's K row and V^T row within each of its load instructions.
+    const int lrow = lane >> 3, lchunk = lane & 7;
+    auto issue = [&](int stage, int kb) {
+        char *base = ring + stage * SBYTES;
+#if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
-        for (int i = 0; i < KB * D / 8 / 256; ++i) {
-            const int v = tid + 256 * i, row = v / (D / 8), c = (v % (D / 8)) * 8;
-            vec4 x = vec4{0, 0, 0, 0};
-            if (kb + row < len) x = *(const vec4 *)(K + (size_t)(kb + row) * D + c);
-            *(vec4 *)&ks[row * KS + c] = x;
+        for (int i = 0; i < 2; ++i) {
+            const int row = (wave * 2 + i) * 8 + lrow;               // key within the block
+            const int key = min(kb + row, len - 1);
+            const T *src = K + (size_t)key * D + 8 * (lchunk ^ att_swz(row));
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(base + (wave * 2 + i) * 8 * KROW),
+                                             16, 0, 0);
         }
-        // V^T columns kb .. kb + 63 of each of the D rows.
 #pragma unroll
-        for (int i = 0; i < KB * D / 8 / 256; ++i) {
-            const int v = tid + 256 * i, c = v / (KB / 8), j = (v % (KB / 8)) * 8;
-            const T *src = Vt + (size_t)c * tcap + kb + j;
-            vec4 x;
-            if (kb + j + 8 <= len) {
-                x = *(const vec4 *)src;
-            } else {
-                T tmp[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) tmp[e] = kb + j + e < len ? src[e] : from_f32<T>(0.0f);
-                x = *(const vec4 *)tmp;
-            }
-            *(vec4 *)&vts[c * VS + j] = x;
+        for (int i = 0; i < 2; ++i) {
+            const int c = (wave * 2 + i) * 8 + lrow;                 // column of d
+            // Keys kb + 8 slot .. + 7 of column c; a chunk wholly past the
+            // row reads the row's last chunk instead (it weighs 0).
+            const int slot = lchunk ^ att_swz(c);
+            int k0 = kb + 8 * slot;
+            if (k0 >= len) k0 = max(0, (len - 1) & ~7);
+            const T *src = Vt + (size_t)c * tcap + start + k0;
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(base + KBYTES + (wave * 2 + i) * 8 * 128),
+                                             16, 0, 0);
         }
-        if (tid < KB) live[tid] = (kb + tid < len && mk[kb + tid] != 0) ? 1.0f : 0.0f;
+#else
+        (void)base;
+        (void)kb;
+#endif
+        if (wave == 0) {
+            const int key = kb + lane;
+            const bool on = key < len && mk[key] != 0;
+            const uint64_t bits = __ballot(on);
+            if (lane == 0) live_bits[stage] = bits;
+        }
+    };
+    (void)LK;
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+        if (st < nb) issue(st, k_lo + st * KB);
+
+    for (int bi = 0; bi < nb; ++bi) {
+        const int kb = k_lo + bi * KB;
+        const int later = min(STAGES - 2, nb - 1 - bi);
+        if (later >= 1) att_wait_vmcnt<4>();
+        else att_wait_vmcnt<0>();
         __syncthreads();
+        if (bi + STAGES - 1 < nb) issue((bi + STAGES - 1) % STAGES, kb + (STAGES - 1) * KB);
+        const int stage = bi % STAGES;
+        const char *kbase = ring + stage * SBYTES;
+        const char *vbase = kbase + KBYTES;
+        const uint64_t bits = live_bits[stage];
 
         floatx16_t sc[2];
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             floatx16_t a = floatx16_t{};
-            const T *krow = &ks[(sub * 32 + swap23(ql)) * KS + h * 8];
+            const int row = sub * 32 + swap23(ql);
 #pragma unroll
-            for (int s = 0; s < D / 16; ++s) a = AttnMma<T>::run(*(const frag *)(krow + s * 16), qf[s], a);
+            for (int s = 0; s < D / 16; ++s) {
+                const int c = 2 * s + h;
+                a = AttnMma<T>::run(*(const frag *)(kbase + row * KROW + 16 * (c ^ att_swz(row))), qf[s], a);
+            }
             sc[sub] = a;
         }
-        // Scale, mask, and the block's max for this query.
+        // Scale, mask (a block wholly live and in every query's window skips
+        // the per-key tests), and the block's max for this query.
+        const bool all_live = bits == ~0ull && (window == INT32_MAX ||
+                                                 (kb >= q0 + QB - 1 - window && kb + KB - 1 <= q0 + window));
         float mx = -INFINITY;
+        const uint32_t lh = (uint32_t)(bits >> (8 * h)), hh = (uint32_t)(bits >> (32 + 8 * h));
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
             for (int rr = 0; rr < 16; ++rr) {
-                const int j = sub * 32 + 16 * (rr >> 3) + 8 * h + (rr & 7);
-                const int key = kb + j;
-                bool ok = live[j] != 0.0f;
-                if (window < INT32_MAX) ok = ok && key + window >= query && key <= query + window;
-                const float v = ok ? sc[sub][rr] * scale : -INFINITY;
+                float v = sc[sub][rr] * scale;
+                if (!all_live) {
+                    const int j = 16 * (rr >> 3) + (rr & 7);       // key - sub * 32 - 8 h
+                    const uint32_t word = sub ? hh : lh;
+                    bool ok = (word >> j) & 1u;
+                    if (window < INT32_MAX) {
+                        const int key = kb + sub * 32 + 8 * h + j;
+                        ok = ok && key + window >= query && key <= query + window;
+                    }
+                    v = ok ? v : -INFINITY;
+                }
                 sc[sub][rr] = v;
                 mx = fmaxf(mx, v);
             }
@@ -249,7 +305,7 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
         const float m_use = none ? 0.0f : m_new;
         const float alpha = m_run == -INFINITY ? (none ? 1.0f : 0.0f) : __builtin_amdgcn_exp2f(m_run - m_use);
         float rs = 0.0f;
-        typename AttnMma<T>::frag pf[2][2];
+        frag pf[2][2];
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -257,8 +313,7 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
                 T pv[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float x = sc[sub][step * 8 + e];
-                    const float pe = x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x - m_use);
+                    const float pe = __builtin_amdgcn_exp2f(sc[sub][step * 8 + e] - m_use);
                     rs += pe;
                     pv[e] = from_f32<T>(pe);
                 }
@@ -274,7 +329,9 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
             for (int step = 0; step < 2; ++step)
 #pragma unroll
                 for (int t = 0; t < D / 32; ++t) {
-                    const frag vf = *(const frag *)&vts[(32 * t + ql) * VS + sub * 32 + step * 16 + h * 8];
+                    const int row = 32 * t + ql;
+                    const int c = sub * 4 + step * 2 + h;
+                    const frag vf = *(const frag *)(vbase + row * 128 + 16 * (c ^ att_swz(row)));
                     o[t] = AttnMma<T>::run(vf, pf[sub][step], o[t]);
                 }
     }
@@ -285,9 +342,12 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
 #pragma unroll
     for (int t = 0; t < D / 32; ++t)
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) {
-            const int c = 32 * t + 8 * (rr >> 2) + 4 * h + (rr & 3);
-            out[c] = from_f32<T>(o[t][rr] * inv);
+        for (int rr = 0; rr < 16; rr += 4) {
+            const int c = 32 * t + 8 * (rr >> 2) + 4 * h;
+            T v4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v4[q] = from_f32<T>(o[t][rr + q] * inv);
+            *(uint2 *)(out + c) = *(const uint2 *)v4;
         }
 }
 
@@ -295,28 +355,18 @@ template <typename T>
 static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
                                    const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx) {
     const dim3 grid((max_len + 127) / 128, heads, batch);
-    switch (d) {
-    case 32:
-        hipLaunchKernelGGL((attention_mfma_kernel<T, 32>), grid, dim3(256), 0, s, (const T *)qkv, tcap, heads, p, mask,
-                           seq, window, (T *)ctx);
-        break;
-    case 64:
-        hipLaunchKernelGGL((attention_mfma_kernel<T, 64>), grid, dim3(256), 0, s, (const T *)qkv, tcap, heads, p, mask,
-                           seq, window, (T *)ctx);
-        break;
-    case 128:
-        hipLaunchKernelGGL((attention_mfma_kernel<T, 128>), grid, dim3(256), 0, s, (const T *)qkv, tcap, heads, p,
-                           mask, seq, window, (T *)ctx);
-        break;
-    default: return hipErrorInvalidValue;
-    }
+    if (d != 64) return hipErrorInvalidValue;
+    // Three stages of K (64 x 64) and V^T (64 x 64) blocks, then three live masks.
+    constexpr int bytes = 3 * 2 * 64 * 64 * 2 + 3 * 8;
+    hipLaunchKernelGGL((attention_mfma_kernel<T, 64>), grid, dim3(256), bytes, s, (const T *)qkv, tcap, heads, p, mask,
+                       seq, window, (T *)ctx);
     return hipGetLastError();
 }
 
 hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
                      const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx, bool simple) {
     if (max_len <= 0) return hipSuccess;
-    const bool mfma = (d == 32 || d == 64 || d == 128) && !simple;
+    const bool mfma = d == 64 && !simple;
     switch (dt) {
     case Dt::F16:
         return mfma ? attention_mfma_t<_Float16>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, window, ctx)

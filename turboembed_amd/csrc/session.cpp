@@ -460,7 +460,11 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     s->pk.tokens = pk + 2 * B + 2 * s->tcap;
     s->x = static_cast<float *>(alloc(s->tcap * H * 4, "session states"));
     s->xh = alloc(s->tcap * H * 4, "session states");
-    s->qkv = alloc(3 * s->tcap * H * el, "session qkv");
+    // Q, K and V, plus a 256-byte tail: the attention kernel's 16-byte loads
+    // of V^T may run a few elements past a row. Zeroed once, so every value
+    // it can read is finite.
+    s->qkv = alloc(3 * s->tcap * H * el + 256, "session qkv");
+    check(hipMemset(s->qkv, 0, 3 * s->tcap * H * el + 256), "session qkv");
     s->ctxb = alloc(s->tcap * H * el, "session context");
     s->ffn = alloc(s->tcap * (m->rotary ? I : I) * el, "session ffn");
     const size_t outs = std::max<size_t>(B, s->max_ranges);
