@@ -30,6 +30,13 @@ extern const turbo_backend turbo_rocm_backend;
  * (core/src/tuning.rs:32-41) needs for a BF16-stored model. */
 #define TURBO_ROCM_NUMERIC_BF16_F32ACC 16u
 
+/* The numeric class of int8 operands with int32 sums, dequantized in F32: a
+ * symmetric scale per weight row (output channel) and per token, this
+ * backend's I8 tier. It runs for a model whose turbo_backend_model.compute_dtype
+ * is TURBO_DTYPE_I8, at MODEL and FASTEST; the reference's only I8 encoder is
+ * a compiled Hailo graph (core/hailo/backend.cpp:441-443, 510). */
+#define TURBO_ROCM_NUMERIC_I8_I32ACC 32u
+
 /* ---- The core's checks of a write (core/src/session/tokens.rs:274-384) ----
  *
  * turbo_rocm_check_tokens: the rows' shape within max_batch x max_seq, each id

@@ -31,7 +31,7 @@ def assert_close(got, want, compute_dtype):
 # ---- The GEMM kernel alone ------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [S.TURBO_DTYPE_F32, S.TURBO_DTYPE_F16, S.TURBO_DTYPE_BF16])
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 200, 96), (33, 96, 32), (1000, 768, 768), (517, 2304, 1152)])
 def test_gemm_matches_numpy(runtime, dtype, tile, mnk):
     m, n, k = mnk
@@ -222,4 +222,89 @@ def test_matrix_core_attention_meets_the_oracle(context, family, heads, monkeypa
         got[path] = s.embed(ids, mask, types)
         assert_close(got[path], want, s.compute_dtype)
         s.close()
+    model.close()
+
+
+# ---- The int8 tier ---------------------------------------------------------------------
+#
+# No reference kernel exists for it (the reference's one I8 encoder is a
+# compiled Hailo graph); its bound is the conformance floor for I8, cosine
+# >= 0.93 against the F32 oracle (core/tests/common/conformance.rs:15).
+
+I8_FLOOR = 0.93
+
+
+def quantize_rows(x):
+    """Symmetric int8 rows as the kernels make them: scale = max|x| / 127,
+    q = round-half-even(x * (127 / max|x|)), all in F32."""
+    x = np.asarray(x, np.float32)
+    mx = np.abs(x).max(1).astype(np.float32)
+    inv = np.where(mx > 0, np.float32(127) / np.where(mx > 0, mx, 1), 0).astype(np.float32)
+    q = np.clip(np.rint(x * inv[:, None]), -127, 127).astype(np.int64)
+    return q, (mx / np.float32(127)).astype(np.float32)
+
+
+@pytest.mark.parametrize("tile", [0, 7, 9])
+@pytest.mark.parametrize("mnk", [(256, 256, 128), (300, 200, 64), (1000, 768, 768), (517, 2304, 3072), (33, 96, 192)])
+def test_int8_gemm_is_the_integer_product(runtime, tile, mnk):
+    # The int32 sums are exact; the dequantized F32 result differs from
+    # (sum * a_scale * w_scale + bias), computed the same way, by F32
+    # rounding of a sum past 2^24 at most.
+    m, n, k = mnk
+    g = np.random.Generator(np.random.PCG64(m * 5 + n + k))
+    a = g.standard_normal((m, k)).astype(np.float32)
+    w = (g.standard_normal((n, k)) * 0.05).astype(np.float32)
+    a[3] = 0.0   # a zero row: scale 0, output the bias
+    b = g.standard_normal(n).astype(np.float32)
+    got = T.gemm_check(a, w, b, dtype=S.TURBO_DTYPE_I8, tile=tile)
+    qa, sa = quantize_rows(a)
+    qw, sw = quantize_rows(w)
+    acc = (qa @ qw.T).astype(np.float64)
+    want = acc * sa[:, None].astype(np.float64) * sw[None, :].astype(np.float64) + b
+    scale = np.abs(acc).max() * sa.max() * sw.max() + 1
+    assert np.abs(got - want).max() <= 1e-6 * scale, np.abs(got - want).max()
+    np.testing.assert_array_equal(got[3], b)
+
+
+def int8_model(desc):
+    desc.compute_dtype = S.TURBO_DTYPE_I8
+    return desc
+
+
+@pytest.mark.parametrize("family", ["bert", "modernbert", "nomic"])
+def test_int8_ragged_rows_meet_the_oracle(context, family):
+    kw = dict(seed=31, hidden=128, inter=256)
+    desc = int8_model(MODELS[family](**kw))
+    ids, mask, types = small.ragged_rows(31, 7, 48, desc.vocab_size)
+    if family == "modernbert":
+        types = None
+    model = context.load(desc)
+    s = model.session(8, 64, S.TURBO_PRECISION_FASTEST)
+    assert s.compute_dtype == S.TURBO_DTYPE_I8
+    for pooling in (S.TURBO_POOLING_MEAN, S.TURBO_POOLING_CLS):
+        got = s.embed(ids, mask, types, pooling=pooling)
+        want = oracle.encode(desc, ids, mask, types, pooling=pooling)
+        cos = small.cosine_rows(got, want)
+        assert cos.min() >= I8_FLOOR, cos.min()
+    s.close()
+    # EXACT on the same model computes in F32.
+    s = model.session(8, 64, S.TURBO_PRECISION_EXACT)
+    assert s.compute_dtype == S.TURBO_DTYPE_F32
+    assert_close(s.embed(ids, mask, types), oracle.encode(desc, ids, mask, types), s.compute_dtype)
+    s.close()
+    model.close()
+
+
+def test_int8_bert_base_meets_the_oracle(context):
+    sh = W.SHAPES["bert-base"]
+    desc = int8_model(W.model(sh, layers=2))
+    ids, mask, types = W.rows(sh, batch=6, lengths=(64, 512))
+    model = context.load(desc)
+    s = model.session(64, 512, S.TURBO_PRECISION_FASTEST)
+    assert s.compute_dtype == S.TURBO_DTYPE_I8
+    got = s.embed(ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
+    want = oracle.encode(desc, ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
+    cos = small.cosine_rows(got, want)
+    assert cos.min() >= I8_FLOOR, cos.min()
+    s.close()
     model.close()

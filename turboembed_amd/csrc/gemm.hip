@@ -20,6 +20,8 @@
 // blocks are renumbered so that each XCD takes a contiguous run of output
 // tiles, along N first: the run shares its A rows, which then stay in that
 // XCD's L2.
+#include <type_traits>
+
 #include "kernels.h"
 #include "devmath.h"
 
@@ -32,9 +34,13 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <typename T> struct Mma;
 
+typedef int int32x4 __attribute__((ext_vector_type(4)));
+typedef int int32x16 __attribute__((ext_vector_type(16)));
+
 template <> struct Mma<_Float16> {
     static constexpr int EPM = 8;   // elements a lane feeds one MFMA
     typedef half8 frag;
+    typedef floatx16 acc;
     static __device__ __forceinline__ floatx16 run(frag a, frag b, floatx16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }
@@ -43,14 +49,25 @@ template <> struct Mma<_Float16> {
 template <> struct Mma<__bf16> {
     static constexpr int EPM = 8;
     typedef bf16x8 frag;
+    typedef floatx16 acc;
     static __device__ __forceinline__ floatx16 run(frag a, frag b, floatx16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <> struct Mma<int8_t> {
+    static constexpr int EPM = 16;
+    typedef int32x4 frag;
+    typedef int32x16 acc;
+    static __device__ __forceinline__ int32x16 run(frag a, frag b, int32x16 c) {
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
     }
 };
 
 template <> struct Mma<float> {
     static constexpr int EPM = 1;
     typedef float frag;
+    typedef floatx16 acc;
     static __device__ __forceinline__ floatx16 run(frag a, frag b, floatx16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
     }
@@ -250,6 +267,10 @@ static hipError_t launch(hipStream_t s, int M, int N, int K, const void *A, int 
 // load instruction fills slot (lane & 7) of row (lane >> 3) of its 8-row
 // group, so it fetches global chunk (lane & 7) ^ f(row).
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+// Rows of 64 bytes (BK 32) hold 4 chunks: chunk c of row r at slot
+// c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1)), distinct over 8 and over 16 rows alike.
+__device__ __forceinline__ int swz4(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
+template <int ROWB> __device__ __forceinline__ int swz_of(int row) { return ROWB == 128 ? swz(row) : swz4(row); }
 
 // s_waitcnt vmcnt(N) with the other counters left free (gfx9 encoding).
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
@@ -272,38 +293,52 @@ __device__ __forceinline__ void store8(T *dst, const float (&v)[8]) {
     *(vec4 *)dst = *(const vec4 *)tmp;
 }
 
-template <typename T, Epi KIND, int TM, int TN>
+template <typename T, Epi KIND, int TM, int TN, int PASS, bool SCALED, typename ACC>
 __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int mw, int nw, float *scratch,
-                                             const floatx16 (&acc)[TM][TN]) {
+                                             const ACC (&acc)[TM][TN]) {
     typedef float float4_t __attribute__((ext_vector_type(4)));
     constexpr int COLS = TN * 32, SROW = COLS + 4, CH = COLS / 8;   // 8-column chunks per row
+    static_assert(PASS == 32 || PASS == 16, "32 or 16 rows a pass");
     const int lane = threadIdx.x & 63, h = lane >> 5, ql = lane & 31;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        // Registers to LDS: row 8 (r / 4) + 4 h + r % 4, column 32 j + ql.
+    for (int pi = 0; pi < TM * (32 / PASS); ++pi) {
+        const int i = pi / (32 / PASS), half = pi % (32 / PASS);
+        // Registers to LDS: row 8 (r / 4) + 4 h + r % 4 of the 32, column
+        // 32 j + ql; a 16-row pass takes registers r < 8 (rows 0-15), then the rest.
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) scratch[((r >> 2) * 8 + h * 4 + (r & 3)) * SROW + j * 32 + ql] = acc[i][j][r];
+            for (int r = 0; r < 16; ++r) {
+                if (PASS == 16 && (r >> 3) != half) continue;
+                const int row = (r >> 2) * 8 + h * 4 + (r & 3) - (PASS == 16 ? half * 16 : 0);
+                scratch[row * SROW + j * 32 + ql] = (float)acc[i][j][r];
+            }
         __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
         __builtin_amdgcn_wave_barrier();
-        const int mt = mw + i * 32;
+        const int mt = mw + i * 32 + half * PASS;
         if constexpr (KIND == Epi::Qkv || KIND == Epi::QkvRope) {
             const int which = nw / e.hidden;   // a wave's 64 columns lie in one of Q, K, V
             if (which == 2) {
                 // V^T: for each column, 8 consecutive tokens a lane.
 #pragma unroll
-                for (int k = 0; k < COLS * 4 / 64; ++k) {
-                    const int u = lane + 64 * k, col = u >> 2, g = (u & 3) * 8;
+                for (int k = 0; k < COLS * (PASS / 8) / 64; ++k) {
+                    const int u = lane + 64 * k, col = u / (PASS / 8), g = (u % (PASS / 8)) * 8;
                     const int n = nw + col;
                     if (n >= N) continue;
                     const int rem = n - 2 * e.hidden, head = rem / e.d, c = rem - head * e.d;
                     float v[8];
                     const float bias = e.bias ? e.bias[n] : 0.0f;
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) v[q] = scratch[(g + q) * SROW + col] + bias;
-                    T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + ((size_t)head * e.d + c) * e.tcap;
                     const int m = mt + g;
+                    if constexpr (SCALED) {
+                        const float ws = e.w_scale[n];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q)
+                            v[q] = scratch[(g + q) * SROW + col] * (m + q < M ? e.a_scale[m + q] : 0.0f) * ws + bias;
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) v[q] = scratch[(g + q) * SROW + col] + bias;
+                    }
+                    T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + ((size_t)head * e.d + c) * e.tcap;
                     if (m + 8 <= M && (e.tcap & 7) == 0) {
                         store8<T>(out + m, v);
                     } else {
@@ -320,11 +355,14 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
         // are the same on every pass (64 is a multiple of the chunks a row has).
         static_assert(64 % CH == 0, "a lane keeps its columns");
         const int cc = (lane % CH) * 8, n = nw + cc;
-        float bias[8];
+        float bias[8], wsc[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) bias[q] = (e.bias && n + q < N) ? e.bias[n + q] : 0.0f;
+        for (int q = 0; q < 8; ++q) {
+            bias[q] = (e.bias && n + q < N) ? e.bias[n + q] : 0.0f;
+            wsc[q] = (SCALED && n + q < N) ? e.w_scale[n + q] : 1.0f;
+        }
 #pragma unroll
-        for (int k = 0; k < 32 * CH / 64; ++k) {
+        for (int k = 0; k < PASS * CH / 64; ++k) {
             const int row = (lane + 64 * k) / CH;
             const int m = mt + row;
             if (m >= M || n >= N) continue;
@@ -332,10 +370,16 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
             float v[8];
             const float4_t lo = *(const float4_t *)&scratch[row * SROW + cc];
             const float4_t hi = *(const float4_t *)&scratch[row * SROW + cc + 4];
+            const float as = SCALED ? e.a_scale[m] : 1.0f;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                v[q] = lo[q] + bias[q];
-                v[4 + q] = hi[q] + bias[4 + q];
+                if constexpr (SCALED) {
+                    v[q] = lo[q] * as * wsc[q] + bias[q];
+                    v[4 + q] = hi[q] * as * wsc[4 + q] + bias[4 + q];
+                } else {
+                    v[q] = lo[q] + bias[q];
+                    v[4 + q] = hi[q] + bias[4 + q];
+                }
             }
             if constexpr (KIND == Epi::Plain) {
                 float *o = (float *)e.out + (size_t)m * e.ldo + n;
@@ -396,20 +440,24 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
     }
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int STAGES, Epi KIND>
-__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <typename T, typename OT, int BM, int BN, int WM, int WN, int STAGES, int BK, int OCC, Epi KIND>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *__restrict__ W, EpiArgs e,
                 int grid_n) {
     constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
-    constexpr int BK = 64, ROWB = 128;
+    constexpr int EPC = 16 / (int)sizeof(T);                 // elements in a 16-byte chunk
+    constexpr int ROWB = BK * (int)sizeof(T), CHUNKS = ROWB / 16;   // bytes and chunks of a tile row
+    constexpr int RPI = 64 / CHUNKS;                      // rows one load instruction fills
     constexpr int TILE = (BM + BN) * ROWB;             // bytes of one stage
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA tiles per wave
-    constexpr int LA = BM / 8 / WAVES, LB = BN / 8 / WAVES;   // 8-row load instructions per wave per stage
+    constexpr int LA = BM / RPI / WAVES, LB = BN / RPI / WAVES;   // load instructions per wave per stage
     constexpr int L = LA + LB;
-    static_assert(LA * 8 * WAVES == BM && LB * 8 * WAVES == BN, "whole 8-row groups per wave");
+    static_assert(ROWB == 128 || ROWB == 64, "tile rows of 64 or 128 bytes");
+    static_assert(LA * RPI * WAVES == BM && LB * RPI * WAVES == BN, "whole row groups per wave");
     static_assert(STAGES >= 2 && STAGES * TILE <= 160 * 1024, "LDS");
     static_assert((STAGES - 2) * L < 64, "vmcnt");
     typedef typename Mma<T>::frag frag;
+    typedef typename Mma<T>::acc acc_t;
     extern __shared__ __attribute__((aligned(1024))) char smem[];
 
     const int nb = gridDim.x, per = nb / 8;
@@ -425,13 +473,13 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
     const T *src_b[LB];
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
-        const int row = (wave * LA + i) * 8 + (lane >> 3);
-        src_a[i] = A + (size_t)min(m0 + row, M - 1) * lda + 8 * ((lane & 7) ^ swz(row));
+        const int row = (wave * LA + i) * RPI + lane / CHUNKS;
+        src_a[i] = A + (size_t)min(m0 + row, M - 1) * lda + EPC * ((lane % CHUNKS) ^ swz_of<ROWB>(row));
     }
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
-        const int row = (wave * LB + i) * 8 + (lane >> 3);
-        src_b[i] = W + (size_t)min(n0 + row, N - 1) * K + 8 * ((lane & 7) ^ swz(row));
+        const int row = (wave * LB + i) * RPI + lane / CHUNKS;
+        src_b[i] = W + (size_t)min(n0 + row, N - 1) * K + EPC * ((lane % CHUNKS) ^ swz_of<ROWB>(row));
     }
     // (The host pass of the compiler sees no LDS address space: the loads
     // are device code alone.)
@@ -441,12 +489,12 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
 #pragma unroll
         for (int i = 0; i < LA; ++i)
             __builtin_amdgcn_global_load_lds(src_a[i] + k0,
-                                             (__attribute__((address_space(3))) void *)(base + (wave * LA + i) * 8 * ROWB),
+                                             (__attribute__((address_space(3))) void *)(base + (wave * LA + i) * RPI * ROWB),
                                              16, 0, 0);
 #pragma unroll
         for (int i = 0; i < LB; ++i)
             __builtin_amdgcn_global_load_lds(
-                src_b[i] + k0, (__attribute__((address_space(3))) void *)(base + BM * ROWB + (wave * LB + i) * 8 * ROWB),
+                src_b[i] + k0, (__attribute__((address_space(3))) void *)(base + BM * ROWB + (wave * LB + i) * RPI * ROWB),
                 16, 0, 0);
 #else
         (void)stage;
@@ -454,11 +502,11 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
 #endif
     };
 
-    floatx16 acc[TM][TN];
+    acc_t acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = floatx16{};
+        for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{};
 
     const int nk = K / BK;
 #pragma unroll
@@ -472,7 +520,7 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
     for (int i = 0; i < TM; ++i) off_a[i] = (ra + i * 32) * ROWB;
 #pragma unroll
     for (int j = 0; j < TN; ++j) off_b[j] = BM * ROWB + (rb + j * 32) * ROWB;
-    const int sw_a = swz(ra), sw_b = swz(rb);   // rows 32 apart share the swizzle
+    const int sw_a = swz_of<ROWB>(ra), sw_b = swz_of<ROWB>(rb);   // rows 32 apart share the swizzle
     frag fa[2][TM], fb[2][TN];
     auto fetch = [&](const char *base, int s, int set) {
         const int c = 2 * s + h;
@@ -496,8 +544,8 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
         // under the products that do not need them.)
         fetch(base, 0, 0);
 #pragma unroll
-        for (int s = 0; s < BK / 16; ++s) {
-            if (s + 1 < BK / 16) fetch(base, s + 1, (s + 1) & 1);
+        for (int s = 0; s < ROWB / 32; ++s) {
+            if (s + 1 < ROWB / 32) fetch(base, s + 1, (s + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -510,37 +558,44 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
     // Every wave is done with the stages: their LDS becomes each wave's
     // staging area for the stores.
     __syncthreads();
-    static_assert(WAVES * 32 * (TN * 32 + 4) * 4 <= STAGES * TILE, "epilogue staging fits the stages");
-    epilogue_lds<T, KIND, TM, TN>(e, M, N, m0 + wm * (BM / WM), n0 + wn * (BN / WN),
-                                  reinterpret_cast<float *>(smem) + wave * 32 * (TN * 32 + 4), acc);
+    constexpr int PASS = WAVES * 32 * (TN * 32 + 4) * 4 <= STAGES * TILE ? 32 : 16;
+    static_assert(WAVES * PASS * (TN * 32 + 4) * 4 <= STAGES * TILE, "epilogue staging fits the stages");
+    epilogue_lds<OT, KIND, TM, TN, PASS, sizeof(T) == 1>(e, M, N, m0 + wm * (BM / WM), n0 + wn * (BN / WN),
+                                                         reinterpret_cast<float *>(smem) + wave * PASS * (TN * 32 + 4),
+                                                         acc);
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int STAGES, Epi KIND>
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK, int OCC, Epi KIND>
 static hipError_t launch_lds_k(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W,
                                const EpiArgs &e) {
-    constexpr int bytes = STAGES * (BM + BN) * 128;
+    // int8 operands write F16 activations.
+    typedef typename std::conditional<sizeof(T) == 1, _Float16, T>::type OT;
+    constexpr int bytes = STAGES * (BM + BN) * BK * (int)sizeof(T);
     // Dynamic LDS up to the device's 160 KB per workgroup needs no attribute on gfx950.
     const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM;
-    hipLaunchKernelGGL((gemm_lds_kernel<T, BM, BN, WM, WN, STAGES, KIND>), dim3(gn * gm), dim3(64 * WM * WN), bytes,
-                       s, M, N, K, (const T *)A, lda, (const T *)W, e, gn);
+    hipLaunchKernelGGL((gemm_lds_kernel<T, OT, BM, BN, WM, WN, STAGES, BK, OCC, KIND>), dim3(gn * gm),
+                       dim3(64 * WM * WN), bytes, s, M, N, K, (const T *)A, lda, (const T *)W, e, gn);
     return hipGetLastError();
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int STAGES>
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK = 64, int OCC = 1>
 static hipError_t launch_lds(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W,
                              const EpiArgs &e) {
+#define LDS_CASE(E) \
+    case Epi::E: return launch_lds_k<T, BM, BN, WM, WN, STAGES, BK, OCC, Epi::E>(s, M, N, K, A, lda, W, e);
     switch (e.kind) {
-    case Epi::Plain: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Plain>(s, M, N, K, A, lda, W, e);
-    case Epi::Qkv: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Qkv>(s, M, N, K, A, lda, W, e);
-    case Epi::Gelu: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Gelu>(s, M, N, K, A, lda, W, e);
-    case Epi::Residual: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Residual>(s, M, N, K, A, lda, W, e);
-    case Epi::QkvRope: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::QkvRope>(s, M, N, K, A, lda, W, e);
-    case Epi::Gated: return launch_lds_k<T, BM, BN, WM, WN, STAGES, Epi::Gated>(s, M, N, K, A, lda, W, e);
+        LDS_CASE(Plain)
+        LDS_CASE(Qkv)
+        LDS_CASE(Gelu)
+        LDS_CASE(Residual)
+        LDS_CASE(QkvRope)
+        LDS_CASE(Gated)
     }
+#undef LDS_CASE
     return hipErrorInvalidValue;
 }
 
-int gemm_tiles() { return 8; }
+int gemm_tiles() { return 12; }
 
 // Block shapes by number: 1-3 stage operands through registers (any K a
 // multiple of 8, and the F32 tier); 4-6 are the pipelined kernel, for 16-bit
@@ -564,14 +619,33 @@ static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int 
         case 6: return launch_lds<T, 128, 256, 2, 2, 3>(s, M, N, K, A, lda, W, e);
         case 7: return launch_lds<T, 256, 256, 2, 4, 2>(s, M, N, K, A, lda, W, e);
         case 8: return launch_lds<T, 128, 128, 2, 2, 2>(s, M, N, K, A, lda, W, e);
+        // BK 32 with two workgroups a CU, so one's epilogue overlaps the other's products.
+        case 9: return launch_lds<T, 256, 128, 2, 2, 2, 32, 2>(s, M, N, K, A, lda, W, e);
+        case 10: return launch_lds<T, 128, 256, 2, 2, 2, 32, 2>(s, M, N, K, A, lda, W, e);
+        case 11: return launch_lds<T, 256, 128, 2, 2, 3, 32, 2>(s, M, N, K, A, lda, W, e);
+        case 12: return launch_lds<T, 256, 256, 2, 4, 3, 32, 1>(s, M, N, K, A, lda, W, e);
         }
     }
     return hipErrorInvalidValue;
 }
 
+// The int8 tier: the pipelined kernel alone, on 128-byte rows (K a multiple
+// of 128) or 64-byte rows (K a multiple of 64).
+static hipError_t gemm_i8(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
+                          int tile) {
+    if (K % 64 != 0 || lda % 16 != 0 || !e.a_scale || !e.w_scale) return hipErrorInvalidValue;
+    if (tile == 0) tile = K % 128 == 0 ? 7 : 9;
+    if (tile == 7 && K % 128 != 0) tile = 9;
+    switch (tile) {
+    case 7: return launch_lds<int8_t, 256, 256, 2, 4, 2, 128, 1>(s, M, N, K, A, lda, W, e);
+    default: return launch_lds<int8_t, 256, 128, 2, 2, 2, 64, 2>(s, M, N, K, A, lda, W, e);
+    }
+}
+
 hipError_t gemm(hipStream_t s, Dt dt, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
                 int tile) {
     if (M <= 0) return hipSuccess;
+    if (dt == Dt::I8) return gemm_i8(s, M, N, K, A, lda, W, e, tile);
     if (K % (16 / (int)dt_bytes(dt)) != 0 || lda % (16 / (int)dt_bytes(dt)) != 0) return hipErrorInvalidValue;
     if ((e.kind == Epi::QkvRope || e.kind == Epi::Gated) && N % 2 != 0) return hipErrorInvalidValue;
     switch (dt) {

@@ -7,10 +7,12 @@
 
 namespace rocm {
 
-// The arithmetic type of a session's GEMM operands and activations.
-enum class Dt : int { F32 = 0, F16 = 1, BF16 = 2 };
+// The arithmetic type of a session's GEMM operands and activations. I8 is
+// GEMM operands alone: int8 weights (per output channel) and activations (per
+// token), int32 sums; its activations are F16.
+enum class Dt : int { F32 = 0, F16 = 1, BF16 = 2, I8 = 3 };
 
-inline size_t dt_bytes(Dt d) { return d == Dt::F32 ? 4 : 2; }
+inline size_t dt_bytes(Dt d) { return d == Dt::F32 ? 4 : d == Dt::I8 ? 1 : 2; }
 
 // Where each packed token of a run sits, written on the device by pack_rows
 // (reference core/src/cpu/encoder/mod.rs:379-424; core/cuda/kernels.h:56-77).
@@ -61,6 +63,8 @@ struct EpiArgs {
     const int32_t *at = nullptr;   // QkvRope: each token's r * seq + p
     int seq = 0;
     int silu = 0;                  // Gated: SiLU instead of GELU
+    // I8 operands: output (m, n) is the int32 sum times a_scale[m] * w_scale[n].
+    const float *a_scale = nullptr, *w_scale = nullptr;
 };
 
 // C[m, n] = sum_k A[m, k] W[n, k] over m < M (rows of A, ld lda), n < N, k < K,
@@ -84,6 +88,16 @@ hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads,
 // normalized when l2, into out [count, output_dim] F32.
 hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
                 int count, const uint32_t *ranges, int pooling, int output_dim, int l2, float *out);
+
+// Symmetric int8 rows: for each of `rows` rows of `cols` values (row stride
+// ld, F32 or F16 per src_dt), scale = max |x| / 127 and q = round(x / scale)
+// (q = 0 and scale 0 for a zero row), into dst [rows][cols] and scale [rows].
+// Per output channel for weights, per token for activations.
+hipError_t quantize_rows(hipStream_t s, const void *src, Dt src_dt, int rows, int cols, int ld, int8_t *dst,
+                         float *scale);
+
+// n values uniform in [-amp, amp) from a counter hash of (seed, index).
+hipError_t fill_uniform(hipStream_t s, float *dst, size_t n, float amp, uint32_t seed);
 
 // F32 -> F16 (round to nearest even) or BF16 copies of weights; `overflow`
 // (device int, may be NULL) is set to 1 when an F16 value overflows.

@@ -2,6 +2,8 @@
 // pooling (rows and ranges) with the cut and L2, and weight narrowing.
 // All are HBM-bound; each reads its input once, coalesced, with wave64
 // shuffle reductions and no atomics on floats.
+#include <algorithm>
+
 #include "kernels.h"
 #include "devmath.h"
 
@@ -310,6 +312,69 @@ hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, con
     if (count <= 0) return hipSuccess;
     hipLaunchKernelGGL(pool_kernel, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq,
                        ranges ? 1 : 0, ranges, pooling, output_dim, l2, out);
+    return hipGetLastError();
+}
+
+// ---- Symmetric int8 rows -------------------------------------------------------------
+//
+// One wave per row: the row's absolute maximum by a wave reduction, scale =
+// max / 127, q = round-to-nearest-even(x * (127 / max)) within [-127, 127].
+template <typename S>
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const S *__restrict__ src, int rows, int cols, int ld,
+                                                            int8_t *__restrict__ dst, float *__restrict__ scale) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const S *row = src + (size_t)r * ld;
+    float mx = 0.0f;
+    for (int c = lane; c < cols; c += 64) mx = fmaxf(mx, fabsf(to_f32(row[c])));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+    int8_t *out = dst + (size_t)r * cols;
+    for (int c = lane; c < cols; c += 64) {
+        const float q = rintf(to_f32(row[c]) * inv);
+        out[c] = (int8_t)fminf(fmaxf(q, -127.0f), 127.0f);
+    }
+    if (lane == 0) scale[r] = mx / 127.0f;
+}
+
+hipError_t quantize_rows(hipStream_t s, const void *src, Dt src_dt, int rows, int cols, int ld, int8_t *dst,
+                         float *scale) {
+    if (rows <= 0) return hipSuccess;
+    const dim3 grid((rows + 3) / 4);
+    if (src_dt == Dt::F32)
+        hipLaunchKernelGGL(quantize_rows_kernel<float>, grid, dim3(256), 0, s, (const float *)src, rows, cols, ld, dst,
+                           scale);
+    else if (src_dt == Dt::F16)
+        hipLaunchKernelGGL(quantize_rows_kernel<_Float16>, grid, dim3(256), 0, s, (const _Float16 *)src, rows, cols,
+                           ld, dst, scale);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// ---- Uniform fill (measurement operands) ---------------------------------------------
+//
+// Each value from a 32-bit integer hash of its index and the seed (the
+// "lowbias32" mixer: xorshift-multiply rounds), top 24 bits to [-amp, amp).
+__global__ void __launch_bounds__(256) fill_uniform_kernel(float *__restrict__ dst, size_t n, float amp,
+                                                           uint32_t seed) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        uint32_t h = (uint32_t)i * 0x9e3779b9u ^ (uint32_t)(i >> 32) ^ seed * 0x85ebca6bu;
+        h ^= h >> 16;
+        h *= 0x7feb352du;
+        h ^= h >> 15;
+        h *= 0x846ca68bu;
+        h ^= h >> 16;
+        dst[i] = amp * ((float)(h >> 8) * (2.0f / 16777216.0f) - 1.0f);
+    }
+}
+
+hipError_t fill_uniform(hipStream_t s, float *dst, size_t n, float amp, uint32_t seed) {
+    if (n == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(fill_uniform_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, n, amp, seed);
     return hipGetLastError();
 }
 

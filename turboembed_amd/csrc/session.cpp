@@ -109,8 +109,17 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
                                       " must be multiples of 8, hidden at most 2048");
     if (d->head && d->head_out) fail(TURBO_E_UNSUPPORTED, "rocm: a token head on the device");
 
+    // compute_dtype I8 on raw weights: the manifest asks for int8 GEMMs
+    // (per-channel weights, per-token activations), as a compiled I8 graph
+    // fixes them for the reference's Hailo backend (core/hailo/backend.cpp:441-443).
+    const uint32_t fixed = d->struct_size >= offsetof(turbo_backend_model, compute_dtype) + 4 ? d->compute_dtype : 0;
+    if (fixed != 0 && fixed != TURBO_DTYPE_I8 && fixed != TURBO_DTYPE_F32 && fixed != TURBO_DTYPE_F16 &&
+        fixed != TURBO_DTYPE_BF16)
+        fail(TURBO_E_UNSUPPORTED, "rocm: compute_dtype " + std::to_string(fixed));
+
     auto m = std::make_unique<Model>();
     m->ctx = c;
+    m->int8 = fixed == TURBO_DTYPE_I8;
     m->family = d->family;
     m->dtype = d->dtype;
     m->layers = d->layers;
@@ -296,6 +305,35 @@ std::vector<LayerWeights> &Model::weights_in(Dt dt) {
     size_t total = 0;
     for (const Layer &L : ls) total += L.n_qkv * H + H * H + L.n_in * H + H * inter;
     OnDevice on(ctx->ordinal);
+    if (dt == Dt::I8) {
+        // Symmetric per-output-channel int8: each weight row's scale is its
+        // largest magnitude over 127.
+        size_t rows = 0;
+        for (const Layer &L : ls) rows += L.n_qkv + H + L.n_in + H;
+        narrowed[(int)dt].reset(dev_alloc(total + rows * 4 + 256, "int8 weights"));
+        int8_t *q = static_cast<int8_t *>(narrowed[(int)dt].get());
+        float *sc = reinterpret_cast<float *>(q + ((total + 255) & ~(size_t)255));
+        std::vector<LayerWeights> out;
+        auto one = [&](const float *src, size_t n, size_t k, const float **scale) {
+            check(quantize_rows(ctx->stream, src, Dt::F32, (int)n, (int)k, (int)k, q, sc), "quantizing weights");
+            const void *at = q;
+            *scale = sc;
+            q += n * k;
+            sc += n;
+            return at;
+        };
+        for (const Layer &L : ls) {
+            LayerWeights lw;
+            lw.qkv = one(L.wqkv, L.n_qkv, H, &lw.s_qkv);
+            lw.out = one(L.wo, H, H, &lw.s_out);
+            lw.ffn_in = one(L.w1, L.n_in, H, &lw.s_ffn_in);
+            lw.ffn_out = one(L.w2, H, inter, &lw.s_ffn_out);
+            out.push_back(lw);
+        }
+        check(hipStreamSynchronize(ctx->stream), "quantizing weights");
+        w = std::move(out);
+        return w;
+    }
     narrowed[(int)dt].reset(dev_alloc(total * 2 + 256, "narrowed weights"));
     char *p = static_cast<char *>(narrowed[(int)dt].get());
     int32_t *flag = reinterpret_cast<int32_t *>(p + total * 2);
@@ -339,18 +377,20 @@ void model_release(Model *m) {
 
 namespace {
 
-// The numeric class a dtype's GEMMs compute in. BF16 has none in the
-// reference's header; this backend's is the next free bit.
+// The numeric class a dtype's GEMMs compute in. BF16 and I8 have none in
+// the reference's header; this backend's are the next free bits.
 uint32_t numeric_of(Dt dt) {
     switch (dt) {
     case Dt::F16: return TURBO_NUMERIC_F16_F32ACC;
     case Dt::BF16: return TURBO_ROCM_NUMERIC_BF16_F32ACC;
+    case Dt::I8: return TURBO_ROCM_NUMERIC_I8_I32ACC;
     default: return TURBO_NUMERIC_F32_FMA;
     }
 }
 
 uint32_t dtype_of(Dt dt) {
     switch (dt) {
+    case Dt::I8: return TURBO_DTYPE_I8;
     case Dt::F16: return TURBO_DTYPE_F16;
     case Dt::BF16: return TURBO_DTYPE_BF16;
     default: return TURBO_DTYPE_F32;
@@ -400,6 +440,12 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     case TURBO_PRECISION_FASTEST: dt = m->dtype == TURBO_DTYPE_BF16 ? Dt::BF16 : Dt::F16; break;
     default: fail(TURBO_E_INVALID_ENUM, "rocm: precision " + std::to_string(desc->precision), 3);
     }
+    if (m->int8 && desc->precision != TURBO_PRECISION_EXACT) {
+        // The int8 kernel reads whole 64-byte rows of both operands.
+        if (m->hidden % 64 != 0 || m->inter % 64 != 0)
+            fail(TURBO_E_UNSUPPORTED, "rocm: int8 GEMMs need hidden and intermediate sizes in multiples of 64");
+        dt = Dt::I8;
+    }
     auto s = std::make_unique<Session>();
     s->model = m;
     s->ctx = m->ctx;
@@ -418,6 +464,7 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     }
     if (dt == Dt::F32) s->w = &m->weights_in(Dt::F32);
     s->dt = dt;
+    s->act = dt == Dt::I8 ? Dt::F16 : dt;
     s->compute_dtype = dtype_of(dt);
     if (tuning && tuning->struct_size >= offsetof(turbo_backend_tuning, numerics_used) + 4) {
         if (tuning->numerics_allowed && !(tuning->numerics_allowed & numeric_of(dt)))
@@ -430,7 +477,7 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         if (tuning) tuning->tuned = TURBO_TUNED_FORCED;
     }
     s->choices = "gemm=" + std::to_string(s->gemm_tile) +
-                 (s->simple_attention || dt == Dt::F32 ? " attention=simple" : " attention=mfma");
+                 (s->simple_attention || s->act == Dt::F32 ? " attention=simple" : " attention=mfma");
     if (tuning) {
         std::snprintf(tuning->choices, sizeof tuning->choices, "%s", s->choices.c_str());
         if (tuning->struct_size >= offsetof(turbo_backend_tuning, numerics_used) + 4)
@@ -439,7 +486,7 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
 
     const size_t H = m->hidden, I = m->inter, B = s->max_batch, S = s->max_seq;
     s->tcap = B * S;
-    const size_t el = dt_bytes(dt);
+    const size_t el = dt_bytes(s->act);
     OnDevice on(m->ctx->ordinal);
     auto alloc = [&](size_t bytes, const char *what) {
         s->owned.emplace_back(dev_alloc(bytes, what));
@@ -466,7 +513,11 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     s->qkv = alloc(3 * s->tcap * H * el + 256, "session qkv");
     check(hipMemset(s->qkv, 0, 3 * s->tcap * H * el + 256), "session qkv");
     s->ctxb = alloc(s->tcap * H * el, "session context");
-    s->ffn = alloc(s->tcap * (m->rotary ? I : I) * el, "session ffn");
+    s->ffn = alloc(s->tcap * I * el, "session ffn");
+    if (dt == Dt::I8) {
+        s->aq = static_cast<int8_t *>(alloc(s->tcap * std::max(H, I), "session int8 operand"));
+        s->ascale = static_cast<float *>(alloc(s->tcap * 4, "session int8 scales"));
+    }
     const size_t outs = std::max<size_t>(B, s->max_ranges);
     s->out = static_cast<float *>(alloc(outs * H * 4, "session output"));
     s->output.ctx = m->ctx;
@@ -586,8 +637,8 @@ void encode(Session &s) {
     Model &m = *s.model;
     hipStream_t st = s.ctx->stream;
     const int T = (int)s.tokens, H = (int)m.hidden, I = (int)m.inter, heads = (int)m.heads, dh = H / heads;
-    const Dt dt = s.dt;
-    const bool f32 = dt == Dt::F32;
+    const Dt dt = s.act;   // activations; the GEMMs take s.dt
+    const bool f32 = dt == Dt::F32, i8 = s.dt == Dt::I8;
     Timer tm(s);
     auto run = [&](const char *name, hipError_t e) {
         (void)name;
@@ -599,6 +650,17 @@ void encode(Session &s) {
         run(NAME, CALL);   \
         tm.end();          \
     } while (0)
+    // One GEMM of the layer. On the I8 tier its operand rows are quantized
+    // first (per token), and the epilogue takes both scales.
+    auto mm = [&](const char *name, int N, int K, const void *A, const void *Wt, const float *wscale, EpiArgs &e) {
+        if (i8) {
+            LAUNCH("quantize", quantize_rows(st, A, Dt::F16, T, K, K, s.aq, s.ascale));
+            e.a_scale = s.ascale;
+            e.w_scale = wscale;
+            A = s.aq;
+        }
+        LAUNCH(name, gemm(st, s.dt, T, N, K, A, K, Wt, e, s.gemm_tile));
+    };
     LAUNCH("pack_rows", pack_rows(st, s.mask, (int)s.batch, (int)s.seq, s.pk));
     // The GEMM operand copy of x: x itself on the F32 tier.
     void *xa = f32 ? (void *)s.x : s.xh;
@@ -636,7 +698,7 @@ void encode(Session &s) {
         } else {
             q.kind = Epi::Qkv;
         }
-        LAUNCH("gemm_qkv", gemm(st, dt, T, (int)L.n_qkv, H, src, H, W.qkv, q, s.gemm_tile));
+        mm("gemm_qkv", (int)L.n_qkv, H, src, W.qkv, W.s_qkv, q);
         LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, (int)s.seq, (int)s.batch,
                                       (int)s.max_len, window, s.ctxb, s.simple_attention));
         EpiArgs o;
@@ -644,7 +706,7 @@ void encode(Session &s) {
         o.bias = L.bo;
         o.x = s.x;
         o.ldo = H;
-        LAUNCH("gemm_out", gemm(st, dt, T, H, H, s.ctxb, H, W.out, o, s.gemm_tile));
+        mm("gemm_out", H, H, s.ctxb, W.out, W.s_out, o);
         const void *ffn_src = xa;
         if (m.modern) {
             LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln2_w, nullptr, m.eps, f32 ? (float *)s.xh : nullptr,
@@ -663,13 +725,13 @@ void encode(Session &s) {
         } else {
             f.kind = Epi::Gelu;
         }
-        LAUNCH("gemm_ffn_in", gemm(st, dt, T, (int)L.n_in, H, ffn_src, H, W.ffn_in, f, s.gemm_tile));
+        mm("gemm_ffn_in", (int)L.n_in, H, ffn_src, W.ffn_in, W.s_ffn_in, f);
         EpiArgs f2;
         f2.kind = Epi::Residual;
         f2.bias = L.b2;
         f2.x = s.x;
         f2.ldo = H;
-        LAUNCH("gemm_ffn_out", gemm(st, dt, T, H, I, s.ffn, I, W.ffn_out, f2, s.gemm_tile));
+        mm("gemm_ffn_out", H, I, s.ffn, W.ffn_out, W.s_ffn_out, f2);
         if (!m.modern)
             LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln2_w, L.ln2_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
     }
@@ -815,32 +877,64 @@ int32_t turbo_rocm_session_choices(void *session, char *out, uint32_t len, turbo
     });
 }
 
+// The hooks' dtype: TURBO_DTYPE_F16, BF16, I8 or F32.
+static Dt hook_dt(uint32_t dtype) {
+    switch (dtype) {
+    case TURBO_DTYPE_F16: return Dt::F16;
+    case TURBO_DTYPE_BF16: return Dt::BF16;
+    case TURBO_DTYPE_I8: return Dt::I8;
+    case TURBO_DTYPE_F32: return Dt::F32;
+    default: fail(TURBO_E_INVALID_ENUM, "rocm: dtype " + std::to_string(dtype));
+    }
+}
+
+// F32 operands on the device in the GEMM's operand type: narrowed copies,
+// or int8 rows with their scales (into e).
+struct Operands {
+    DevPtr a, w, scales;
+    const void *pa = nullptr, *pw = nullptr;
+    Operands(Dt dt, const float *a32, const float *w32, size_t M, size_t N, size_t K, EpiArgs &e) {
+        const size_t na = M * K, nw = N * K;
+        pa = a32;
+        pw = w32;
+        if (dt == Dt::F32) return;
+        a.reset(dev_alloc(na * 2, "gemm operands"));
+        w.reset(dev_alloc(nw * 2, "gemm operands"));
+        if (dt == Dt::I8) {
+            scales.reset(dev_alloc((M + N) * 4, "gemm operands"));
+            float *sa = static_cast<float *>(scales.get()), *sw = sa + M;
+            check(quantize_rows(nullptr, a32, Dt::F32, (int)M, (int)K, (int)K, (int8_t *)a.get(), sa), "gemm operands");
+            check(quantize_rows(nullptr, w32, Dt::F32, (int)N, (int)K, (int)K, (int8_t *)w.get(), sw), "gemm operands");
+            e.a_scale = sa;
+            e.w_scale = sw;
+        } else {
+            check(narrow(nullptr, a32, a.get(), na, dt, nullptr), "gemm operands");
+            check(narrow(nullptr, w32, w.get(), nw, dt, nullptr), "gemm operands");
+        }
+        pa = a.get();
+        pw = w.get();
+    }
+};
+
 int32_t turbo_rocm_gemm_check(uint32_t ordinal, uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, const float *A,
                               const float *W, const float *bias, float *out, uint32_t tile, turbo_error *err) {
     return guarded(err, [&] {
         if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device");
-        const Dt dt = dtype == TURBO_DTYPE_F16 ? Dt::F16 : dtype == TURBO_DTYPE_BF16 ? Dt::BF16 : Dt::F32;
+        const Dt dt = hook_dt(dtype);
         OnDevice on(devices()[ordinal]);
         const size_t na = (size_t)M * K, nw = (size_t)N * K;
         DevPtr a32(dev_alloc(na * 4, "gemm check")), w32(dev_alloc(nw * 4, "gemm check"));
-        DevPtr a(dev_alloc(na * 4, "gemm check")), w(dev_alloc(nw * 4, "gemm check"));
         DevPtr b(dev_alloc((size_t)N * 4, "gemm check")), o(dev_alloc((size_t)M * N * 4, "gemm check"));
         check(hipMemcpy(a32.get(), A, na * 4, hipMemcpyHostToDevice), "gemm check");
         check(hipMemcpy(w32.get(), W, nw * 4, hipMemcpyHostToDevice), "gemm check");
         if (bias) check(hipMemcpy(b.get(), bias, (size_t)N * 4, hipMemcpyHostToDevice), "gemm check");
-        const void *pa = a32.get(), *pw = w32.get();
-        if (dt != Dt::F32) {
-            check(narrow(nullptr, (const float *)a32.get(), a.get(), na, dt, nullptr), "gemm check");
-            check(narrow(nullptr, (const float *)w32.get(), w.get(), nw, dt, nullptr), "gemm check");
-            pa = a.get();
-            pw = w.get();
-        }
         EpiArgs e;
         e.kind = Epi::Plain;
         e.bias = bias ? (const float *)b.get() : nullptr;
         e.out = o.get();
         e.ldo = (int)N;
-        check(gemm(nullptr, dt, (int)M, (int)N, (int)K, pa, (int)K, pw, e, (int)tile), "gemm check");
+        Operands ops(dt, (const float *)a32.get(), (const float *)w32.get(), M, N, K, e);
+        check(gemm(nullptr, dt, (int)M, (int)N, (int)K, ops.pa, (int)K, ops.pw, e, (int)tile), "gemm check");
         check(hipDeviceSynchronize(), "gemm check");
         check(hipMemcpy(out, o.get(), (size_t)M * N * 4, hipMemcpyDeviceToHost), "gemm check");
         return TURBO_OK;
@@ -852,14 +946,15 @@ int32_t turbo_rocm_gemm_time(uint32_t ordinal, uint32_t dtype, uint32_t M, uint3
     return guarded(err, [&] {
         if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device");
         if (iters == 0) fail(TURBO_E_INVALID_ARGUMENT, "rocm: iters");
-        const Dt dt = dtype == TURBO_DTYPE_F16 ? Dt::F16 : dtype == TURBO_DTYPE_BF16 ? Dt::BF16 : Dt::F32;
+        const Dt dt = hook_dt(dtype);
         OnDevice on(devices()[ordinal]);
-        const size_t el = dt_bytes(dt);
-        DevPtr a(dev_alloc((size_t)M * K * el, "gemm time")), w(dev_alloc((size_t)N * K * el, "gemm time"));
+        DevPtr a32(dev_alloc((size_t)M * K * 4, "gemm time")), w32(dev_alloc((size_t)N * K * 4, "gemm time"));
         DevPtr x(dev_alloc((size_t)M * N * 4, "gemm time")), b(dev_alloc((size_t)N * 4, "gemm time"));
-        // Small finite operands (every 16-bit value 0x1111, about 6.6e-4 in F16).
-        check(hipMemset(a.get(), 0x11, (size_t)M * K * el), "gemm time");
-        check(hipMemset(w.get(), 0x11, (size_t)N * K * el), "gemm time");
+        // Uniform operands in [-1, 1) and [-1/16, 1/16): the multipliers
+        // toggle as they do on real activations and weights (a constant
+        // pattern draws less power and runs faster).
+        check(fill_uniform(nullptr, (float *)a32.get(), (size_t)M * K, 1.0f, 1), "gemm time");
+        check(fill_uniform(nullptr, (float *)w32.get(), (size_t)N * K, 0.0625f, 2), "gemm time");
         check(hipMemset(x.get(), 0, (size_t)M * N * 4), "gemm time");
         check(hipMemset(b.get(), 0, (size_t)N * 4), "gemm time");
         EpiArgs e;
@@ -867,13 +962,15 @@ int32_t turbo_rocm_gemm_time(uint32_t ordinal, uint32_t dtype, uint32_t M, uint3
         e.bias = (const float *)b.get();
         e.x = (float *)x.get();
         e.ldo = (int)N;
+        Operands ops(dt, (const float *)a32.get(), (const float *)w32.get(), M, N, K, e);
         hipEvent_t e0, e1;
         check(hipEventCreate(&e0), "gemm time");
         check(hipEventCreate(&e1), "gemm time");
-        for (int i = 0; i < 3; ++i) check(gemm(nullptr, dt, (int)M, (int)N, (int)K, a.get(), (int)K, w.get(), e, (int)tile), "gemm time");
+        for (int i = 0; i < 3; ++i)
+            check(gemm(nullptr, dt, (int)M, (int)N, (int)K, ops.pa, (int)K, ops.pw, e, (int)tile), "gemm time");
         check(hipEventRecord(e0, nullptr), "gemm time");
         for (uint32_t i = 0; i < iters; ++i)
-            check(gemm(nullptr, dt, (int)M, (int)N, (int)K, a.get(), (int)K, w.get(), e, (int)tile), "gemm time");
+            check(gemm(nullptr, dt, (int)M, (int)N, (int)K, ops.pa, (int)K, ops.pw, e, (int)tile), "gemm time");
         check(hipEventRecord(e1, nullptr), "gemm time");
         check(hipEventSynchronize(e1), "gemm time");
         float t = 0;

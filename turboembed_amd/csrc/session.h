@@ -80,9 +80,11 @@ struct Buffer {
     bool owned = false;
 };
 
-// One layer's GEMM weights in one dtype: [n, k] row-major, as the kernels read them.
+// One layer's GEMM weights in one dtype: [n, k] row-major, as the kernels
+// read them; int8 weights with a scale per output row.
 struct LayerWeights {
     const void *qkv, *out, *ffn_in, *ffn_out;
+    const float *s_qkv = nullptr, *s_out = nullptr, *s_ffn_in = nullptr, *s_ffn_out = nullptr;
 };
 
 struct Model {
@@ -91,6 +93,7 @@ struct Model {
              types = 0, position_offset = 0;
     float eps = 0;
     bool rotary = false, modern = false, silu = false;
+    bool int8 = false;   // the model asks for int8 GEMMs (compute_dtype I8) below EXACT
     uint32_t window = 0, global_every = 0, pairs = 0;   // window: keys each side, 0 for none
     DevPtr f32;                                         // every tensor in F32, one allocation
     // F32 device pointers (NULL where absent).
@@ -103,8 +106,8 @@ struct Model {
     std::vector<Layer> ls;
     // Narrowed GEMM weights, per dtype (index Dt), made on first need.
     std::mutex lock;
-    DevPtr narrowed[3];
-    std::vector<LayerWeights> gemm_w[3];
+    DevPtr narrowed[4];
+    std::vector<LayerWeights> gemm_w[4];
     bool f16_overflow = false;
     std::vector<LayerWeights> &weights_in(Dt dt);
 };
@@ -113,7 +116,8 @@ struct Session {
     Model *model = nullptr;
     Context *ctx = nullptr;
     uint32_t task = 0, max_batch = 0, max_seq = 0, max_ranges = 0, precision = 0, compute_dtype = 0;
-    Dt dt = Dt::F32;
+    Dt dt = Dt::F32;    // GEMM operands
+    Dt act = Dt::F32;   // activations between the GEMMs: dt, or F16 for I8
     size_t tcap = 0;
     std::vector<DevPtr> owned;
     int32_t *ids = nullptr, *mask = nullptr, *types = nullptr;
@@ -124,6 +128,8 @@ struct Session {
     void *qkv = nullptr;     // [3][heads][tcap][d] (dt)
     void *ctxb = nullptr;    // [tcap, H] (dt)
     void *ffn = nullptr;     // [tcap, I] (dt)
+    int8_t *aq = nullptr;    // I8: a GEMM's quantized operand [tcap, max(H, I)]
+    float *ascale = nullptr; // I8: its per-token scales [tcap]
     float *out = nullptr;    // [max(max_batch, max_ranges), H] F32
     Buffer output;
     int32_t *staging = nullptr;   // pinned: ids, mask, types planes then ranges
