@@ -56,6 +56,44 @@ int32_t turbo_rocm_check_ranges(uint32_t batch, uint32_t seq, uint32_t row_strid
                                 const turbo_token_range *ranges, uint32_t count, uint32_t max_ranges,
                                 turbo_error *err);
 
+/* ---- The rerank caller (core/src/tokenizer/pair.rs:27-99,
+ * core/src/session/rerank.rs:47-219) ----
+ *
+ * turbo_rocm_pair_windows: a query and a passage, as token ids, into the
+ * encoder windows of the pair template [start] query [end] passage [end]
+ * (RoBERTa, roberta != 0: [start] query [end] [end] passage [end], one
+ * segment): the query cut to query_tokens on the right, the passage covered
+ * by windows of max_tokens - specials - query tokens, stride apart (0:
+ * disjoint). Each window is a row of max_tokens ids and types (BERT: type 1
+ * from the passage on) padded with id 0, and its length. Writes up to
+ * capacity windows and *windows = their number; TURBO_E_CAPACITY when more
+ * are needed. Errors as the reference's: field 2 max_tokens, 1 query_tokens,
+ * 3 stride. */
+int32_t turbo_rocm_pair_windows(const int32_t *query, uint32_t query_len, const int32_t *passage, uint32_t passage_len,
+                                int32_t start_id, int32_t end_id, uint32_t roberta, uint32_t query_tokens,
+                                uint32_t max_tokens, uint32_t stride, int32_t *ids, int32_t *types, uint32_t *lengths,
+                                uint32_t capacity, uint32_t *windows, turbo_error *err);
+
+/* turbo_rocm_rerank_scores: the sequence classification head over n CLS
+ * states [n, hidden] F32 (core/src/session/rerank.rs:166-191): the pooler
+ * (dense [hidden, hidden] + bias, tanh; skipped when pooler_weight is NULL)
+ * and the one-logit classifier, each summed in F64 from its bias and rounded
+ * to F32. A non-finite state or logit is TURBO_E_INTERNAL. */
+int32_t turbo_rocm_rerank_scores(const float *states, uint32_t n, uint32_t hidden, const float *pooler_weight,
+                                 const float *pooler_bias, const float *classifier_weight, float classifier_bias,
+                                 float *scores, turbo_error *err);
+
+/* turbo_rocm_rerank_run: the windows of `pairs` pairs ([windows, seq] ids and
+ * types, each window's length, and the pair it belongs to) through a
+ * TURBO_TASK_RERANK session of this backend, max_batch windows a run, as
+ * CLS rows at full width with no normalization, then the head above; each
+ * pair's score is the largest of its windows' (core/src/session/rerank.rs:
+ * 111-219). pairs may not exceed the session's max_batch. */
+int32_t turbo_rocm_rerank_run(void *session, const int32_t *ids, const int32_t *types, const uint32_t *lengths,
+                              uint32_t windows, uint32_t seq, const uint32_t *owner, uint32_t pairs,
+                              const float *pooler_weight, const float *pooler_bias, const float *classifier_weight,
+                              float classifier_bias, float *scores, turbo_error *err);
+
 /* ---- Test and measurement hooks (no counterpart in the reference's seam; the
  * reference's CUDA backend keeps similar ones, core/src/cuda.rs:177-499) ---- */
 
@@ -85,14 +123,15 @@ int32_t turbo_rocm_session_choices(void *session, char *out, uint32_t len, turbo
 
 /* One GEMM, out [M, N] = A [M, K] W [N, K]^T + bias (bias may be NULL), with
  * the operands narrowed on the device to dtype (TURBO_DTYPE_F32, F16 or
- * BF16) and block shape `tile` (0 = the default choice). Allocates its own
- * device memory; for kernel tests. */
+ * BF16) or quantized to int8 rows (TURBO_DTYPE_I8: a symmetric scale per row
+ * of A and of W, int32 sums, dequantized in F32), and block shape `tile`
+ * (0 = the default choice). Allocates its own device memory; for kernel tests. */
 int32_t turbo_rocm_gemm_check(uint32_t ordinal, uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, const float *A,
                               const float *W, const float *bias, float *out, uint32_t tile, turbo_error *err);
 
 /* The average milliseconds of `iters` back-to-back launches of the GEMM
  * [M, K] x [N, K]^T with the residual epilogue, block shape `tile`, on
- * device-resident operands; for tuning sweeps. */
+ * device-resident uniform random operands of dtype; for tuning sweeps. */
 int32_t turbo_rocm_gemm_time(uint32_t ordinal, uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, uint32_t tile,
                              uint32_t iters, float *ms, turbo_error *err);
 

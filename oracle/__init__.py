@@ -135,3 +135,88 @@ def fixture_rows(ids, lengths):
     """The reference cases as rows: each case's ids, mask 1 through its length."""
     mask = (np.arange(ids.shape[1])[None, :] < lengths[:, None]).astype(np.int32)
     return np.ascontiguousarray(ids, dtype=np.int32), mask
+
+
+# ---- The rerank caller (pure Python and numpy: a handful of windows) ----------
+
+def pair_windows(query, passage, start_id, end_id, roberta=False, query_tokens=8, max_tokens=512, stride=0):
+    """[(ids, types)] of one pair's encoder windows, restating
+    core/src/tokenizer/pair.rs:27-99 over token ids."""
+    specials = 4 if roberta else 3
+    if max_tokens <= specials + 1 or query_tokens >= max_tokens - specials:
+        raise ValueError("pair limits leave no passage token")
+    q = list(query)[:query_tokens]
+    room = max_tokens - specials - len(q)
+    step = room if stride == 0 else stride
+    if step == 0 or step > room:
+        raise ValueError("pair stride must be within passage capacity")
+    out, start = [], 0
+    while True:
+        end = min(start + room, len(passage))
+        ids = [start_id] + q + [end_id] + ([end_id] if roberta else [])
+        boundary = len(ids)
+        ids += list(passage[start:end]) + [end_id]
+        types = [0] * len(ids)
+        if not roberta:
+            types[boundary:] = [1] * (len(ids) - boundary)
+        out.append((ids, types))
+        if end == len(passage):
+            return out
+        start += step
+
+
+def rerank_head(states, classifier_weight, classifier_bias, pooler_weight=None, pooler_bias=None):
+    """Logits of CLS states [n, hidden], restating core/src/session/rerank.rs:166-191:
+    the pooler's rows summed in F64 from the bias, tanh, rounded to F32, then
+    the classifier's row the same way."""
+    x = np.asarray(states, np.float32).astype(np.float64)
+    if pooler_weight is not None:
+        pb = np.zeros(x.shape[1]) if pooler_bias is None else np.asarray(pooler_bias, np.float64)
+        x = np.tanh(pb[None, :] + x @ np.asarray(pooler_weight, np.float64).T).astype(np.float32).astype(np.float64)
+    w = np.asarray(classifier_weight, np.float64).ravel()
+    return (float(classifier_bias) + x @ w).astype(np.float32)
+
+
+def rerank(desc, pairs, head, start_id, end_id, roberta=False, query_tokens=8, max_tokens=512, stride=0):
+    """Each pair's score: its windows through the oracle encoder as CLS rows
+    (no normalization, full width), the head, the largest window logit
+    (core/src/session/rerank.rs:111-219)."""
+    wins, owner = [], []
+    for i, (q, p) in enumerate(pairs):
+        w = pair_windows(q, p, start_id, end_id, roberta, query_tokens, max_tokens, stride)
+        wins += w
+        owner += [i] * len(w)
+    seq = max(len(ids) for ids, _ in wins)
+    ids = np.zeros((len(wins), seq), np.int32)
+    types = np.zeros_like(ids)
+    mask = np.zeros_like(ids)
+    for r, (wi, wt) in enumerate(wins):
+        ids[r, :len(wi)] = wi
+        types[r, :len(wt)] = wt
+        mask[r, :len(wi)] = 1
+    states = encode(desc, ids, mask, types, pooling=S.TURBO_POOLING_CLS, normalize=S.TURBO_NORMALIZE_NONE)
+    logits = rerank_head(states, **head)
+    scores = np.full(len(pairs), -np.inf, np.float32)
+    for r, i in enumerate(owner):
+        scores[i] = max(scores[i], logits[r])
+    return scores
+
+
+def rerank_fixture():
+    """(ModelDesc, pairs, head, info, reference) of tests/golden/tiny_rerank:
+    the tiny BERT encoder, its (query ids, passage ids) pairs, the head as
+    rerank_head's keywords, and the reference's first windows and
+    transformers scores."""
+    from safetensors.numpy import load_file
+    t = load_file(os.path.join(GOLDEN, "tiny_rerank.safetensors"))
+    info = json.load(open(os.path.join(GOLDEN, "tiny_rerank.json")))
+    a = info["architecture"]
+    desc = ModelDesc(S.TURBO_FAMILY_BERT, a["layers"], a["hidden"], a["heads"], a["intermediate"],
+                     info["vocab_rows_kept"], a["max_positions"], a["token_types"], a["layer_norm_eps"],
+                     [t[k] for k in info["order"]], names=info["order"])
+    pairs = list(zip(info["queries"], info["passages"]))
+    head = dict(classifier_weight=t["head.classifier.weight"], classifier_bias=float(t["head.classifier.bias"][0]),
+                pooler_weight=t["head.bert.pooler.dense.weight"], pooler_bias=t["head.bert.pooler.dense.bias"])
+    ref = dict(first_ids=t["case.first_ids"], first_types=t["case.first_types"],
+               first_lengths=t["case.first_lengths"], scores=t["case.scores"])
+    return desc, pairs, head, info, ref

@@ -89,6 +89,78 @@ def one(bundle, out_name):
     print(out_name, len(used), "word rows,", sum(v.nbytes for v in tensors.values()), "bytes")
 
 
+def rerank_fixture():
+    """tiny_rerank: testdata/tiny-rerank-reference's transformers scores for
+    four (query, passage) pairs over the tiny BERT encoder, with its pooler
+    and classifier (head.safetensors), the encoder's weights (word rows
+    reduced as above), and each pair's query and passage token ids.
+
+    The reference holds each pair's first window (ids, types, length) and
+    its max-over-windows score. Query and passage ids are read from that
+    window ([CLS] query [SEP] passage [SEP], types 1 from the passage on);
+    the one pair whose window is full (length 32 = max_tokens) repeats one
+    word in both texts (cases.json), so its query and passage are that
+    word's one token id repeated as many times as the text has words."""
+    d = os.path.join(REF, "tiny-rerank-reference")
+    ref = load_file(os.path.join(d, "reference.safetensors"))
+    head = load_file(os.path.join(d, "head.safetensors"))
+    cases = json.load(open(os.path.join(d, "cases.json")))
+    bundle = os.path.join(REF, "tiny-bert-bundle")
+    m = json.load(open(os.path.join(bundle, "manifest.json")))
+    arch = m["architecture"]
+    art = m["artifacts"][0]
+    names = art["tensor_names"]
+    weights = load_file(os.path.join(bundle, art["files"][0]))
+    max_tokens, query_tokens = 32, 8
+    queries, passages = [], []
+    for i, case in enumerate(cases):
+        n = int(ref["lengths"][i])
+        row, ty = ref["ids"][i, :n], ref["types"][i, :n]
+        b = int(np.argmax(ty == 1))
+        q, p = [int(v) for v in row[1:b - 1]], [int(v) for v in row[b:n - 1]]
+        if n == max_tokens:
+            qw, pw = case["text"].split(), case["passage"].split()
+            assert len(set(qw)) == 1 and len(set(pw)) == 1 and len(set(q)) == 1 and len(set(p)) == 1
+            q, p = q[:1] * len(qw), p[:1] * len(pw)
+        queries.append(q)
+        passages.append(p)
+    used = sorted({0, 101, 102} | {v for q in queries for v in q} | {v for p in passages for v in p})
+    remap = {old: new for new, old in enumerate(used)}
+    emb, per = bert_order(arch["layers"])
+    tensors, order = {}, []
+    for key in emb:
+        t = weights[names[key]]
+        if key == "word_embeddings":
+            t = t[used]
+        tensors[f"emb.{key}"] = np.ascontiguousarray(t)
+        order.append(f"emb.{key}")
+    for layer in range(arch["layers"]):
+        for key in per:
+            name = names[key].replace("{layer}", str(layer))
+            tensors[f"layer{layer}.{key}"] = np.ascontiguousarray(weights[name])
+            order.append(f"layer{layer}.{key}")
+    for k in ("bert.pooler.dense.weight", "bert.pooler.dense.bias", "classifier.weight", "classifier.bias"):
+        tensors["head." + k] = np.ascontiguousarray(head[k])
+    first = np.vectorize(lambda v: remap[int(v)] if int(v) in remap else 0)(ref["ids"]).astype(np.int32)
+    tensors["case.first_ids"] = first
+    tensors["case.first_types"] = ref["types"].astype(np.int32)
+    tensors["case.first_lengths"] = ref["lengths"].astype(np.int32)
+    tensors["case.scores"] = ref["scores"].astype(np.float32).ravel()
+    info = {
+        "source": "testdata/tiny-rerank-reference (reference.safetensors, head.safetensors, cases.json) over "
+                  "testdata/tiny-bert-bundle (manifest.json, weights)",
+        "family": arch["family"], "architecture": arch, "order": order, "vocab_rows_kept": len(used),
+        "word_rows": used, "start_id": remap[101], "end_id": remap[102], "pad_id": 0,
+        "max_tokens": max_tokens, "query_tokens": query_tokens, "max_batch": 4, "template": "PAIR_BERT",
+        "queries": [[remap[v] for v in q] for q in queries],
+        "passages": [[remap[v] for v in p] for p in passages],
+    }
+    save_file(tensors, os.path.join(HERE, "tiny_rerank.safetensors"))
+    with open(os.path.join(HERE, "tiny_rerank.json"), "w") as f:
+        json.dump(info, f, indent=1)
+    print("tiny_rerank", len(used), "word rows")
+
+
 def quantize_golden():
     src = os.path.join(REF, "quantize", "sentence-transformers-145ef47d.txt")
     dst = os.path.join(HERE, "quantize-sentence-transformers-145ef47d.txt")
@@ -102,4 +174,5 @@ if __name__ == "__main__":
     one("tiny-bert-bundle", "tiny_bert")
     one("tiny-modernbert-bundle", "tiny_modernbert")
     one("tiny-nomic-bundle", "tiny_nomic")
+    rerank_fixture()
     quantize_golden()

@@ -308,3 +308,81 @@ def test_int8_bert_base_meets_the_oracle(context):
     assert cos.min() >= I8_FLOOR, cos.min()
     s.close()
     model.close()
+
+
+# ---- Rerank ------------------------------------------------------------------------------
+#
+# Scores are bounded one by one, as a fraction of the run's scale (the largest
+# reference score in magnitude): F32 1e-4, F16 1e-2, BF16 4e-2, I8 0.15
+# (docs/conformance.md "Scores"; core/tests/conformance/scores.rs).
+
+SCORE_BOUND = {S.TURBO_DTYPE_F32: 1e-4, S.TURBO_DTYPE_F16: 1e-2, S.TURBO_DTYPE_BF16: 4e-2, S.TURBO_DTYPE_I8: 0.15}
+
+
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+def test_rerank_scores_meet_transformers(context, precision):
+    from turboembed_amd.rerank import RerankHead
+    desc, pairs, head, info, ref = oracle.rerank_fixture()
+    model = context.load(desc)
+    s = model.session(info["max_batch"], info["max_tokens"], precision, task=S.TURBO_TASK_RERANK)
+    h = RerankHead(**head)
+    kw = dict(query_tokens=info["query_tokens"], max_tokens=info["max_tokens"])
+    scale = np.abs(ref["scores"]).max()
+    bound = SCORE_BOUND[s.compute_dtype] * scale
+    # All pairs in one write (their 7 windows in two runs of max_batch), then one pair a write.
+    got = s.rerank(pairs, h, info["start_id"], info["end_id"], **kw)
+    assert np.abs(got - ref["scores"]).max() <= bound, (got, ref["scores"])
+    for i, pair in enumerate(pairs):
+        one = s.rerank([pair], h, info["start_id"], info["end_id"], **kw)
+        assert abs(one[0] - ref["scores"][i]) <= bound
+    s.close()
+    model.close()
+
+
+def test_rerank_refuses_what_the_core_refuses(context):
+    from turboembed_amd.rerank import RerankHead
+    desc, pairs, head, info, ref = oracle.rerank_fixture()
+    model = context.load(desc)
+    h = RerankHead(**head)
+    s = model.session(2, 32, S.TURBO_PRECISION_EXACT, task=S.TURBO_TASK_RERANK)
+    with pytest.raises(T.TurboError) as e:
+        s.rerank(pairs, h, info["start_id"], info["end_id"], query_tokens=8)
+    assert e.value.code == S.TURBO_E_CAPACITY
+    s.close()
+    s = model.session(4, 32, S.TURBO_PRECISION_EXACT)
+    with pytest.raises(T.TurboError) as e:
+        s.rerank(pairs, h, info["start_id"], info["end_id"], query_tokens=8)
+    assert e.value.code == S.TURBO_E_UNSUPPORTED_TASK
+    s.close()
+    model.close()
+
+
+def test_int8_cross_encoder_meets_the_oracle(context):
+    # The int8 rerank workload at full width on 2 of its 12 layers and 12 of
+    # its 256 pairs: scores within I8's bound of the F32 oracle's, and the
+    # CLS states the head reads within I8's cosine floor.
+    from turboembed_amd.rerank import RerankHead, pair_windows
+    sh = W.SHAPES["rerank"]
+    desc = W.model(sh, layers=2)
+    pairs = W.rerank_pairs(sh, n=12)
+    head = W.rerank_head(sh)
+    qt = sh.extra["query_tokens"]
+    model = context.load(desc)
+    s = model.session(16, sh.seq, sh.precision, task=S.TURBO_TASK_RERANK)
+    assert s.compute_dtype == S.TURBO_DTYPE_I8
+    got = s.rerank(pairs, RerankHead(**head), sh.cls_id, sh.sep_id, query_tokens=qt, max_tokens=sh.seq)
+    want = oracle.rerank(desc, pairs, head, sh.cls_id, sh.sep_id, query_tokens=qt, max_tokens=sh.seq)
+    scale = np.abs(want).max()
+    assert np.abs(got - want).max() <= SCORE_BOUND[S.TURBO_DTYPE_I8] * scale, (got, want)
+    wins = [pair_windows(q, p, sh.cls_id, sh.sep_id, query_tokens=qt, max_tokens=sh.seq) for q, p in pairs]
+    ids = np.concatenate([w[0] for w in wins])
+    types = np.concatenate([w[1] for w in wins])
+    lengths = np.concatenate([w[2] for w in wins])
+    mask = (np.arange(sh.seq)[None, :] < lengths[:, None]).astype(np.int32)
+    kw = dict(pooling=S.TURBO_POOLING_CLS, normalize=S.TURBO_NORMALIZE_NONE)
+    cos = small.cosine_rows(s.embed(ids, mask, types, **kw), oracle.encode(desc, ids, mask, types, **kw))
+    assert cos.min() >= I8_FLOOR, cos.min()
+    print(f"int8 cross-encoder: min CLS cosine {cos.min():.5f}, "
+          f"largest score difference {np.abs(got - want).max() / scale:.4f} of the scale")
+    s.close()
+    model.close()

@@ -57,6 +57,10 @@ def library():
         "turbo_rocm_session_replay": [P, u32, E],
         "turbo_rocm_gemm_check": [u32, u32, u32, u32, u32, P, P, P, P, u32, E],
         "turbo_rocm_gemm_time": [u32, u32, u32, u32, u32, u32, u32, C.POINTER(C.c_float), E],
+        "turbo_rocm_pair_windows": [P, u32, P, u32, C.c_int32, C.c_int32, u32, u32, u32, u32, P, P, P, u32,
+                                    C.POINTER(u32), E],
+        "turbo_rocm_rerank_scores": [P, u32, u32, P, P, P, C.c_float, P, E],
+        "turbo_rocm_rerank_run": [P, P, P, P, u32, u32, P, u32, P, P, P, C.c_float, P, E],
     }
     for name, args in protos.items():
         f = getattr(lib, name)
@@ -238,6 +242,11 @@ class Session:
         self.write_tokens(ids, mask, types, **kw)
         self.run()
         return self.read()
+
+    def rerank(self, pairs, head, start_id, end_id, **kw):
+        """Scores of (query ids, passage ids) pairs; see rerank.rerank."""
+        from .rerank import rerank
+        return rerank(self, pairs, head, start_id, end_id, **kw)
 
     # -- hooks ---------------------------------------------------------------------
     def packing(self):

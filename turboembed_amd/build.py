@@ -16,7 +16,7 @@ OUT = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libturbo_rocm.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["rowwise.hip", "gemm.hip", "attention.hip", "session.cpp", "backend.cpp", "checks.cpp"]
+SOURCES = ["rowwise.hip", "gemm.hip", "attention.hip", "session.cpp", "backend.cpp", "checks.cpp", "rerank.cpp"]
 
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",

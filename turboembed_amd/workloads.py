@@ -16,6 +16,11 @@ Five encoder shapes with seeded random weights and seeded synthetic rows:
                (768 -> 2 x 1152, 1152 -> 768), no biases, RoPE theta 160000 global /
                10000 local, every 3rd layer global, 128-token window otherwise, vocab
                50368; 16 rows x 8192, lengths U[2048, 8192]; MEAN; F16.
+  rerank       a BERT-base-shaped cross-encoder in the int8 tier (int8 weights per
+               output channel, int8 activations per token): 256 (query, passage)
+               pairs, queries U[8, 32] tokens, passages U[64, 480] cut so each pair's
+               one window [CLS] q [SEP] p [SEP] fits 512; types 0 then 1; CLS ->
+               pooler (dense 768 + tanh) -> one logit.
 
 Weights are N(0, 0.02) from numpy's PCG64 seeded by (workload seed, tensor
 index), so every tensor is reproducible on its own; LayerNorm weights are 1
@@ -59,6 +64,8 @@ class Shape:
     seq: int = 128
     lengths: tuple = None       # (lo, hi) uniform, or None for all full
     ranges_per_row: int = 0
+    compute_dtype: int = 0      # TURBO_DTYPE_I8 for the int8 tier
+    task: int = S.TURBO_TASK_EMBED
     extra: dict = field(default_factory=dict)
 
 
@@ -77,6 +84,11 @@ SHAPES = {
                         rope=(160000.0, 10000.0), window=128, global_every=3, seed=4, cls_id=50281, sep_id=50282,
                         pad_id=50283, precision=S.TURBO_PRECISION_FASTEST, pooling=S.TURBO_POOLING_MEAN,
                         normalize=S.TURBO_NORMALIZE_NONE, batch=16, seq=8192, lengths=(2048, 8192)),
+    "rerank": Shape("rerank", S.TURBO_FAMILY_BERT, 12, 768, 12, 3072, 30522, 512, 2, 1e-12, seed=5,
+                    precision=S.TURBO_PRECISION_FASTEST, pooling=S.TURBO_POOLING_CLS,
+                    normalize=S.TURBO_NORMALIZE_NONE, batch=256, seq=512, compute_dtype=S.TURBO_DTYPE_I8,
+                    task=S.TURBO_TASK_RERANK,
+                    extra=dict(query=(8, 32), passage=(64, 480), query_tokens=32)),
 }
 
 
@@ -111,7 +123,31 @@ def model(shape: Shape, layers=None):
                          activation=S.TURBO_ACTIVATION_GELU_ERF, norm=S.TURBO_NORM_LAYER_NO_BIAS)
     else:
         raise ValueError(shape.family)
+    desc.compute_dtype = shape.compute_dtype
     return with_dtype(desc, shape.store) if shape.store != "f32" else desc
+
+
+def rerank_pairs(shape: Shape, n=None, seed=0):
+    """(query ids, passage ids) pairs: lengths uniform in the shape's
+    ranges, ids U[1000, vocab), each passage cut so its pair fits one window."""
+    n = shape.batch if n is None else n
+    g = np.random.Generator(np.random.PCG64([shape.seed, 3000 + seed]))
+    (qlo, qhi), (plo, phi) = shape.extra["query"], shape.extra["passage"]
+    out = []
+    for _ in range(n):
+        q = g.integers(1000, shape.vocab, size=int(g.integers(qlo, qhi + 1))).astype(np.int32)
+        p = g.integers(1000, shape.vocab, size=int(g.integers(plo, phi + 1))).astype(np.int32)
+        out.append((q, p[: shape.seq - 3 - len(q)]))
+    return out
+
+
+def rerank_head(shape: Shape):
+    """The cross-encoder head's tensors, as keywords of RerankHead:
+    pooler [H, H] and [H], classifier [H] and its bias, all N(0, 0.02)."""
+    H = shape.hidden
+    return dict(pooler_weight=_normal(shape.seed, 900001, (H, H)), pooler_bias=_normal(shape.seed, 900002, (H,)),
+                classifier_weight=_normal(shape.seed, 900003, (H,)),
+                classifier_bias=float(_normal(shape.seed, 900004, (1,))[0]))
 
 
 def rows(shape: Shape, batch=None, seq=None, lengths="default", seed=0):
