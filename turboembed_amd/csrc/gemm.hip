@@ -284,6 +284,8 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 // a 16-byte vector of 8 consecutive outputs: coalesced stores of the outputs,
 // and coalesced reads and writes of x for the residual. The values are the
 // accumulators exactly; only the order of the stores changes.
+constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+
 template <typename T>
 __device__ __forceinline__ void store8(T *dst, const float (&v)[8]) {
     typedef uint32_t vec4 __attribute__((ext_vector_type(4)));
@@ -351,18 +353,29 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                 continue;
             }
         }
-        // Row-wise: 8 consecutive columns of one row a lane; a lane's columns
-        // are the same on every pass (64 is a multiple of the chunks a row has).
-        static_assert(64 % CH == 0, "a lane keeps its columns");
-        const int cc = (lane % CH) * 8, n = nw + cc;
-        float bias[8], wsc[8];
+        // Row-wise: 8 consecutive columns of one row a lane, item u = lane +
+        // 64 k taking chunk u % CH of row u / CH. A lane's chunk repeats every
+        // PH items (64 PH is a multiple of CH), so its biases and scales are
+        // read once per phase.
+        constexpr int PH = CH / gcd_c(64, CH);
+        static_assert((PASS * CH) % 64 == 0 && ((PASS * CH) / 64) % PH == 0, "whole items per lane");
+        int ccs[PH];
+        float biases[PH][8], wscs[PH][8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            bias[q] = (e.bias && n + q < N) ? e.bias[n + q] : 0.0f;
-            wsc[q] = (SCALED && n + q < N) ? e.w_scale[n + q] : 1.0f;
+        for (int p = 0; p < PH; ++p) {
+            ccs[p] = ((lane + 64 * p) % CH) * 8;
+            const int n = nw + ccs[p];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                biases[p][q] = (e.bias && n + q < N) ? e.bias[n + q] : 0.0f;
+                wscs[p][q] = (SCALED && n + q < N) ? e.w_scale[n + q] : 1.0f;
+            }
         }
 #pragma unroll
         for (int k = 0; k < PASS * CH / 64; ++k) {
+            const int cc = ccs[k % PH], n = nw + cc;
+            const float(&bias)[8] = biases[k % PH];
+            const float(&wsc)[8] = wscs[k % PH];
             const int row = (lane + 64 * k) / CH;
             const int m = mt + row;
             if (m >= M || n >= N) continue;
@@ -468,34 +481,46 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
 
-    // This lane's source in each of its load instructions.
-    const T *src_a[LA];
-    const T *src_b[LB];
+    // The operands are read through buffer resources based at the tile's
+    // first row (buffer_load_dwordx4 ... lds: the MUBUF form of the direct
+    // load counts on vmcnt alone, so the compiler keeps the fragment reads'
+    // lgkmcnt waits partial and the LDS reads stay pipelined). Each lane's
+    // byte offset in each of its load instructions, rows past the operand's
+    // last clamped to it.
+    int src_a[LA], src_b[LB];
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
         const int row = (wave * LA + i) * RPI + lane / CHUNKS;
-        src_a[i] = A + (size_t)min(m0 + row, M - 1) * lda + EPC * ((lane % CHUNKS) ^ swz_of<ROWB>(row));
+        src_a[i] = (min(row, M - 1 - m0) * lda + EPC * ((lane % CHUNKS) ^ swz_of<ROWB>(row))) * (int)sizeof(T);
     }
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
         const int row = (wave * LB + i) * RPI + lane / CHUNKS;
-        src_b[i] = W + (size_t)min(n0 + row, N - 1) * K + EPC * ((lane % CHUNKS) ^ swz_of<ROWB>(row));
+        src_b[i] = (min(row, N - 1 - n0) * K + EPC * ((lane % CHUNKS) ^ swz_of<ROWB>(row))) * (int)sizeof(T);
     }
-    // (The host pass of the compiler sees no LDS address space: the loads
-    // are device code alone.)
+    // (The host pass of the compiler sees no LDS address space or buffer
+    // resources: the loads are device code alone.)
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint64_t bytes_a = ((uint64_t)(M - 1 - m0) * lda + K) * sizeof(T);
+    const uint64_t bytes_b = (uint64_t)(N - n0) * K * sizeof(T);
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(A + (size_t)m0 * lda), (short)0, (int)min(bytes_a, (uint64_t)0xffffffffu), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(W + (size_t)n0 * K), (short)0, (int)min(bytes_b, (uint64_t)0xffffffffu), 0x00020000);
+#endif
     auto issue = [&](int stage, int k0) {
 #if defined(__HIP_DEVICE_COMPILE__)
         char *base = smem + stage * TILE;
+        const int kb = k0 * (int)sizeof(T);
 #pragma unroll
         for (int i = 0; i < LA; ++i)
-            __builtin_amdgcn_global_load_lds(src_a[i] + k0,
-                                             (__attribute__((address_space(3))) void *)(base + (wave * LA + i) * RPI * ROWB),
-                                             16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsa, (__attribute__((address_space(3))) void *)(base + (wave * LA + i) * RPI * ROWB), 16, src_a[i] + kb, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < LB; ++i)
-            __builtin_amdgcn_global_load_lds(
-                src_b[i] + k0, (__attribute__((address_space(3))) void *)(base + BM * ROWB + (wave * LB + i) * RPI * ROWB),
-                16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsb, (__attribute__((address_space(3))) void *)(base + BM * ROWB + (wave * LB + i) * RPI * ROWB), 16,
+                src_b[i] + kb, 0, 0, 0);
 #else
         (void)stage;
         (void)k0;
@@ -595,18 +620,46 @@ static hipError_t launch_lds(hipStream_t s, int M, int N, int K, const void *A, 
     return hipErrorInvalidValue;
 }
 
-int gemm_tiles() { return 12; }
+int gemm_tiles() { return 13; }
+
+// The device's compute units, for the launch-shape choice.
+static int cu_count() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    return n;
+}
+
+// The pipelined block shape for a large product: 256 x 256 or 256 x 192
+// output tiles, whichever leaves the compute units the least idle over the
+// launch's rounds of tiles (time ~ rounds x tile area; the wider tile reads
+// its operands a little more efficiently, so it wins ties). Q, K and V must
+// each start on a wave's column boundary (64 or 96 columns).
+static int wide_tile(int M, int N, const EpiArgs &e) {
+    const bool qkv = e.kind == Epi::Qkv || e.kind == Epi::QkvRope;
+    const long cus = cu_count();
+    auto cost = [&](int bm, int bn) {
+        const long tiles = (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        return (double)((tiles + cus - 1) / cus) * bm * bn;
+    };
+    const bool can192 = !qkv || e.hidden % 96 == 0;
+    if (can192 && cost(256, 192) * 1.03 < cost(256, 256)) return 13;
+    return 7;
+}
 
 // Block shapes by number: 1-3 stage operands through registers (any K a
-// multiple of 8, and the F32 tier); 4-6 are the pipelined kernel, for 16-bit
+// multiple of 8, and the F32 tier); 4-13 are the pipelined kernel, for 16-bit
 // operands with K a multiple of 64 (every encoder shape here).
 template <typename T, int BK>
 static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
                          int tile) {
     const bool pipelined = sizeof(T) == 2 && K % 64 == 0 && lda % 8 == 0;
-    if (tile == 0) tile = pipelined ? (M >= 2048 ? 7 : 5) : 1;
+    if (tile == 0) tile = pipelined ? (M >= 2048 ? wide_tile(M, N, e) : 5) : 1;
     // A pipelined shape asked of an operand it cannot take runs the staged kernel.
     if (tile >= 4 && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
+    // 96-column wave tiles need Q, K and V to start on their boundaries.
+    if (tile == 13 && (e.kind == Epi::Qkv || e.kind == Epi::QkvRope) && e.hidden % 96 != 0) tile = 7;
     switch (tile) {
     case 1: return launch<T, 128, 128, BK>(s, M, N, K, A, lda, W, e);
     case 2: return launch<T, 256, 128, BK>(s, M, N, K, A, lda, W, e);
@@ -624,6 +677,8 @@ static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int 
         case 10: return launch_lds<T, 128, 256, 2, 2, 2, 32, 2>(s, M, N, K, A, lda, W, e);
         case 11: return launch_lds<T, 256, 128, 2, 2, 3, 32, 2>(s, M, N, K, A, lda, W, e);
         case 12: return launch_lds<T, 256, 256, 2, 4, 3, 32, 1>(s, M, N, K, A, lda, W, e);
+        // 8 waves as 4 x 2 of 64 x 96: N = 768, 2304 and 3072 in whole rounds of tiles.
+        case 13: return launch_lds<T, 256, 192, 4, 2, 2>(s, M, N, K, A, lda, W, e);
         }
     }
     return hipErrorInvalidValue;
