@@ -18,6 +18,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["rowwise.hip", "gemm.hip", "attention.hip", "session.cpp", "backend.cpp", "checks.cpp", "rerank.cpp"]
 
+# Per-source device flags. Attention: matrix-core results in ordinary VGPRs,
+# so the softmax's vector ops on its accumulators need no copies through the
+# accumulation registers.
+EXTRA = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
     # No packed FP32 instructions in device code.
@@ -37,7 +42,7 @@ HOST_FLAGS = [
 def _compile(src):
     obj = os.path.join(OUT, src + ".o")
     if src.endswith(".hip"):
-        cmd = [HIPCC] + FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [HIPCC] + FLAGS + EXTRA.get(src, []) + ["-c", os.path.join(CSRC, src), "-o", obj]
     else:
         cmd = [os.environ.get("CXX", "g++")] + HOST_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -102,26 +102,32 @@ static hipError_t attention_t(hipStream_t s, const void *qkv, int tcap, int head
 
 // ---- The matrix-core path (F16 and BF16 operands, F32 softmax and sums) ----------
 //
-// One workgroup of 4 waves per (128-query block, head, row); each wave owns
-// 32 queries. Keys go 64 at a time through LDS: K as stored, and V already
-// transposed by the QKV epilogue, both loaded as 16-byte vectors.
+// One workgroup of 4 waves per (256-query block, head, row); each wave owns
+// 64 queries as two tiles of 32. Keys go 64 at a time through LDS: K as
+// stored, and V already transposed by the QKV epilogue, both loaded as
+// 16-byte vectors; each fragment a wave reads from LDS feeds both of its
+// query tiles, so the LDS reads per product are half a 32-query wave's.
 //
 // Scores are computed transposed, S^T = K Q^T on v_mfma_f32_32x32x16, so that
-// each lane holds one query (its column, lane % 32) and 16 of the 32 keys of
-// a sub-block, the other 16 in the lane 32 away. The online softmax then
-// needs one cross-lane step per block (the max with lane ^ 32), and each
-// query's running max and sum are a lane's own scalars. The context is also
-// computed transposed, O^T += V^T P^T: P^T is the B operand straight from the
-// score registers (converted to the operand type), and O^T keeps a query per
-// lane, so rescaling by exp(m_old - m_new) is a per-lane multiply.
+// each lane holds one query of a tile (its column, lane % 32) and 16 of the
+// 32 keys of a sub-block, the other 16 in the lane 32 away. The online
+// softmax runs per 32-key sub-block and needs one cross-lane step there (the
+// max with lane ^ 32); each query's running max is a lane's own scalar. The
+// context is also computed transposed, O^T += V^T P^T: P^T is the B operand
+// straight from the score registers (converted to the operand type), and O^T
+// keeps a query per lane, so rescaling is a per-lane multiply.
 //
 // Key order inside a 32-key sub-block: MFMA row m of the scores reads key
 // swap23(m) (bits 2 and 3 of m exchanged). Score register r of a lane in
 // half h then holds key 16 (r / 8) + 8 h + r % 8, so registers 0..7 and
 // 8..15 are each 8 consecutive keys: exactly the 8 k-slots the lane feeds
 // the P^T V^T product per 16-key step, matching 16-byte reads of V^T rows.
-// Softmax runs in base 2 on v_exp_f32. A query with no live key in reach
-// gets a zero context.
+// Softmax runs in base 2 on v_exp_f32, one multiply-add and one exp2 a
+// score (the scale folded into the exponent); the row sums come from the
+// matrix cores (an all-ones tile times P^T, so they are the sums of the very
+// p values the context used), and the context is rescaled only when a
+// sub-block raises some query's max by more than 2^8. A query with no live
+// key in reach gets a zero context.
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16_t __attribute__((ext_vector_type(16)));
@@ -152,54 +158,83 @@ template <int N> __device__ __forceinline__ void att_wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Keys stream through a STAGES-deep LDS ring filled by global_load_lds
-// (lane l of a load instruction writes 16 bytes at its base + 16 l): each
-// 64-key block is K (64 rows of d) and V^T (d rows of 64 keys), 8 rows per
-// instruction. Loads never leave the buffer: a key past the row's end reads a
-// clamped address, and its score is -inf, so it weighs exactly 0 (the
-// session zeroes Q, K and V once, so every value read is finite). Each
-// block's live keys are a 64-bit mask, the same for the whole workgroup.
+// Keys stream through a STAGES-deep LDS ring filled by buffer loads straight
+// into LDS (lane l of a load instruction writes 16 bytes at its base + 16 l;
+// the MUBUF form counts on vmcnt alone, so the fragment reads' waits stay
+// partial): each 64-key block is K (64 rows of d) and V^T (d rows of 64
+// keys), 8 rows per instruction. Loads never leave the buffer: a key past the
+// row's end reads a clamped address, and its score is -inf, so it weighs
+// exactly 0 (the session zeroes Q, K and V once, so every value read is
+// finite). Each block's live keys are a 64-bit mask, the same for the whole
+// workgroup.
 template <typename T, int D>
-__global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads,
-                                                             Packing p, const int32_t *__restrict__ mask, int seq,
+__global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads, int batch,
+                                                             int nqb, Packing p, const int32_t *__restrict__ mask, int seq,
                                                              int window, T *__restrict__ ctx) {
-    constexpr int QB = 128, KB = 64, STAGES = 3;
+    constexpr int WQ = 64, QB = 4 * WQ, KB = 64, STAGES = 3;
     constexpr int KBYTES = KB * D * 2, VBYTES = D * KB * 2, SBYTES = KBYTES + VBYTES;
-    constexpr int LK = KB / 8 / 4 * (D / 64 > 0 ? D / 64 : 1);   // K load instructions per wave
-    constexpr int KROW = D * 2;                                   // bytes of one K row
+    constexpr int KROW = D * 2;   // bytes of one K row
     typedef typename AttnMma<T>::frag frag;
     typedef uint32_t vec4 __attribute__((ext_vector_type(4)));
     static_assert(D == 64, "the ring kernel is written for 64-wide heads");
-    // The ring is dynamic LDS (STAGES * SBYTES bytes, the launch's), then the
-    // live masks: memory the compiler sees written only through the loads.
+    // The ring is dynamic LDS (STAGES * SBYTES bytes), then one live-key mask
+    // per 64-key block of the longest row (the launch sizes both): memory the
+    // compiler sees written only through the loads.
     extern __shared__ __attribute__((aligned(1024))) char ring[];
     uint64_t *live_bits = reinterpret_cast<uint64_t *>(ring + STAGES * SBYTES);
 
-    const int r = blockIdx.z, head = blockIdx.y, q0 = blockIdx.x * QB;
+    // XCD-aware numbering of a 1-D grid: the hardware hands block L to XCD
+    // L % 8, so the query blocks of one (row, head) pair take numbers 8 apart
+    // (same XCD, dispatched together) and share its K and V through that
+    // XCD's L2. Pairs go 8 to a group of 8 nqb blocks.
+    const int L = blockIdx.x;
+    const int pair = (L / (8 * nqb)) * 8 + L % 8, qb = (L / 8) % nqb;
+    if (pair >= heads * batch) return;
+    const int r = pair / heads, head = pair % heads, q0 = qb * QB;
     const int len = p.len[r];
     if (q0 >= len) return;
     const int start = p.start[r];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, ql = lane & 31;
-    const int query = q0 + wave * 32 + ql;
+    // The wave's number as a scalar (readfirstlane): everything derived from
+    // it (its queries, its window tests, its branches) stays uniform.
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, ql = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qw = q0 + wave * WQ;   // this wave's first query
     const T *Q = qkv + ((size_t)head * tcap + start) * D;
     const T *K = qkv + ((size_t)(heads + head) * tcap + start) * D;
     const T *Vt = qkv + (size_t)2 * heads * tcap * D + (size_t)head * D * tcap;
     const int32_t *mk = mask + (size_t)r * seq;
+    const bool wave_live = qw < len;   // a wave past the row's end loads and syncs but computes nothing
 
-    frag qf[D / 16];
-    {
-        const T *qrow = Q + (size_t)min(query, len - 1) * D + h * 8;
+    frag qf[2][D / 16];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const T *qrow = Q + (size_t)min(qw + 32 * qt + ql, len - 1) * D + h * 8;
 #pragma unroll
         for (int s = 0; s < D / 16; ++s) {
             const vec4 v = *(const vec4 *)(qrow + s * 16);
-            qf[s] = *(const frag *)&v;
+            qf[qt][s] = *(const frag *)&v;
         }
     }
     const float scale = 1.4426950408889634f / sqrtf((float)D);
-    floatx16_t o[D / 32];
+    // o[qt][0 .. D/32 - 1]: the context of tile qt, transposed; o[qt][D/32]:
+    // its softmax sums, as the product of an all-ones V^T tile with P^T (every
+    // row of it is the sum of the p values the context used, summed in F32 by
+    // the matrix core).
+    floatx16_t o[2][D / 32 + 1];
 #pragma unroll
-    for (int t = 0; t < D / 32; ++t) o[t] = floatx16_t{};
-    float m_run = -INFINITY, l_run = 0.0f;
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int t = 0; t <= D / 32; ++t) o[qt][t] = floatx16_t{};
+    frag ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (T)1.0f;
+    // The running max of each tile's query, in scaled (log2) units. It moves
+    // only when a sub-block's max passes it by more than RESCALE (p <=
+    // 2^RESCALE stays exact enough in the operand type and finite in F32), so
+    // a wave rescales its context rarely; every p and the sums share the max
+    // in use, so the quotient is the softmax whatever that max is.
+    constexpr float RESCALE = 8.0f;
+    float m_run[2] = {-INFINITY, -INFINITY};
 
     int k_lo = 0, k_hi = len;
     if (window < INT32_MAX) {
@@ -207,6 +242,12 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
         k_hi = min(len, q0 + QB + window);
     }
     const int nb = (k_hi - k_lo + KB - 1) / KB;
+    // Buffer resources over this head's K rows and V^T columns of the run.
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void *)K, (short)0, len * KROW, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void *)Vt, (short)0, (int)min((size_t)D * tcap * 2 + 256, (size_t)0x7fffffff), 0x00020000);
+#endif
     // This lane's K row and V^T row within each of its load instructions.
     const int lrow = lane >> 3, lchunk = lane & 7;
     auto issue = [&](int stage, int kb) {
@@ -216,9 +257,9 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
         for (int i = 0; i < 2; ++i) {
             const int row = (wave * 2 + i) * 8 + lrow;               // key within the block
             const int key = min(kb + row, len - 1);
-            const T *src = K + (size_t)key * D + 8 * (lchunk ^ att_swz(row));
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(base + (wave * 2 + i) * 8 * KROW),
-                                             16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rk, (__attribute__((address_space(3))) void *)(base + (wave * 2 + i) * 8 * KROW), 16,
+                key * KROW + 16 * (lchunk ^ att_swz(row)), 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -228,25 +269,26 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
             const int slot = lchunk ^ att_swz(c);
             int k0 = kb + 8 * slot;
             if (k0 >= len) k0 = max(0, (len - 1) & ~7);
-            const T *src = Vt + (size_t)c * tcap + start + k0;
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(base + KBYTES + (wave * 2 + i) * 8 * 128),
-                                             16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rv, (__attribute__((address_space(3))) void *)(base + KBYTES + (wave * 2 + i) * 8 * 128), 16,
+                (c * tcap + start + k0) * 2, 0, 0, 0);
         }
 #else
         (void)base;
         (void)kb;
 #endif
-        if (wave == 0) {
-            const int key = kb + lane;
-            const bool on = key < len && mk[key] != 0;
-            const uint64_t bits = __ballot(on);
-            if (lane == 0) live_bits[stage] = bits;
-        }
     };
-    (void)LK;
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
         if (st < nb) issue(st, k_lo + st * KB);
+    // Every block's live keys, once, before the loop (a mask read inside it
+    // would make its wave wait on the prefetch loads too): block b's 64 keys
+    // as one 64-bit word, by wave b % 4.
+    for (int b = wave; b < nb; b += 4) {
+        const int key = k_lo + b * KB + lane;
+        const uint64_t bits = __ballot(key < len && mk[key] != 0);
+        if (lane == 0) live_bits[b] = bits;
+    }
 
     for (int bi = 0; bi < nb; ++bi) {
         const int kb = k_lo + bi * KB;
@@ -258,108 +300,154 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
         const int stage = bi % STAGES;
         const char *kbase = ring + stage * SBYTES;
         const char *vbase = kbase + KBYTES;
-        const uint64_t bits = live_bits[stage];
+        const uint64_t bits = live_bits[bi];
 
-        floatx16_t sc[2];
+        // Both sub-blocks' scores first: the second's products are still in
+        // the matrix cores while the first's softmax runs, and the first's
+        // context products while the second's softmax runs. A wave computes
+        // nothing past the row's end or outside its queries' windows
+        // (wave-uniform).
+        bool work[2];
+        floatx16_t scs[2][2];
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
-            floatx16_t a = floatx16_t{};
-            const int row = sub * 32 + swap23(ql);
+            const int ks = kb + sub * 32;
+            work[sub] = wave_live && !(window < INT32_MAX && (ks + 31 < qw - window || ks > qw + WQ - 1 + window));
+            floatx16_t a0 = floatx16_t{}, a1 = floatx16_t{};
+            if (work[sub]) {
+                const int row = sub * 32 + swap23(ql);
 #pragma unroll
-            for (int s = 0; s < D / 16; ++s) {
-                const int c = 2 * s + h;
-                a = AttnMma<T>::run(*(const frag *)(kbase + row * KROW + 16 * (c ^ att_swz(row))), qf[s], a);
-            }
-            sc[sub] = a;
-        }
-        // Scale, mask (a block wholly live and in every query's window skips
-        // the per-key tests), and the block's max for this query.
-        const bool all_live = bits == ~0ull && (window == INT32_MAX ||
-                                                 (kb >= q0 + QB - 1 - window && kb + KB - 1 <= q0 + window));
-        float mx = -INFINITY;
-        const uint32_t lh = (uint32_t)(bits >> (8 * h)), hh = (uint32_t)(bits >> (32 + 8 * h));
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-            for (int rr = 0; rr < 16; ++rr) {
-                float v = sc[sub][rr] * scale;
-                if (!all_live) {
-                    const int j = 16 * (rr >> 3) + (rr & 7);       // key - sub * 32 - 8 h
-                    const uint32_t word = sub ? hh : lh;
-                    bool ok = (word >> j) & 1u;
-                    if (window < INT32_MAX) {
-                        const int key = kb + sub * 32 + 8 * h + j;
-                        ok = ok && key + window >= query && key <= query + window;
-                    }
-                    v = ok ? v : -INFINITY;
+                for (int s = 0; s < D / 16; ++s) {
+                    const int c = 2 * s + h;
+                    const frag kf = *(const frag *)(kbase + row * KROW + 16 * (c ^ att_swz(row)));
+                    a0 = AttnMma<T>::run(kf, qf[0][s], a0);
+                    a1 = AttnMma<T>::run(kf, qf[1][s], a1);
                 }
-                sc[sub][rr] = v;
-                mx = fmaxf(mx, v);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        // Every lane runs the same instructions below (the matrix cores take
-        // the whole wave): a query with nothing live in reach yet adds zeros
-        // and keeps its state.
-        const float m_new = fmaxf(m_run, mx);
-        const bool none = m_new == -INFINITY;
-        const float m_use = none ? 0.0f : m_new;
-        const float alpha = m_run == -INFINITY ? (none ? 1.0f : 0.0f) : __builtin_amdgcn_exp2f(m_run - m_use);
-        float rs = 0.0f;
-        frag pf[2][2];
+            scs[sub][0] = a0;
+            scs[sub][1] = a1;
+        }
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
+        for (int sub = 0; sub < 2; ++sub) {
+            const int ks = kb + sub * 32;   // the sub-block's first key
+            if (!work[sub]) continue;
+            floatx16_t (&sc)[2] = scs[sub];
+            // Mask (a sub-block wholly live and in every query's window skips
+            // the per-key tests) and take each tile's max of the raw scores
+            // for this lane's query (the scale is positive, so it keeps their
+            // order).
+            const uint32_t sbits = (uint32_t)(bits >> (32 * sub));
+            const bool all_live = sbits == ~0u && (window == INT32_MAX || (ks >= qw + WQ - 1 - window && ks + 31 <= qw + window));
+            float mx[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                if (all_live) {
+#pragma unroll
+                    for (int rr = 0; rr < 16; rr += 2) mx[qt] = fmaxf(mx[qt], fmaxf(sc[qt][rr], sc[qt][rr + 1]));
+                } else {
+                    // This lane's live keys in reach as a mask over the
+                    // sub-block; register rr holds key 8 h + j, j = 16 (rr / 8) + rr % 8.
+                    uint32_t okm = sbits;
+                    if (window < INT32_MAX) {
+                        const int query = qw + 32 * qt + ql;
+                        const int lo = query - window - ks, hi = query + window - ks;   // keys lo .. hi of the sub-block
+                        if (hi < 0 || lo > 31) {
+                            okm = 0;
+                        } else {
+                            const uint32_t upto = hi >= 31 ? ~0u : (2u << hi) - 1;
+                            const uint32_t from = lo <= 0 ? ~0u : ~((1u << lo) - 1);
+                            okm &= upto & from;
+                        }
+                    }
+                    const uint32_t word = okm >> (8 * h);
+#pragma unroll
+                    for (int rr = 0; rr < 16; ++rr) {
+                        const int j = 16 * (rr >> 3) + (rr & 7);
+                        const float v = (word >> j) & 1u ? sc[qt][rr] : -INFINITY;
+                        sc[qt][rr] = v;
+                        mx[qt] = fmaxf(mx[qt], v);
+                    }
+                }
+                mx[qt] = fmaxf(mx[qt], __shfl_xor(mx[qt], 32, 64));
+            }
+            // Every lane runs the same instructions below (the matrix cores
+            // take the whole wave): a query with nothing live in reach yet adds
+            // zeros and keeps its state (-inf > -inf + RESCALE is false).
+            const float mxs0 = mx[0] * scale, mxs1 = mx[1] * scale;
+            const bool grow0 = mxs0 > m_run[0] + RESCALE, grow1 = mxs1 > m_run[1] + RESCALE;
+            if (__ballot(grow0 || grow1) != 0) {
+                const float a0 = grow0 ? __builtin_amdgcn_exp2f(m_run[0] - mxs0) : 1.0f;   // 0 from -inf
+                const float a1 = grow1 ? __builtin_amdgcn_exp2f(m_run[1] - mxs1) : 1.0f;
+#pragma unroll
+                for (int t = 0; t <= D / 32; ++t) {
+                    o[0][t] *= a0;
+                    o[1][t] *= a1;
+                }
+                m_run[0] = grow0 ? mxs0 : m_run[0];
+                m_run[1] = grow1 ? mxs1 : m_run[1];
+            }
+            frag pf[2][2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                const float neg = m_run[qt] == -INFINITY ? 0.0f : -m_run[qt];
+#pragma unroll
+                for (int step = 0; step < 2; ++step) {
+                    T pv[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        pv[e] = from_f32<T>(__builtin_amdgcn_exp2f(fmaf(sc[qt][step * 8 + e], scale, neg)));
+                    pf[qt][step] = *(const frag *)pv;
+                }
+            }
 #pragma unroll
             for (int step = 0; step < 2; ++step) {
-                T pv[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float pe = __builtin_amdgcn_exp2f(sc[sub][step * 8 + e] - m_use);
-                    rs += pe;
-                    pv[e] = from_f32<T>(pe);
-                }
-                pf[sub][step] = *(const frag *)pv;
-            }
-        l_run = l_run * alpha + rs;
-        m_run = m_new;
-#pragma unroll
-        for (int t = 0; t < D / 32; ++t) o[t] *= alpha;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-            for (int step = 0; step < 2; ++step)
 #pragma unroll
                 for (int t = 0; t < D / 32; ++t) {
                     const int row = 32 * t + ql;
                     const int c = sub * 4 + step * 2 + h;
                     const frag vf = *(const frag *)(vbase + row * 128 + 16 * (c ^ att_swz(row)));
-                    o[t] = AttnMma<T>::run(vf, pf[sub][step], o[t]);
+                    o[0][t] = AttnMma<T>::run(vf, pf[0][step], o[0][t]);
+                    o[1][t] = AttnMma<T>::run(vf, pf[1][step], o[1][t]);
                 }
-    }
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-    if (query >= len) return;
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    T *out = ctx + (size_t)(start + query) * heads * D + head * D;
-#pragma unroll
-    for (int t = 0; t < D / 32; ++t)
-#pragma unroll
-        for (int rr = 0; rr < 16; rr += 4) {
-            const int c = 32 * t + 8 * (rr >> 2) + 4 * h;
-            T v4[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) v4[q] = from_f32<T>(o[t][rr + q] * inv);
-            *(uint2 *)(out + c) = *(const uint2 *)v4;
+                o[0][D / 32] = AttnMma<T>::run(ones, pf[0][step], o[0][D / 32]);
+                o[1][D / 32] = AttnMma<T>::run(ones, pf[1][step], o[1][D / 32]);
+            }
         }
+    }
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int query = qw + 32 * qt + ql;
+        if (query >= len) continue;
+        const float l_tot = o[qt][D / 32][0];
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        T *out = ctx + (size_t)(start + query) * heads * D + head * D;
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+            for (int rr = 0; rr < 16; rr += 4) {
+                const int c = 32 * t + 8 * (rr >> 2) + 4 * h;
+                T v4[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v4[q] = from_f32<T>(o[qt][t][rr + q] * inv);
+                *(uint2 *)(out + c) = *(const uint2 *)v4;
+            }
+    }
 }
 
 template <typename T>
 static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
                                    const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx) {
-    const dim3 grid((max_len + 127) / 128, heads, batch);
+    // A 1-D grid of groups of 8 (row, head) pairs times nqb query blocks.
+    const int nqb = (max_len + 255) / 256, pairs = heads * batch;
+    const int blocks = ((pairs + 7) / 8) * 8 * nqb;
     if (d != 64) return hipErrorInvalidValue;
-    // Three stages of K (64 x 64) and V^T (64 x 64) blocks, then three live masks.
-    constexpr int bytes = 3 * 2 * 64 * 64 * 2 + 3 * 8;
-    hipLaunchKernelGGL((attention_mfma_kernel<T, 64>), grid, dim3(256), bytes, s, (const T *)qkv, tcap, heads, p, mask,
-                       seq, window, (T *)ctx);
+    // Three stages of K (64 x 64) and V^T (64 x 64) blocks, then a live mask
+    // per 64-key block a workgroup can reach (its keys start on a multiple of
+    // 64 at most 63 before the row's, so ceil(max_len / 64) + 1 blocks).
+    const int bytes = 3 * 2 * 64 * 64 * 2 + ((max_len + 127) / 64) * 8;
+    if (bytes > 160 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attention_mfma_kernel<T, 64>), dim3(blocks), dim3(256), bytes, s, (const T *)qkv, tcap, heads,
+                       batch, nqb, p, mask, seq, window, (T *)ctx);
     return hipGetLastError();
 }
 
