@@ -53,6 +53,9 @@ def main():
     ap.add_argument("--lengths", default="default", help="'default', 'full', or lo,hi")
     ap.add_argument("--cpu-rows", type=int, default=4, help="rows of the CPU baseline's sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--autotune", default="on", choices=["off", "on"],
+                    help="the session's kernel choices: measured at session creation (on, the default) or the rule's")
+    ap.add_argument("--budget-ms", type=int, default=750, help="the tuner's budget (the core's with a disk cache)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run (each row's encoder is "
@@ -72,7 +75,8 @@ def main():
     assert rt.device_count() >= 1, "no gfx950 device"
     ctx = rt.context(0)
     model = ctx.load(desc)
-    sess = model.session(shape.batch, shape.seq, shape.precision)
+    mode = S.TURBO_AUTOTUNE_ON if args.autotune == "on" else S.TURBO_AUTOTUNE_OFF
+    sess = model.session(shape.batch, shape.seq, shape.precision, autotune=mode, budget_ms=args.budget_ms)
     dtype = {S.TURBO_DTYPE_F16: "f16", S.TURBO_DTYPE_BF16: "bf16", S.TURBO_DTYPE_F32: "f32"}[sess.compute_dtype]
     sess.write_tokens(ids, mask, types, pooling=shape.pooling, normalize=shape.normalize)
     sess.run()
@@ -143,6 +147,8 @@ def main():
         "algorithmic_tflop_per_step": total_flops / 1e12,
         "min_cosine_vs_cpu": min_cos,
         "kernel_ms": {k: round(v, 4) for k, v in times.items()},
+        "kernel_choices": sess.choices(),
+        "tune_ms": sess.tuning.tune_ms,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

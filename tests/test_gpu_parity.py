@@ -218,7 +218,10 @@ def test_matrix_core_attention_meets_the_oracle(context, family, heads, monkeypa
     for path in ("mfma", "simple"):
         monkeypatch.setenv("TURBO_ROCM_CHOICES", f"attention={path}")
         s = model.session(8, 320, S.TURBO_PRECISION_FASTEST)
-        assert f"attention={path}" in s.choices()
+        # The string names the path that runs: the matrix-core kernel takes
+        # heads of 64 alone.
+        runs = path if desc.hidden // desc.heads == 64 else "simple"
+        assert f"attn={runs}" in s.choices() and "forced=attn" in s.choices()
         got[path] = s.embed(ids, mask, types)
         assert_close(got[path], want, s.compute_dtype)
         s.close()
@@ -385,4 +388,76 @@ def test_int8_cross_encoder_meets_the_oracle(context):
     print(f"int8 cross-encoder: min CLS cosine {cos.min():.5f}, "
           f"largest score difference {np.abs(got - want).max() / scale:.4f} of the scale")
     s.close()
+    model.close()
+
+
+# ---- Kernel choices and the autotune cache ------------------------------------------------
+#
+# The seam's tuning protocol (reference include/turbo/turbo_backend.h:231-257,
+# 561-586): ON measures when nothing is cached and reuses a cached choice
+# unmeasured, RETUNE measures against it, the environment forces choices in
+# every mode; the tuned session's vectors meet the oracle as the default's do.
+
+def test_autotune_measures_caches_and_reuses(context, tmp_path):
+    from turboembed_amd import tuning as TU
+    desc = small.bert(seed=31, hidden=128, heads=2, inter=256, positions=320, std=0.1)
+    ids, mask, types = small.ragged_rows(31, 5, 300, desc.vocab_size)
+    want = oracle.encode(desc, ids, mask, types)
+    model = context.load(desc)
+    cache = TU.TuneCache(str(tmp_path))
+    s = model.session(8, 320, S.TURBO_PRECISION_FASTEST, autotune=S.TURBO_AUTOTUNE_ON, cache=cache, budget_ms=2000)
+    assert s.tuned == S.TURBO_TUNED_MEASURED, s.tuned
+    ch = s.choices()
+    # Every bin the session reaches (8 x 320 tokens: up to le4k), the four
+    # products and attention.
+    for b in ("le256", "le1k", "le4k"):
+        assert b + ":qkv=" in ch, ch
+    assert "le16k" not in ch and "gt16k" not in ch, ch
+    assert ch.endswith("forced=none"), ch
+    assert any(k.startswith("le1k/ffn1/") for k in s.timings), s.timings
+    assert all(v >= 0 for v in s.timings.values())
+    assert_close(s.embed(ids, mask, types), want, s.compute_dtype)
+    s.close()
+    # The same key again: the cached choice, unmeasured; then from disk alone.
+    s2 = model.session(8, 320, S.TURBO_PRECISION_FASTEST, autotune=S.TURBO_AUTOTUNE_ON, cache=cache)
+    assert s2.tuned == S.TURBO_TUNED_CACHE and s2.choices() == ch and not s2.timings
+    s2.close()
+    s3 = model.session(8, 320, S.TURBO_PRECISION_FASTEST, autotune=S.TURBO_AUTOTUNE_ON,
+                       cache=TU.TuneCache(str(tmp_path)))
+    assert s3.tuned == S.TURBO_TUNED_CACHE and s3.choices() == ch
+    s3.close()
+    # RETUNE measures again, with the cached choice as the incumbent.
+    s4 = model.session(8, 320, S.TURBO_PRECISION_FASTEST, autotune=S.TURBO_AUTOTUNE_RETUNE, cache=cache,
+                       budget_ms=2000)
+    assert s4.tuned == S.TURBO_TUNED_MEASURED
+    s4.close()
+    # OFF: the backend's rule, nothing timed.
+    s5 = model.session(8, 320, S.TURBO_PRECISION_FASTEST)
+    assert s5.tuned == S.TURBO_TUNED_DEFAULT and "qkv=auto" in s5.choices() and not s5.timings
+    s5.close()
+    model.close()
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x192", "128x128", "256x128k32", "r128x128"])
+def test_forced_tiles_meet_the_oracle(context, tile, monkeypatch):
+    desc = small.bert(seed=32, hidden=192, heads=3, inter=384, positions=320, std=0.1)
+    ids, mask, types = small.ragged_rows(32, 6, 300, desc.vocab_size)
+    want = oracle.encode(desc, ids, mask, types)
+    model = context.load(desc)
+    monkeypatch.setenv("TURBO_ROCM_CHOICES", f"all:qkv={tile},out={tile},ffn1={tile},ffn2={tile},attn=mfma")
+    s = model.session(8, 320, S.TURBO_PRECISION_FASTEST, autotune=S.TURBO_AUTOTUNE_ON, budget_ms=2000)
+    assert s.tuned == S.TURBO_TUNED_FORCED and f"ffn2={tile}" in s.choices() and not s.timings
+    assert_close(s.embed(ids, mask, types), want, s.compute_dtype)
+    s.close()
+    model.close()
+
+
+def test_a_bad_choices_string_is_refused(context, monkeypatch):
+    desc = small.bert(seed=33)
+    model = context.load(desc)
+    for bad in ("qkv=999", "le9k:qkv=auto", "attn=fast", "tile=7"):
+        monkeypatch.setenv("TURBO_ROCM_CHOICES", bad)
+        with pytest.raises(T.TurboError) as e:
+            model.session(4, 64, S.TURBO_PRECISION_FASTEST)
+        assert e.value.code == S.TURBO_E_INVALID_ARGUMENT and "TURBO_ROCM_CHOICES" in e.value.message
     model.close()

@@ -118,7 +118,7 @@ class Runtime:
 
 class Context:
     def __init__(self, rt, ordinal):
-        self.rt, self.t = rt, rt.t
+        self.rt, self.t, self.ordinal = rt, rt.t, ordinal
         h = C.c_void_p()
         err = S.new_error()
         _ok(self.t.context_create(ordinal, rt._log, None, C.byref(h), C.byref(err)), err)
@@ -142,8 +142,9 @@ class Model:
         self.h = h
 
     def session(self, max_batch, max_seq, precision=S.TURBO_PRECISION_MODEL, max_ranges=0, task=S.TURBO_TASK_EMBED,
-                numerics_allowed=0):
-        return Session(self, max_batch, max_seq, precision, max_ranges, task, numerics_allowed)
+                numerics_allowed=0, autotune=S.TURBO_AUTOTUNE_OFF, cache=None, budget_ms=None):
+        return Session(self, max_batch, max_seq, precision, max_ranges, task, numerics_allowed, autotune, cache,
+                       budget_ms)
 
     def close(self):
         if self.h:
@@ -155,7 +156,15 @@ class Session:
     """A session opened through session_open, as the core opens one
     (core/src/session/create.rs:151-180)."""
 
-    def __init__(self, model, max_batch, max_seq, precision, max_ranges, task, numerics_allowed):
+    def __init__(self, model, max_batch, max_seq, precision, max_ranges, task, numerics_allowed,
+                 autotune=S.TURBO_AUTOTUNE_OFF, cache=None, budget_ms=None):
+        """autotune: TURBO_AUTOTUNE_OFF (the backend's rule and what the
+        environment forces), ON (the cached choice for the session's key,
+        else measured now and cached) or RETUNE (measured now against the
+        cached one, which it replaces); cache: a tuning.TuneCache, the
+        process's own by default; budget_ms: the measuring budget, else the
+        cache's (core/src/session/create.rs:82-180, core/src/tuning.rs)."""
+        from . import tuning as TU
         self.model, self.t, self.lib = model, model.t, library()
         d = S.turbo_backend_session_desc()
         d.struct_size = C.sizeof(d)
@@ -164,17 +173,46 @@ class Session:
         self.max_batch, self.max_seq, self.max_ranges = max_batch, max_seq, d.max_ranges
         tun = S.turbo_backend_tuning()
         tun.struct_size = C.sizeof(tun)
-        tun.mode = S.TURBO_AUTOTUNE_OFF
+        tun.mode = autotune
         tun.numerics_allowed = numerics_allowed
+        tuned = autotune in (S.TURBO_AUTOTUNE_ON, S.TURBO_AUTOTUNE_RETUNE)
+        self.key, self.cache = None, None
+        if tuned:
+            self.cache = cache if cache is not None else _process_cache()
+            tun.budget_ms = budget_ms if budget_ms is not None else self.cache.budget_ms()
+            self.key = self._tune_key(model, precision, numerics_allowed, max_batch * max_seq, max_seq)
+            entry = self.cache.get(self.key)
+            self._cached = C.create_string_buffer(entry["choices"].encode()) if entry else None
+            tun.cached = C.cast(self._cached, C.c_char_p) if entry else None
+        self._timings = C.create_string_buffer(16384)
+        tun.timings = C.cast(self._timings, C.c_char_p)
+        tun.timings_len = len(self._timings)
         self.tuning = tun
         cd = C.c_uint32()
         h = C.c_void_p()
         err = S.new_error()
         _ok(self.t.session_open(model.h, C.byref(d), C.byref(tun), C.byref(cd), C.byref(h), C.byref(err)), err)
         self.h, self.compute_dtype = h, cd.value
+        self.tuned = tun.tuned
+        self.timings = TU.parse_timings(self._timings.value.decode())
+        # A measured choice goes into the cache, unless the backend widened
+        # the numeric classes (tuning.rs: such a session is never cached).
+        if tuned and tun.tuned == S.TURBO_TUNED_MEASURED and tun.numerics_used == tun.numerics_allowed:
+            self.cache.put(self.key, tun.choices.decode(), self.timings)
         self.run_info = None
         self.n_out = 0
         self.od = 0
+
+    def _tune_key(self, model, precision, numerics_allowed, tcap, max_seq):
+        from . import tuning as TU
+        ctx = model.ctx
+        info = ctx.rt.device_info(ctx.ordinal)
+        st, dt, _, _ = ctx.rt.capability(ctx.ordinal, S.TURBO_TASK_EMBED, precision)
+        return TU.TuneKey(backend=info.backend.decode(), device_name=info.name.decode(), arch=info.arch.decode(),
+                          runtime_version=info.runtime_version.decode(), library_build=TU.library_build(LIB_PATH),
+                          model=TU.model_fingerprint(model.desc), precision=precision, compute_dtype=dt,
+                          numerics_allowed=numerics_allowed, tcap_bin=TU.tcap_bin(tcap),
+                          max_seq_bin=TU.max_seq_bin(max_seq))
 
     # -- writes ---------------------------------------------------------------
     def _rows(self, ids, mask, types, pooling, normalize, output_dim):
@@ -297,6 +335,18 @@ class Session:
         if self.h:
             self.t.session_release(self.h)
             self.h = None
+
+
+_cache = None
+
+
+def _process_cache():
+    """The process's tune cache (TURBO_AUTOTUNE_CACHE names its directory)."""
+    global _cache
+    if _cache is None:
+        from .tuning import TuneCache
+        _cache = TuneCache()
+    return _cache
 
 
 def gemm_check(a, w, bias=None, dtype=S.TURBO_DTYPE_F32, tile=0, ordinal=0):

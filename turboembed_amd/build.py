@@ -16,7 +16,8 @@ OUT = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libturbo_rocm.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["rowwise.hip", "gemm.hip", "attention.hip", "session.cpp", "backend.cpp", "checks.cpp", "rerank.cpp"]
+SOURCES = ["rowwise.hip", "gemm.hip", "attention.hip", "session.cpp", "backend.cpp", "checks.cpp", "rerank.cpp",
+           "autotune.cpp"]
 
 # Per-source device flags. Attention: matrix-core results in ordinary VGPRs,
 # so the softmax's vector ops on its accumulators need no copies through the

@@ -20,6 +20,7 @@
 // blocks are renumbered so that each XCD takes a contiguous run of output
 // tiles, along N first: the run shares its A rows, which then stay in that
 // XCD's L2.
+#include <cstring>
 #include <type_traits>
 
 #include "kernels.h"
@@ -621,6 +622,57 @@ static hipError_t launch_lds(hipStream_t s, int M, int N, int K, const void *A, 
 }
 
 int gemm_tiles() { return 13; }
+
+// Names of the block shapes, as a choices string spells them: output tile,
+// then what sets it apart (r: operands staged through registers; k32: 32
+// columns of k a stage; s<n>: n stages).
+static const char *const TILE_NAME[14] = {"auto",      "r128x128",   "r256x128",   "r64x128",    "256x128",
+                                          "128x128",   "128x256",    "256x256",    "128x128s2",  "256x128k32",
+                                          "128x256k32", "256x128k32s3", "256x256k32", "256x192"};
+
+const char *gemm_tile_name(int tile) { return tile >= 0 && tile <= 13 ? TILE_NAME[tile] : "?"; }
+
+int gemm_tile_by_name(const char *s, size_t n) {
+    for (int t = 0; t <= 13; ++t)
+        if (std::strlen(TILE_NAME[t]) == n && std::strncmp(TILE_NAME[t], s, n) == 0) return t;
+    // A bare number names a tile too.
+    int v = 0;
+    if (n == 0 || n > 2) return -1;
+    for (size_t i = 0; i < n; ++i) {
+        if (s[i] < '0' || s[i] > '9') return -1;
+        v = v * 10 + (s[i] - '0');
+    }
+    return v <= 13 ? v : -1;
+}
+
+// The tiles worth timing for a product of this type and shape: every
+// pipelined shape when the operands take it, else the staged ones.
+int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap) {
+    int n = 0;
+    auto add = [&](int t) {
+        if (n < cap) out[n++] = t;
+    };
+    const bool qkv = e.kind == Epi::Qkv || e.kind == Epi::QkvRope;
+    if (dt == Dt::I8) {
+        if (K % 128 == 0) add(7);
+        add(9);
+        return n;
+    }
+    if (dt == Dt::F32 || K % 64 != 0 || lda % 8 != 0) {
+        add(1);
+        add(2);
+        add(3);
+        return n;
+    }
+    add(7);
+    if (!qkv || e.hidden % 96 == 0) add(13);
+    add(4);
+    add(6);
+    add(5);
+    add(9);
+    add(10);
+    return n;
+}
 
 // The device's compute units, for the launch-shape choice.
 static int cu_count() {

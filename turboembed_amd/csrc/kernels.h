@@ -73,6 +73,14 @@ struct EpiArgs {
 hipError_t gemm(hipStream_t s, Dt dt, int M, int N, int K, const void *A, int lda, const void *W,
                 const EpiArgs &e, int tile = 0);
 int gemm_tiles();   // how many block shapes `tile` may name (1..n)
+// A block shape's name in a choices string ("auto" for 0, the launcher's
+// rule), and the shape a name (or a bare number) spells, -1 for none.
+const char *gemm_tile_name(int tile);
+int gemm_tile_by_name(const char *s, size_t n);
+// The block shapes worth timing for products of this operand type and
+// shape (K, lda and the epilogue decide which kernels take them) into out:
+// how many.
+int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap);
 
 // Softmax attention within each row and head over Q and K ([heads][tcap][d]
 // each) and V transposed ([heads][d][tcap]), in `dt`, one after another in

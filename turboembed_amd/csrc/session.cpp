@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -397,23 +398,9 @@ uint32_t dtype_of(Dt dt) {
     }
 }
 
-// TURBO_ROCM_CHOICES: "gemm=<tile>" forces the GEMM block shape,
-// "attention=simple" the scalar attention path on every tier.
-bool parse_choices(const char *s, int &tile, bool &simple) {
-    if (!s || !*s) return false;
-    bool any = false;
-    if (const char *g = std::strstr(s, "gemm=")) {
-        tile = std::atoi(g + 5);
-        if (tile < 0 || tile > gemm_tiles())
-            fail(TURBO_E_INVALID_ARGUMENT, std::string("rocm: TURBO_ROCM_CHOICES ") + s);
-        any = true;
-    }
-    if (const char *a = std::strstr(s, "attention=")) {
-        simple = std::strncmp(a + 10, "simple", 6) == 0;
-        any = true;
-    }
-    return any;
-}
+// Whether a session's attention can take the matrix-core path: 16-bit
+// activations and 64-wide heads.
+bool mfma_attention(Dt act, uint32_t head_width) { return act != Dt::F32 && head_width == 64; }
 
 }  // namespace
 
@@ -473,16 +460,36 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
                      std::to_string(numeric_of(dt)),
                  3);
     }
-    if (parse_choices(std::getenv("TURBO_ROCM_CHOICES"), s->gemm_tile, s->simple_attention)) {
-        if (tuning) tuning->tuned = TURBO_TUNED_FORCED;
+    // Kernel choices: the rule's, then a cached string (ON and RETUNE), then
+    // what TURBO_ROCM_CHOICES forces (every mode).
+    const uint32_t mode = tuning && tuning->struct_size >= offsetof(turbo_backend_tuning, mode) + 4 ? tuning->mode
+                                                                                                     : TURBO_AUTOTUNE_OFF;
+    const bool tuned_mode = mode == TURBO_AUTOTUNE_ON || mode == TURBO_AUTOTUNE_RETUNE;
+    Choices &kc = s->kc;
+    kc.bins = bins_for((uint64_t)desc->max_batch * desc->max_seq);
+    const bool mfma_attn = mfma_attention(s->act, m->hidden / m->heads);
+    for (int b = 0; b < kc.bins; ++b) kc.bin[b].simple_attention = !mfma_attn;
+    bool cached = false;
+    if (tuned_mode && tuning->cached && *tuning->cached) {
+        std::string why;
+        Choices c = kc;
+        if (parse_choices(tuning->cached, &c, false, &why)) {
+            kc = c;
+            cached = true;
+            m->ctx->say(LOG_DEBUG, "rocm: kernels from the cache: " + std::string(tuning->cached));
+        } else {
+            m->ctx->say(LOG_DEBUG, "rocm: the cached kernels are not taken (" + why + "): " + tuning->cached);
+        }
     }
-    s->choices = "gemm=" + std::to_string(s->gemm_tile) +
-                 (s->simple_attention || s->act == Dt::F32 ? " attention=simple" : " attention=mfma");
-    if (tuning) {
-        std::snprintf(tuning->choices, sizeof tuning->choices, "%s", s->choices.c_str());
-        if (tuning->struct_size >= offsetof(turbo_backend_tuning, numerics_used) + 4)
-            tuning->numerics_used = tuning->numerics_allowed;
+    if (const char *env = std::getenv("TURBO_ROCM_CHOICES")) {
+        std::string why;
+        if (!parse_choices(env, &kc, true, &why))
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: TURBO_ROCM_CHOICES " + std::string(env) + ": " + why);
     }
+    // The scalar path is the only one some sessions have.
+    for (int b = 0; b < kc.bins; ++b)
+        if (!mfma_attn) kc.bin[b].simple_attention = true;
+    const bool measure = ((mode == TURBO_AUTOTUNE_ON && !cached) || mode == TURBO_AUTOTUNE_RETUNE) && !all_forced(kc);
 
     const size_t H = m->hidden, I = m->inter, B = s->max_batch, S = s->max_seq;
     s->tcap = B * S;
@@ -526,6 +533,42 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     s->output.bytes = outs * H * 4;
     s->output.owned = false;
     check(hipHostMalloc((void **)&s->staging, s->staging_ints * 4, hipHostMallocDefault), "session staging");
+
+    const auto t0 = std::chrono::steady_clock::now();
+    std::string timings;
+    bool measured = false;
+    if (measure) {
+        measured = tune(*s, tuning->budget_ms, &timings);
+        // The tuner's products leave Q, K and V holding its values: zero
+        // them again, so every value attention can read stays finite.
+        check(hipMemsetAsync(s->qkv, 0, 3 * s->tcap * H * el + 256, m->ctx->stream), "session qkv");
+        check(hipStreamSynchronize(m->ctx->stream), "session qkv");
+    }
+    s->choices = format_choices(kc);
+    if (tuning) {
+        const uint32_t k = forced_knobs(kc);
+        tuning->tuned = all_forced(kc) ? TURBO_TUNED_FORCED
+                        : measured     ? TURBO_TUNED_MEASURED
+                        : cached       ? TURBO_TUNED_CACHE
+                        : k            ? TURBO_TUNED_FORCED
+                                       : TURBO_TUNED_DEFAULT;
+        tuning->tune_ms = (uint32_t)std::chrono::duration_cast<std::chrono::milliseconds>(
+                              std::chrono::steady_clock::now() - t0)
+                              .count();
+        std::snprintf(tuning->choices, sizeof tuning->choices, "%s", s->choices.c_str());
+        if (tuning->timings && tuning->timings_len) {
+            // What fits, cut at a line's end.
+            std::string t = timings;
+            if (t.size() + 1 > tuning->timings_len) {
+                t.resize(tuning->timings_len - 1);
+                const size_t nl = t.rfind('\n');
+                t.resize(nl == std::string::npos ? 0 : nl + 1);
+            }
+            std::memcpy(tuning->timings, t.c_str(), t.size() + 1);
+        }
+        if (tuning->struct_size >= offsetof(turbo_backend_tuning, numerics_used) + 4)
+            tuning->numerics_used = tuning->numerics_allowed;
+    }
     return s.release();
 }
 
@@ -633,12 +676,88 @@ struct Timer {
     }
 };
 
+// One of a layer's four products: its output columns N, inner size K,
+// operand rows A, weights and epilogue, as the run launches it.
+struct LayerGemm {
+    int N = 0, K = 0;
+    const void *A = nullptr, *W = nullptr;
+    const float *wscale = nullptr;
+    EpiArgs e;
+};
+
+// The operand the QKV and FFN-in products read: x itself on the F32 tier
+// (post-norm), else the narrowed copy or the pre-norm rows in xh.
+static const void *layer_input(const Session &s) {
+    const Model &m = *s.model;
+    return s.act == Dt::F32 && !m.modern ? (const void *)s.x : s.xh;
+}
+
+static LayerGemm layer_gemm(Session &s, uint32_t l, GemmSlot g) {
+    Model &m = *s.model;
+    const Model::Layer &L = m.ls[l];
+    const LayerWeights &W = (*s.w)[l];
+    const int H = (int)m.hidden, I = (int)m.inter, dh = H / (int)m.heads;
+    LayerGemm r;
+    switch (g) {
+    case G_QKV:
+        r.N = (int)L.n_qkv;
+        r.K = H;
+        r.A = layer_input(s);
+        r.W = W.qkv;
+        r.wscale = W.s_qkv;
+        r.e.bias = L.bqkv;
+        r.e.out = s.qkv;
+        r.e.tcap = (int)s.tcap;
+        r.e.heads = (int)m.heads;
+        r.e.d = dh;
+        r.e.hidden = H;
+        if (m.rotary) {
+            const bool global = m.global_every == 0 || l % m.global_every == 0;
+            const size_t half = (size_t)m.positions * m.pairs;
+            r.e.kind = Epi::QkvRope;
+            r.e.cos = m.rope + (global ? 0 : 2 * half);
+            r.e.sin = r.e.cos + half;
+            r.e.at = s.pk.at;
+            r.e.seq = (int)s.seq;
+        } else {
+            r.e.kind = Epi::Qkv;
+        }
+        break;
+    case G_OUT:
+    case G_FFN2:
+        r.N = H;
+        r.K = g == G_OUT ? H : I;
+        r.A = g == G_OUT ? s.ctxb : s.ffn;
+        r.W = g == G_OUT ? W.out : W.ffn_out;
+        r.wscale = g == G_OUT ? W.s_out : W.s_ffn_out;
+        r.e.kind = Epi::Residual;
+        r.e.bias = g == G_OUT ? L.bo : L.b2;
+        r.e.x = s.x;
+        r.e.ldo = H;
+        break;
+    default:
+        r.N = (int)L.n_in;
+        r.K = H;
+        r.A = layer_input(s);
+        r.W = W.ffn_in;
+        r.wscale = W.s_ffn_in;
+        r.e.out = s.ffn;
+        r.e.ldo = I;
+        r.e.bias = L.b1;
+        r.e.kind = m.rotary ? Epi::Gated : Epi::Gelu;
+        r.e.silu = m.silu ? 1 : 0;
+        break;
+    }
+    return r;
+}
+
 void encode(Session &s) {
     Model &m = *s.model;
     hipStream_t st = s.ctx->stream;
-    const int T = (int)s.tokens, H = (int)m.hidden, I = (int)m.inter, heads = (int)m.heads, dh = H / heads;
+    const int T = (int)s.tokens, H = (int)m.hidden, heads = (int)m.heads, dh = H / heads;
     const Dt dt = s.act;   // activations; the GEMMs take s.dt
     const bool f32 = dt == Dt::F32, i8 = s.dt == Dt::I8;
+    const BinChoice &bc = s.kc.bin[bin_of(s.tokens, s.kc.bins)];
     Timer tm(s);
     auto run = [&](const char *name, hipError_t e) {
         (void)name;
@@ -652,86 +771,49 @@ void encode(Session &s) {
     } while (0)
     // One GEMM of the layer. On the I8 tier its operand rows are quantized
     // first (per token), and the epilogue takes both scales.
-    auto mm = [&](const char *name, int N, int K, const void *A, const void *Wt, const float *wscale, EpiArgs &e) {
+    static const char *const NAMES[G_COUNT] = {"gemm_qkv", "gemm_out", "gemm_ffn_in", "gemm_ffn_out"};
+    auto mm = [&](uint32_t l, GemmSlot g) {
+        LayerGemm lg = layer_gemm(s, l, g);
+        const void *A = lg.A;
         if (i8) {
-            LAUNCH("quantize", quantize_rows(st, A, Dt::F16, T, K, K, s.aq, s.ascale));
-            e.a_scale = s.ascale;
-            e.w_scale = wscale;
+            LAUNCH("quantize", quantize_rows(st, A, Dt::F16, T, lg.K, lg.K, s.aq, s.ascale));
+            lg.e.a_scale = s.ascale;
+            lg.e.w_scale = lg.wscale;
             A = s.aq;
         }
-        LAUNCH(name, gemm(st, s.dt, T, N, K, A, K, Wt, e, s.gemm_tile));
+        LAUNCH(NAMES[g], gemm(st, s.dt, T, lg.N, lg.K, A, lg.K, lg.W, lg.e, bc.tile[g]));
     };
     LAUNCH("pack_rows", pack_rows(st, s.mask, (int)s.batch, (int)s.seq, s.pk));
-    // The GEMM operand copy of x: x itself on the F32 tier.
-    void *xa = f32 ? (void *)s.x : s.xh;
     LAUNCH("embed_ln", embed_ln(st, T, H, s.ids, s.types, s.pk, (int)s.seq, (int)m.position_offset, m.word, m.pos,
                                 m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
     for (uint32_t l = 0; l < m.layers; ++l) {
         const Model::Layer &L = m.ls[l];
-        const LayerWeights &W = (*s.w)[l];
-        EpiArgs q;
-        q.bias = L.bqkv;
-        q.out = s.qkv;
-        q.tcap = (int)s.tcap;
-        q.heads = heads;
-        q.d = dh;
-        q.hidden = H;
         int window = INT32_MAX;
-        const void *src = xa;
         if (m.rotary) {
             const bool global = m.global_every == 0 || l % m.global_every == 0;
-            const size_t half = (size_t)m.positions * m.pairs;
-            q.kind = Epi::QkvRope;
-            q.cos = m.rope + (global ? 0 : 2 * half);
-            q.sin = q.cos + half;
-            q.at = s.pk.at;
-            q.seq = (int)s.seq;
             if (!global) window = (int)m.window;
-            if (m.modern && l > 0) {
-                // xn = LN(x) into xh (F32 on the F32 tier), x kept.
+        }
+        if (m.modern) {
+            // Pre-norm: xn = LN(x) into xh (F32 on the F32 tier), x kept; the
+            // first layer's attention reads the embeddings' rows as they are.
+            if (l > 0)
                 LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln1_w, nullptr, m.eps, f32 ? (float *)s.xh : nullptr,
                                                 f32 ? nullptr : s.xh, dt));
-                src = s.xh;
-            } else if (m.modern) {
-                src = xa;
-            }
-        } else {
-            q.kind = Epi::Qkv;
+            else if (f32)
+                check(hipMemcpyAsync(s.xh, s.x, (size_t)T * H * 4, hipMemcpyDeviceToDevice, st), "pre-norm rows");
         }
-        mm("gemm_qkv", (int)L.n_qkv, H, src, W.qkv, W.s_qkv, q);
+        mm(l, G_QKV);
         LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, (int)s.seq, (int)s.batch,
-                                      (int)s.max_len, window, s.ctxb, s.simple_attention));
-        EpiArgs o;
-        o.kind = Epi::Residual;
-        o.bias = L.bo;
-        o.x = s.x;
-        o.ldo = H;
-        mm("gemm_out", H, H, s.ctxb, W.out, W.s_out, o);
-        const void *ffn_src = xa;
+                                      (int)s.max_len, window, s.ctxb, bc.simple_attention));
+        mm(l, G_OUT);
         if (m.modern) {
             LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln2_w, nullptr, m.eps, f32 ? (float *)s.xh : nullptr,
                                             f32 ? nullptr : s.xh, dt));
-            ffn_src = s.xh;
         } else {
             LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln1_w, L.ln1_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
         }
-        EpiArgs f;
-        f.out = s.ffn;
-        f.ldo = I;
-        f.bias = L.b1;
-        if (m.rotary) {
-            f.kind = Epi::Gated;
-            f.silu = m.silu ? 1 : 0;
-        } else {
-            f.kind = Epi::Gelu;
-        }
-        mm("gemm_ffn_in", (int)L.n_in, H, ffn_src, W.ffn_in, W.s_ffn_in, f);
-        EpiArgs f2;
-        f2.kind = Epi::Residual;
-        f2.bias = L.b2;
-        f2.x = s.x;
-        f2.ldo = H;
-        mm("gemm_ffn_out", H, I, s.ffn, W.ffn_out, W.s_ffn_out, f2);
+        mm(l, G_FFN1);
+        mm(l, G_FFN2);
         if (!m.modern)
             LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln2_w, L.ln2_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
     }
@@ -740,6 +822,107 @@ void encode(Session &s) {
     LAUNCH("pool", pool(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.count ? s.ranges : nullptr, (int)s.pooling,
                         (int)s.output_dim, s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0, s.out));
 #undef LAUNCH
+}
+
+// The tuner: each bin's four products timed at the bin's token count with
+// each candidate block shape, on operands of uniform values in the
+// session's own buffers; a candidate replaces the bin's choice (the rule's,
+// or the cached one: the incumbent, timed first) when it is faster by the
+// margin. Largest bins first, as they cost the most; stops at the budget.
+// Returns whether anything was timed.
+bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
+    using Clock = std::chrono::steady_clock;
+    const Clock::time_point deadline = Clock::now() + std::chrono::milliseconds(budget_ms);
+    constexpr float MARGIN = 0.97f;   // a candidate must be 3% faster
+    constexpr int REPS = 3;
+    Model &m = *s.model;
+    hipStream_t st = s.ctx->stream;
+    const size_t H = m.hidden, I = m.inter, tcap = s.tcap;
+    // Operands: x uniform in [-1, 1), and the activations from it.
+    check(fill_uniform(st, s.x, tcap * H, 1.0f, 17), "the tuner's operands");
+    if (s.act == Dt::F32) {
+        check(fill_uniform(st, (float *)s.xh, tcap * H, 1.0f, 18), "the tuner's operands");
+        check(fill_uniform(st, (float *)s.ctxb, tcap * H, 1.0f, 19), "the tuner's operands");
+        check(fill_uniform(st, (float *)s.ffn, tcap * I, 1.0f, 20), "the tuner's operands");
+    } else {
+        check(narrow(st, s.x, s.xh, tcap * H, s.act, nullptr), "the tuner's operands");
+        check(narrow(st, s.x, s.ctxb, tcap * H, s.act, nullptr), "the tuner's operands");
+        const size_t el = dt_bytes(s.act);
+        for (size_t o = 0; o < tcap * I; o += tcap * H)
+            check(narrow(st, s.x, static_cast<char *>(s.ffn) + o * el, std::min(tcap * H, tcap * I - o), s.act, nullptr),
+                  "the tuner's operands");
+    }
+    // No rows are written yet: the rotary epilogue reads each token's
+    // position as pk.at % seq, so every token sits at position 0 of rows of
+    // max_seq for the tuner's products.
+    check(hipMemsetAsync(s.pk.at, 0, tcap * 4, st), "the tuner's operands");
+    struct Seq {
+        Session &s;
+        uint32_t was;
+        ~Seq() { s.seq = was; }
+    } seq_guard{s, s.seq};
+    s.seq = s.max_seq;
+    hipEvent_t ev[2 * REPS];
+    for (hipEvent_t &e : ev) check(hipEventCreate(&e), "the tuner's events");
+    struct Events {
+        hipEvent_t *ev;
+        ~Events() {
+            for (int i = 0; i < 2 * REPS; ++i) (void)hipEventDestroy(ev[i]);
+        }
+    } guard{ev};
+    bool any = false;
+    char line[160];
+    for (int b = s.kc.bins - 1; b >= 0; --b) {
+        const int M = (int)bin_tokens(b, tcap);
+        BinChoice &bc = s.kc.bin[b];
+        for (int g = 0; g < G_COUNT; ++g) {
+            if (bc.tile_forced[g]) continue;
+            LayerGemm lg = layer_gemm(s, 0, (GemmSlot)g);
+            const void *A = lg.A;
+            if (s.dt == Dt::I8) {
+                check(quantize_rows(st, A, Dt::F16, M, lg.K, lg.K, s.aq, s.ascale), "the tuner's operands");
+                lg.e.a_scale = s.ascale;
+                lg.e.w_scale = lg.wscale;
+                A = s.aq;
+            }
+            int cand[16];
+            cand[0] = bc.tile[g];
+            const int n = 1 + gemm_candidates(s.dt, lg.K, lg.K, lg.e, cand + 1, 15);
+            float incumbent = 0, fastest = 0;
+            int best = -1;
+            for (int i = 0; i < n; ++i) {
+                if (i > 0 && cand[i] == cand[0]) continue;
+                if (Clock::now() >= deadline) break;
+                auto launch = [&]() { return gemm(st, s.dt, M, lg.N, lg.K, A, lg.K, lg.W, lg.e, cand[i]); };
+                check(launch(), "the tuner's GEMM");
+                for (int r = 0; r < REPS; ++r) {
+                    check(hipEventRecord(ev[2 * r], st), "the tuner's events");
+                    check(launch(), "the tuner's GEMM");
+                    check(hipEventRecord(ev[2 * r + 1], st), "the tuner's events");
+                }
+                check(hipStreamSynchronize(st), "the tuner's GEMM");
+                float least = 0;
+                for (int r = 0; r < REPS; ++r) {
+                    float ms = 0;
+                    check(hipEventElapsedTime(&ms, ev[2 * r], ev[2 * r + 1]), "the tuner's events");
+                    least = r == 0 ? ms : std::min(least, ms);
+                }
+                std::snprintf(line, sizeof line, "%s/%s/%s=%.4f\n", BIN_NAME[b], GEMM_NAME[g], gemm_tile_name(cand[i]),
+                              least);
+                *timings += line;
+                any = true;
+                if (i == 0) {
+                    incumbent = least;
+                } else if (best < 0 || least < fastest) {
+                    best = i;
+                    fastest = least;
+                }
+            }
+            if (incumbent > 0 && best > 0 && fastest <= MARGIN * incumbent) bc.tile[g] = cand[best];
+        }
+    }
+    s.ctx->say(LOG_DEBUG, "rocm: tuned kernels: " + format_choices(s.kc));
+    return any;
 }
 
 // After a synchronized run: each kernel's milliseconds, summed by name.

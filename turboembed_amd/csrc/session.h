@@ -10,9 +10,13 @@
 #include <vector>
 
 #include "turbo/turbo_seam.h"
+#include "autotune.h"
 #include "kernels.h"
 
 namespace rocm {
+
+// Log levels of turbo_log_fn (reference include/turbo/turbo.h:276).
+constexpr uint32_t LOG_WARNING = 1, LOG_INFO = 2, LOG_DEBUG = 3;
 
 struct Failure {
     int32_t code;
@@ -140,9 +144,8 @@ struct Session {
     bool has_types = false;
     uint64_t h2d = 0;
     std::vector<LayerWeights> *w = nullptr;
-    std::string choices;
-    int gemm_tile = 0;
-    bool simple_attention = false;
+    Choices kc;            // kernel choices per bin of packed tokens
+    std::string choices;   // kc as a choices string
     // Per-launch timing (a test and benchmark hook): events around each
     // kernel of a run, by name.
     bool timing = false;
@@ -158,5 +161,8 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
 void session_release(Session *s);
 void session_write(Session *s, const turbo_backend_embed_rows *rows, const turbo_token_range *ranges, uint32_t count);
 void session_run(Session *s, turbo_backend_run *out);
+// Times the session's candidate kernels within budget_ms and keeps the
+// fastest in s.kc; timing lines into *timings. Whether anything was timed.
+bool tune(Session &s, uint32_t budget_ms, std::string *timings);
 
 }  // namespace rocm
