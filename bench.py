@@ -44,6 +44,55 @@ def kernel_flops(shape, tokens, lengths):
     return f
 
 
+COPY_PROBE_BYTES = 256 << 20   # the traffic counters' reference copy: read and write this much
+
+
+def traffic_file(workload):
+    return os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+
+
+def summarize_pmc(fetch_dir, write_dir, workload, command):
+    """HBM bytes per launch of the GEMM kernel (every instantiation in the
+    run) from two rocprofv3 --pmc runs of this script with --copy-probe
+    (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
+    same counter read for the plain copy of COPY_PROBE_BYTES; written to
+    profiles/traffic_<workload>.json and .md."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        vals = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] == counter:
+                    vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return vals
+
+    out = {"workload": workload, "command": command, "copy_probe_bytes": COPY_PROBE_BYTES}
+    lines = [f"# HBM traffic per launch: {workload}", "", "Commands (from the repository root, one MI355X):", "",
+             "```", *command, "```", "",
+             "| counter | copy probe reads (KiB/dispatch) | expected KiB | factor | GEMM kernel KiB/dispatch (mean) "
+             "| scaled bytes/launch | dispatches |", "|---|---|---|---|---|---|---|"]
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        v = per_kernel(d, counter)
+        copy = [x for k, xs in v.items() if "copy_kernel" in k for x in xs]
+        gemm = [x for k, xs in v.items() if "gemm_lds_kernel" in k for x in xs]
+        expected = COPY_PROBE_BYTES / 1024.0
+        factor = expected / (sum(copy) / len(copy))
+        mean = sum(gemm) / len(gemm)
+        out[counter] = {"copy_kib": sum(copy) / len(copy), "factor": factor, "gemm_kib": mean,
+                        "gemm_bytes": mean * 1024.0 * factor, "dispatches": len(gemm)}
+        lines.append(f"| {counter} | {sum(copy) / len(copy):.0f} | {expected:.0f} | {factor:.4f} | {mean:.0f} | "
+                     f"{mean * 1024.0 * factor:.4g} | {len(gemm)} |")
+    out["traffic_bytes_per_launch"] = out["FETCH_SIZE"]["gemm_bytes"] + out["WRITE_SIZE"]["gemm_bytes"]
+    lines += ["", f"Traffic per GEMM launch (fetch + write, scaled): {out['traffic_bytes_per_launch']:.4g} bytes."]
+    with open(traffic_file(workload), "w") as f:
+        json.dump(out, f, indent=1)
+    with open(traffic_file(workload)[:-5] + ".md", "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -56,12 +105,20 @@ def main():
     ap.add_argument("--autotune", default="on", choices=["off", "on"],
                     help="the session's kernel choices: measured at session creation (on, the default) or the rule's")
     ap.add_argument("--budget-ms", type=int, default=750, help="the tuner's budget (the core's with a disk cache)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after the timed steps, copy 256 MiB on the device (the traffic counters' reference)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/traffic_<workload>.json from two rocprofv3 --pmc runs and exit")
+    ap.add_argument("--pmc-command", action="append", default=[], help="the profiling commands, for the summary")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run (each row's encoder is "
               "independent, so more GPUs would shard rows with no exchange)", file=sys.stderr)
         sys.exit(2)
 
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.workload, args.pmc_command)
+        return
     shape = W.SHAPES[args.workload]
     lengths = {"default": "default", "full": None}.get(args.lengths)
     if lengths is None and args.lengths not in ("default", "full"):
@@ -112,8 +169,14 @@ def main():
     else:
         dom, dom_ms, dom_flops, dom_launches = "gemm", gemm_ms, gemm_flops, len(gemm_names) * shape.layers
     achieved = dom_flops / (dom_ms / 1e3)
+    traffic = None
+    if dom == "gemm" and os.path.exists(traffic_file(args.workload)):
+        with open(traffic_file(args.workload)) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
+    if args.copy_probe:
+        T.copy_probe(COPY_PROBE_BYTES, iters=3)
     roofline = {"kernel": dom, "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[dtype] / 1e12,
-                "unit": "TFLOP/s", "frac": achieved / PEAK[dtype], "traffic": None,
+                "unit": "TFLOP/s", "frac": achieved / PEAK[dtype], "traffic": traffic,
                 "launches_per_step": dom_launches, "avg_launch_us": dom_ms / dom_launches * 1e3,
                 "flops_per_launch": dom_flops / dom_launches}
 

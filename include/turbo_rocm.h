@@ -135,6 +135,13 @@ int32_t turbo_rocm_gemm_check(uint32_t ordinal, uint32_t dtype, uint32_t M, uint
 int32_t turbo_rocm_gemm_time(uint32_t ordinal, uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, uint32_t tile,
                              uint32_t iters, float *ms, turbo_error *err);
 
+/* A plain device copy of `bytes` (a multiple of 16) from one buffer to
+ * another, `iters` times, on device `ordinal`: the average milliseconds of
+ * a launch into *ms. A measurement hook with no counterpart
+ * in the reference: its launches read and write exactly `bytes`, so the
+ * profiler's traffic counters can be scaled by what they read for it. */
+int32_t turbo_rocm_copy_probe(uint32_t ordinal, uint64_t bytes, uint32_t iters, float *ms, turbo_error *err);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,7 @@ def library():
         "turbo_rocm_session_replay": [P, u32, E],
         "turbo_rocm_gemm_check": [u32, u32, u32, u32, u32, P, P, P, P, u32, E],
         "turbo_rocm_gemm_time": [u32, u32, u32, u32, u32, u32, u32, C.POINTER(C.c_float), E],
+        "turbo_rocm_copy_probe": [u32, C.c_uint64, u32, C.POINTER(C.c_float), E],
         "turbo_rocm_pair_windows": [P, u32, P, u32, C.c_int32, C.c_int32, u32, u32, u32, u32, P, P, P, u32,
                                     C.POINTER(u32), E],
         "turbo_rocm_rerank_scores": [P, u32, u32, P, P, P, C.c_float, P, E],
@@ -369,4 +370,13 @@ def gemm_time(m, n, k, dtype=S.TURBO_DTYPE_F16, tile=0, iters=20, ordinal=0):
     ms = C.c_float()
     err = S.new_error()
     _ok(library().turbo_rocm_gemm_time(ordinal, dtype, m, n, k, tile, iters, C.byref(ms), C.byref(err)), err)
+    return ms.value
+
+
+def copy_probe(nbytes, iters=5, ordinal=0):
+    """Average milliseconds of a plain device copy of nbytes (read and
+    write nbytes each): the reference for the profiler's traffic counters."""
+    ms = C.c_float()
+    err = S.new_error()
+    _ok(library().turbo_rocm_copy_probe(ordinal, nbytes, iters, C.byref(ms), C.byref(err)), err)
     return ms.value

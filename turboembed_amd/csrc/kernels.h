@@ -104,6 +104,9 @@ hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, con
 hipError_t quantize_rows(hipStream_t s, const void *src, Dt src_dt, int rows, int cols, int ld, int8_t *dst,
                          float *scale);
 
+// dst = src over `bytes` (a multiple of 16), 16-byte vectors, one pass.
+hipError_t copy_bytes(hipStream_t s, const void *src, void *dst, size_t bytes);
+
 // n values uniform in [-amp, amp) from a counter hash of (seed, index).
 hipError_t fill_uniform(hipStream_t s, float *dst, size_t n, float amp, uint32_t seed);
 

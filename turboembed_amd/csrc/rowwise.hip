@@ -378,6 +378,21 @@ hipError_t fill_uniform(hipStream_t s, float *dst, size_t n, float amp, uint32_t
     return hipGetLastError();
 }
 
+// ---- Plain copy (the traffic counters' reference) ---------------------------------------
+
+__global__ void __launch_bounds__(256) copy_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t copy_bytes(hipStream_t s, const void *src, void *dst, size_t bytes) {
+    if (bytes % 16 != 0) return hipErrorInvalidValue;
+    const size_t n = bytes / 16;
+    if (n == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 256 * 32);
+    hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const uint4 *)src, (uint4 *)dst, n);
+    return hipGetLastError();
+}
+
 // ---- Weight narrowing ------------------------------------------------------------------
 
 template <typename H>

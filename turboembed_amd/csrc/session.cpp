@@ -1165,4 +1165,28 @@ int32_t turbo_rocm_gemm_time(uint32_t ordinal, uint32_t dtype, uint32_t M, uint3
     });
 }
 
+int32_t turbo_rocm_copy_probe(uint32_t ordinal, uint64_t bytes, uint32_t iters, float *ms, turbo_error *err) {
+    return guarded(err, [&] {
+        if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device");
+        if (iters == 0 || bytes == 0 || bytes % 16 != 0) fail(TURBO_E_INVALID_ARGUMENT, "rocm: bytes and iters");
+        OnDevice on(devices()[ordinal]);
+        DevPtr src(dev_alloc(bytes, "copy probe")), dst(dev_alloc(bytes, "copy probe"));
+        check(hipMemset(src.get(), 1, bytes), "copy probe");
+        hipEvent_t e0, e1;
+        check(hipEventCreate(&e0), "copy probe");
+        check(hipEventCreate(&e1), "copy probe");
+        check(copy_bytes(nullptr, src.get(), dst.get(), bytes), "copy probe");
+        check(hipEventRecord(e0, nullptr), "copy probe");
+        for (uint32_t i = 0; i < iters; ++i) check(copy_bytes(nullptr, src.get(), dst.get(), bytes), "copy probe");
+        check(hipEventRecord(e1, nullptr), "copy probe");
+        check(hipEventSynchronize(e1), "copy probe");
+        float t = 0;
+        check(hipEventElapsedTime(&t, e0, e1), "copy probe");
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        *ms = t / iters;
+        return TURBO_OK;
+    });
+}
+
 }  // extern "C"
