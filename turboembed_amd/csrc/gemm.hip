@@ -84,7 +84,7 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
     const int mb = mt + (lane >> 5) * 4;   // row of register r: mb + 8 (r / 4) + r % 4
     const bool col_ok = n < N;
     const float bias = (e.bias && col_ok) ? e.bias[n] : 0.0f;
-    if constexpr (KIND == Epi::Plain || KIND == Epi::Gelu || KIND == Epi::Residual) {
+    if constexpr (KIND == Epi::Plain || KIND == Epi::Gelu || KIND == Epi::Residual || KIND == Epi::Bias) {
         if (!col_ok) return;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -93,6 +93,10 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
             const float v = acc[r] + bias;
             const size_t at = (size_t)m * e.ldo + n;
             if constexpr (KIND == Epi::Plain) ((float *)e.out)[at] = v;
+            else if constexpr (KIND == Epi::Bias) {
+                if (e.out_f32) ((float *)e.out)[at] = v;
+                else ((T *)e.out)[at] = from_f32<T>(v);
+            }
             else if constexpr (KIND == Epi::Gelu)
                 ((T *)e.out)[at] = from_f32<T>(sizeof(T) == 2 ? dev_gelu_fast(v) : dev_gelu(v));
             else e.x[at] = e.x[at] + v;
@@ -249,6 +253,7 @@ static hipError_t launch(hipStream_t s, int M, int N, int K, const void *A, int 
     case Epi::Residual: return launch_k<T, BM, BN, BK, Epi::Residual>(s, M, N, K, A, lda, W, e);
     case Epi::QkvRope: return launch_k<T, BM, BN, BK, Epi::QkvRope>(s, M, N, K, A, lda, W, e);
     case Epi::Gated: return launch_k<T, BM, BN, BK, Epi::Gated>(s, M, N, K, A, lda, W, e);
+    case Epi::Bias: return launch_k<T, BM, BN, BK, Epi::Bias>(s, M, N, K, A, lda, W, e);
     }
     return hipErrorInvalidValue;
 }
@@ -395,13 +400,19 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                     v[4 + q] = hi[q] + bias[4 + q];
                 }
             }
-            if constexpr (KIND == Epi::Plain) {
-                float *o = (float *)e.out + (size_t)m * e.ldo + n;
-                if (full) {
-                    *(float4_t *)o = float4_t{v[0], v[1], v[2], v[3]};
-                    *(float4_t *)(o + 4) = float4_t{v[4], v[5], v[6], v[7]};
+            if constexpr (KIND == Epi::Plain || KIND == Epi::Bias) {
+                if (KIND == Epi::Plain || e.out_f32) {
+                    float *o = (float *)e.out + (size_t)m * e.ldo + n;
+                    if (full) {
+                        *(float4_t *)o = float4_t{v[0], v[1], v[2], v[3]};
+                        *(float4_t *)(o + 4) = float4_t{v[4], v[5], v[6], v[7]};
+                    } else {
+                        for (int q = 0; n + q < N; ++q) o[q] = v[q];
+                    }
                 } else {
-                    for (int q = 0; n + q < N; ++q) o[q] = v[q];
+                    T *o = (T *)e.out + (size_t)m * e.ldo + n;
+                    if (full) store8<T>(o, v);
+                    else for (int q = 0; n + q < N; ++q) o[q] = from_f32<T>(v[q]);
                 }
             } else if constexpr (KIND == Epi::Residual) {
                 float *o = e.x + (size_t)m * e.ldo + n;
@@ -616,6 +627,7 @@ static hipError_t launch_lds(hipStream_t s, int M, int N, int K, const void *A, 
         LDS_CASE(Residual)
         LDS_CASE(QkvRope)
         LDS_CASE(Gated)
+        LDS_CASE(Bias)
     }
 #undef LDS_CASE
     return hipErrorInvalidValue;

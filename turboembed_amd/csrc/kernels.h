@@ -42,6 +42,13 @@ hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, c
 hipError_t layer_norm(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
                       float eps, float *out_f32, void *out_h, Dt dt);
 
+// The residual add and a LayerNorm in one pass, row by row: v = x + y (y in
+// ydt: F32, F16 or BF16). Post-norm (pre_norm 0): x = LN(v), and out_h =
+// LN(v) in `dt` when not NULL. Pre-norm (pre_norm 1): x = v, and out_h =
+// LN(v) in `dt` (out_h F32 on the F32 tier). ln_b NULL is no bias.
+hipError_t add_layer_norm(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
+                          const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt);
+
 // What a GEMM does with each output once its sum is done.
 enum class Epi : int {
     Plain = 0,     // outf[m, n] = acc + bias (F32 out; kernel tests)
@@ -50,6 +57,7 @@ enum class Epi : int {
     Residual = 3,  // x[m, n] += acc + bias (F32)
     QkvRope = 4,   // as Qkv, Q and K rotated by their tokens' positions (pair-adjacent columns)
     Gated = 5,     // out[m, n / 2] = act(acc_n + b_n) * (acc_{n+1} + b_{n+1}) in the operand type
+    Bias = 6,      // out[m, n] = acc + bias, in the operand type or (out_f32) F32: a product the next kernel adds
 };
 
 struct EpiArgs {
@@ -63,6 +71,7 @@ struct EpiArgs {
     const int32_t *at = nullptr;   // QkvRope: each token's r * seq + p
     int seq = 0;
     int silu = 0;                  // Gated: SiLU instead of GELU
+    int out_f32 = 0;               // Bias: F32 outputs (else the operand type; F16 for int8 operands)
     // I8 operands: output (m, n) is the int32 sum times a_scale[m] * w_scale[n].
     const float *a_scale = nullptr, *w_scale = nullptr;
 };

@@ -52,48 +52,74 @@ hipError_t pack_rows(hipStream_t s, const int32_t *mask, int batch, int seq, Pac
 
 // ---- LayerNorm over one token per wave ------------------------------------------
 //
-// Each lane holds V values of the row, columns lane + 64 * v. The mean and
-// the biased variance are summed in F32 across the wave, the variance about
-// the mean (two passes over registers).
-template <int V>
-__device__ __forceinline__ void ln_wave(float (&v)[V], int hidden, const float *__restrict__ w,
+// Each lane holds G groups of 4 consecutive columns of the row, columns
+// 4 (lane + 64 g) .. + 3, read and written as 16-byte (F32) or 8-byte
+// (16-bit) vectors (hidden is a multiple of 8). The mean and the biased
+// variance are summed in F32 across the wave, the variance about the mean
+// (two passes over registers).
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void load4(const float *p, float (&v)[4]) {
+    const float4_t q = *(const float4_t *)p;
+    v[0] = q[0], v[1] = q[1], v[2] = q[2], v[3] = q[3];
+}
+template <typename H> __device__ __forceinline__ void load4(const H *p, float (&v)[4]) {
+    typedef H h4 __attribute__((ext_vector_type(4)));
+    const h4 q = *(const h4 *)p;
+    v[0] = to_f32(q[0]), v[1] = to_f32(q[1]), v[2] = to_f32(q[2]), v[3] = to_f32(q[3]);
+}
+__device__ __forceinline__ void store4(float *p, const float (&v)[4]) { *(float4_t *)p = float4_t{v[0], v[1], v[2], v[3]}; }
+template <typename H> __device__ __forceinline__ void store4(H *p, const float (&v)[4]) {
+    typedef H h4 __attribute__((ext_vector_type(4)));
+    *(h4 *)p = h4{from_f32<H>(v[0]), from_f32<H>(v[1]), from_f32<H>(v[2]), from_f32<H>(v[3])};
+}
+
+template <int G>
+__device__ __forceinline__ void ln_wave(float (&v)[G][4], int hidden, const float *__restrict__ w,
                                         const float *__restrict__ b, float eps) {
     const int lane = threadIdx.x & 63;
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < V; ++i)
-        if (lane + 64 * i < hidden) s += v[i];
+    for (int g = 0; g < G; ++g)
+        if (4 * (lane + 64 * g) < hidden) s += (v[g][0] + v[g][1]) + (v[g][2] + v[g][3]);
     const float mean = wave_sum(s) / (float)hidden;
     float q = 0.0f;
 #pragma unroll
-    for (int i = 0; i < V; ++i)
-        if (lane + 64 * i < hidden) {
-            const float c = v[i] - mean;
-            q = fmaf(c, c, q);
-        }
+    for (int g = 0; g < G; ++g)
+        if (4 * (lane + 64 * g) < hidden)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float c = v[g][k] - mean;
+                q = fmaf(c, c, q);
+            }
     const float var = wave_sum(q) / (float)hidden;
     const float inv = 1.0f / sqrtf(var + eps);
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-        const int c = lane + 64 * i;
-        if (c < hidden) v[i] = (v[i] - mean) * inv * w[c] + (b ? b[c] : 0.0f);
+    for (int g = 0; g < G; ++g) {
+        const int c = 4 * (lane + 64 * g);
+        if (c >= hidden) continue;
+        float wv[4], bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        load4(w + c, wv);
+        if (b) load4(b + c, bv);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[g][k] = (v[g][k] - mean) * inv * wv[k] + bv[k];
     }
 }
 
-template <int V, typename H>
-__device__ __forceinline__ void store_row(const float (&v)[V], int hidden, float *xf, H *xh) {
+template <int G, typename H>
+__device__ __forceinline__ void store_row(const float (&v)[G][4], int hidden, float *xf, H *xh) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-        const int c = lane + 64 * i;
+    for (int g = 0; g < G; ++g) {
+        const int c = 4 * (lane + 64 * g);
         if (c < hidden) {
-            if (xf) xf[c] = v[i];
-            if (xh) xh[c] = from_f32<H>(v[i]);
+            if (xf) store4(xf + c, v[g]);
+            if (xh) store4(xh + c, v[g]);
         }
     }
 }
 
-template <int V, typename H>
+template <int G, typename H>
 __global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, const int32_t *__restrict__ ids,
                                                        const int32_t *__restrict__ types, Packing p, int seq,
                                                        int offset, const float *__restrict__ word,
@@ -109,23 +135,33 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, c
     const float *wr = word + (size_t)id * hidden;
     const float *pr = pos ? pos + (size_t)(at % seq + offset) * hidden : nullptr;
     const float *tr = type ? type + (size_t)ty * hidden : nullptr;
-    float v[V];
+    float v[G][4];
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-        const int c = lane + 64 * i;
-        float a = 0.0f;
+    for (int g = 0; g < G; ++g) {
+        const int c = 4 * (lane + 64 * g);
         if (c < hidden) {
-            a = wr[c];
-            if (pr) a = a + pr[c];
-            if (tr) a = a + tr[c];
+            load4(wr + c, v[g]);
+            float a[4];
+            if (pr) {
+                load4(pr + c, a);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[g][k] = v[g][k] + a[k];
+            }
+            if (tr) {
+                load4(tr + c, a);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[g][k] = v[g][k] + a[k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[g][k] = 0.0f;
         }
-        v[i] = a;
     }
-    ln_wave<V>(v, hidden, ln_w, ln_b, eps);
-    store_row<V, H>(v, hidden, x + (size_t)t * hidden, xh ? xh + (size_t)t * hidden : nullptr);
+    ln_wave<G>(v, hidden, ln_w, ln_b, eps);
+    store_row<G, H>(v, hidden, x + (size_t)t * hidden, xh ? xh + (size_t)t * hidden : nullptr);
 }
 
-template <int V, typename H>
+template <int G, typename H>
 __global__ void __launch_bounds__(256) layer_norm_kernel(int tokens, int hidden, const float *__restrict__ in,
                                                          const float *__restrict__ ln_w,
                                                          const float *__restrict__ ln_b, float eps, float *out_f32,
@@ -134,46 +170,101 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(int tokens, int hidden,
     if (t >= tokens) return;
     const int lane = threadIdx.x & 63;
     const float *row = in + (size_t)t * hidden;
-    float v[V];
+    float v[G][4];
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-        const int c = lane + 64 * i;
-        v[i] = c < hidden ? row[c] : 0.0f;
+    for (int g = 0; g < G; ++g) {
+        const int c = 4 * (lane + 64 * g);
+        if (c < hidden) load4(row + c, v[g]);
+        else
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[g][k] = 0.0f;
     }
-    ln_wave<V>(v, hidden, ln_w, ln_b, eps);
-    store_row<V, H>(v, hidden, out_f32 ? out_f32 + (size_t)t * hidden : nullptr,
+    ln_wave<G>(v, hidden, ln_w, ln_b, eps);
+    store_row<G, H>(v, hidden, out_f32 ? out_f32 + (size_t)t * hidden : nullptr,
                     out_h ? out_h + (size_t)t * hidden : nullptr);
 }
 
-template <typename H, int V>
+// The residual add and a LayerNorm in one pass (a wave a token): v = x + y,
+// then x = LN(v) (post-norm) or x = v (pre-norm), and out_h = LN(v). One
+// read of x and of the product, one write of x and of the operand copy.
+template <int G, typename Y, typename H>
+__global__ void __launch_bounds__(256) add_layer_norm_kernel(int tokens, int hidden, float *__restrict__ x,
+                                                             const Y *__restrict__ y, const float *__restrict__ ln_w,
+                                                             const float *__restrict__ ln_b, float eps, int pre_norm,
+                                                             H *__restrict__ out_h) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    const int lane = threadIdx.x & 63;
+    float *row = x + (size_t)t * hidden;
+    const Y *yr = y + (size_t)t * hidden;
+    float v[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int c = 4 * (lane + 64 * g);
+        if (c < hidden) {
+            float a[4];
+            load4(row + c, v[g]);
+            load4(yr + c, a);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[g][k] = v[g][k] + a[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[g][k] = 0.0f;
+        }
+    }
+    if (pre_norm) store_row<G, H>(v, hidden, row, nullptr);
+    ln_wave<G>(v, hidden, ln_w, ln_b, eps);
+    store_row<G, H>(v, hidden, pre_norm ? nullptr : row, out_h ? out_h + (size_t)t * hidden : nullptr);
+}
+
+template <typename H, int G, typename Y>
+static hipError_t add_ln_v(hipStream_t s, int tokens, int hidden, float *x, const void *y, const float *ln_w,
+                           const float *ln_b, float eps, int pre_norm, void *out_h) {
+    hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, x,
+                       (const Y *)y, ln_w, ln_b, eps, pre_norm, (H *)out_h);
+    return hipGetLastError();
+}
+
+template <typename H, int G>
+static hipError_t add_ln_y(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
+                           const float *ln_b, float eps, int pre_norm, void *out_h) {
+    switch (ydt) {
+    case Dt::F16: return add_ln_v<H, G, _Float16>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h);
+    case Dt::BF16: return add_ln_v<H, G, __bf16>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h);
+    case Dt::F32: return add_ln_v<H, G, float>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <typename H, int G>
 static hipError_t embed_ln_v(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                              const Packing &p, int seq, int offset, const float *word, const float *pos,
                              const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh) {
-    hipLaunchKernelGGL((embed_ln_kernel<V, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, ids, types, p,
+    hipLaunchKernelGGL((embed_ln_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, ids, types, p,
                        seq, offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh);
     return hipGetLastError();
 }
 
-template <typename H, int V>
+template <typename H, int G>
 static hipError_t ln_v(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
                        float eps, float *out_f32, void *out_h) {
-    hipLaunchKernelGGL((layer_norm_kernel<V, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, in, ln_w,
+    hipLaunchKernelGGL((layer_norm_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, in, ln_w,
                        ln_b, eps, out_f32, (H *)out_h);
     return hipGetLastError();
 }
 
-// The lane count V = ceil(hidden / 64), up to hidden 2048.
+// The groups of 4 columns a lane holds, G = ceil(hidden / 256), up to
+// hidden 2048; hidden a multiple of 4 (the model's is of 8).
 #define ROWWISE_DISPATCH(FN, ...)                                                              \
     {                                                                                          \
-        const int v = (hidden + 63) / 64;                                                      \
-        if (v <= 1) return FN<H, 1>(__VA_ARGS__);                                              \
-        if (v <= 2) return FN<H, 2>(__VA_ARGS__);                                              \
-        if (v <= 4) return FN<H, 4>(__VA_ARGS__);                                              \
-        if (v <= 6) return FN<H, 6>(__VA_ARGS__);                                              \
-        if (v <= 8) return FN<H, 8>(__VA_ARGS__);                                              \
-        if (v <= 12) return FN<H, 12>(__VA_ARGS__);                                            \
-        if (v <= 16) return FN<H, 16>(__VA_ARGS__);                                            \
-        if (v <= 32) return FN<H, 32>(__VA_ARGS__);                                            \
+        if (hidden % 4 != 0) return hipErrorInvalidValue;                                      \
+        const int g = (hidden + 255) / 256;                                                    \
+        if (g <= 1) return FN<H, 1>(__VA_ARGS__);                                              \
+        if (g <= 2) return FN<H, 2>(__VA_ARGS__);                                              \
+        if (g <= 3) return FN<H, 3>(__VA_ARGS__);                                              \
+        if (g <= 4) return FN<H, 4>(__VA_ARGS__);                                              \
+        if (g <= 6) return FN<H, 6>(__VA_ARGS__);                                              \
+        if (g <= 8) return FN<H, 8>(__VA_ARGS__);                                              \
         return hipErrorInvalidValue;                                                           \
     }
 
@@ -190,6 +281,12 @@ static hipError_t ln_t(hipStream_t s, int tokens, int hidden, const float *in, c
     ROWWISE_DISPATCH(ln_v, s, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h)
 }
 
+template <typename H>
+static hipError_t add_ln_t(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
+                           const float *ln_b, float eps, int pre_norm, void *out_h) {
+    ROWWISE_DISPATCH(add_ln_y, s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h)
+}
+
 hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                     const Packing &p, int seq, int position_offset, const float *word, const float *pos,
                     const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt) {
@@ -204,6 +301,16 @@ hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, c
     default:
         return embed_ln_t<float>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w, ln_b,
                                  eps, x, xh);
+    }
+}
+
+hipError_t add_layer_norm(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
+                          const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt) {
+    if (tokens <= 0) return hipSuccess;
+    switch (dt) {
+    case Dt::F16: return add_ln_t<_Float16>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h);
+    case Dt::BF16: return add_ln_t<__bf16>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h);
+    default: return add_ln_t<float>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h);
     }
 }
 

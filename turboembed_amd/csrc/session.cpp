@@ -521,6 +521,13 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     check(hipMemset(s->qkv, 0, 3 * s->tcap * H * el + 256), "session qkv");
     s->ctxb = alloc(s->tcap * H * el, "session context");
     s->ffn = alloc(s->tcap * I * el, "session ffn");
+    // The out and FFN-out products go to y and are added to x by the
+    // LayerNorm that follows: in F16 on F16 post-norm sessions (the
+    // reference's CUDA backend adds an F16 product, core/cuda/kernels.cu:466-509),
+    // in F32 on the other tiers and on the rotary families (the reference's
+    // ModernBERT needs the F32 product, core/cuda/backend.cpp:2319-2324).
+    s->ydt = s->act == Dt::F16 && !m->rotary ? Dt::F16 : Dt::F32;
+    s->y = alloc(s->tcap * H * dt_bytes(s->ydt), "session products");
     if (dt == Dt::I8) {
         s->aq = static_cast<int8_t *>(alloc(s->tcap * std::max(H, I), "session int8 operand"));
         s->ascale = static_cast<float *>(alloc(s->tcap * 4, "session int8 scales"));
@@ -725,15 +732,17 @@ static LayerGemm layer_gemm(Session &s, uint32_t l, GemmSlot g) {
         break;
     case G_OUT:
     case G_FFN2:
+        // The residual's product alone: the add + LayerNorm after it adds it to x.
         r.N = H;
         r.K = g == G_OUT ? H : I;
         r.A = g == G_OUT ? s.ctxb : s.ffn;
         r.W = g == G_OUT ? W.out : W.ffn_out;
         r.wscale = g == G_OUT ? W.s_out : W.s_ffn_out;
-        r.e.kind = Epi::Residual;
+        r.e.kind = Epi::Bias;
         r.e.bias = g == G_OUT ? L.bo : L.b2;
-        r.e.x = s.x;
+        r.e.out = s.y;
         r.e.ldo = H;
+        r.e.out_f32 = s.ydt == Dt::F32 ? 1 : 0;
         break;
     default:
         r.N = (int)L.n_in;
@@ -786,6 +795,12 @@ void encode(Session &s) {
     LAUNCH("pack_rows", pack_rows(st, s.mask, (int)s.batch, (int)s.seq, s.pk));
     LAUNCH("embed_ln", embed_ln(st, T, H, s.ids, s.types, s.pk, (int)s.seq, (int)m.position_offset, m.word, m.pos,
                                 m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
+    // ModernBERT's first layer reads the embeddings' rows as they are (no
+    // attention norm); on the F32 tier xh is the pre-norm rows' F32 copy.
+    if (m.modern && f32) check(hipMemcpyAsync(s.xh, s.x, (size_t)T * H * 4, hipMemcpyDeviceToDevice, st), "pre-norm rows");
+    // The GEMM operand copy of x after an add + LayerNorm: xh, or on the F32
+    // tier x itself (post-norm) or xh as F32 (pre-norm).
+    void *norm_out = f32 && !m.modern ? nullptr : s.xh;
     for (uint32_t l = 0; l < m.layers; ++l) {
         const Model::Layer &L = m.ls[l];
         int window = INT32_MAX;
@@ -793,31 +808,27 @@ void encode(Session &s) {
             const bool global = m.global_every == 0 || l % m.global_every == 0;
             if (!global) window = (int)m.window;
         }
-        if (m.modern) {
-            // Pre-norm: xn = LN(x) into xh (F32 on the F32 tier), x kept; the
-            // first layer's attention reads the embeddings' rows as they are.
-            if (l > 0)
-                LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln1_w, nullptr, m.eps, f32 ? (float *)s.xh : nullptr,
-                                                f32 ? nullptr : s.xh, dt));
-            else if (f32)
-                check(hipMemcpyAsync(s.xh, s.x, (size_t)T * H * 4, hipMemcpyDeviceToDevice, st), "pre-norm rows");
-        }
         mm(l, G_QKV);
         LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, (int)s.seq, (int)s.batch,
                                       (int)s.max_len, window, s.ctxb, bc.simple_attention));
         mm(l, G_OUT);
-        if (m.modern) {
-            LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln2_w, nullptr, m.eps, f32 ? (float *)s.xh : nullptr,
-                                            f32 ? nullptr : s.xh, dt));
-        } else {
-            LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln1_w, L.ln1_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
-        }
+        // Post-norm: x = LN1(x + y). Pre-norm: x += y, xh = LN_mlp(x).
+        if (m.modern)
+            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt));
+        else
+            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out, dt));
         mm(l, G_FFN1);
         mm(l, G_FFN2);
+        // Post-norm: x = LN2(x + y). Pre-norm: x += y and the next layer's
+        // attention norm into xh, or after the last layer x = LN_final(x + y).
         if (!m.modern)
-            LAUNCH("layer_norm", layer_norm(st, T, H, s.x, L.ln2_w, L.ln2_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
+            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out, dt));
+        else if (l + 1 < m.layers)
+            LAUNCH("add_layer_norm",
+                   add_layer_norm(st, T, H, s.x, s.y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps, 1, norm_out, dt));
+        else
+            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
     }
-    if (m.modern) LAUNCH("layer_norm", layer_norm(st, T, H, s.x, m.final_w, nullptr, m.eps, s.x, nullptr, dt));
     const int n_out = s.count ? (int)s.count : (int)s.batch;
     LAUNCH("pool", pool(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.count ? s.ranges : nullptr, (int)s.pooling,
                         (int)s.output_dim, s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0, s.out));

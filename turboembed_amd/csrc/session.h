@@ -132,6 +132,8 @@ struct Session {
     void *qkv = nullptr;     // [3][heads][tcap][d] (dt)
     void *ctxb = nullptr;    // [tcap, H] (dt)
     void *ffn = nullptr;     // [tcap, I] (dt)
+    void *y = nullptr;       // [tcap, H] a residual product, in ydt, for the add + LayerNorm after it
+    Dt ydt = Dt::F32;        // F16 for post-norm 16-bit sessions, else F32
     int8_t *aq = nullptr;    // I8: a GEMM's quantized operand [tcap, max(H, I)]
     float *ascale = nullptr; // I8: its per-token scales [tcap]
     float *out = nullptr;    // [max(max_batch, max_ranges), H] F32
