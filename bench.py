@@ -100,7 +100,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="bert-base", choices=sorted(W.SHAPES))
     ap.add_argument("--lengths", default="default", help="'default', 'full', or lo,hi")
-    ap.add_argument("--cpu-rows", type=int, default=4, help="rows of the CPU baseline's sample")
+    ap.add_argument("--cpu-rows", type=int, default=0,
+                    help="rows of the CPU baseline's sample (0: 4 rows, 1 on rows over 1024 tokens)")
+    ap.add_argument("--also-lengths", default="auto",
+                    help="lo,hi: also time the same session on rows of lengths uniform in [lo, hi] under the mask "
+                         "('auto': 64,512 for bert-base, none otherwise)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--autotune", default="on", choices=["off", "on"],
                     help="the session's kernel choices: measured at session creation (on, the default) or the rule's")
@@ -133,9 +137,16 @@ def main():
     ctx = rt.context(0)
     model = ctx.load(desc)
     mode = S.TURBO_AUTOTUNE_ON if args.autotune == "on" else S.TURBO_AUTOTUNE_OFF
-    sess = model.session(shape.batch, shape.seq, shape.precision, autotune=mode, budget_ms=args.budget_ms)
+    # A range workload embeds once and mean-pools contiguous ranges of each
+    # row's tokens (embed_write_ranges); the others pool each row.
+    rngs = W.ranges(shape, mask) if shape.ranges_per_row else None
+    sess = model.session(shape.batch, shape.seq, shape.precision, autotune=mode, budget_ms=args.budget_ms,
+                         max_ranges=len(rngs) if rngs else 0)
     dtype = {S.TURBO_DTYPE_F16: "f16", S.TURBO_DTYPE_BF16: "bf16", S.TURBO_DTYPE_F32: "f32"}[sess.compute_dtype]
-    sess.write_tokens(ids, mask, types, pooling=shape.pooling, normalize=shape.normalize)
+    if rngs:
+        sess.write_ranges(ids, mask, rngs, types, normalize=shape.normalize)
+    else:
+        sess.write_tokens(ids, mask, types, pooling=shape.pooling, normalize=shape.normalize)
     sess.run()
     gpu_vecs = sess.read()
     print(f"# loaded, first run done in {time.time() - t0:.1f}s; choices {sess.choices()}", file=sys.stderr,
@@ -180,21 +191,52 @@ def main():
                 "launches_per_step": dom_launches, "avg_launch_us": dom_ms / dom_launches * 1e3,
                 "flops_per_launch": dom_flops / dom_launches}
 
+    # The same session on variable-length rows under the mask (the second
+    # run of the workload), timed the same way.
+    extra_runs = {}
+    also = ("64,512" if args.workload == "bert-base" else "") if args.also_lengths == "auto" else args.also_lengths
+    if also and not rngs:
+        lo, hi = (int(v) for v in also.split(","))
+        vids, vmask, vtypes = W.rows(shape, lengths=(lo, hi), seed=1)
+        sess.write_tokens(vids, vmask, vtypes, pooling=shape.pooling, normalize=shape.normalize)
+        sess.replay(args.warmup)
+        v0 = time.perf_counter()
+        sess.replay(args.steps)
+        vms = (time.perf_counter() - v0) / args.steps * 1e3
+        vt = int(vmask.sum())
+        vflops = W.gemm_flops_per_token(shape) * vt + W.attention_flops(shape, vmask.sum(1))
+        extra_runs[f"lengths_{lo}_{hi}"] = {"ms_per_step": vms, "sequences_per_s": shape.batch / (vms / 1e3),
+                                            "tokens_per_s": vt / (vms / 1e3), "live_tokens": vt,
+                                            "mfma_util_pct": 100.0 * vflops / (vms / 1e3) / PEAK[dtype]}
+
     cpu = None
     min_cos = None
     if not args.no_cpu:
         import oracle
-        n = min(args.cpu_rows, shape.batch)
+        # A bounded sample (about 10-30 s of CPU work): 4 rows, or on rows
+        # over 1024 tokens the batch's shortest row; its ranges with it.
+        n = args.cpu_rows or (1 if shape.seq > 1024 else 4)
+        n = min(n, shape.batch)
+        pick = np.argsort(lens, kind="stable")[:n] if shape.seq > 1024 else np.arange(n)
         threads = min(16, os.cpu_count() or 1)
+        print(f"# timed; CPU baseline on rows {pick.tolist()} ({int(lens[pick].sum())} tokens) on {threads} threads",
+              file=sys.stderr, flush=True)
+        sample_ranges, got_idx = None, pick
+        if rngs:
+            where = {int(r): i for i, r in enumerate(pick)}
+            got_idx = [k for k, r in enumerate(rngs) if r[0] in where]
+            sample_ranges = [(where[rngs[k][0]], rngs[k][1], rngs[k][2]) for k in got_idx]
         c0 = time.perf_counter()
-        want = oracle.encode(desc, ids[:n], mask[:n], types[:n], pooling=shape.pooling, normalize=shape.normalize,
-                             threads=threads)
+        want = oracle.encode(desc, ids[pick], mask[pick], types[pick], pooling=shape.pooling,
+                             normalize=shape.normalize, ranges=sample_ranges, threads=threads)
         cpu_s = time.perf_counter() - c0
-        cos = (gpu_vecs[:n] * want).sum(1) / np.linalg.norm(gpu_vecs[:n], axis=1) / np.linalg.norm(want, axis=1)
+        got = gpu_vecs[got_idx]
+        cos = (got * want).sum(1) / np.linalg.norm(got, axis=1) / np.linalg.norm(want, axis=1)
         min_cos = float(cos.min())
+        what = f", {len(sample_ranges)} ranges" if sample_ranges else ""
         cpu = {"value": n / cpu_s, "unit": "sequences/s", "cores": threads, "kind": "port",
-               "sample": f"{n} of the {shape.batch} rows ({int(lens[:n].sum())} tokens), all {shape.layers} layers, "
-                         f"one pass, {cpu_s:.1f} s on {threads} threads"}
+               "sample": f"{n} of the {shape.batch} rows ({int(lens[pick].sum())} tokens{what}), all {shape.layers} "
+                         f"layers, one pass, {cpu_s:.1f} s on {threads} threads"}
 
     line = {
         "metric": f"sequences/s ({args.workload}, {dtype}, {shape.batch}x{shape.seq})",
@@ -211,6 +253,8 @@ def main():
         "min_cosine_vs_cpu": min_cos,
         "kernel_ms": {k: round(v, 4) for k, v in times.items()},
         "kernel_choices": sess.choices(),
+        "other_runs": extra_runs,
+        "ranges": len(rngs) if rngs else 0,
         "tune_ms": sess.tuning.tune_ms,
         "roofline": roofline,
         "cpu_baseline": cpu,
