@@ -461,3 +461,35 @@ def test_a_bad_choices_string_is_refused(context, monkeypatch):
             model.session(4, 64, S.TURBO_PRECISION_FASTEST)
         assert e.value.code == S.TURBO_E_INVALID_ARGUMENT and "TURBO_ROCM_CHOICES" in e.value.message
     model.close()
+
+
+# ---- Runs replayed from HIP graphs --------------------------------------------------------
+#
+# A run's launches are captured once per run shape and replayed: every
+# replay, with the host's own work (the rows' writes and the reads' syncs)
+# between them, gives the eager launches' vectors bit for bit, for two
+# shapes alternating in one session.
+
+@pytest.mark.parametrize("family", ["bert", "modernbert"])
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+def test_graph_replays_are_the_eager_runs(context, family, precision, monkeypatch):
+    desc = MODELS[family](seed=41)
+    a = small.ragged_rows(41, 5, 48, desc.vocab_size)
+    b = small.ragged_rows(42, 7, 30, desc.vocab_size)
+    if family == "modernbert":
+        a, b = (a[0], a[1], None), (b[0], b[1], None)
+    model = context.load(desc)
+    monkeypatch.setenv("TURBO_ROCM_GRAPHS", "0")
+    eager = model.session(8, 64, precision)
+    want_a, want_b = eager.embed(*a), eager.embed(*b)
+    eager.close()
+    monkeypatch.delenv("TURBO_ROCM_GRAPHS")
+    s = model.session(8, 64, precision)
+    for _ in range(3):
+        assert np.array_equal(s.embed(*a), want_a)
+        assert np.array_equal(s.embed(*b), want_b)
+    # A replay of resident rows, then a read: the same vectors again.
+    s.replay(2)
+    assert np.array_equal(s.read(), want_b)
+    s.close()
+    model.close()

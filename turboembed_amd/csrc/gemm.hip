@@ -695,19 +695,21 @@ static int cu_count() {
     return n;
 }
 
-// The pipelined block shape for a large product: 256 x 256 or 256 x 192
-// output tiles, whichever leaves the compute units the least idle over the
-// launch's rounds of tiles (time ~ rounds x tile area; the wider tile reads
-// its operands a little more efficiently, so it wins ties). Q, K and V must
-// each start on a wave's column boundary (64 or 96 columns).
-static int wide_tile(int M, int N, const EpiArgs &e) {
+// The pipelined block shape for a large product: 256 x 256 output tiles,
+// or 256 x 192 on a long inner dimension when they leave the compute units
+// less idle over the launch's rounds of tiles (time ~ rounds x tile area).
+// Measured on MI355X at 32768 tokens: 256 x 192 is faster at N = 768,
+// K = 3072 (whole rounds against one and a half), slower at K = 768, where
+// its 96-column waves' operand reads and epilogue cost more than the rounds
+// save. Q, K and V must each start on a wave's column boundary (64 or 96).
+static int wide_tile(int M, int N, int K, const EpiArgs &e) {
     const bool qkv = e.kind == Epi::Qkv || e.kind == Epi::QkvRope;
     const long cus = cu_count();
     auto cost = [&](int bm, int bn) {
         const long tiles = (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
         return (double)((tiles + cus - 1) / cus) * bm * bn;
     };
-    const bool can192 = !qkv || e.hidden % 96 == 0;
+    const bool can192 = (!qkv || e.hidden % 96 == 0) && K >= 2048;
     if (can192 && cost(256, 192) * 1.03 < cost(256, 256)) return 13;
     return 7;
 }
@@ -719,7 +721,7 @@ template <typename T, int BK>
 static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
                          int tile) {
     const bool pipelined = sizeof(T) == 2 && K % 64 == 0 && lda % 8 == 0;
-    if (tile == 0) tile = pipelined ? (M >= 2048 ? wide_tile(M, N, e) : 5) : 1;
+    if (tile == 0) tile = pipelined ? (M >= 2048 ? wide_tile(M, N, K, e) : 5) : 1;
     // A pipelined shape asked of an operand it cannot take runs the staged kernel.
     if (tile >= 4 && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
     // 96-column wave tiles need Q, K and V to start on their boundaries.

@@ -490,6 +490,7 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     for (int b = 0; b < kc.bins; ++b)
         if (!mfma_attn) kc.bin[b].simple_attention = true;
     const bool measure = ((mode == TURBO_AUTOTUNE_ON && !cached) || mode == TURBO_AUTOTUNE_RETUNE) && !all_forced(kc);
+    if (const char *g = std::getenv("TURBO_ROCM_GRAPHS")) s->graphs = std::strcmp(g, "0") != 0;
 
     const size_t H = m->hidden, I = m->inter, B = s->max_batch, S = s->max_seq;
     s->tcap = B * S;
@@ -585,6 +586,7 @@ void session_release(Session *s) {
         OnDevice on(s->ctx->ordinal);
         (void)hipStreamSynchronize(s->ctx->stream);
         if (s->staging) (void)hipHostFree(s->staging);
+        for (auto &g : s->graph_of) (void)hipGraphExecDestroy(g.second);
         for (hipEvent_t e : s->ev) (void)hipEventDestroy(e);
         s->owned.clear();
     }
@@ -797,7 +799,7 @@ void encode(Session &s) {
                                 m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
     // ModernBERT's first layer reads the embeddings' rows as they are (no
     // attention norm); on the F32 tier xh is the pre-norm rows' F32 copy.
-    if (m.modern && f32) check(hipMemcpyAsync(s.xh, s.x, (size_t)T * H * 4, hipMemcpyDeviceToDevice, st), "pre-norm rows");
+    if (m.modern && f32) LAUNCH("copy", copy_bytes(st, s.x, s.xh, (size_t)T * H * 4));
     // The GEMM operand copy of x after an add + LayerNorm: xh, or on the F32
     // tier x itself (post-norm) or xh as F32 (pre-norm).
     void *norm_out = f32 && !m.modern ? nullptr : s.xh;
@@ -833,6 +835,41 @@ void encode(Session &s) {
     LAUNCH("pool", pool(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.count ? s.ranges : nullptr, (int)s.pooling,
                         (int)s.output_dim, s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0, s.out));
 #undef LAUNCH
+}
+
+void launch_run(Session &s) {
+    if (s.timing || !s.graphs) {
+        encode(s);
+        return;
+    }
+    const Session::RunShape key{s.tokens, s.batch, s.seq, s.max_len, s.count, s.pooling, s.normalize, s.output_dim};
+    auto it = s.graph_of.find(key);
+    if (it == s.graph_of.end()) {
+        constexpr size_t KEEP = 16;
+        if (s.graph_of.size() >= KEEP) {
+            (void)hipGraphExecDestroy(s.graph_of[s.graph_order.front()]);
+            s.graph_of.erase(s.graph_order.front());
+            s.graph_order.erase(s.graph_order.begin());
+        }
+        hipStream_t st = s.ctx->stream;
+        check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capturing the run");
+        hipGraph_t g = nullptr;
+        try {
+            encode(s);
+        } catch (...) {
+            (void)hipStreamEndCapture(st, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        check(hipStreamEndCapture(st, &g), "capturing the run");
+        hipGraphExec_t exec = nullptr;
+        const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        check(e, "instantiating the run's graph");
+        it = s.graph_of.emplace(key, exec).first;
+        s.graph_order.push_back(key);
+    }
+    check(hipGraphLaunch(it->second, s.ctx->stream), "launching the run's graph");
 }
 
 // The tuner: each bin's four products timed at the bin's token count with
@@ -960,7 +997,7 @@ void session_run(Session *s, turbo_backend_run *out) {
         std::lock_guard<std::mutex> g(s->ctx->lock);
         OnDevice on(s->ctx->ordinal);
         try {
-            encode(*s);
+            launch_run(*s);
         } catch (...) {
             (void)hipStreamSynchronize(s->ctx->stream);
             throw;
@@ -1056,7 +1093,7 @@ int32_t turbo_rocm_session_replay(void *session, uint32_t runs, turbo_error *err
         if (s->tokens == 0) fail(TURBO_E_INVALID_STATE, "rocm: the session has no rows written");
         std::lock_guard<std::mutex> g(s->ctx->lock);
         OnDevice on(s->ctx->ordinal);
-        for (uint32_t i = 0; i < runs; ++i) encode(*s);
+        for (uint32_t i = 0; i < runs; ++i) launch_run(*s);
         check(hipStreamSynchronize(s->ctx->stream), "replay");
         collect_times(*s);
         return TURBO_OK;

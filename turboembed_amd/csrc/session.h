@@ -3,7 +3,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -148,6 +150,21 @@ struct Session {
     std::vector<LayerWeights> *w = nullptr;
     Choices kc;            // kernel choices per bin of packed tokens
     std::string choices;   // kc as a choices string
+    // A run's launches captured as a graph, per run shape (tokens, rows,
+    // columns, longest row, ranges, pooling, normalize, output width): a run
+    // of a shape seen before is one graph launch. Off while timing, or with
+    // TURBO_ROCM_GRAPHS=0.
+    struct RunShape {
+        uint32_t tokens, batch, seq, max_len, count, pooling, normalize, output_dim;
+        bool operator<(const RunShape &o) const {
+            const uint32_t a[8] = {tokens, batch, seq, max_len, count, pooling, normalize, output_dim};
+            const uint32_t b[8] = {o.tokens, o.batch, o.seq, o.max_len, o.count, o.pooling, o.normalize, o.output_dim};
+            return std::lexicographical_compare(a, a + 8, b, b + 8);
+        }
+    };
+    bool graphs = true;
+    std::map<RunShape, hipGraphExec_t> graph_of;
+    std::vector<RunShape> graph_order;   // oldest first, for eviction
     // Per-launch timing (a test and benchmark hook): events around each
     // kernel of a run, by name.
     bool timing = false;
@@ -166,5 +183,8 @@ void session_run(Session *s, turbo_backend_run *out);
 // Times the session's candidate kernels within budget_ms and keeps the
 // fastest in s.kc; timing lines into *timings. Whether anything was timed.
 bool tune(Session &s, uint32_t budget_ms, std::string *timings);
+// One run's launches on the session's stream: replayed from its graph when
+// the shape was captured before, else captured (or launched directly).
+void launch_run(Session &s);
 
 }  // namespace rocm
