@@ -42,6 +42,8 @@ def lib():
             getattr(_lib, f).restype = C.c_float
             getattr(_lib, f).argtypes = [C.c_float]
         _lib.oracle_layer_norm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_float]
+        _lib.oracle_quantize.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
+        _lib.oracle_quantize.restype = None
     return _lib
 
 
@@ -87,6 +89,20 @@ def encode(desc: ModelDesc, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN,
     if hidden:
         _, ln, _ = pack(mask, ranges)
         return out, hid[: int(ln.sum())]
+    return out
+
+
+def quantize(x, mode, ranges=None):
+    """Codes of the rows of x (F32, [rows, dim]): mode 2 int8 with ranges
+    [2, dim], mode 3 ubinary; as the reference core makes them
+    (core/src/quantize.rs:48-80)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, dim = x.shape
+    width = dim if mode == 2 else (dim + 7) // 8
+    out = np.zeros((rows, width), np.uint8)
+    rr = None if ranges is None else np.ascontiguousarray(ranges, np.float32)
+    lib().oracle_quantize(C.c_void_p(x.ctypes.data), rows, dim, mode, None if rr is None else C.c_void_p(rr.ctypes.data),
+                          C.c_void_p(out.ctypes.data))
     return out
 
 

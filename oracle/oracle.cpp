@@ -743,4 +743,31 @@ float oracle_gelu(float x) { return gelu_erf(x); }
 float oracle_silu(float x) { return silu(x); }
 void oracle_layer_norm(float *y, const float *w, const float *b, uint32_t n, float eps) { layer_norm(y, w, b, n, eps); }
 
+// int8: step = (max - min) / 255 in F32, 1 where that is 0; the code is
+// clamp(floor((x - min) / step), 0, 255) - 128, a NaN in the bottom bucket
+// (core/src/quantize.rs:60-70). ubinary: bit x > 0, eight to a byte, the first
+// value in the top bit, a last byte padded with 0 bits (:72-83).
+void oracle_quantize(const float *x, uint32_t rows, uint32_t dim, uint32_t mode, const float *ranges, uint8_t *out) {
+    if (mode == 2) {
+        for (uint32_t r = 0; r < rows; ++r)
+            for (uint32_t d = 0; d < dim; ++d) {
+                const float lo = ranges[d], hi = ranges[dim + d];
+                float step = (hi - lo) / 255.0f;
+                if (step == 0.0f) step = 1.0f;
+                float q = std::floor((x[(size_t)r * dim + d] - lo) / step);
+                q = q != q ? 0.0f : q < 0.0f ? 0.0f : q > 255.0f ? 255.0f : q;
+                out[(size_t)r * dim + d] = (uint8_t)(int8_t)((int)q - 128);
+            }
+    } else {
+        const uint32_t per = (dim + 7) / 8;
+        for (uint32_t r = 0; r < rows; ++r)
+            for (uint32_t b = 0; b < per; ++b) {
+                uint32_t byte = 0;
+                for (uint32_t k = 0; k < 8 && 8 * b + k < dim; ++k)
+                    if (x[(size_t)r * dim + 8 * b + k] > 0.0f) byte |= 0x80u >> k;
+                out[(size_t)r * per + b] = (uint8_t)byte;
+            }
+    }
+}
+
 }  // extern "C"

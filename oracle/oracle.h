@@ -34,6 +34,10 @@ uint32_t oracle_pack(const int32_t *mask, uint32_t batch, uint32_t seq, uint32_t
                      uint32_t *start, uint32_t *len, uint32_t *at);
 
 /* The scalar functions the encoder uses, for their own tests. */
+// Vector codes as the reference core makes them on the host
+// (core/src/quantize.rs:48-80): mode 2 int8 with ranges [2][dim], mode 3
+// ubinary. out holds rows * dim or rows * ((dim + 7) / 8) bytes.
+void  oracle_quantize(const float *x, uint32_t rows, uint32_t dim, uint32_t mode, const float *ranges, uint8_t *out);
 float oracle_exp(float x);
 float oracle_gelu(float x);
 float oracle_silu(float x);

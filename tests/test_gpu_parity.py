@@ -493,3 +493,51 @@ def test_graph_replays_are_the_eager_runs(context, family, precision, monkeypatc
     assert np.array_equal(s.read(), want_b)
     s.close()
     model.close()
+
+
+# ---- Vector codes on the device (buffer_quantize) --------------------------------------------
+#
+# Byte-exact against the reference's golden codes (testdata/quantize, copied
+# as data) and against the oracle's codes of the session's own vectors.
+
+def test_buffer_quantize_makes_the_golden_codes(context):
+    import test_quantize as TQ
+    for x, r, i8, ub in TQ.golden_rows():
+        dim = x.shape[1]
+        for mode, want in ((S.TURBO_QUANTIZE_INT8, i8), (S.TURBO_QUANTIZE_UBINARY, ub)):
+            buf = context.buffer(4 * dim, S.TURBO_PLACE_SHARED)
+            buf.view(np.float32)[:] = x[0]
+            buf.quantize(mode, 1, dim, r.reshape(2, dim) if mode == S.TURBO_QUANTIZE_INT8 else None)
+            assert buf.read(len(want)).tobytes() == want
+            buf.close()
+
+
+@pytest.mark.parametrize("mode", [S.TURBO_QUANTIZE_INT8, S.TURBO_QUANTIZE_UBINARY])
+def test_a_session_s_codes_are_the_oracle_s(context, mode):
+    desc = small.bert(seed=51, hidden=96, heads=3, inter=192)
+    ids, mask, types = small.ragged_rows(51, 6, 40, desc.vocab_size)
+    model = context.load(desc)
+    s = model.session(8, 64, S.TURBO_PRECISION_FASTEST)
+    vecs = s.embed(ids, mask, types, output_dim=77)
+    g = np.random.Generator(np.random.PCG64(51))
+    lo = (g.standard_normal(77) * 0.05 - 0.1).astype(np.float32)
+    ranges = np.stack([lo, lo + np.abs(g.standard_normal(77)).astype(np.float32) * 0.2]).astype(np.float32)
+    ranges[:, 5] = 0.03   # a dimension whose step is 0
+    codes = s.read_quantized(mode, ranges)
+    want = oracle.quantize(vecs, mode, ranges)
+    assert np.array_equal(codes.view(np.uint8), want)
+    if mode == S.TURBO_QUANTIZE_INT8:
+        assert s.run_info.device_allocs == 2 and s.run_info.h2d_bytes >= 2 * 77 * 4
+    s.close()
+    model.close()
+
+
+def test_buffer_quantize_refuses_what_it_cannot_do(context):
+    buf = context.buffer(64, S.TURBO_PLACE_SHARED)
+    for mode, rows, dim, ranges in ((S.TURBO_QUANTIZE_NONE, 1, 4, None), (S.TURBO_QUANTIZE_INT8, 1, 4, None),
+                                    (S.TURBO_QUANTIZE_UBINARY, 5, 4, None),
+                                    (S.TURBO_QUANTIZE_INT8, 1, 2, np.array([[1.0, 0.0], [0.0, 1.0]], np.float32))):
+        with pytest.raises(T.TurboError) as e:
+            buf.quantize(mode, rows, dim, ranges)
+        assert e.value.code == S.TURBO_E_INVALID_ARGUMENT
+    buf.close()

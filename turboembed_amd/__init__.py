@@ -128,9 +128,57 @@ class Context:
     def load(self, desc: ModelDesc):
         return Model(self, desc)
 
+    def buffer(self, nbytes, placement=S.TURBO_PLACE_SHARED):
+        """A buffer of the context's device (buffer_alloc): DEVICE, PINNED,
+        SHARED or HOST; the last three have a host pointer."""
+        return Buffer(self, nbytes, placement)
+
     def close(self):
         if self.h:
             self.t.context_release(self.h)
+            self.h = None
+
+
+class Buffer:
+    """A buffer the core allocates through the table (core/src/buffer_api.rs:83-211)."""
+
+    def __init__(self, ctx, nbytes, placement):
+        self.ctx, self.t, self.nbytes, self.placement = ctx, ctx.t, nbytes, placement
+        d = S.turbo_buffer_desc()
+        d.struct_size = C.sizeof(d)
+        d.placement, d.dtype, d.ndim, d.bytes = placement, S.TURBO_DTYPE_U8, 1, nbytes
+        d.shape[0] = nbytes
+        h, host = C.c_void_p(), C.c_void_p()
+        err = S.new_error()
+        _ok(self.t.buffer_alloc(ctx.h, C.byref(d), C.byref(h), C.byref(host), C.byref(err)), err)
+        self.h, self.host = h, host.value
+
+    def view(self, dtype=np.uint8):
+        """The host view of a buffer that has one."""
+        if not self.host:
+            raise TurboError(S.TURBO_E_UNSUPPORTED, 0, "a device buffer has no host view")
+        return np.ctypeslib.as_array((C.c_uint8 * self.nbytes).from_address(self.host)).view(dtype)
+
+    def read(self, nbytes=None):
+        out = np.empty(self.nbytes if nbytes is None else nbytes, np.uint8)
+        err = S.new_error()
+        _ok(self.t.buffer_read(self.h, out.ctypes.data, out.nbytes, C.byref(err)), err)
+        return out
+
+    def quantize(self, quantization, rows, dim, int8_ranges=None, run=None):
+        """buffer_quantize: the first rows x dim F32 values as codes, over
+        the buffer's leading bytes."""
+        rr = None
+        if int8_ranges is not None:
+            rr = np.ascontiguousarray(int8_ranges, np.float32)
+        err = S.new_error()
+        _ok(self.t.buffer_quantize(self.h, quantization,
+                                   None if rr is None else rr.ctypes.data_as(C.POINTER(C.c_float)), rows, dim,
+                                   None if run is None else C.byref(run), C.byref(err)), err)
+
+    def close(self):
+        if self.h:
+            self.t.buffer_release(self.h)
             self.h = None
 
 
@@ -276,6 +324,27 @@ class Session:
         err = S.new_error()
         _ok(self.t.buffer_read(self.run_info.output, v.ctypes.data, v.nbytes, C.byref(err)), err)
         return v
+
+    def read_quantized(self, quantization, int8_ranges=None):
+        """The last run's vectors as codes made on the device, as the core
+        reads a quantized write (core/src/session/result.rs:84-102):
+        buffer_quantize over the session's output, then buffer_read of the
+        codes alone. int8: [n, output_dim] int8 with ranges [2, output_dim];
+        ubinary: [n, ceil(output_dim / 8)] uint8. The output holds codes,
+        not vectors, afterwards."""
+        rr = None
+        if quantization == S.TURBO_QUANTIZE_INT8:
+            rr = np.ascontiguousarray(int8_ranges, np.float32)
+            if rr.shape != (2, self.od):
+                raise TurboError(S.TURBO_E_INVALID_ARGUMENT, 8, f"int8 ranges must be [2, {self.od}]")
+        err = S.new_error()
+        _ok(self.t.buffer_quantize(self.run_info.output, quantization,
+                                   None if rr is None else rr.ctypes.data_as(C.POINTER(C.c_float)), self.n_out,
+                                   self.od, C.byref(self.run_info), C.byref(err)), err)
+        width = self.od if quantization == S.TURBO_QUANTIZE_INT8 else (self.od + 7) // 8
+        v = np.empty((self.n_out, width), np.uint8)
+        _ok(self.t.buffer_read(self.run_info.output, v.ctypes.data, v.nbytes, C.byref(err)), err)
+        return v.view(np.int8) if quantization == S.TURBO_QUANTIZE_INT8 else v
 
     def embed(self, ids, mask, types=None, **kw):
         self.write_tokens(ids, mask, types, **kw)

@@ -238,8 +238,11 @@ int32_t buffer_alloc(void *ctx, const turbo_buffer_desc *desc, void **out, void 
             b->dev = b->host;
             break;
         case TURBO_PLACE_SHARED:
-            check(hipMallocManaged(&b->dev, b->bytes, hipMemAttachGlobal), "hipMallocManaged");
-            b->host = b->dev;
+            // One allocation both address: pinned, mapped host memory (the
+            // device reads and writes it over the bus). Managed memory is
+            // not host-addressable on a device without XNACK.
+            check(hipHostMalloc(&b->host, b->bytes ? b->bytes : 1, hipHostMallocDefault), "hipHostMalloc");
+            b->dev = b->host;
             break;
         case TURBO_PLACE_HOST:
             b->host = std::malloc(b->bytes ? b->bytes : 1);
@@ -284,8 +287,8 @@ void buffer_release(void *buf) {
     if (b->owned) {
         OnDevice on(b->ctx->ordinal);
         switch (b->placement) {
-        case TURBO_PLACE_DEVICE:
-        case TURBO_PLACE_SHARED: (void)hipFree(b->dev); break;
+        case TURBO_PLACE_DEVICE: (void)hipFree(b->dev); break;
+        case TURBO_PLACE_SHARED:
         case TURBO_PLACE_PINNED: (void)hipHostFree(b->host); break;
         case TURBO_PLACE_HOST: std::free(b->host); break;
         }
@@ -323,6 +326,60 @@ int32_t buffer_read(void *buf, void *dst, uint64_t bytes, turbo_error *err) {
         OnDevice on(b->ctx->ordinal);
         check(hipMemcpyAsync(dst, b->dev ? b->dev : b->host, bytes, hipMemcpyDefault, b->ctx->stream), "buffer_read");
         check(hipStreamSynchronize(b->ctx->stream), "buffer_read");
+        return TURBO_OK;
+    });
+}
+
+// On-device vector codes (turbo_backend.h:610-626): the first rows x dim F32
+// values of a device buffer as int8 or ubinary codes, written over the
+// buffer's leading bytes. The codes go to a temporary device buffer first,
+// so the write never races the read; the int8 ranges are sent to the device.
+// Both allocations and the ranges' bytes are added to the run's counts.
+int32_t buffer_quantize(void *buf, uint32_t quantization, const float *int8_ranges, uint32_t rows, uint32_t dim,
+                        turbo_backend_run *run, turbo_error *err) {
+    return guarded(err, [&] {
+        Buffer *b = static_cast<Buffer *>(buf);
+        if (quantization != TURBO_QUANTIZE_INT8 && quantization != TURBO_QUANTIZE_UBINARY)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: quantization " + std::to_string(quantization) +
+                                               " is not int8 or ubinary");
+        if (!b->dev || (b->placement != TURBO_PLACE_DEVICE && b->placement != TURBO_PLACE_SHARED))
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: buffer_quantize needs a device or shared buffer");
+        const uint64_t floats = (uint64_t)rows * dim;
+        if (floats * 4 > b->bytes)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: " + std::to_string(rows) + " by " + std::to_string(dim) +
+                                               " values over the buffer's " + std::to_string(b->bytes) + " bytes");
+        if (rows == 0 || dim == 0) return TURBO_OK;
+        if (rows > (uint32_t)INT32_MAX || dim > (uint32_t)INT32_MAX)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: rows and dim must fit in 31 bits");
+        const bool i8 = quantization == TURBO_QUANTIZE_INT8;
+        if (i8) {
+            if (!int8_ranges) fail(TURBO_E_INVALID_ARGUMENT, "rocm: int8 codes need the [2, dim] ranges");
+            for (uint32_t d = 0; d < dim; ++d)
+                if (!std::isfinite(int8_ranges[d]) || !std::isfinite(int8_ranges[dim + d]) ||
+                    int8_ranges[d] > int8_ranges[dim + d])
+                    fail(TURBO_E_INVALID_ARGUMENT, "rocm: int8 ranges of dimension " + std::to_string(d));
+        }
+        const uint64_t code_bytes = i8 ? floats : (uint64_t)rows * ((dim + 7) / 8);
+        std::lock_guard<std::mutex> g(b->ctx->lock);
+        OnDevice on(b->ctx->ordinal);
+        const uint64_t dev0 = device_allocs.load();
+        DevPtr codes(dev_alloc(code_bytes, "quantized codes"));
+        DevPtr ranges;
+        hipStream_t st = b->ctx->stream;
+        if (i8) {
+            ranges.reset(dev_alloc((size_t)2 * dim * 4, "int8 ranges"));
+            check(hipMemcpyAsync(ranges.get(), int8_ranges, (size_t)2 * dim * 4, hipMemcpyHostToDevice, st),
+                  "int8 ranges");
+        }
+        check(quantize_codes(st, static_cast<const float *>(b->dev), (int)rows, (int)dim, (int)quantization,
+                             static_cast<const float *>(ranges.get()), static_cast<uint8_t *>(codes.get())),
+              "buffer_quantize");
+        check(hipMemcpyAsync(b->dev, codes.get(), code_bytes, hipMemcpyDeviceToDevice, st), "buffer_quantize");
+        check(hipStreamSynchronize(st), "buffer_quantize");
+        if (run) {
+            run->device_allocs += device_allocs.load() - dev0;
+            if (i8) run->h2d_bytes += (uint64_t)2 * dim * 4;
+        }
         return TURBO_OK;
     });
 }
@@ -424,7 +481,7 @@ const turbo_backend turbo_rocm_backend = {
     embed_write_ranges_fn,
     0,
     0,
-    nullptr,
+    buffer_quantize,
 };
 
 }  // extern "C"

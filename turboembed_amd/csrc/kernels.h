@@ -113,6 +113,16 @@ hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, con
 hipError_t quantize_rows(hipStream_t s, const void *src, Dt src_dt, int rows, int cols, int ld, int8_t *dst,
                          float *scale);
 
+// Vector codes of rows x dim F32 values (reference core/src/quantize.rs:48-80,
+// sentence-transformers' quantize_embeddings layout): mode 2 (int8) with
+// ranges [2][dim] (minimums, then maximums) on the device, a byte a value,
+// clamp(floor((x - min) / step), 0, 255) - 128 with step = (max - min) / 255
+// or 1 where that is 0, every step in F32; mode 3 (ubinary) the sign bits
+// x > 0, eight to a byte, the first value in the top bit, a last byte padded
+// with 0 bits. Into out (rows * dim or rows * ((dim + 7) / 8) bytes).
+hipError_t quantize_codes(hipStream_t s, const float *x, int rows, int dim, int mode, const float *ranges,
+                          uint8_t *out);
+
 // dst = src over `bytes` (a multiple of 16), 16-byte vectors, one pass.
 hipError_t copy_bytes(hipStream_t s, const void *src, void *dst, size_t bytes);
 

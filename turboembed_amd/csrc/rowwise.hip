@@ -485,6 +485,55 @@ hipError_t fill_uniform(hipStream_t s, float *dst, size_t n, float amp, uint32_t
     return hipGetLastError();
 }
 
+// ---- Vector codes (int8 and ubinary) ----------------------------------------------------
+//
+// int8: a thread a value, IEEE F32 subtraction, division and floor as the
+// reference computes them on the host (core/src/quantize.rs:60-70); a NaN
+// lands in the bottom bucket there, and does here (fmaxf/fminf drop NaN).
+// ubinary: a thread an output byte, its eight values' signs.
+__global__ void __launch_bounds__(256) int8_codes_kernel(const float *__restrict__ x, int rows, int dim,
+                                                         const float *__restrict__ ranges, uint8_t *__restrict__ out) {
+    const size_t n = (size_t)rows * dim;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const int d = (int)(i % dim);
+        const float lo = ranges[d], hi = ranges[dim + d];
+        float step = __fdiv_rn(__fsub_rn(hi, lo), 255.0f);
+        if (step == 0.0f) step = 1.0f;
+        const float q = fminf(fmaxf(floorf(__fdiv_rn(__fsub_rn(x[i], lo), step)), 0.0f), 255.0f);
+        out[i] = (uint8_t)(int8_t)((int)q - 128);
+    }
+}
+
+__global__ void __launch_bounds__(256) ubinary_codes_kernel(const float *__restrict__ x, int rows, int dim,
+                                                            uint8_t *__restrict__ out) {
+    const int per = (dim + 7) / 8;
+    const size_t n = (size_t)rows * per;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const int r = (int)(i / per), b = (int)(i % per);
+        const float *row = x + (size_t)r * dim;
+        uint32_t byte = 0;
+        for (int k = 0; k < 8; ++k) {
+            const int d = 8 * b + k;
+            if (d < dim && row[d] > 0.0f) byte |= 0x80u >> k;
+        }
+        out[i] = (uint8_t)byte;
+    }
+}
+
+hipError_t quantize_codes(hipStream_t s, const float *x, int rows, int dim, int mode, const float *ranges,
+                          uint8_t *out) {
+    if (rows <= 0 || dim <= 0) return hipSuccess;
+    const size_t n = mode == 2 ? (size_t)rows * dim : (size_t)rows * ((dim + 7) / 8);
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
+    if (mode == 2)
+        hipLaunchKernelGGL(int8_codes_kernel, dim3(blocks), dim3(256), 0, s, x, rows, dim, ranges, out);
+    else if (mode == 3)
+        hipLaunchKernelGGL(ubinary_codes_kernel, dim3(blocks), dim3(256), 0, s, x, rows, dim, out);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 // ---- Plain copy (the traffic counters' reference) ---------------------------------------
 
 __global__ void __launch_bounds__(256) copy_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst, size_t n) {

@@ -41,6 +41,7 @@ TURBO_DTYPE_F32 = 12
 TURBO_PLACE_HOST = 1
 TURBO_PLACE_PINNED = 2
 TURBO_PLACE_DEVICE = 3
+TURBO_PLACE_SHARED = 4
 
 TURBO_STAGE_MAX = 16
 TURBO_STAGE_UNUSED, TURBO_STAGE_HOST, TURBO_STAGE_DEVICE, TURBO_STAGE_FUSED = 0, 1, 2, 3
@@ -55,6 +56,8 @@ TURBO_PRECISION_MODEL = 0
 TURBO_PRECISION_FASTEST = 1
 TURBO_PRECISION_EXACT = 2
 
+TURBO_QUANTIZE_MODEL = 0
+TURBO_QUANTIZE_NONE = 1
 TURBO_QUANTIZE_INT8 = 2
 TURBO_QUANTIZE_UBINARY = 3
 
