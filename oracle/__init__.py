@@ -68,14 +68,16 @@ def ranges_array(ranges):
 
 
 def encode(desc: ModelDesc, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN, normalize=S.TURBO_NORMALIZE_L2,
-           output_dim=None, ranges=None, threads=0, hidden=False):
+           output_dim=None, ranges=None, threads=0, hidden=False, head=False):
     """The oracle's vectors for the rows (and ranges); with hidden=True also
-    the final hidden states of the packed tokens."""
+    the final hidden states of the packed tokens. head=True on a range write
+    to a model with a span head: each range's row is the head's logits."""
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     mask = np.ascontiguousarray(mask, dtype=np.int32)
     types = None if types is None else np.ascontiguousarray(types, dtype=np.int32)
-    od = output_dim or desc.hidden
+    od = desc.span_head[0].shape[0] if head and desc.span_head is not None else output_dim or desc.hidden
     r = rows_struct(ids, mask, types, pooling, normalize, od)
+    r.head = 1 if head else 0
     ranges = list(ranges or [])
     rr = ranges_array(ranges)
     n_out = len(ranges) if ranges else ids.shape[0]
@@ -145,6 +147,40 @@ def fixture(name):
                      a["max_positions"], max(1, a["token_types"]), a["layer_norm_eps"], tensors,
                      names=[k or "absent" for k in info["order"]], **kw)
     return desc, t["case.ids"], t["case.lengths"], t["case.vectors"], info
+
+
+def qa_fixture():
+    """(ModelDesc, windows, logits, info) of tests/golden/tiny_qa: the tiny
+    BERT encoder with its span head, the reference's QA windows as
+    [(ids, types)], and the transformers logits [tokens, 2] (start, end) of
+    every window's tokens in order."""
+    from safetensors.numpy import load_file
+    t = load_file(os.path.join(GOLDEN, "tiny_qa.safetensors"))
+    info = json.load(open(os.path.join(GOLDEN, "tiny_qa.json")))
+    a = info["architecture"]
+    desc = ModelDesc(S.TURBO_FAMILY_BERT, a["layers"], a["hidden"], a["heads"], a["intermediate"],
+                     info["vocab_rows_kept"], a["max_positions"], a["token_types"], a["layer_norm_eps"],
+                     [t[k] for k in info["order"]], names=info["order"],
+                     span_head=(t["head.weight"], t["head.bias"]))
+    windows = [(t["case.ids"][i, :n].copy(), t["case.types"][i, :n].copy())
+               for i, n in enumerate(t["case.lengths"])]
+    return desc, windows, t["case.logits"], info
+
+
+def qa_logits(desc, windows, pad_id=0):
+    """The start and end logits [tokens, 2] of every window's tokens, in
+    order, restating core/src/qa/session.rs:196-290: the windows as rows
+    padded with pad_id (types 0, mask 0), each live token a range of its
+    own, through the span head."""
+    seq = max(len(w) for w, _ in windows)
+    ids = np.full((len(windows), seq), pad_id, np.int32)
+    types = np.zeros_like(ids)
+    mask = np.zeros_like(ids)
+    ranges = []
+    for r, (wi, wt) in enumerate(windows):
+        ids[r, :len(wi)], types[r, :len(wt)], mask[r, :len(wi)] = wi, wt, 1
+        ranges += [(r, i, i + 1) for i in range(len(wi))]
+    return encode(desc, ids, mask, types, normalize=S.TURBO_NORMALIZE_NONE, ranges=ranges, head=True)
 
 
 def fixture_rows(ids, lengths):

@@ -717,7 +717,34 @@ int32_t oracle_encode(const turbo_backend_model *d, const turbo_backend_embed_ro
         if (threads == 0) threads = std::max(1u, std::thread::hardware_concurrency());
         Model m;
         load(m, d);
-        encode(m, rows, ranges, count, threads, out, hidden);
+        if (!rows->head) {
+            encode(m, rows, ranges, count, threads, out, hidden);
+            say(why, why_len, "");
+            return TURBO_OK;
+        }
+        // A range write through the span head (turbo_backend.h:418-422):
+        // each range's mean over all hidden values, not normalized, then
+        // the head's rows summed in F64 from the bias and rounded to F32
+        // once (core/src/qa/session.rs:268-276).
+        if (!d->head || d->head_out == 0 || count == 0)
+            throw Failure(TURBO_E_INVALID_ARGUMENT, "oracle: a head write needs ranges and a model with a head");
+        const uint32_t H = d->hidden, O = d->head_out;
+        const turbo_backend_tensor &hw = d->head[0], &hb = d->head[1];
+        if (hw.bytes != (uint64_t)O * H * 4 || hb.bytes != (uint64_t)O * 4)
+            throw Failure(TURBO_E_INVALID_ARGUMENT, "oracle: the head is [head_out, hidden] and [head_out] F32");
+        turbo_backend_embed_rows plain = *rows;
+        plain.head = 0;
+        plain.output_dim = H;
+        plain.normalize = TURBO_NORMALIZE_NONE;
+        std::vector<float> v((size_t)count * H);
+        encode(m, &plain, ranges, count, threads, v.data(), hidden);
+        const float *w = static_cast<const float *>(hw.data), *b = static_cast<const float *>(hb.data);
+        for (uint32_t i = 0; i < count; ++i)
+            for (uint32_t o = 0; o < O; ++o) {
+                double acc = (double)b[o];
+                for (uint32_t c = 0; c < H; ++c) acc += (double)w[(size_t)o * H + c] * (double)v[(size_t)i * H + c];
+                out[(size_t)i * O + o] = (float)acc;
+            }
         say(why, why_len, "");
         return TURBO_OK;
     } catch (const Failure &f) {

@@ -20,6 +20,10 @@ extern "C" {
  * encoder `m` describes, into out: [batch, output_dim] or [count, output_dim]
  * F32. `hidden`, when not NULL, receives the final hidden states of the
  * packed tokens, [tokens, hidden] F32 (room for batch * seq rows).
+ * With rows->head 1 on a range write to a model with a span head (m->head,
+ * m->head_out), out is [count, head_out]: each range's mean over all hidden
+ * values, not normalized, through the head, its sums in F64 from the bias
+ * (reference core/src/qa/session.rs:268-276).
  * `threads` 0 is one per processor. Returns TURBO_OK or a status; `why`
  * (may be NULL) receives a message of up to why_len bytes. */
 int32_t oracle_encode(const turbo_backend_model *m, const turbo_backend_embed_rows *rows,

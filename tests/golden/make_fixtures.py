@@ -161,6 +161,59 @@ def rerank_fixture():
     print("tiny_rerank", len(used), "word rows")
 
 
+def qa_fixture():
+    """tiny_qa: testdata/tiny-qa-reference's transformers start and end
+    logits for every token of six QA windows over the tiny BERT encoder,
+    with its span head (head.safetensors: qa_outputs, [2, hidden] and [2]),
+    the encoder's weights (word rows reduced as above) and the windows'
+    ids, types and lengths as the reference holds them. Logits are [105, 2]:
+    the windows' live tokens in order, start then end."""
+    d = os.path.join(REF, "tiny-qa-reference")
+    ref = load_file(os.path.join(d, "reference.safetensors"))
+    head = load_file(os.path.join(d, "head.safetensors"))
+    cases = json.load(open(os.path.join(d, "cases.json")))
+    bundle = os.path.join(REF, "tiny-bert-bundle")
+    m = json.load(open(os.path.join(bundle, "manifest.json")))
+    arch = m["architecture"]
+    names = m["artifacts"][0]["tensor_names"]
+    weights = load_file(os.path.join(bundle, m["artifacts"][0]["files"][0]))
+    ids, lengths = ref["ids"], ref["lengths"]
+    used = sorted({0} | {int(v) for r, n in zip(ids, lengths) for v in r[:n]})
+    remap = {old: new for new, old in enumerate(used)}
+    new_ids = np.zeros_like(ids)
+    for i, (r, n) in enumerate(zip(ids, lengths)):
+        new_ids[i, :n] = [remap[int(v)] for v in r[:n]]
+    emb, per = bert_order(arch["layers"])
+    tensors, order = {}, []
+    for key in emb:
+        t = weights[names[key]]
+        if key == "word_embeddings":
+            t = t[used]
+        tensors[f"emb.{key}"] = np.ascontiguousarray(t)
+        order.append(f"emb.{key}")
+    for layer in range(arch["layers"]):
+        for key in per:
+            name = names[key].replace("{layer}", str(layer))
+            tensors[f"layer{layer}.{key}"] = np.ascontiguousarray(weights[name])
+            order.append(f"layer{layer}.{key}")
+    tensors["head.weight"] = np.ascontiguousarray(head["qa_outputs.weight"], np.float32)
+    tensors["head.bias"] = np.ascontiguousarray(head["qa_outputs.bias"], np.float32)
+    tensors["case.ids"] = new_ids.astype(np.int32)
+    tensors["case.types"] = ref["types"].astype(np.int32)
+    tensors["case.lengths"] = lengths.astype(np.int32)
+    tensors["case.logits"] = ref["logits"].astype(np.float32)
+    info = {
+        "source": "testdata/tiny-qa-reference (reference.safetensors, head.safetensors, cases.json) over "
+                  "testdata/tiny-bert-bundle (manifest.json, weights)",
+        "family": arch["family"], "architecture": arch, "order": order, "vocab_rows_kept": len(used),
+        "word_rows": used, "pad_id": 0, "qa": cases["qa"],
+    }
+    save_file(tensors, os.path.join(HERE, "tiny_qa.safetensors"))
+    with open(os.path.join(HERE, "tiny_qa.json"), "w") as f:
+        json.dump(info, f, indent=1)
+    print("tiny_qa", len(used), "word rows")
+
+
 def quantize_golden():
     src = os.path.join(REF, "quantize", "sentence-transformers-145ef47d.txt")
     dst = os.path.join(HERE, "quantize-sentence-transformers-145ef47d.txt")
@@ -175,4 +228,5 @@ if __name__ == "__main__":
     one("tiny-modernbert-bundle", "tiny_modernbert")
     one("tiny-nomic-bundle", "tiny_nomic")
     rerank_fixture()
+    qa_fixture()
     quantize_golden()

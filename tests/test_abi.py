@@ -60,8 +60,9 @@ def test_the_table_is_one_the_core_accepts():
     for f in ("device_count", "device_info", "capability", "embed_write", "buffer_read", "session_open",
               "embed_write_ranges"):
         assert has(f), f
-    # token_head is 0: heads are applied on the host.
-    assert t.token_head == 0
+    # token_head is 1: a QA model's span head runs on the device, which only
+    # a backend offering embed_write_ranges may claim.
+    assert t.token_head == 1 and has("embed_write_ranges")
 
 
 def test_device_count_answers_without_a_device():

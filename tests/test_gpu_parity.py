@@ -6,6 +6,8 @@ Tolerances are the reference's conformance floors
 <= 1e-4; F16 and BF16 cosine >= 0.999. Bookkeeping (packing) is held bit
 for bit, and so is the reference's whole-row range rule.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -358,6 +360,113 @@ def test_rerank_refuses_what_the_core_refuses(context):
     assert e.value.code == S.TURBO_E_UNSUPPORTED_TASK
     s.close()
     model.close()
+
+
+# ---- Extractive QA: the span head on the device ------------------------------------------
+#
+# testdata/tiny-qa-reference's transformers logits for every token of six
+# windows, through headed range writes (include/turbo/turbo.h:699-710), at
+# the reference's score bounds; and the head on multi-token ranges of every
+# family against the oracle.
+
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+@pytest.mark.parametrize("max_batch", [1, 2, 6])
+def test_span_head_meets_the_upstream_logits(context, precision, max_batch):
+    desc, windows, logits, info = oracle.qa_fixture()
+    model = context.load(desc)
+    s = model.session(max_batch, info["qa"]["max_seq"], precision, task=S.TURBO_TASK_EXTRACTIVE_QA)
+    got = s.span_logits(windows, info["pad_id"])
+    assert [len(a) for a, _ in got] == [len(w) for w, _ in windows]
+    flat = np.stack([np.concatenate([a for a, _ in got]), np.concatenate([e for _, e in got])], 1)
+    scale = np.abs(logits).max()
+    d = np.abs(flat - logits).max() / scale
+    assert d <= SCORE_BOUND[s.compute_dtype], d
+    want = oracle.qa_logits(desc, windows, info["pad_id"])
+    dw = np.abs(flat - want).max() / scale
+    assert dw <= SCORE_BOUND[s.compute_dtype], dw
+    print(f"QA max_batch {max_batch} dtype {s.compute_dtype}: {d:.2e} of the scale from transformers, "
+          f"{dw:.2e} from the oracle")
+    s.close()
+    model.close()
+
+
+@pytest.mark.parametrize("family", ["bert", "modernbert", "nomic"])
+def test_span_head_on_ranges_meets_the_oracle(context, family):
+    base = MODELS[family](seed=11)
+    g = np.random.Generator(np.random.PCG64(12))
+    w = (g.standard_normal((3, base.hidden)) * 0.3).astype(np.float32)
+    b = g.standard_normal(3).astype(np.float32)
+    from turboembed_amd.model import ModelDesc
+    desc = ModelDesc(base.family, base.layers, base.hidden, base.heads, base.intermediate, base.vocab_size,
+                     base.max_positions, base.token_types, base.layer_norm_eps, base.tensors, base.position_offset,
+                     base.rope, base.attention_window, base.global_every, base.mlp, base.activation, base.norm,
+                     base.names, base.compute_dtype, span_head=(w, b))
+    ids, mask, types = small.ragged_rows(21, 5, 40, base.vocab_size, types=max(1, base.token_types))
+    live = [np.flatnonzero(m) for m in mask]
+    ranges = [(r, int(c), int(c) + 1) for r in range(5) for c in live[r][:3]]
+    ranges += [(r, int(live[r][0]), int(live[r][-1]) + 1) for r in range(5)]
+    model = context.load(desc)
+    s = model.session(5, 40, S.TURBO_PRECISION_EXACT, max_ranges=len(ranges))
+    s.write_ranges(ids, mask, ranges, types, normalize=S.TURBO_NORMALIZE_NONE)
+    s.run()
+    got = s.read()
+    want = oracle.encode(desc, ids, mask, types, normalize=S.TURBO_NORMALIZE_NONE, ranges=ranges, head=True)
+    assert got.shape == want.shape == (len(ranges), 3)
+    scale = np.abs(want).max()
+    assert np.abs(got - want).max() <= SCORE_BOUND[S.TURBO_DTYPE_F32] * scale, np.abs(got - want).max() / scale
+    # The same shape again replays the run's graph; a row write on the
+    # headed model is a plain embedding write.
+    s.write_ranges(ids, mask, ranges, types, normalize=S.TURBO_NORMALIZE_NONE)
+    s.run()
+    assert np.array_equal(s.read(), got)
+    v = s.embed(ids, mask, types, normalize=S.TURBO_NORMALIZE_NONE)
+    assert_close(v, oracle.encode(base, ids, mask, types, normalize=S.TURBO_NORMALIZE_NONE), s.compute_dtype)
+    s.close()
+    model.close()
+
+
+def test_span_head_refuses_what_the_core_refuses(context):
+    desc, windows, logits, info = oracle.qa_fixture()
+    model = context.load(desc)
+    s = model.session(2, 24, S.TURBO_PRECISION_EXACT, task=S.TURBO_TASK_EXTRACTIVE_QA)
+    ids = np.zeros((1, 24), np.int32)
+    mask = np.zeros((1, 24), np.int32)
+    n = len(windows[0][0])
+    ids[0, :n], mask[0, :n] = windows[0][0], 1
+    for kw, field in ((dict(normalize=S.TURBO_NORMALIZE_L2), 4), (dict(normalize=S.TURBO_NORMALIZE_NONE, output_dim=8), 6)):
+        with pytest.raises(T.TurboError) as e:
+            s.write_ranges(ids, mask, [(0, 0, 1)], **kw)
+        assert (e.value.code, e.value.field) == (S.TURBO_E_UNSUPPORTED_OPTION, field)
+    s.write_ranges(ids, mask, [(0, 0, 1), (0, 1, 3)], normalize=S.TURBO_NORMALIZE_NONE)
+    s.run()
+    assert s.read().shape == (2, 2)
+    with pytest.raises(T.TurboError) as e:
+        s.read_quantized(S.TURBO_QUANTIZE_UBINARY)
+    assert (e.value.code, e.value.field) == (S.TURBO_E_UNSUPPORTED_OPTION, 7)
+    # Through the seam itself: the backend holds the same rules.
+    r = S.turbo_backend_embed_rows()
+    r.struct_size = C.sizeof(r)
+    r.batch, r.seq, r.row_stride = 1, 24, 24
+    r.ids, r.mask = ids.ctypes.data_as(C.POINTER(C.c_int32)), mask.ctypes.data_as(C.POINTER(C.c_int32))
+    r.pooling, r.normalize, r.output_dim, r.head, r.taps = S.TURBO_POOLING_MEAN, S.TURBO_NORMALIZE_L2, 2, 1, 1
+    rg = (S.turbo_token_range * 1)()
+    rg[0].row, rg[0].start, rg[0].end = 0, 0, 1
+    err = S.new_error()
+    assert s.t.embed_write_ranges(s.h, C.byref(r), rg, 1, C.byref(err)) == S.TURBO_E_UNSUPPORTED_OPTION
+    r.normalize, r.output_dim = S.TURBO_NORMALIZE_NONE, 32
+    assert s.t.embed_write_ranges(s.h, C.byref(r), rg, 1, C.byref(err)) == S.TURBO_E_UNSUPPORTED_OPTION
+    r.output_dim = 2
+    assert s.t.embed_write(s.h, C.byref(r), C.byref(err)) == S.TURBO_E_INVALID_ARGUMENT   # no ranges
+    s.close()
+    model.close()
+    # A headed write to a model loaded without a head.
+    plain = context.load(oracle.fixture("tiny_bert")[0])
+    s = plain.session(1, 24, S.TURBO_PRECISION_EXACT, max_ranges=1)
+    assert s.t.embed_write_ranges(s.h, C.byref(r), rg, 1, C.byref(err)) == S.TURBO_E_INVALID_ARGUMENT
+    with pytest.raises(T.TurboError):
+        s.span_logits(windows[:1])
+    s.close()
+    plain.close()
 
 
 def test_int8_cross_encoder_meets_the_oracle(context):

@@ -217,6 +217,12 @@ class Session:
         self.model, self.t, self.lib = model, model.t, library()
         d = S.turbo_backend_session_desc()
         d.struct_size = C.sizeof(d)
+        # A QA session's encoder is the embedding encoder, with a range for
+        # every token a run may hold (core/src/session/create.rs:61-62,
+        # core/src/qa/session.rs:138-140).
+        self.task = task
+        if task == S.TURBO_TASK_EXTRACTIVE_QA:
+            task, max_ranges = S.TURBO_TASK_EMBED, max_ranges or max_batch * max_seq
         d.task, d.max_batch, d.max_seq, d.precision = task, max_batch, max_seq, precision
         d.max_ranges = max_ranges or max_batch
         self.max_batch, self.max_seq, self.max_ranges = max_batch, max_seq, d.max_ranges
@@ -249,7 +255,7 @@ class Session:
         if tuned and tun.tuned == S.TURBO_TUNED_MEASURED and tun.numerics_used == tun.numerics_allowed:
             self.cache.put(self.key, tun.choices.decode(), self.timings)
         self.run_info = None
-        self.n_out = 0
+        self.n_out, self.headed = 0, False
         self.od = 0
 
     def _tune_key(self, model, precision, numerics_allowed, tcap, max_seq):
@@ -292,12 +298,27 @@ class Session:
         r = self._rows(ids, mask, types, pooling, normalize, output_dim)
         err = S.new_error()
         _ok(self.t.embed_write(self.h, C.byref(r), C.byref(err)), err)
-        self.n_out, self.od = r.batch, r.output_dim
+        self.n_out, self.od, self.headed = r.batch, r.output_dim, False
 
     def write_ranges(self, ids, mask, ranges, types=None, normalize=S.TURBO_NORMALIZE_L2, output_dim=0):
         """Ranges are (row, start, end) triples; pooled by the mean, as the
-        core forces for a range write (core/src/session/tokens.rs:132-146)."""
+        core forces for a range write (core/src/session/tokens.rs:132-146).
+
+        On a model loaded with a span head each range's row is the head's
+        logits, [count, head_out]: normalize must be NONE (else
+        TURBO_E_UNSUPPORTED_OPTION naming field 4) and output_dim 0 or the
+        hidden width (field 6), as the core holds them
+        (tokens.rs:140-143, 217-235)."""
+        head = self.model.desc.span_head
+        if head is not None:
+            if normalize != S.TURBO_NORMALIZE_NONE:
+                raise TurboError(S.TURBO_E_UNSUPPORTED_OPTION, 4, "normalize: the span head's logits are not normalized")
+            if output_dim not in (0, self.model.desc.hidden):
+                raise TurboError(S.TURBO_E_UNSUPPORTED_OPTION, 6, f"output_dim {output_dim}: the span head reads all "
+                                                                  f"{self.model.desc.hidden} values of a range's vector")
         r = self._rows(ids, mask, types, S.TURBO_POOLING_MEAN, normalize, output_dim)
+        if head is not None:
+            r.head, r.output_dim = 1, head[0].shape[0]
         ranges = list(ranges)
         arr = (S.turbo_token_range * max(1, len(ranges)))()
         for i, (row, start, end) in enumerate(ranges):
@@ -307,7 +328,7 @@ class Session:
         _ok(self.lib.turbo_rocm_check_ranges(r.batch, r.seq, r.seq, _i32(mask), arr, len(ranges), self.max_ranges,
                                              C.byref(err)), err)
         _ok(self.t.embed_write_ranges(self.h, C.byref(r), arr, len(ranges), C.byref(err)), err)
-        self.n_out, self.od = len(ranges), r.output_dim
+        self.n_out, self.od, self.headed = len(ranges), r.output_dim, head is not None
 
     # -- run and read -----------------------------------------------------------
     def run(self):
@@ -332,6 +353,8 @@ class Session:
         codes alone. int8: [n, output_dim] int8 with ranges [2, output_dim];
         ubinary: [n, ceil(output_dim / 8)] uint8. The output holds codes,
         not vectors, afterwards."""
+        if getattr(self, "headed", False):
+            raise TurboError(S.TURBO_E_UNSUPPORTED_OPTION, 7, "quantization: the span head's rows are logits, not vectors")
         rr = None
         if quantization == S.TURBO_QUANTIZE_INT8:
             rr = np.ascontiguousarray(int8_ranges, np.float32)
@@ -355,6 +378,11 @@ class Session:
         """Scores of (query ids, passage ids) pairs; see rerank.rerank."""
         from .rerank import rerank
         return rerank(self, pairs, head, start_id, end_id, **kw)
+
+    def span_logits(self, windows, fill_id=0):
+        """Start and end logits of QA windows; see qa.span_logits."""
+        from .qa import span_logits
+        return span_logits(self, windows, fill_id)
 
     # -- hooks ---------------------------------------------------------------------
     def packing(self):

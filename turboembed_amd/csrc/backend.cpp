@@ -479,7 +479,7 @@ const turbo_backend turbo_rocm_backend = {
     session_create_tuned_fn,
     session_open_fn,
     embed_write_ranges_fn,
-    0,
+    1,   // token_head: model_load takes a QA model's span head; headed range writes apply it
     0,
     buffer_quantize,
 };

@@ -106,6 +106,14 @@ hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads,
 hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
                 int count, const uint32_t *ranges, int pooling, int output_dim, int l2, float *out);
 
+// The span head's outputs at most (2 for start and end).
+constexpr int HEAD_MAX = 16;
+
+// Range i's mean over all `hidden` values (as pool's mode 1) through a linear
+// head, w [hout, hidden] and b [hout] F32, its sums in F64: out [count, hout].
+hipError_t pool_head(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
+                     int count, const uint32_t *ranges, const float *hw, const float *hb, int hout, float *out);
+
 // Symmetric int8 rows: for each of `rows` rows of `cols` values (row stride
 // ld, F32 or F16 per src_dt), scale = max |x| / 127 and q = round(x / scale)
 // (q = 0 and scale 0 for a zero row), into dst [rows][cols] and scale [rows].

@@ -333,13 +333,22 @@ hipError_t layer_norm(hipStream_t s, int tokens, int hidden, const float *in, co
 // (row, 0, len) through the same code, so a whole-row range gives the row's
 // vector bit for bit. The cut to output_dim comes before the L2 norm, summed
 // in F64 and floored at 1e-12 (mod.rs:470-482).
+//
+// HEAD: range i's mean over all hidden values goes through the span head
+// instead, out[i, o] = bias[o] + sum_c w[o, c] * mean[c] with the products
+// and sums in F64, rounded to F32 once (include/turbo/turbo_backend.h:418-422;
+// the core's host head, core/src/qa/session.rs:268-276, sums the same terms).
 constexpr int POOL_THREADS = 256;
 
+template <bool HEAD>
 __global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const float *__restrict__ x, int hidden, Packing p,
                                                             const int32_t *__restrict__ mask, int seq, int mode,
                                                             const uint32_t *__restrict__ ranges, int pooling, int od,
-                                                            int l2, float *__restrict__ out) {
+                                                            int l2, float *__restrict__ out,
+                                                            const float *__restrict__ hw,
+                                                            const float *__restrict__ hb, int hout) {
     __shared__ double part[POOL_THREADS / 64];
+    __shared__ double hpart[HEAD ? HEAD_MAX : 1][POOL_THREADS / 64];
     __shared__ int flag;
     const int i = blockIdx.x;
     int r, c0, c1;
@@ -388,6 +397,27 @@ __global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const float *__restr
 #pragma unroll
         for (int v = 0; v < MAXV; ++v) acc[v] = __fmul_rn(acc[v], inv);
     }
+    if constexpr (HEAD) {
+        // od is hidden here: every value of the mean meets the head.
+        for (int o = 0; o < hout; ++o) {
+            double t = 0.0;
+#pragma unroll
+            for (int v = 0; v < MAXV; ++v) {
+                const int c = threadIdx.x + POOL_THREADS * v;
+                if (c < od) t = fma((double)hw[(size_t)o * hidden + c], (double)acc[v], t);
+            }
+            t = wave_sum(t);
+            if ((threadIdx.x & 63) == 0) hpart[o][threadIdx.x >> 6] = t;
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < hout) {
+            double tot = (double)hb[threadIdx.x];
+#pragma unroll
+            for (int w = 0; w < POOL_THREADS / 64; ++w) tot += hpart[threadIdx.x][w];
+            out[(size_t)i * hout + threadIdx.x] = (float)tot;
+        }
+        return;
+    }
     if (l2) {
         double s = 0.0;
 #pragma unroll
@@ -417,8 +447,17 @@ hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, con
                 const uint32_t *ranges, int pooling, int output_dim, int l2, float *out) {
     if (output_dim > 8 * POOL_THREADS) return hipErrorInvalidValue;
     if (count <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pool_kernel, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq,
-                       ranges ? 1 : 0, ranges, pooling, output_dim, l2, out);
+    hipLaunchKernelGGL(pool_kernel<false>, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq,
+                       ranges ? 1 : 0, ranges, pooling, output_dim, l2, out, nullptr, nullptr, 0);
+    return hipGetLastError();
+}
+
+hipError_t pool_head(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
+                     int count, const uint32_t *ranges, const float *hw, const float *hb, int hout, float *out) {
+    if (hidden > 8 * POOL_THREADS || hout < 1 || hout > HEAD_MAX || !ranges) return hipErrorInvalidValue;
+    if (count <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pool_kernel<true>, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq, 1, ranges,
+                       1 /* the mean */, hidden, 0, out, hw, hb, hout);
     return hipGetLastError();
 }
 

@@ -108,7 +108,19 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
     if (H % 8 != 0 || I % 8 != 0 || H > 2048)
         fail(TURBO_E_UNSUPPORTED, "rocm: hidden " + std::to_string(H) + " and intermediate " + std::to_string(I) +
                                       " must be multiples of 8, hidden at most 2048");
-    if (d->head && d->head_out) fail(TURBO_E_UNSUPPORTED, "rocm: a token head on the device");
+    // A span head (TASK_EXTRACTIVE_QA): [head_out, hidden] and [head_out]
+    // F32, applied to a headed range write's means (turbo_backend.h:332-337).
+    const bool headed = d->struct_size >= offsetof(turbo_backend_model, head_out) + 4 && d->head && d->head_out;
+    if (headed) {
+        if (d->head_out > HEAD_MAX || d->head_out > H)
+            fail(TURBO_E_UNSUPPORTED, "rocm: a head of " + std::to_string(d->head_out) + " outputs (at most " +
+                                          std::to_string(HEAD_MAX) + ")");
+        const turbo_backend_tensor &w = d->head[0], &b = d->head[1];
+        if (!w.data || !b.data || w.dtype != TURBO_DTYPE_F32 || b.dtype != TURBO_DTYPE_F32 ||
+            w.bytes != (uint64_t)d->head_out * H * 4 || b.bytes != (uint64_t)d->head_out * 4)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: the head is [" + std::to_string(d->head_out) + ", " +
+                                               std::to_string(H) + "] and [" + std::to_string(d->head_out) + "] F32");
+    }
 
     // compute_dtype I8 on raw weights: the manifest asks for int8 GEMMs
     // (per-channel weights, per-token activations), as a compiled I8 graph
@@ -260,6 +272,15 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
         }
     }
 
+    size_t head_w = SIZE_MAX, head_b = SIZE_MAX;
+    if (headed) {
+        head_w = img.add((size_t)d->head_out * H);
+        std::memcpy(&img.data[head_w], d->head[0].data, (size_t)d->head_out * H * 4);
+        head_b = img.add(d->head_out);
+        std::memcpy(&img.data[head_b], d->head[1].data, (size_t)d->head_out * 4);
+        m->head_out = d->head_out;
+    }
+
     OnDevice on(c->ordinal);
     m->f32.reset(dev_alloc(img.data.size() * 4, "model weights"));
     check(hipMemcpy(m->f32.get(), img.data.data(), img.data.size() * 4, hipMemcpyHostToDevice), "model weights");
@@ -272,6 +293,8 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
     m->emb_b = at(off.emb_b);
     m->final_w = at(off.final_w);
     m->rope = at(off.rope);
+    m->head_w = at(head_w);
+    m->head_b = at(head_b);
     for (const LOff &o : loff) {
         Model::Layer L{};
         L.wqkv = at(o.wqkv);
@@ -600,9 +623,21 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
                                    " over the session's " + std::to_string(s->max_batch) + " of " +
                                    std::to_string(s->max_seq));
     if (r->taps > 1) fail(TURBO_E_UNSUPPORTED_OPTION, "rocm: pooling from earlier layers", 9);
-    if (r->head) fail(TURBO_E_UNSUPPORTED, "rocm: a token head on the device");
-    if (r->output_dim == 0 || r->output_dim > s->model->hidden)
+    // A headed write (turbo_backend.h:418-422): ranges on a model with a
+    // span head, rows [count, head_out], normalize NONE.
+    const bool head = r->struct_size >= offsetof(turbo_backend_embed_rows, head) + 4 && r->head;
+    if (head) {
+        if (!s->model->head_out) fail(TURBO_E_INVALID_ARGUMENT, "rocm: a head write to a model loaded without one");
+        if (count == 0) fail(TURBO_E_INVALID_ARGUMENT, "rocm: a head write pools ranges");
+        if (r->normalize != TURBO_NORMALIZE_NONE)
+            fail(TURBO_E_UNSUPPORTED_OPTION, "rocm: the span head's logits are not normalized", 4);
+        if (r->output_dim != s->model->head_out)
+            fail(TURBO_E_UNSUPPORTED_OPTION, "rocm: output_dim " + std::to_string(r->output_dim) +
+                                                 ": a head write's rows are the head's " +
+                                                 std::to_string(s->model->head_out) + " logits", 6);
+    } else if (r->output_dim == 0 || r->output_dim > s->model->hidden) {
         fail(TURBO_E_INVALID_ARGUMENT, "rocm: output_dim " + std::to_string(r->output_dim));
+    }
     if (count > s->max_ranges) fail(TURBO_E_CAPACITY, "rocm: " + std::to_string(count) + " ranges over max_ranges");
     const uint32_t B = r->batch, S = r->seq, stride = r->row_stride ? r->row_stride : r->seq;
     if (stride < S) fail(TURBO_E_INVALID_SHAPE, "rocm: row_stride under seq");
@@ -662,6 +697,7 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     s->pooling = r->pooling;
     s->normalize = r->normalize;
     s->output_dim = r->output_dim;
+    s->head = head;
     s->count = count;
     s->tokens = tokens;
     s->max_len = max_len;
@@ -832,8 +868,12 @@ void encode(Session &s) {
             LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
     }
     const int n_out = s.count ? (int)s.count : (int)s.batch;
-    LAUNCH("pool", pool(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.count ? s.ranges : nullptr, (int)s.pooling,
-                        (int)s.output_dim, s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0, s.out));
+    if (s.head)
+        LAUNCH("pool_head", pool_head(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.ranges, m.head_w, m.head_b,
+                                      (int)m.head_out, s.out));
+    else
+        LAUNCH("pool", pool(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.count ? s.ranges : nullptr,
+                            (int)s.pooling, (int)s.output_dim, s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0, s.out));
 #undef LAUNCH
 }
 
@@ -842,7 +882,8 @@ void launch_run(Session &s) {
         encode(s);
         return;
     }
-    const Session::RunShape key{s.tokens, s.batch, s.seq, s.max_len, s.count, s.pooling, s.normalize, s.output_dim};
+    const Session::RunShape key{s.tokens, s.batch,     s.seq,        s.max_len,       s.count,
+                                s.pooling, s.normalize, s.output_dim, (uint32_t)s.head};
     auto it = s.graph_of.find(key);
     if (it == s.graph_of.end()) {
         constexpr size_t KEEP = 16;

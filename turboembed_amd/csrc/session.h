@@ -105,6 +105,9 @@ struct Model {
     // F32 device pointers (NULL where absent).
     const float *word = nullptr, *pos = nullptr, *type = nullptr, *emb_w = nullptr, *emb_b = nullptr,
                 *final_w = nullptr, *rope = nullptr;
+    // The span head, [head_out, hidden] and [head_out] F32 (head_out 0: none).
+    const float *head_w = nullptr, *head_b = nullptr;
+    uint32_t head_out = 0;
     struct Layer {
         const float *wqkv, *bqkv, *wo, *bo, *ln1_w, *ln1_b, *w1, *b1, *w2, *b2, *ln2_w, *ln2_b;
         size_t n_qkv, n_in;   // output rows of the QKV and FFN-in products
@@ -146,6 +149,7 @@ struct Session {
     bool written = false;
     uint32_t batch = 0, seq = 0, pooling = 0, normalize = 0, output_dim = 0, count = 0, tokens = 0, max_len = 0;
     bool has_types = false;
+    bool head = false;   // ranges through the span head
     uint64_t h2d = 0;
     std::vector<LayerWeights> *w = nullptr;
     Choices kc;            // kernel choices per bin of packed tokens
@@ -155,11 +159,12 @@ struct Session {
     // of a shape seen before is one graph launch. Off while timing, or with
     // TURBO_ROCM_GRAPHS=0.
     struct RunShape {
-        uint32_t tokens, batch, seq, max_len, count, pooling, normalize, output_dim;
+        uint32_t tokens, batch, seq, max_len, count, pooling, normalize, output_dim, head;
         bool operator<(const RunShape &o) const {
-            const uint32_t a[8] = {tokens, batch, seq, max_len, count, pooling, normalize, output_dim};
-            const uint32_t b[8] = {o.tokens, o.batch, o.seq, o.max_len, o.count, o.pooling, o.normalize, o.output_dim};
-            return std::lexicographical_compare(a, a + 8, b, b + 8);
+            const uint32_t a[9] = {tokens, batch, seq, max_len, count, pooling, normalize, output_dim, head};
+            const uint32_t b[9] = {o.tokens,  o.batch,     o.seq,        o.max_len, o.count,
+                                   o.pooling, o.normalize, o.output_dim, o.head};
+            return std::lexicographical_compare(a, a + 9, b, b + 9);
         }
     };
     bool graphs = true;

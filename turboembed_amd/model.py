@@ -48,7 +48,7 @@ class ModelDesc:
     def __init__(self, family, layers, hidden, heads, intermediate, vocab_size, max_positions, token_types,
                  layer_norm_eps, tensors, position_offset=0, rope=None, attention_window=0, global_every=0,
                  mlp=S.TURBO_MLP_DENSE, activation=S.TURBO_ACTIVATION_GELU_ERF, norm=S.TURBO_NORM_LAYER,
-                 names=None, compute_dtype=0):
+                 names=None, compute_dtype=0, span_head=None):
         self.family, self.layers, self.hidden, self.heads = family, layers, hidden, heads
         self.intermediate, self.vocab_size, self.max_positions = intermediate, vocab_size, max_positions
         self.token_types, self.layer_norm_eps, self.position_offset = token_types, layer_norm_eps, position_offset
@@ -66,6 +66,14 @@ class ModelDesc:
         self.names = names or [f"tensor{i}" for i in range(len(self.tensors))]
         # TURBO_DTYPE_I8 asks for int8 GEMMs below EXACT; 0 leaves it to the precision.
         self.compute_dtype = compute_dtype
+        # An extractive QA model's span head, (weight [head_out, hidden],
+        # bias [head_out]) in F32, for a backend that applies it
+        # (turbo_backend.h:332-337); None on every other model.
+        self.span_head = None
+        if span_head is not None:
+            w, b = (np.ascontiguousarray(a, np.float32) for a in span_head)
+            assert w.ndim == 2 and w.shape[1] == hidden and b.shape == (w.shape[0],), "head is [out, hidden], [out]"
+            self.span_head = (w, b)
         self._struct = None
 
     @property
@@ -114,6 +122,16 @@ class ModelDesc:
             m.rope_pairs = pairs
             m.mlp, m.activation, m.norm = self.mlp, self.activation, self.norm
             m.attention_window, m.global_every = self.attention_window, self.global_every
+        if self.span_head is not None:
+            harr = (S.turbo_backend_tensor * 2)()
+            self._head_names = [b"head.weight", b"head.bias"]
+            for e, t, name in zip(harr, self.span_head, self._head_names):
+                e.name, e.data, e.ndim, e.dtype, e.bytes = name, t.ctypes.data, t.ndim, S.TURBO_DTYPE_F32, t.nbytes
+                e.shape[0] = t.shape[0]
+                e.shape[1] = t.shape[1] if t.ndim == 2 else 0
+            m.head = C.cast(harr, C.POINTER(S.turbo_backend_tensor))
+            m.head_out = self.span_head[0].shape[0]
+            self._harr = harr
         self._arr = arr
         self._struct = m
         return m
@@ -133,5 +151,5 @@ def with_dtype(desc, dtype):
                     desc.max_positions, desc.token_types, desc.layer_norm_eps,
                     [None if t is None else conv(t) for t in desc.tensors], desc.position_offset, desc.rope,
                     desc.attention_window, desc.global_every, desc.mlp, desc.activation, desc.norm, desc.names,
-                    desc.compute_dtype)
+                    desc.compute_dtype, desc.span_head)
     return out

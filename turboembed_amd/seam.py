@@ -27,6 +27,7 @@ STATUS_NAMES = {v: k for k, v in dict(globals()).items() if k.startswith("TURBO_
 
 TURBO_TASK_EMBED = 1
 TURBO_TASK_RERANK = 2
+TURBO_TASK_EXTRACTIVE_QA = 3
 
 TURBO_CAP_UNSUPPORTED = 0
 TURBO_CAP_EXPERIMENTAL = 1
