@@ -68,19 +68,23 @@ def ranges_array(ranges):
 
 
 def encode(desc: ModelDesc, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN, normalize=S.TURBO_NORMALIZE_L2,
-           output_dim=None, ranges=None, threads=0, hidden=False, head=False):
+           output_dim=None, ranges=None, threads=0, hidden=False, head=False, taps=1, tap_alone=False):
     """The oracle's vectors for the rows (and ranges); with hidden=True also
     the final hidden states of the packed tokens. head=True on a range write
-    to a model with a span head: each range's row is the head's logits."""
+    to a model with a span head: each range's row is the head's logits.
+    taps > 1 on a range write: the ranges pooled from each of the last taps
+    layers, [taps * count, od] block by block; with tap_alone the first of
+    those layers alone, [count, od]."""
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     mask = np.ascontiguousarray(mask, dtype=np.int32)
     types = None if types is None else np.ascontiguousarray(types, dtype=np.int32)
     od = desc.span_head[0].shape[0] if head and desc.span_head is not None else output_dim or desc.hidden
     r = rows_struct(ids, mask, types, pooling, normalize, od)
     r.head = 1 if head else 0
+    r.taps, r.tap_alone = taps, 1 if tap_alone else 0
     ranges = list(ranges or [])
     rr = ranges_array(ranges)
-    n_out = len(ranges) if ranges else ids.shape[0]
+    n_out = len(ranges) * (1 if tap_alone else max(1, taps)) if ranges else ids.shape[0]
     out = np.zeros((n_out, od), dtype=np.float32)
     hid = np.zeros((ids.shape[0] * ids.shape[1], desc.hidden), dtype=np.float32) if hidden else None
     why = C.create_string_buffer(512)

@@ -581,8 +581,16 @@ struct Run {
 
 void encode(const Model &m, const turbo_backend_embed_rows *rows, const turbo_token_range *ranges, uint32_t count,
             uint32_t threads, float *out, float *hidden) {
-    if (rows->taps > 1 || rows->head)
-        throw Failure(TURBO_E_UNSUPPORTED, "the oracle pools the final layer alone, with no head");
+    if (rows->head) throw Failure(TURBO_E_UNSUPPORTED, "encode pools vectors; the head is applied after it");
+    // Layer reads (core/src/cpu/encoder/mod.rs:292-303): the last `taps`
+    // layers' states pooled per range, or with tap_alone the model cut after
+    // the first of them, read plainly.
+    const uint32_t taps = rows->taps > 1 ? rows->taps : 1;
+    if (taps > 1 && (count == 0 || taps > m.layers))
+        throw Failure(TURBO_E_INVALID_ARGUMENT, "oracle: layer reads need ranges and at most the model's layers");
+    if (rows->tap_alone && taps == 1) throw Failure(TURBO_E_INVALID_ARGUMENT, "oracle: tap_alone with one layer read");
+    const uint32_t nl = rows->tap_alone ? m.layers + 1 - taps : m.layers;
+    const uint32_t reads = rows->tap_alone ? 1 : taps;
     Run run(m, threads);
     const uint32_t B = rows->batch, S = rows->seq, stride = rows->row_stride ? rows->row_stride : rows->seq;
     run.batch = B;
@@ -610,7 +618,30 @@ void encode(const Model &m, const turbo_backend_embed_rows *rows, const turbo_to
         float *y = x + (size_t)t * H + c0;
         for (uint32_t j = 0; j < cols; ++j) y[j] += acc[j] + w.bias[c0 + j];
     };
-    for (uint32_t l = 0; l < m.layers; ++l) {
+    const uint32_t od = rows->output_dim;
+    // Each range pooled from src into block k of out (mod.rs:336-345).
+    auto pool_ranges = [&](const float *src, uint32_t k) {
+        for (uint32_t i = 0; i < count; ++i) {
+            const turbo_token_range g = ranges[i];
+            float *dst = out + ((size_t)k * count + i) * od;
+            run.mean(src, g.row, g.start, std::min(g.end, run.pk.len[g.row]), dst, od);
+            Run::finish(dst, od, rows->normalize);
+        }
+    };
+    // After layer l: a read before the last layer run goes into its block; a
+    // ModernBERT read is final_norm(x) (rotary/mod.rs:161-168).
+    std::vector<float> normed;
+    auto tapped = [&](uint32_t l) {
+        if (reads == 1 || l + 1 >= nl || l + reads < nl) return;
+        const float *src = x;
+        if (m.modern) {
+            normed.assign(run.x.begin(), run.x.end());
+            run.norm(normed.data(), m.final_w, nullptr);
+            src = normed.data();
+        }
+        pool_ranges(src, l + reads - nl);
+    };
+    for (uint32_t l = 0; l < nl; ++l) {
         const Layer &L = m.ls[l];
         if (!m.rotary) {
             run.linear(x, H, L.qkv, [&](uint32_t t, uint32_t c0, uint32_t cols, const float *acc) {
@@ -629,6 +660,7 @@ void encode(const Model &m, const turbo_backend_embed_rows *rows, const turbo_to
                 residual(t, c0, cols, acc, L.ffn_out);
             });
             run.norm(x, L.ffn_ln_w, L.ffn_ln_b);
+            tapped(l);
             continue;
         }
         // Rotary layer (rotary/mod.rs:119-160).
@@ -676,10 +708,10 @@ void encode(const Model &m, const turbo_backend_embed_rows *rows, const turbo_to
         run.linear(run.ffn.data(), I, L.ffn_out,
                    [&](uint32_t t, uint32_t c0, uint32_t cols, const float *acc) { residual(t, c0, cols, acc, L.ffn_out); });
         if (!m.modern) run.norm(x, L.ffn_ln_w, L.ffn_ln_b);
+        tapped(l);
     }
     if (m.modern) run.norm(x, m.final_w, nullptr);
     if (hidden) std::copy(run.x.begin(), run.x.end(), hidden);
-    const uint32_t od = rows->output_dim;
     if (count == 0) {
         for (uint32_t r = 0; r < B; ++r) {
             float *dst = out + (size_t)r * od;
@@ -692,12 +724,7 @@ void encode(const Model &m, const turbo_backend_embed_rows *rows, const turbo_to
         }
         return;
     }
-    for (uint32_t i = 0; i < count; ++i) {
-        const turbo_token_range g = ranges[i];
-        float *dst = out + (size_t)i * od;
-        run.mean(x, g.row, g.start, std::min(g.end, run.pk.len[g.row]), dst, od);
-        Run::finish(dst, od, rows->normalize);
-    }
+    pool_ranges(x, reads - 1);
 }
 
 void say(char *why, uint32_t len, const char *msg) {

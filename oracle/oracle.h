@@ -23,7 +23,12 @@ extern "C" {
  * With rows->head 1 on a range write to a model with a span head (m->head,
  * m->head_out), out is [count, head_out]: each range's mean over all hidden
  * values, not normalized, through the head, its sums in F64 from the bias
- * (reference core/src/qa/session.rs:268-276).
+ * (reference core/src/qa/session.rs:268-276). With rows->taps T > 1 on a
+ * range write, out is [T, count, output_dim]: block k the ranges pooled
+ * after layer L - T + k + 1 of L (a ModernBERT's through final_norm), the
+ * last block the final layer's; with rows->tap_alone 1 it is the first of
+ * those alone, [count, output_dim], the model cut after that layer
+ * (core/src/cpu/encoder/mod.rs:292-373).
  * `threads` 0 is one per processor. Returns TURBO_OK or a status; `why`
  * (may be NULL) receives a message of up to why_len bytes. */
 int32_t oracle_encode(const turbo_backend_model *m, const turbo_backend_embed_rows *rows,

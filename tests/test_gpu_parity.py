@@ -469,6 +469,117 @@ def test_span_head_refuses_what_the_core_refuses(context):
     plain.close()
 
 
+# ---- Layer reads (taps): ranges from each of the last layers ------------------------------
+#
+# turbo_embed_write_layer_ranges (include/turbo/turbo.h:712-738): every block
+# against the oracle at the tier's bound, and bit for bit the invariants the
+# reference's tests hold (core/tests/ranges/layers.rs:18-49, alone.rs:25-84):
+# the last block is the plain range write, one layer alone is block 0, and
+# block k is the model cut after its layer.
+
+def _cut(desc, layers):
+    per = {S.TURBO_FAMILY_BERT: (S.BERT_EMBEDDING_TENSORS, S.BERT_LAYER_TENSORS),
+           S.TURBO_FAMILY_MODERNBERT: (S.MODERNBERT_EMBEDDING_TENSORS, S.MODERNBERT_LAYER_TENSORS),
+           S.TURBO_FAMILY_NOMIC_BERT: (S.NOMIC_EMBEDDING_TENSORS, S.NOMIC_LAYER_TENSORS)}[desc.family]
+    n = per[0] + layers * per[1]
+    from turboembed_amd.model import ModelDesc
+    return ModelDesc(desc.family, layers, desc.hidden, desc.heads, desc.intermediate, desc.vocab_size,
+                     desc.max_positions, desc.token_types, desc.layer_norm_eps, desc.tensors[:n], desc.position_offset,
+                     desc.rope, desc.attention_window, desc.global_every, desc.mlp, desc.activation, desc.norm,
+                     desc.names[:n], desc.compute_dtype)
+
+
+@pytest.mark.parametrize("family", ["bert", "modernbert", "nomic"])
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+def test_layer_reads_meet_the_oracle(context, family, precision):
+    desc = MODELS[family](seed=13, layers=3)
+    ids, mask, types = small.ragged_rows(31, 4, 48, desc.vocab_size, types=max(1, desc.token_types))
+    live = [np.flatnonzero(m) for m in mask]
+    ranges = [(r, int(live[r][0]), int(live[r][-1]) + 1) for r in range(4)]
+    ranges += [(r, int(live[r][0]), int(live[r][0]) + 1) for r in range(4)] + [(0, 5, 17)]
+    n = len(ranges)
+    L = desc.layers
+    model = context.load(desc)
+    s = model.session(4, 48, precision, max_ranges=L * n)
+    s.write_ranges(ids, mask, ranges, types)
+    s.run()
+    plain = s.read()
+    for T in range(1, L + 1):
+        s.write_layer_ranges(ids, mask, ranges, T, types)
+        s.run()
+        got = s.read()
+        assert got.shape == (T * n, desc.hidden)
+        want = oracle.encode(desc, ids, mask, types, ranges=ranges, taps=T)
+        assert_close(got, want, s.compute_dtype)
+        assert np.array_equal(got[(T - 1) * n:], plain), f"last block of {T}"
+        if T > 1:
+            s.write_layer_ranges(ids, mask, ranges, T, types, layer_alone=True)
+            s.run()
+            assert np.array_equal(s.read(), got[:n]), f"{T} alone"
+            # A replay of the same shape gives the same bits.
+            s.write_layer_ranges(ids, mask, ranges, T, types)
+            s.run()
+            assert np.array_equal(s.read(), got)
+    # Block 0 of L against the model cut after layer 1, loaded on its own.
+    cut = context.load(_cut(desc, 1))
+    c = cut.session(4, 48, precision, max_ranges=n)
+    c.write_ranges(ids, mask, ranges, types)
+    c.run()
+    assert np.array_equal(c.read(), got[:n])
+    c.close()
+    cut.close()
+    s.close()
+    model.close()
+
+
+def test_layer_reads_refuse_what_the_core_refuses(context):
+    desc = MODELS["bert"](seed=13, layers=3)
+    ids, mask, types = small.ragged_rows(31, 2, 16, desc.vocab_size)
+    model = context.load(desc)
+    s = model.session(2, 16, S.TURBO_PRECISION_EXACT, max_ranges=4)
+    rg = [(0, 0, 2), (1, 0, 1)]
+    for layers, code, field in ((0, S.TURBO_E_INVALID_ARGUMENT, 9), (4, S.TURBO_E_INVALID_ARGUMENT, 9),
+                                (3, S.TURBO_E_CAPACITY, 0)):
+        with pytest.raises(T.TurboError) as e:
+            s.write_layer_ranges(ids, mask, rg, layers, types)
+        assert (e.value.code, e.value.field) == (code, field)
+    s.write_layer_ranges(ids, mask, rg, 3, types, layer_alone=True)     # one block: within max_ranges
+    s.run()
+    assert s.read().shape == (2, desc.hidden)
+    # Through the seam: the backend holds the same rules.
+    r = S.turbo_backend_embed_rows()
+    r.struct_size = C.sizeof(r)
+    r.batch, r.seq, r.row_stride = 2, 16, 16
+    r.ids, r.mask = ids.ctypes.data_as(C.POINTER(C.c_int32)), mask.ctypes.data_as(C.POINTER(C.c_int32))
+    r.pooling, r.normalize, r.output_dim, r.taps = S.TURBO_POOLING_MEAN, S.TURBO_NORMALIZE_L2, desc.hidden, 2
+    arr = (S.turbo_token_range * 3)()
+    for i, (a, b_, c_) in enumerate([(0, 0, 2), (1, 0, 1), (0, 1, 2)]):
+        arr[i].row, arr[i].start, arr[i].end = a, b_, c_
+    err = S.new_error()
+    assert s.t.embed_write(s.h, C.byref(r), C.byref(err)) == S.TURBO_E_INVALID_ARGUMENT       # no ranges
+    assert err.field == 9
+    assert s.t.embed_write_ranges(s.h, C.byref(r), arr, 3, C.byref(err)) == S.TURBO_E_CAPACITY  # 6 over 4
+    r.taps = 4
+    assert s.t.embed_write_ranges(s.h, C.byref(r), arr, 2, C.byref(err)) == S.TURBO_E_INVALID_ARGUMENT
+    r.taps, r.tap_alone = 2, 2
+    assert s.t.embed_write_ranges(s.h, C.byref(r), arr, 2, C.byref(err)) == S.TURBO_E_INVALID_ARGUMENT
+    assert err.field == 10
+    s.close()
+    model.close()
+    # The span head reads the final layer alone.
+    qd, windows, _, _ = oracle.qa_fixture()
+    qm = context.load(qd)
+    q = qm.session(2, 24, S.TURBO_PRECISION_EXACT, task=S.TURBO_TASK_EXTRACTIVE_QA)
+    w = np.zeros((1, 24), np.int32)
+    m1 = np.zeros((1, 24), np.int32)
+    w[0, :6], m1[0, :6] = windows[0][0][:6], 1
+    with pytest.raises(T.TurboError) as e:
+        q.write_layer_ranges(w, m1, [(0, 0, 1)], 2, normalize=S.TURBO_NORMALIZE_NONE)
+    assert (e.value.code, e.value.field) == (S.TURBO_E_UNSUPPORTED_OPTION, 9)
+    q.close()
+    qm.close()
+
+
 def test_int8_cross_encoder_meets_the_oracle(context):
     # The int8 rerank workload at full width on 2 of its 12 layers and 12 of
     # its 256 pairs: scores within I8's bound of the F32 oracle's, and the

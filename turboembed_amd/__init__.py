@@ -300,7 +300,8 @@ class Session:
         _ok(self.t.embed_write(self.h, C.byref(r), C.byref(err)), err)
         self.n_out, self.od, self.headed = r.batch, r.output_dim, False
 
-    def write_ranges(self, ids, mask, ranges, types=None, normalize=S.TURBO_NORMALIZE_L2, output_dim=0):
+    def write_ranges(self, ids, mask, ranges, types=None, normalize=S.TURBO_NORMALIZE_L2, output_dim=0, layers=1,
+                     layer_alone=False):
         """Ranges are (row, start, end) triples; pooled by the mean, as the
         core forces for a range write (core/src/session/tokens.rs:132-146).
 
@@ -308,8 +309,30 @@ class Session:
         logits, [count, head_out]: normalize must be NONE (else
         TURBO_E_UNSUPPORTED_OPTION naming field 4) and output_dim 0 or the
         hidden width (field 6), as the core holds them
-        (tokens.rs:140-143, 217-235)."""
+        (tokens.rs:140-143, 217-235).
+
+        layers > 1 reads each range from each of the model's last `layers`
+        layers, rows [layers, count, output_dim] block by block, the last
+        the final layer's; with layer_alone the first of them alone,
+        [count, output_dim] (turbo_embed_write_layer_ranges; the core's
+        checks, tokens.rs:99-130, 153-215)."""
         head = self.model.desc.span_head
+        ranges = list(ranges)
+        if not ranges:
+            raise TurboError(S.TURBO_E_INVALID_ARGUMENT, 0, "count is 0: a run needs at least one range")
+        if layers == 0:
+            raise TurboError(S.TURBO_E_INVALID_ARGUMENT, 9, "layers 0: a range write needs at least 1 layer")
+        if layers > 1:
+            if layers > self.model.desc.layers:
+                raise TurboError(S.TURBO_E_INVALID_ARGUMENT, 9,
+                                 f"layers {layers}: the model has 1 to {self.model.desc.layers} to read")
+            if head is not None:
+                raise TurboError(S.TURBO_E_UNSUPPORTED_OPTION, 9, f"layers {layers}: the span head reads the final layer")
+        alone = bool(layer_alone) and layers > 1
+        blocks = 1 if alone else layers
+        if len(ranges) * blocks > self.max_ranges:
+            raise TurboError(S.TURBO_E_CAPACITY, 0, f"{len(ranges)} ranges from {blocks} layers is "
+                                                    f"{len(ranges) * blocks} vectors, over max_ranges {self.max_ranges}")
         if head is not None:
             if normalize != S.TURBO_NORMALIZE_NONE:
                 raise TurboError(S.TURBO_E_UNSUPPORTED_OPTION, 4, "normalize: the span head's logits are not normalized")
@@ -319,7 +342,7 @@ class Session:
         r = self._rows(ids, mask, types, S.TURBO_POOLING_MEAN, normalize, output_dim)
         if head is not None:
             r.head, r.output_dim = 1, head[0].shape[0]
-        ranges = list(ranges)
+        r.taps, r.tap_alone = layers, 1 if alone else 0
         arr = (S.turbo_token_range * max(1, len(ranges)))()
         for i, (row, start, end) in enumerate(ranges):
             arr[i].row, arr[i].start, arr[i].end = row, start, end
@@ -328,7 +351,12 @@ class Session:
         _ok(self.lib.turbo_rocm_check_ranges(r.batch, r.seq, r.seq, _i32(mask), arr, len(ranges), self.max_ranges,
                                              C.byref(err)), err)
         _ok(self.t.embed_write_ranges(self.h, C.byref(r), arr, len(ranges), C.byref(err)), err)
-        self.n_out, self.od, self.headed = len(ranges), r.output_dim, head is not None
+        self.n_out, self.od, self.headed = len(ranges) * blocks, r.output_dim, head is not None
+
+    def write_layer_ranges(self, ids, mask, ranges, layers, types=None, normalize=S.TURBO_NORMALIZE_L2,
+                           output_dim=0, layer_alone=False):
+        """turbo_embed_write_layer_ranges: write_ranges with `layers` layer reads."""
+        self.write_ranges(ids, mask, ranges, types, normalize, output_dim, layers, layer_alone)
 
     # -- run and read -----------------------------------------------------------
     def run(self):

@@ -155,8 +155,10 @@ int32_t device_info(uint32_t ordinal, turbo_device_info *out, turbo_error *err) 
 }
 
 // Fields of turbo_embed_options a run honors: normalize (4), pooling (5)
-// and output_dim (6), every value of each.
-constexpr uint32_t EMBED_HONORED = (1u << 3) | (1u << 4) | (1u << 5);
+// and output_dim (6), every value of each; layers (9) and layer_alone (10),
+// read from the BERT, RoBERTa, ModernBERT and nomic-bert encoders. Field n
+// is bit n - 1 (core/src/session/tokens.rs:157-162).
+constexpr uint32_t EMBED_HONORED = (1u << 3) | (1u << 4) | (1u << 5) | (1u << 8) | (1u << 9);
 
 int32_t capability(uint32_t ordinal, uint32_t task, uint32_t precision, uint32_t *status, uint32_t *dtype,
                    uint32_t *options_honored, char *reason, uint32_t reason_len, turbo_error *err) {

@@ -622,7 +622,25 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
         fail(TURBO_E_CAPACITY, "rocm: " + std::to_string(r->batch) + " rows of " + std::to_string(r->seq) +
                                    " over the session's " + std::to_string(s->max_batch) + " of " +
                                    std::to_string(s->max_seq));
-    if (r->taps > 1) fail(TURBO_E_UNSUPPORTED_OPTION, "rocm: pooling from earlier layers", 9);
+    // Layer reads (turbo_backend.h:423-435): ranges from each of the last
+    // taps layers, or with tap_alone the first of them alone.
+    const bool has_taps = r->struct_size >= offsetof(turbo_backend_embed_rows, tap_alone) + 4;
+    const uint32_t taps = has_taps && r->taps > 1 ? r->taps : 1;
+    const bool alone = has_taps && r->tap_alone != 0;
+    if (has_taps && r->tap_alone > 1)
+        fail(TURBO_E_INVALID_ARGUMENT, "rocm: tap_alone " + std::to_string(r->tap_alone) + " (0 or 1)", 10);
+    if (taps > 1) {
+        if (count == 0) fail(TURBO_E_INVALID_ARGUMENT, "rocm: layer reads pool ranges", 9);
+        if (taps > s->model->layers)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: layers " + std::to_string(taps) + ": the model has 1 to " +
+                                               std::to_string(s->model->layers) + " to read", 9);
+        if (r->head) fail(TURBO_E_UNSUPPORTED_OPTION, "rocm: the span head reads the final layer", 9);
+        if (!alone && (uint64_t)taps * count > s->max_ranges)
+            fail(TURBO_E_CAPACITY, "rocm: " + std::to_string(count) + " ranges from " + std::to_string(taps) +
+                                       " layers over max_ranges " + std::to_string(s->max_ranges));
+    } else if (alone) {
+        fail(TURBO_E_INVALID_ARGUMENT, "rocm: tap_alone with one layer read", 10);
+    }
     // A headed write (turbo_backend.h:418-422): ranges on a model with a
     // span head, rows [count, head_out], normalize NONE.
     const bool head = r->struct_size >= offsetof(turbo_backend_embed_rows, head) + 4 && r->head;
@@ -698,6 +716,8 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     s->normalize = r->normalize;
     s->output_dim = r->output_dim;
     s->head = head;
+    s->taps = taps;
+    s->tap_alone = alone;
     s->count = count;
     s->tokens = tokens;
     s->max_len = max_len;
@@ -839,7 +859,17 @@ void encode(Session &s) {
     // The GEMM operand copy of x after an add + LayerNorm: xh, or on the F32
     // tier x itself (post-norm) or xh as F32 (pre-norm).
     void *norm_out = f32 && !m.modern ? nullptr : s.xh;
-    for (uint32_t l = 0; l < m.layers; ++l) {
+    // Layers run: every one, or through the one read alone (a model cut
+    // after it). Ranges are pooled after each of the last `reads` layers run
+    // into block k of the output, [reads, count, output_dim], the final
+    // layer's last (reference core/src/cpu/encoder/mod.rs:292-373). A
+    // ModernBERT read is final_norm(x), the scale the final states are on
+    // (core/src/cpu/encoder/rotary/mod.rs:84-86, 161-168), normed into y,
+    // which is free between a layer's last add and the next layer's out product.
+    const uint32_t nl = s.tap_alone ? m.layers + 1 - s.taps : m.layers;
+    const uint32_t reads = s.tap_alone ? 1 : s.taps;
+    const int od = (int)s.output_dim, l2 = s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0;
+    for (uint32_t l = 0; l < nl; ++l) {
         const Model::Layer &L = m.ls[l];
         int window = INT32_MAX;
         if (m.rotary) {
@@ -861,11 +891,21 @@ void encode(Session &s) {
         // attention norm into xh, or after the last layer x = LN_final(x + y).
         if (!m.modern)
             LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out, dt));
-        else if (l + 1 < m.layers)
+        else if (l + 1 < nl)
             LAUNCH("add_layer_norm",
                    add_layer_norm(st, T, H, s.x, s.y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps, 1, norm_out, dt));
         else
             LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
+        if (reads > 1 && l + 1 < nl && l + reads >= nl) {
+            const float *src = s.x;
+            if (m.modern) {
+                LAUNCH("layer_norm", layer_norm(st, T, H, s.x, m.final_w, nullptr, m.eps, (float *)s.y, nullptr, Dt::F32));
+                src = (const float *)s.y;
+            }
+            float *block = s.out + (size_t)(l + reads - nl) * s.count * od;
+            LAUNCH("pool", pool(st, src, H, s.pk, s.mask, (int)s.seq, (int)s.count, s.ranges, (int)s.pooling, od, l2,
+                                block));
+        }
     }
     const int n_out = s.count ? (int)s.count : (int)s.batch;
     if (s.head)
@@ -873,7 +913,7 @@ void encode(Session &s) {
                                       (int)m.head_out, s.out));
     else
         LAUNCH("pool", pool(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.count ? s.ranges : nullptr,
-                            (int)s.pooling, (int)s.output_dim, s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0, s.out));
+                            (int)s.pooling, od, l2, s.out + (size_t)(reads - 1) * s.count * od));
 #undef LAUNCH
 }
 
@@ -882,8 +922,9 @@ void launch_run(Session &s) {
         encode(s);
         return;
     }
-    const Session::RunShape key{s.tokens, s.batch,     s.seq,        s.max_len,       s.count,
-                                s.pooling, s.normalize, s.output_dim, (uint32_t)s.head};
+    const Session::RunShape key{s.tokens,         s.batch,  s.seq,  s.max_len,         s.count,
+                                s.pooling,        s.normalize, s.output_dim, (uint32_t)s.head, s.taps,
+                                (uint32_t)s.tap_alone};
     auto it = s.graph_of.find(key);
     if (it == s.graph_of.end()) {
         constexpr size_t KEEP = 16;
@@ -1046,7 +1087,7 @@ void session_run(Session *s, turbo_backend_run *out) {
         check(hipStreamSynchronize(s->ctx->stream), "the run");
         collect_times(*s);
     }
-    const uint32_t n_out = s->count ? s->count : s->batch;
+    const uint32_t n_out = s->count ? s->count * (s->tap_alone ? 1 : s->taps) : s->batch;
     s->output.bytes = (uint64_t)n_out * s->output_dim * 4;
     out->placement = TURBO_PLACE_DEVICE;
     out->output = &s->output;

@@ -150,21 +150,28 @@ struct Session {
     uint32_t batch = 0, seq = 0, pooling = 0, normalize = 0, output_dim = 0, count = 0, tokens = 0, max_len = 0;
     bool has_types = false;
     bool head = false;   // ranges through the span head
+    // Layer reads of a range write: the last `taps` layers' states, [taps,
+    // count, output_dim]; with tap_alone, the first of them alone (the model
+    // cut after layer L - taps + 1).
+    uint32_t taps = 1;
+    bool tap_alone = false;
     uint64_t h2d = 0;
     std::vector<LayerWeights> *w = nullptr;
     Choices kc;            // kernel choices per bin of packed tokens
     std::string choices;   // kc as a choices string
     // A run's launches captured as a graph, per run shape (tokens, rows,
-    // columns, longest row, ranges, pooling, normalize, output width): a run
+    // columns, longest row, ranges, pooling, normalize, output width, head,
+    // layer reads): a run
     // of a shape seen before is one graph launch. Off while timing, or with
     // TURBO_ROCM_GRAPHS=0.
     struct RunShape {
-        uint32_t tokens, batch, seq, max_len, count, pooling, normalize, output_dim, head;
+        uint32_t tokens, batch, seq, max_len, count, pooling, normalize, output_dim, head, taps, tap_alone;
         bool operator<(const RunShape &o) const {
-            const uint32_t a[9] = {tokens, batch, seq, max_len, count, pooling, normalize, output_dim, head};
-            const uint32_t b[9] = {o.tokens,  o.batch,     o.seq,        o.max_len, o.count,
-                                   o.pooling, o.normalize, o.output_dim, o.head};
-            return std::lexicographical_compare(a, a + 9, b, b + 9);
+            const uint32_t a[11] = {tokens, batch, seq, max_len, count, pooling, normalize, output_dim, head, taps,
+                                    tap_alone};
+            const uint32_t b[11] = {o.tokens,     o.batch, o.seq,  o.max_len, o.count,    o.pooling,
+                                    o.normalize, o.output_dim, o.head, o.taps, o.tap_alone};
+            return std::lexicographical_compare(a, a + 11, b, b + 11);
         }
     };
     bool graphs = true;
