@@ -214,6 +214,24 @@ def qa_fixture():
     print("tiny_qa", len(used), "word rows")
 
 
+def bundle_files():
+    """tiny-modernbert-bundle as it is sealed (manifest.json, its weights and
+    its reference; the tokenizer is not read here and stays out), and the
+    manifests of tiny-bert-bundle and tiny-nomic-bundle, whose tensor names
+    the bundle tests build weights files under."""
+    src = os.path.join(REF, "tiny-modernbert-bundle")
+    dst = os.path.join(HERE, "tiny-modernbert-bundle")
+    for rel in ("manifest.json", "weights/model.safetensors", "reference/reference.safetensors"):
+        os.makedirs(os.path.dirname(os.path.join(dst, rel)), exist_ok=True)
+        with open(os.path.join(src, rel), "rb") as f, open(os.path.join(dst, rel), "wb") as g:
+            g.write(f.read())
+    os.makedirs(os.path.join(HERE, "manifests"), exist_ok=True)
+    for b in ("tiny-bert-bundle", "tiny-nomic-bundle"):
+        with open(os.path.join(REF, b, "manifest.json"), "rb") as f, \
+                open(os.path.join(HERE, "manifests", b + ".json"), "wb") as g:
+            g.write(f.read())
+
+
 def quantize_golden():
     src = os.path.join(REF, "quantize", "sentence-transformers-145ef47d.txt")
     dst = os.path.join(HERE, "quantize-sentence-transformers-145ef47d.txt")
@@ -229,4 +247,5 @@ if __name__ == "__main__":
     one("tiny-nomic-bundle", "tiny_nomic")
     rerank_fixture()
     qa_fixture()
+    bundle_files()
     quantize_golden()

@@ -75,6 +75,27 @@ def test_tiny_bundles_meet_the_upstream_vectors(context, name, precision):
     model.close()
 
 
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+def test_a_sealed_bundle_loads_and_meets_its_vectors(context, precision):
+    # The tiny ModernBERT bundle as it is sealed, through load_bundle: its
+    # files verified, its description built from the manifest, its
+    # reference rows at the manifest's pooling, normalization and width.
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny-modernbert-bundle")
+    model = context.load_bundle(path)
+    ref = model.bundle.reference()
+    pooling, normalize, dim, max_seq, max_batch = model.bundle.embed_defaults()
+    ids = ref["ids"].astype(np.int32)
+    mask = (np.arange(ids.shape[1])[None, :] < ref["lengths"][:, None]).astype(np.int32)
+    s = model.session(max_batch, max_seq, precision)
+    for at in range(0, ids.shape[0], max_batch):
+        got = s.embed(ids[at:at + max_batch], mask[at:at + max_batch], pooling=pooling, normalize=normalize,
+                      output_dim=dim)
+        assert_close(got, ref["embeddings"][at:at + max_batch], s.compute_dtype)
+    s.close()
+    model.close()
+
+
 # ---- Small models of every family, ragged rows ------------------------------------------
 
 MODELS = {"bert": small.bert, "modernbert": small.modernbert, "nomic": small.nomic}

@@ -128,6 +128,16 @@ class Context:
     def load(self, desc: ModelDesc):
         return Model(self, desc)
 
+    def load_bundle(self, path, artifact=0):
+        """turbo_model_load of a bundle directory: the manifest's artifact
+        read and verified (bundle.Bundle), then model_load. The model keeps
+        the bundle as .bundle."""
+        from .bundle import Bundle
+        b = Bundle(path)
+        m = Model(self, b.model_desc(artifact))
+        m.bundle = b
+        return m
+
     def buffer(self, nbytes, placement=S.TURBO_PLACE_SHARED):
         """A buffer of the context's device (buffer_alloc): DEVICE, PINNED,
         SHARED or HOST; the last three have a host pointer."""
