@@ -383,6 +383,63 @@ def test_rerank_refuses_what_the_core_refuses(context):
     model.close()
 
 
+# ---- Split runs: two parts of the rows on two streams -------------------------------------
+#
+# A run of at least 4096 packed tokens and two rows or more runs its rows in
+# two parts on the context's two streams. Each part's products, norms and
+# attention read and write its own tokens alone, so the vectors are the
+# oracle's at the tier's bound and, token for token, the unsplit run's.
+
+def _long_rows(seed, batch, seq, vocab, types):
+    g = np.random.Generator(np.random.PCG64(seed))
+    lengths = g.integers(300, seq + 1, batch)
+    ids = g.integers(0, vocab, (batch, seq)).astype(np.int32)
+    mask = (np.arange(seq)[None, :] < lengths[:, None]).astype(np.int32)
+    mask[3, 5] = 0                                   # a hole
+    ty = g.integers(0, types, (batch, seq)).astype(np.int32) if types > 1 else None
+    assert mask.sum() >= 4096
+    return ids, mask, ty
+
+
+def _unsplit(model, monkeypatch, *a, **kw):
+    monkeypatch.setenv("TURBO_ROCM_SPLIT", "0")
+    s = model.session(*a, **kw)
+    monkeypatch.delenv("TURBO_ROCM_SPLIT")
+    return s
+
+
+@pytest.mark.parametrize("family", ["bert", "modernbert", "nomic"])
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST, "int8"])
+def test_split_runs_meet_the_oracle_and_the_unsplit_run(context, monkeypatch, family, precision):
+    kw = dict(seed=41, hidden=128, inter=256, positions=512 if family == "bert" else 1024)
+    desc = MODELS[family](**kw)
+    if precision == "int8":
+        desc, precision = int8_model(desc), S.TURBO_PRECISION_FASTEST
+    ids, mask, types = _long_rows(5, 16, 512, desc.vocab_size, max(1, desc.token_types))
+    model = context.load(desc)
+    s = model.session(16, 512, precision, max_ranges=64)
+    u = _unsplit(model, monkeypatch, 16, 512, precision, max_ranges=64)
+    got = s.embed(ids, mask, types)
+    want = oracle.encode(desc, ids, mask, types)
+    if s.compute_dtype == S.TURBO_DTYPE_I8:
+        assert small.cosine_rows(got, want).min() >= I8_FLOOR
+    else:
+        assert_close(got, want, s.compute_dtype)
+    assert small.cosine_rows(got, u.embed(ids, mask, types)).min() >= 0.99999
+    # The same shape again (a graph replay), then ranges across both parts.
+    np.testing.assert_array_equal(s.embed(ids, mask, types), got)
+    ranges = [(r, 0, 40) for r in range(16)] + [(7, 100, 299), (15, 1, 2)]
+    s.write_ranges(ids, mask, ranges, types)
+    s.run()
+    rg = s.read()
+    u.write_ranges(ids, mask, ranges, types)
+    u.run()
+    assert small.cosine_rows(rg, u.read()).min() >= 0.99999
+    s.close()
+    u.close()
+    model.close()
+
+
 # ---- Extractive QA: the span head on the device ------------------------------------------
 #
 # testdata/tiny-qa-reference's transformers logits for every token of six

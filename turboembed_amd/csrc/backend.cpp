@@ -189,8 +189,19 @@ int32_t context_create(uint32_t ordinal, turbo_log_fn log, void *ud, void **out,
         c->log = log;
         c->log_user_data = ud;
         OnDevice on(c->ordinal);
-        // Default priority: the one stream priority every run uses.
+        // Default priority on both streams: the one stream priority every run
+        // uses. The second carries half of a split run's rows; the events
+        // fork it from the first and join it back.
         check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+        if (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&c->fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&c->join, hipEventDisableTiming) != hipSuccess) {
+            if (c->join) (void)hipEventDestroy(c->join);
+            if (c->fork) (void)hipEventDestroy(c->fork);
+            if (c->side) (void)hipStreamDestroy(c->side);
+            (void)hipStreamDestroy(c->stream);
+            fail(TURBO_E_RUNTIME, "rocm: the context's second stream and its events");
+        }
         *out = c.release();
         return TURBO_OK;
     });
@@ -202,6 +213,10 @@ void context_release(void *ctx) {
     {
         OnDevice on(c->ordinal);
         (void)hipStreamSynchronize(c->stream);
+        (void)hipStreamSynchronize(c->side);
+        (void)hipEventDestroy(c->fork);
+        (void)hipEventDestroy(c->join);
+        (void)hipStreamDestroy(c->side);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;

@@ -115,7 +115,7 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
                 // the neighbouring lane (column n sits in lane n % 32).
                 const float w = __shfl_xor(v, 1, 64);
                 if (which < 2 && col_ok && m < M) {
-                    const int pos = e.at[m] % e.seq;
+                    const int pos = e.at[e.tok0 + m] % e.seq;
                     const float cs = e.cos[(size_t)pos * half + pr], sn = e.sin[(size_t)pos * half + pr];
                     // (x1, x2) -> (x1 cos - x2 sin, x2 cos + x1 sin)
                     v = (c & 1) ? __fadd_rn(__fmul_rn(v, cs), __fmul_rn(w, sn))
@@ -124,7 +124,8 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
             }
             if (!col_ok || m >= M) continue;
             // Q and K token-major per head; V transposed per head.
-            const size_t at = which < 2 ? ((size_t)head * e.tcap + m) * e.d + c : ((size_t)head * e.d + c) * e.tcap + m;
+            const size_t t = (size_t)e.tok0 + m;
+            const size_t at = which < 2 ? ((size_t)head * e.tcap + t) * e.d + c : ((size_t)head * e.d + c) * e.tcap + t;
             out[at] = from_f32<T>(v);
         }
     } else {   // Gated: out[m, n / 2] = act(gate) * up, gate and up in neighbouring columns
@@ -346,8 +347,8 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
 #pragma unroll
                         for (int q = 0; q < 8; ++q) v[q] = scratch[(g + q) * SROW + col] + bias;
                     }
-                    T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + ((size_t)head * e.d + c) * e.tcap;
-                    if (m + 8 <= M && (e.tcap & 7) == 0) {
+                    T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + ((size_t)head * e.d + c) * e.tcap + e.tok0;
+                    if (m + 8 <= M && ((e.tcap | e.tok0) & 7) == 0) {
                         store8<T>(out + m, v);
                     } else {
 #pragma unroll
@@ -442,7 +443,7 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                 const int which = n / e.hidden, rem = n - which * e.hidden;
                 const int head = rem / e.d, c = rem - head * e.d;
                 if constexpr (KIND == Epi::QkvRope) {
-                    const int pos = e.at[m] % e.seq, half = e.d >> 1;
+                    const int pos = e.at[e.tok0 + m] % e.seq, half = e.d >> 1;
 #pragma unroll
                     for (int p = 0; p < 4; ++p) {
                         const int pr = (c >> 1) + p;
@@ -452,11 +453,12 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                         v[2 * p + 1] = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
                     }
                 }
-                T *o = (T *)e.out + (size_t)which * e.heads * e.tcap * e.d + ((size_t)head * e.tcap + m) * e.d + c;
+                const size_t t = (size_t)e.tok0 + m;
+                T *o = (T *)e.out + (size_t)which * e.heads * e.tcap * e.d + ((size_t)head * e.tcap + t) * e.d + c;
                 if (full && (e.d & 7) == 0) store8<T>(o, v);
                 else for (int q = 0; q < 8 && n + q < N; ++q) {
                     const int nq = n + q, wq = nq / e.hidden, rq = nq - wq * e.hidden, hq = rq / e.d, cq = rq - hq * e.d;
-                    ((T *)e.out)[(size_t)wq * e.heads * e.tcap * e.d + ((size_t)hq * e.tcap + m) * e.d + cq] =
+                    ((T *)e.out)[(size_t)wq * e.heads * e.tcap * e.d + ((size_t)hq * e.tcap + t) * e.d + cq] =
                         from_f32<T>(v[q]);
                 }
             }

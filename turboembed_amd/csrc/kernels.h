@@ -67,6 +67,7 @@ struct EpiArgs {
     int ldo = 0;                   // row stride of out (elements)
     float *x = nullptr;            // Residual: [m, ldo] F32
     int tcap = 0, heads = 0, d = 0, hidden = 0;   // Qkv scatter
+    int tok0 = 0;                  // Qkv, QkvRope: the packed token of row 0 of A (of at, and of the scatter)
     const float *cos = nullptr, *sin = nullptr;   // QkvRope: [positions][d / 2]
     const int32_t *at = nullptr;   // QkvRope: each token's r * seq + p
     int seq = 0;

@@ -514,6 +514,7 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         if (!mfma_attn) kc.bin[b].simple_attention = true;
     const bool measure = ((mode == TURBO_AUTOTUNE_ON && !cached) || mode == TURBO_AUTOTUNE_RETUNE) && !all_forced(kc);
     if (const char *g = std::getenv("TURBO_ROCM_GRAPHS")) s->graphs = std::strcmp(g, "0") != 0;
+    if (const char *g = std::getenv("TURBO_ROCM_SPLIT")) s->split_ok = std::strcmp(g, "0") != 0;
 
     const size_t H = m->hidden, I = m->inter, B = s->max_batch, S = s->max_seq;
     s->tcap = B * S;
@@ -616,6 +617,9 @@ void session_release(Session *s) {
     delete s;
 }
 
+// Runs of at least this many packed tokens split their rows over two streams.
+constexpr uint32_t SPLIT_MIN_TOKENS = 4096;
+
 void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_token_range *ranges, uint32_t count) {
     if (r->batch == 0 || r->seq == 0) fail(TURBO_E_INVALID_SHAPE, "rocm: batch and seq may not be 0");
     if (r->batch > s->max_batch || r->seq > s->max_seq)
@@ -667,6 +671,7 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     int32_t *ids = s->staging, *mask = ids + (size_t)B * S, *types = mask + (size_t)B * S;
     uint32_t *rg = reinterpret_cast<uint32_t *>(types + (size_t)B * S);
     uint32_t tokens = 0, max_len = 0;
+    std::vector<uint32_t> lens(B);
     const Model &m = *s->model;
     const int32_t ntypes = (int32_t)std::max(1u, m.types);
     for (uint32_t row = 0; row < B; ++row) {
@@ -689,6 +694,7 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
                 break;
             }
         if (len == 0) fail(TURBO_E_INVALID_ARGUMENT, "rocm: row " + std::to_string(row) + " has no live token");
+        lens[row] = len;
         tokens += len;
         max_len = std::max(max_len, len);
     }
@@ -718,6 +724,19 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     s->head = head;
     s->taps = taps;
     s->tap_alone = alone;
+    // Split the rows in two where the packed tokens (rows in order) reach
+    // half, on runs large enough to fill the device twice over; not when
+    // ranges are read from layers before the last (each read pools every row).
+    s->split_rows = s->split_tokens = s->split_max_len[0] = s->split_max_len[1] = 0;
+    if (s->split_ok && B >= 2 && tokens >= SPLIT_MIN_TOKENS && (alone || taps == 1)) {
+        uint32_t r = 0, t = 0;
+        while (r + 1 < B && 2 * t < tokens) t += lens[r++];
+        if (r == 0) t = lens[r++];
+        s->split_rows = r;
+        s->split_tokens = t;
+        for (uint32_t i = 0; i < B; ++i)
+            s->split_max_len[i < r ? 0 : 1] = std::max(s->split_max_len[i < r ? 0 : 1], lens[i]);
+    }
     s->count = count;
     s->tokens = tokens;
     s->max_len = max_len;
@@ -818,18 +837,30 @@ static LayerGemm layer_gemm(Session &s, uint32_t l, GemmSlot g) {
     return r;
 }
 
-void encode(Session &s) {
+namespace {
+
+// Rows [row0, row0 + rows) of a run and their packed tokens [tok0, tok0 + tokens).
+struct Part {
+    uint32_t row0, rows, tok0, tokens, max_len;
+};
+
+}  // namespace
+
+// The layers over one part of the run's rows, on stream st: every product,
+// norm and attention launch reads and writes that part's tokens alone.
+static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) {
     Model &m = *s.model;
-    hipStream_t st = s.ctx->stream;
-    const int T = (int)s.tokens, H = (int)m.hidden, heads = (int)m.heads, dh = H / heads;
+    const int T = (int)part.tokens, H = (int)m.hidden, I = (int)m.inter, heads = (int)m.heads, dh = H / heads;
     const Dt dt = s.act;   // activations; the GEMMs take s.dt
     const bool f32 = dt == Dt::F32, i8 = s.dt == Dt::I8;
-    const BinChoice &bc = s.kc.bin[bin_of(s.tokens, s.kc.bins)];
-    Timer tm(s);
-    auto run = [&](const char *name, hipError_t e) {
-        (void)name;
-        check(e, name);
+    const size_t el = dt_bytes(dt), t0 = part.tok0;
+    const BinChoice &bc = s.kc.bin[bin_of(part.tokens, s.kc.bins)];
+    auto at = [&](void *base, size_t width, size_t bytes) -> void * {
+        return base ? static_cast<char *>(base) + t0 * width * bytes : nullptr;
     };
+    float *x = s.x + t0 * H;
+    void *xh = at(s.xh, H, el), *y = at(s.y, H, dt_bytes(s.ydt));
+    auto run = [&](const char *name, hipError_t e) { check(e, name); };
 #define LAUNCH(NAME, CALL) \
     do {                   \
         tm.begin(NAME);    \
@@ -837,33 +868,39 @@ void encode(Session &s) {
         tm.end();          \
     } while (0)
     // One GEMM of the layer. On the I8 tier its operand rows are quantized
-    // first (per token), and the epilogue takes both scales.
+    // first (per token; each part's rows at its own tokens of the operand
+    // buffer, whose rows are max(H, I) wide), and the epilogue takes both scales.
     static const char *const NAMES[G_COUNT] = {"gemm_qkv", "gemm_out", "gemm_ffn_in", "gemm_ffn_out"};
     auto mm = [&](uint32_t l, GemmSlot g) {
         LayerGemm lg = layer_gemm(s, l, g);
-        const void *A = lg.A;
+        const void *A = static_cast<const char *>(lg.A) + t0 * lg.K * (lg.A == s.x ? 4 : el);
+        switch (g) {
+        case G_QKV: lg.e.tok0 = (int)t0; break;
+        case G_FFN1: lg.e.out = at(lg.e.out, I, el); break;
+        default: lg.e.out = y; break;
+        }
         if (i8) {
-            LAUNCH("quantize", quantize_rows(st, A, Dt::F16, T, lg.K, lg.K, s.aq, s.ascale));
-            lg.e.a_scale = s.ascale;
+            int8_t *aq = s.aq + t0 * std::max(H, I);
+            LAUNCH("quantize", quantize_rows(st, A, Dt::F16, T, lg.K, lg.K, aq, s.ascale + t0));
+            lg.e.a_scale = s.ascale + t0;
             lg.e.w_scale = lg.wscale;
-            A = s.aq;
+            A = aq;
         }
         LAUNCH(NAMES[g], gemm(st, s.dt, T, lg.N, lg.K, A, lg.K, lg.W, lg.e, bc.tile[g]));
     };
-    LAUNCH("pack_rows", pack_rows(st, s.mask, (int)s.batch, (int)s.seq, s.pk));
-    LAUNCH("embed_ln", embed_ln(st, T, H, s.ids, s.types, s.pk, (int)s.seq, (int)m.position_offset, m.word, m.pos,
-                                m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
-    // ModernBERT's first layer reads the embeddings' rows as they are (no
-    // attention norm); on the F32 tier xh is the pre-norm rows' F32 copy.
-    if (m.modern && f32) LAUNCH("copy", copy_bytes(st, s.x, s.xh, (size_t)T * H * 4));
+    Packing pk = s.pk;
+    pk.start += part.row0;
+    pk.len += part.row0;
+    const int32_t *mask = s.mask + (size_t)part.row0 * s.seq;
     // The GEMM operand copy of x after an add + LayerNorm: xh, or on the F32
     // tier x itself (post-norm) or xh as F32 (pre-norm).
-    void *norm_out = f32 && !m.modern ? nullptr : s.xh;
+    void *norm_out = f32 && !m.modern ? nullptr : xh;
     // Layers run: every one, or through the one read alone (a model cut
     // after it). Ranges are pooled after each of the last `reads` layers run
     // into block k of the output, [reads, count, output_dim], the final
-    // layer's last (reference core/src/cpu/encoder/mod.rs:292-373). A
-    // ModernBERT read is final_norm(x), the scale the final states are on
+    // layer's last (reference core/src/cpu/encoder/mod.rs:292-373); a run
+    // with reads before the last is never split. A ModernBERT read is
+    // final_norm(x), the scale the final states are on
     // (core/src/cpu/encoder/rotary/mod.rs:84-86, 161-168), normed into y,
     // which is free between a layer's last add and the next layer's out product.
     const uint32_t nl = s.tap_alone ? m.layers + 1 - s.taps : m.layers;
@@ -877,25 +914,25 @@ void encode(Session &s) {
             if (!global) window = (int)m.window;
         }
         mm(l, G_QKV);
-        LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, (int)s.seq, (int)s.batch,
-                                      (int)s.max_len, window, s.ctxb, bc.simple_attention));
+        LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, pk, mask, (int)s.seq, (int)part.rows,
+                                      (int)part.max_len, window, s.ctxb, bc.simple_attention));
         mm(l, G_OUT);
         // Post-norm: x = LN1(x + y). Pre-norm: x += y, xh = LN_mlp(x).
         if (m.modern)
-            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt));
+            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, x, y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt));
         else
-            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out, dt));
+            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, x, y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out, dt));
         mm(l, G_FFN1);
         mm(l, G_FFN2);
         // Post-norm: x = LN2(x + y). Pre-norm: x += y and the next layer's
         // attention norm into xh, or after the last layer x = LN_final(x + y).
         if (!m.modern)
-            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out, dt));
+            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, x, y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out, dt));
         else if (l + 1 < nl)
             LAUNCH("add_layer_norm",
-                   add_layer_norm(st, T, H, s.x, s.y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps, 1, norm_out, dt));
+                   add_layer_norm(st, T, H, x, y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps, 1, norm_out, dt));
         else
-            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, s.x, s.y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
+            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, x, y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
         if (reads > 1 && l + 1 < nl && l + reads >= nl) {
             const float *src = s.x;
             if (m.modern) {
@@ -907,6 +944,49 @@ void encode(Session &s) {
                                 block));
         }
     }
+#undef LAUNCH
+}
+
+void encode(Session &s) {
+    Model &m = *s.model;
+    Context &c = *s.ctx;
+    hipStream_t st = c.stream;
+    const int T = (int)s.tokens, H = (int)m.hidden;
+    const Dt dt = s.act;
+    const bool f32 = dt == Dt::F32;
+    Timer tm(s);
+    auto run = [&](const char *name, hipError_t e) { check(e, name); };
+#define LAUNCH(NAME, CALL) \
+    do {                   \
+        tm.begin(NAME);    \
+        run(NAME, CALL);   \
+        tm.end();          \
+    } while (0)
+    LAUNCH("pack_rows", pack_rows(st, s.mask, (int)s.batch, (int)s.seq, s.pk));
+    LAUNCH("embed_ln", embed_ln(st, T, H, s.ids, s.types, s.pk, (int)s.seq, (int)m.position_offset, m.word, m.pos,
+                                m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
+    // ModernBERT's first layer reads the embeddings' rows as they are (no
+    // attention norm); on the F32 tier xh is the pre-norm rows' F32 copy.
+    if (m.modern && f32) LAUNCH("copy", copy_bytes(st, s.x, s.xh, (size_t)T * H * 4));
+    // A split run: the rows' two parts run their layers on the context's two
+    // streams, forked here and joined before the pooling, so one part's
+    // memory-bound and latency-bound launches overlap the other's products.
+    // (Not while timing launches: their events are on the first stream.)
+    if (s.split_rows && !s.timing) {
+        const Part a{0, s.split_rows, 0, s.split_tokens, s.split_max_len[0]};
+        const Part b{s.split_rows, s.batch - s.split_rows, s.split_tokens, s.tokens - s.split_tokens,
+                     s.split_max_len[1]};
+        check(hipEventRecord(c.fork, st), "forking the run");
+        check(hipStreamWaitEvent(c.side, c.fork, 0), "forking the run");
+        run_layers(s, st, a, tm);
+        run_layers(s, c.side, b, tm);
+        check(hipEventRecord(c.join, c.side), "joining the run");
+        check(hipStreamWaitEvent(st, c.join, 0), "joining the run");
+    } else {
+        run_layers(s, st, Part{0, s.batch, 0, s.tokens, s.max_len}, tm);
+    }
+    const uint32_t reads = s.tap_alone ? 1 : s.taps;
+    const int od = (int)s.output_dim, l2 = s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0;
     const int n_out = s.count ? (int)s.count : (int)s.batch;
     if (s.head)
         LAUNCH("pool_head", pool_head(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.ranges, m.head_w, m.head_b,
@@ -922,9 +1002,10 @@ void launch_run(Session &s) {
         encode(s);
         return;
     }
-    const Session::RunShape key{s.tokens,         s.batch,  s.seq,  s.max_len,         s.count,
-                                s.pooling,        s.normalize, s.output_dim, (uint32_t)s.head, s.taps,
-                                (uint32_t)s.tap_alone};
+    const Session::RunShape key{s.tokens,     s.batch,       s.seq,        s.max_len,
+                                s.count,      s.pooling,     s.normalize,  s.output_dim,
+                                s.head,       s.taps,        s.tap_alone,  s.split_rows,
+                                s.split_tokens, s.split_max_len[0], s.split_max_len[1]};
     auto it = s.graph_of.find(key);
     if (it == s.graph_of.end()) {
         constexpr size_t KEEP = 16;

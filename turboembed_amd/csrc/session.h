@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <array>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -71,6 +72,8 @@ using DevPtr = std::unique_ptr<void, DevFree>;
 struct Context {
     int ordinal = 0;                 // the HIP device
     hipStream_t stream = nullptr;
+    hipStream_t side = nullptr;      // a split run's second half of rows
+    hipEvent_t fork = nullptr, join = nullptr;
     turbo_log_fn log = nullptr;
     void *log_user_data = nullptr;
     std::mutex lock;                 // a launch through its sync, and reads
@@ -155,6 +158,11 @@ struct Session {
     // cut after layer L - taps + 1).
     uint32_t taps = 1;
     bool tap_alone = false;
+    // A split run (split_rows > 0): rows [0, split_rows) and the rest run
+    // their layers on two streams; the first part's packed tokens and each
+    // part's longest row. Off with TURBO_ROCM_SPLIT=0.
+    bool split_ok = true;
+    uint32_t split_rows = 0, split_tokens = 0, split_max_len[2] = {0, 0};
     uint64_t h2d = 0;
     std::vector<LayerWeights> *w = nullptr;
     Choices kc;            // kernel choices per bin of packed tokens
@@ -164,16 +172,9 @@ struct Session {
     // layer reads): a run
     // of a shape seen before is one graph launch. Off while timing, or with
     // TURBO_ROCM_GRAPHS=0.
-    struct RunShape {
-        uint32_t tokens, batch, seq, max_len, count, pooling, normalize, output_dim, head, taps, tap_alone;
-        bool operator<(const RunShape &o) const {
-            const uint32_t a[11] = {tokens, batch, seq, max_len, count, pooling, normalize, output_dim, head, taps,
-                                    tap_alone};
-            const uint32_t b[11] = {o.tokens,     o.batch, o.seq,  o.max_len, o.count,    o.pooling,
-                                    o.normalize, o.output_dim, o.head, o.taps, o.tap_alone};
-            return std::lexicographical_compare(a, a + 11, b, b + 11);
-        }
-    };
+    // tokens, batch, seq, max_len, count, pooling, normalize, output_dim,
+    // head, taps, tap_alone, split_rows, split_tokens, split_max_len[0, 1].
+    using RunShape = std::array<uint32_t, 15>;
     bool graphs = true;
     std::map<RunShape, hipGraphExec_t> graph_of;
     std::vector<RunShape> graph_order;   // oldest first, for eviction
