@@ -408,15 +408,17 @@ def _unsplit(model, monkeypatch, *a, **kw):
     return s
 
 
+@pytest.mark.parametrize("parts", ["2", "4"])
 @pytest.mark.parametrize("family", ["bert", "modernbert", "nomic"])
 @pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST, "int8"])
-def test_split_runs_meet_the_oracle_and_the_unsplit_run(context, monkeypatch, family, precision):
+def test_split_runs_meet_the_oracle_and_the_unsplit_run(context, monkeypatch, parts, family, precision):
     kw = dict(seed=41, hidden=128, inter=256, positions=512 if family == "bert" else 1024)
     desc = MODELS[family](**kw)
     if precision == "int8":
         desc, precision = int8_model(desc), S.TURBO_PRECISION_FASTEST
     ids, mask, types = _long_rows(5, 16, 512, desc.vocab_size, max(1, desc.token_types))
     model = context.load(desc)
+    monkeypatch.setenv("TURBO_ROCM_SPLIT", parts)      # at most 3 parts of these rows' tokens
     s = model.session(16, 512, precision, max_ranges=64)
     u = _unsplit(model, monkeypatch, 16, 512, precision, max_ranges=64)
     got = s.embed(ids, mask, types)

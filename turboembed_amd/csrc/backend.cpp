@@ -189,18 +189,22 @@ int32_t context_create(uint32_t ordinal, turbo_log_fn log, void *ud, void **out,
         c->log = log;
         c->log_user_data = ud;
         OnDevice on(c->ordinal);
-        // Default priority on both streams: the one stream priority every run
-        // uses. The second carries half of a split run's rows; the events
-        // fork it from the first and join it back.
+        // Default priority on every stream: the one stream priority every run
+        // uses. The side streams carry a split run's other parts of rows; the
+        // events fork them from the first and join them back.
         check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
-        if (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
-            hipEventCreateWithFlags(&c->fork, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&c->join, hipEventDisableTiming) != hipSuccess) {
-            if (c->join) (void)hipEventDestroy(c->join);
+        bool ok = hipEventCreateWithFlags(&c->fork, hipEventDisableTiming) == hipSuccess;
+        for (int i = 0; i < Context::SIDES && ok; ++i)
+            ok = hipStreamCreateWithFlags(&c->side[i], hipStreamNonBlocking) == hipSuccess &&
+                 hipEventCreateWithFlags(&c->join[i], hipEventDisableTiming) == hipSuccess;
+        if (!ok) {
+            for (int i = 0; i < Context::SIDES; ++i) {
+                if (c->join[i]) (void)hipEventDestroy(c->join[i]);
+                if (c->side[i]) (void)hipStreamDestroy(c->side[i]);
+            }
             if (c->fork) (void)hipEventDestroy(c->fork);
-            if (c->side) (void)hipStreamDestroy(c->side);
             (void)hipStreamDestroy(c->stream);
-            fail(TURBO_E_RUNTIME, "rocm: the context's second stream and its events");
+            fail(TURBO_E_RUNTIME, "rocm: the context's side streams and their events");
         }
         *out = c.release();
         return TURBO_OK;
@@ -213,10 +217,12 @@ void context_release(void *ctx) {
     {
         OnDevice on(c->ordinal);
         (void)hipStreamSynchronize(c->stream);
-        (void)hipStreamSynchronize(c->side);
+        for (int i = 0; i < Context::SIDES; ++i) {
+            (void)hipStreamSynchronize(c->side[i]);
+            (void)hipEventDestroy(c->join[i]);
+            (void)hipStreamDestroy(c->side[i]);
+        }
         (void)hipEventDestroy(c->fork);
-        (void)hipEventDestroy(c->join);
-        (void)hipStreamDestroy(c->side);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;

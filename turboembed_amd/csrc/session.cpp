@@ -514,7 +514,8 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         if (!mfma_attn) kc.bin[b].simple_attention = true;
     const bool measure = ((mode == TURBO_AUTOTUNE_ON && !cached) || mode == TURBO_AUTOTUNE_RETUNE) && !all_forced(kc);
     if (const char *g = std::getenv("TURBO_ROCM_GRAPHS")) s->graphs = std::strcmp(g, "0") != 0;
-    if (const char *g = std::getenv("TURBO_ROCM_SPLIT")) s->split_ok = std::strcmp(g, "0") != 0;
+    if (const char *g = std::getenv("TURBO_ROCM_SPLIT"))
+        s->split_parts = (uint32_t)std::min<long>(std::max<long>(std::strtol(g, nullptr, 10), 1), Session::MAX_PARTS);
 
     const size_t H = m->hidden, I = m->inter, B = s->max_batch, S = s->max_seq;
     s->tcap = B * S;
@@ -724,18 +725,30 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     s->head = head;
     s->taps = taps;
     s->tap_alone = alone;
-    // Split the rows in two where the packed tokens (rows in order) reach
-    // half, on runs large enough to fill the device twice over; not when
-    // ranges are read from layers before the last (each read pools every row).
-    s->split_rows = s->split_tokens = s->split_max_len[0] = s->split_max_len[1] = 0;
-    if (s->split_ok && B >= 2 && tokens >= SPLIT_MIN_TOKENS && (alone || taps == 1)) {
+    // Split the rows into parts of about equal packed tokens (rows in
+    // order: part i ends at the first row where the tokens reach i + 1
+    // parts' share), on runs large enough to fill the device once a part;
+    // not when ranges are read from layers before the last (each read pools
+    // every row).
+    uint32_t parts = 1;
+    if (B >= 2 && tokens >= SPLIT_MIN_TOKENS && (alone || taps == 1))
+        parts = std::min(s->split_parts, std::min(B, tokens / (SPLIT_MIN_TOKENS / 2)));
+    s->parts = std::max(parts, 1u);
+    {
         uint32_t r = 0, t = 0;
-        while (r + 1 < B && 2 * t < tokens) t += lens[r++];
-        if (r == 0) t = lens[r++];
-        s->split_rows = r;
-        s->split_tokens = t;
-        for (uint32_t i = 0; i < B; ++i)
-            s->split_max_len[i < r ? 0 : 1] = std::max(s->split_max_len[i < r ? 0 : 1], lens[i]);
+        for (uint32_t i = 0; i < s->parts; ++i) {
+            s->part_row[i] = r;
+            s->part_tok[i] = t;
+            s->part_len[i] = 0;
+            const uint64_t share = (uint64_t)tokens * (i + 1) / s->parts;
+            // At least one row a part, and one left for each part after it.
+            do {
+                s->part_len[i] = std::max(s->part_len[i], lens[r]);
+                t += lens[r++];
+            } while (r < B - (s->parts - 1 - i) && (i + 1 == s->parts || t < share));
+        }
+        s->part_row[s->parts] = r;
+        s->part_tok[s->parts] = t;
     }
     s->count = count;
     s->tokens = tokens;
@@ -968,20 +981,22 @@ void encode(Session &s) {
     // ModernBERT's first layer reads the embeddings' rows as they are (no
     // attention norm); on the F32 tier xh is the pre-norm rows' F32 copy.
     if (m.modern && f32) LAUNCH("copy", copy_bytes(st, s.x, s.xh, (size_t)T * H * 4));
-    // A split run: the rows' two parts run their layers on the context's two
+    // A split run: the rows' parts run their layers on the context's
     // streams, forked here and joined before the pooling, so one part's
-    // memory-bound and latency-bound launches overlap the other's products.
+    // memory-bound and latency-bound launches overlap another's products.
     // (Not while timing launches: their events are on the first stream.)
-    if (s.split_rows && !s.timing) {
-        const Part a{0, s.split_rows, 0, s.split_tokens, s.split_max_len[0]};
-        const Part b{s.split_rows, s.batch - s.split_rows, s.split_tokens, s.tokens - s.split_tokens,
-                     s.split_max_len[1]};
+    if (s.parts > 1 && !s.timing) {
         check(hipEventRecord(c.fork, st), "forking the run");
-        check(hipStreamWaitEvent(c.side, c.fork, 0), "forking the run");
-        run_layers(s, st, a, tm);
-        run_layers(s, c.side, b, tm);
-        check(hipEventRecord(c.join, c.side), "joining the run");
-        check(hipStreamWaitEvent(st, c.join, 0), "joining the run");
+        for (uint32_t i = 1; i < s.parts; ++i) check(hipStreamWaitEvent(c.side[i - 1], c.fork, 0), "forking the run");
+        for (uint32_t i = 0; i < s.parts; ++i) {
+            const Part p{s.part_row[i], s.part_row[i + 1] - s.part_row[i], s.part_tok[i],
+                         s.part_tok[i + 1] - s.part_tok[i], s.part_len[i]};
+            run_layers(s, i == 0 ? st : c.side[i - 1], p, tm);
+        }
+        for (uint32_t i = 1; i < s.parts; ++i) {
+            check(hipEventRecord(c.join[i - 1], c.side[i - 1]), "joining the run");
+            check(hipStreamWaitEvent(st, c.join[i - 1], 0), "joining the run");
+        }
     } else {
         run_layers(s, st, Part{0, s.batch, 0, s.tokens, s.max_len}, tm);
     }
@@ -1002,10 +1017,13 @@ void launch_run(Session &s) {
         encode(s);
         return;
     }
-    const Session::RunShape key{s.tokens,     s.batch,       s.seq,        s.max_len,
-                                s.count,      s.pooling,     s.normalize,  s.output_dim,
-                                s.head,       s.taps,        s.tap_alone,  s.split_rows,
-                                s.split_tokens, s.split_max_len[0], s.split_max_len[1]};
+    Session::RunShape key{s.tokens, s.batch, s.seq,  s.max_len, s.count,     s.pooling,
+                          s.normalize, s.output_dim, s.head, s.taps, s.tap_alone, s.parts};
+    for (uint32_t i = 0; i < s.parts; ++i) {
+        key[12 + 3 * i] = s.part_row[i];
+        key[13 + 3 * i] = s.part_tok[i];
+        key[14 + 3 * i] = s.part_len[i];
+    }
     auto it = s.graph_of.find(key);
     if (it == s.graph_of.end()) {
         constexpr size_t KEEP = 16;

@@ -72,8 +72,11 @@ using DevPtr = std::unique_ptr<void, DevFree>;
 struct Context {
     int ordinal = 0;                 // the HIP device
     hipStream_t stream = nullptr;
-    hipStream_t side = nullptr;      // a split run's second half of rows
-    hipEvent_t fork = nullptr, join = nullptr;
+    // A split run's streams after the first, and the events that fork them
+    // from it and join them back.
+    static constexpr int SIDES = 3;
+    hipStream_t side[SIDES] = {};
+    hipEvent_t fork = nullptr, join[SIDES] = {};
     turbo_log_fn log = nullptr;
     void *log_user_data = nullptr;
     std::mutex lock;                 // a launch through its sync, and reads
@@ -158,11 +161,14 @@ struct Session {
     // cut after layer L - taps + 1).
     uint32_t taps = 1;
     bool tap_alone = false;
-    // A split run (split_rows > 0): rows [0, split_rows) and the rest run
-    // their layers on two streams; the first part's packed tokens and each
-    // part's longest row. Off with TURBO_ROCM_SPLIT=0.
-    bool split_ok = true;
-    uint32_t split_rows = 0, split_tokens = 0, split_max_len[2] = {0, 0};
+    // A split run (parts > 1): the rows in `parts` parts of about equal
+    // packed tokens, each part's layers on its own stream; part i is rows
+    // [part_row[i], part_row[i + 1]), tokens [part_tok[i], part_tok[i + 1]),
+    // its longest row part_len[i]. TURBO_ROCM_SPLIT=n asks for n parts (0 or
+    // 1: none).
+    static constexpr int MAX_PARTS = 4;
+    uint32_t split_parts = MAX_PARTS;
+    uint32_t parts = 1, part_row[MAX_PARTS + 1] = {}, part_tok[MAX_PARTS + 1] = {}, part_len[MAX_PARTS] = {};
     uint64_t h2d = 0;
     std::vector<LayerWeights> *w = nullptr;
     Choices kc;            // kernel choices per bin of packed tokens
@@ -173,8 +179,9 @@ struct Session {
     // of a shape seen before is one graph launch. Off while timing, or with
     // TURBO_ROCM_GRAPHS=0.
     // tokens, batch, seq, max_len, count, pooling, normalize, output_dim,
-    // head, taps, tap_alone, split_rows, split_tokens, split_max_len[0, 1].
-    using RunShape = std::array<uint32_t, 15>;
+    // head, taps, tap_alone, parts, then each part's first row, first token
+    // and longest row.
+    using RunShape = std::array<uint32_t, 12 + 3 * MAX_PARTS>;
     bool graphs = true;
     std::map<RunShape, hipGraphExec_t> graph_of;
     std::vector<RunShape> graph_order;   // oldest first, for eviction
