@@ -184,6 +184,16 @@ def main():
     if dom == "gemm" and os.path.exists(traffic_file(args.workload)):
         with open(traffic_file(args.workload)) as f:
             traffic = json.load(f).get("traffic_bytes_per_launch")
+    # The matrix cores' sustained F16 rate with random operands (as a GEMM's)
+    # and with fixed ones, and the clock under that load: the ceiling the
+    # chip's power lets a real GEMM reach, beside the published peak.
+    ceiling = None
+    if dtype in ("f16", "bf16"):
+        rnd_tf, rnd_mhz = T.mfma_probe(random=True)
+        fix_tf, fix_mhz = T.mfma_probe(random=False)
+        ceiling = {"random_operands_tflops": round(rnd_tf, 1), "random_operands_mhz": round(rnd_mhz),
+                   "fixed_operands_tflops": round(fix_tf, 1), "fixed_operands_mhz": round(fix_mhz),
+                   "end_to_end_frac_of_random_ceiling": total_flops / (ms / 1e3) / (rnd_tf * 1e12)}
     if args.copy_probe:
         T.copy_probe(COPY_PROBE_BYTES, iters=3)
     roofline = {"kernel": dom, "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[dtype] / 1e12,
@@ -258,6 +268,7 @@ def main():
         "tune_ms": sess.tuning.tune_ms,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "mfma_ceiling_measured": ceiling,
     }
     print(json.dumps(line), flush=True)
     sess.close()

@@ -142,6 +142,15 @@ int32_t turbo_rocm_gemm_time(uint32_t ordinal, uint32_t dtype, uint32_t M, uint3
  * profiler's traffic counters can be scaled by what they read for it. */
 int32_t turbo_rocm_copy_probe(uint32_t ordinal, uint64_t bytes, uint32_t iters, float *ms, turbo_error *err);
 
+/* The matrix cores' sustained rate: every compute unit's 4 waves issue 8
+ * independent chains of 32x32x16 F16 products for iters rounds, with fixed
+ * operands, or with random ones changing every product (random 1), as a
+ * GEMM's do; *tflops is the rate, *mhz the shader clock under that load. A
+ * measurement hook with no counterpart in the reference: the ceiling a
+ * GEMM's data lets the chip sustain, beside the published peak. */
+int32_t turbo_rocm_mfma_probe(uint32_t ordinal, uint32_t random, uint32_t iters, float *tflops, float *mhz,
+                              turbo_error *err);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,15 @@ def test_gemm_matches_numpy(runtime, dtype, tile, mnk):
     assert err < 1e-4, err
 
 
+def test_the_mfma_probe_reports_a_rate_and_a_clock(runtime):
+    # Random operands never run the matrix cores faster than fixed ones, and
+    # the clock under the load is a shader clock (MHz, not a count).
+    rnd, rnd_mhz = T.mfma_probe(random=True, iters=2000)
+    fix, fix_mhz = T.mfma_probe(random=False, iters=2000)
+    assert 50 < rnd <= 1.1 * fix < 3000, (rnd, fix)
+    assert 500 < rnd_mhz < 3000 and 500 < fix_mhz < 3000, (rnd_mhz, fix_mhz)
+
+
 # ---- The sealed tiny bundles ---------------------------------------------------------
 
 @pytest.mark.parametrize("name", ["tiny_bert", "tiny_modernbert", "tiny_nomic"])

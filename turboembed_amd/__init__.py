@@ -58,6 +58,7 @@ def library():
         "turbo_rocm_gemm_check": [u32, u32, u32, u32, u32, P, P, P, P, u32, E],
         "turbo_rocm_gemm_time": [u32, u32, u32, u32, u32, u32, u32, C.POINTER(C.c_float), E],
         "turbo_rocm_copy_probe": [u32, C.c_uint64, u32, C.POINTER(C.c_float), E],
+        "turbo_rocm_mfma_probe": [u32, u32, u32, C.POINTER(C.c_float), C.POINTER(C.c_float), E],
         "turbo_rocm_pair_windows": [P, u32, P, u32, C.c_int32, C.c_int32, u32, u32, u32, u32, P, P, P, u32,
                                     C.POINTER(u32), E],
         "turbo_rocm_rerank_scores": [P, u32, u32, P, P, P, C.c_float, P, E],
@@ -506,6 +507,17 @@ def gemm_time(m, n, k, dtype=S.TURBO_DTYPE_F16, tile=0, iters=20, ordinal=0):
     err = S.new_error()
     _ok(library().turbo_rocm_gemm_time(ordinal, dtype, m, n, k, tile, iters, C.byref(ms), C.byref(err)), err)
     return ms.value
+
+
+def mfma_probe(random=True, iters=20000, ordinal=0):
+    """(TFLOP/s, MHz): the matrix cores' sustained F16 rate on every compute
+    unit, with random operands changing every product (as a GEMM's) or
+    fixed ones, and the clock under that load."""
+    tf, mhz = C.c_float(), C.c_float()
+    err = S.new_error()
+    _ok(library().turbo_rocm_mfma_probe(ordinal, 1 if random else 0, iters, C.byref(tf), C.byref(mhz), C.byref(err)),
+        err)
+    return tf.value, mhz.value
 
 
 def copy_probe(nbytes, iters=5, ordinal=0):

@@ -778,4 +778,55 @@ hipError_t gemm(hipStream_t s, Dt dt, int M, int N, int K, const void *A, int ld
     }
 }
 
+// ---- MFMA rate probe ----------------------------------------------------------
+//
+// Every wave issues 8 independent v_mfma_f32_32x32x16_f16 chains for `iters`
+// rounds: with fixed operands (the same in every round), or with random ones,
+// four sets of fragments taken in turn, as a GEMM's change every k-step. The
+// chip's clock under the load is the shader clock count over the 100 MHz
+// real-time count of block 0's first wave.
+__global__ void __launch_bounds__(256) mfma_probe_kernel(float *out, unsigned long long *clk, int iters, int random) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    typedef float f16x __attribute__((ext_vector_type(16)));
+    f16x acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f16x{};
+    h8 a[4], b[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t h = (threadIdx.x * 8 + i + 2048 * v) * 0x9e3779b9u;
+            h ^= h >> 16;
+            h *= 0x7feb352du;
+            h ^= h >> 15;
+            a[v][i] = random ? (_Float16)((float)(h & 0xffff) / 32768.0f - 1.0f) : (_Float16)(0.5f + i);
+            b[v][i] = random ? (_Float16)((float)(h >> 16) / 32768.0f - 1.0f) : (_Float16)0.25f;
+        }
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[2 * v + j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[v], b[(v + j) & 3], acc[2 * v + j], 0, 0, 0);
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[j][r];
+    if (s == 1234.5f) out[threadIdx.x] = s;   // keeps the products
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        clk[0] = t1 - t0;
+        clk[1] = r1 - r0;
+    }
+}
+
+hipError_t mfma_probe(hipStream_t s, int blocks, int iters, int random, float *out, unsigned long long *clk) {
+    hipLaunchKernelGGL(mfma_probe_kernel, dim3(blocks), dim3(256), 0, s, out, clk, iters, random);
+    return hipGetLastError();
+}
+
 }  // namespace rocm

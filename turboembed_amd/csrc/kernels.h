@@ -107,6 +107,11 @@ hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads,
 hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
                 int count, const uint32_t *ranges, int pooling, int output_dim, int l2, float *out);
 
+// The MFMA rate probe: `blocks` workgroups of 4 waves, each wave 8 chains of
+// 32x32x16 F16 products for `iters` rounds, fixed or random operands; out
+// takes 256 floats, clk the shader and real-time (100 MHz) counts of one wave.
+hipError_t mfma_probe(hipStream_t s, int blocks, int iters, int random, float *out, unsigned long long *clk);
+
 // The span head's outputs at most (2 for start and end).
 constexpr int HEAD_MAX = 16;
 

@@ -1418,4 +1418,36 @@ int32_t turbo_rocm_copy_probe(uint32_t ordinal, uint64_t bytes, uint32_t iters, 
     });
 }
 
+int32_t turbo_rocm_mfma_probe(uint32_t ordinal, uint32_t random, uint32_t iters, float *tflops, float *mhz,
+                              turbo_error *err) {
+    return guarded(err, [&] {
+        if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device");
+        if (iters == 0 || !tflops || !mhz) fail(TURBO_E_INVALID_ARGUMENT, "rocm: iters, tflops and mhz");
+        OnDevice on(devices()[ordinal]);
+        int cus = 0;
+        check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, devices()[ordinal]), "mfma probe");
+        DevPtr out(dev_alloc(256 * 4, "mfma probe")), clk(dev_alloc(16, "mfma probe"));
+        float *o = static_cast<float *>(out.get());
+        unsigned long long *c = static_cast<unsigned long long *>(clk.get());
+        hipEvent_t e0, e1;
+        check(hipEventCreate(&e0), "mfma probe");
+        check(hipEventCreate(&e1), "mfma probe");
+        check(mfma_probe(nullptr, cus, 100, (int)random, o, c), "mfma probe");
+        check(hipEventRecord(e0, nullptr), "mfma probe");
+        check(mfma_probe(nullptr, cus, (int)iters, (int)random, o, c), "mfma probe");
+        check(hipEventRecord(e1, nullptr), "mfma probe");
+        check(hipEventSynchronize(e1), "mfma probe");
+        float ms = 0;
+        check(hipEventElapsedTime(&ms, e0, e1), "mfma probe");
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        unsigned long long counts[2] = {0, 0};
+        check(hipMemcpy(counts, c, 16, hipMemcpyDeviceToHost), "mfma probe");
+        // 4 waves a workgroup, 8 products a round, 2 * 32 * 32 * 16 flops a product.
+        *tflops = (float)((double)cus * 4 * iters * 8 * 32768.0 / (ms * 1e-3) / 1e12);
+        *mhz = counts[1] ? (float)(100.0 * (double)counts[0] / (double)counts[1]) : 0.0f;
+        return TURBO_OK;
+    });
+}
+
 }  // extern "C"
