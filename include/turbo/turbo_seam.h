@@ -208,6 +208,14 @@ typedef struct turbo_token_range {
 #define TURBO_BERT_FFN_LN_BIAS    15
 #define TURBO_BERT_LAYER_TENSORS  16
 
+#define TURBO_DEBERTA_WORD_EMBEDDINGS        0
+#define TURBO_DEBERTA_EMBEDDINGS_LN_WEIGHT   1
+#define TURBO_DEBERTA_EMBEDDINGS_LN_BIAS     2
+#define TURBO_DEBERTA_RELATIVE_EMBEDDINGS    3
+#define TURBO_DEBERTA_RELATIVE_LN_WEIGHT     4
+#define TURBO_DEBERTA_RELATIVE_LN_BIAS       5
+#define TURBO_DEBERTA_EMBEDDING_TENSORS      6
+
 #define TURBO_MODERNBERT_WORD_EMBEDDINGS        0
 #define TURBO_MODERNBERT_EMBEDDINGS_LN_WEIGHT   1
 #define TURBO_MODERNBERT_FINAL_NORM_WEIGHT      2

@@ -44,6 +44,8 @@ def lib():
         _lib.oracle_layer_norm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_float]
         _lib.oracle_quantize.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
         _lib.oracle_quantize.restype = None
+        _lib.oracle_deberta_bucket.argtypes = [C.c_int64, C.c_uint32, C.c_uint32]
+        _lib.oracle_deberta_bucket.restype = C.c_uint32
     return _lib
 
 
@@ -127,7 +129,7 @@ def pack(mask, ranges=()):
 # ---- The reference's sealed tiny bundles (tests/golden/) --------------------
 
 _FAMILIES = {"FAMILY_BERT": S.TURBO_FAMILY_BERT, "FAMILY_MODERNBERT": S.TURBO_FAMILY_MODERNBERT,
-             "FAMILY_NOMIC_BERT": S.TURBO_FAMILY_NOMIC_BERT}
+             "FAMILY_NOMIC_BERT": S.TURBO_FAMILY_NOMIC_BERT, "FAMILY_DEBERTA_V2": S.TURBO_FAMILY_DEBERTA_V2}
 
 
 def fixture(name):
@@ -144,6 +146,8 @@ def fixture(name):
         kw = dict(rope=(a["rope"]["global_theta"], a["rope"]["local_theta"]), attention_window=a["attention"]["window"],
                   global_every=a["attention"]["global_every"], mlp=S.TURBO_MLP_GATED,
                   activation=S.TURBO_ACTIVATION_GELU_ERF, norm=S.TURBO_NORM_LAYER_NO_BIAS)
+    elif family == S.TURBO_FAMILY_DEBERTA_V2:
+        kw = dict(relative=(a["relative"]["position_buckets"], a["relative"]["max_relative_positions"]))
     elif family == S.TURBO_FAMILY_NOMIC_BERT:
         g = a["rope"]["global_theta"]
         kw = dict(rope=(g, g), mlp=S.TURBO_MLP_GATED, activation=S.TURBO_ACTIVATION_SILU, norm=S.TURBO_NORM_LAYER)

@@ -135,6 +135,38 @@ void layer_norm(float *y, const float *w, const float *b, uint32_t n, float eps)
     for (uint32_t i = 0; i < n; ++i) y[i] = (float)(((double)y[i] - mean) * inv) * w[i] + (b ? b[i] : 0.0f);
 }
 
+// DeBERTa's LayerNorm (core/src/deberta/math.rs:9-27): the mean and the
+// biased variance summed in F64 in order, the scale 1 / sqrt(var + eps) in
+// F64, y = (x - mean) * scale * w + b in F64, rounded once. eps is the
+// architecture's (F64).
+void deberta_norm(float *y, const float *w, const float *b, uint32_t n, double eps) {
+    double sum = 0.0;
+    for (uint32_t i = 0; i < n; ++i) sum += (double)y[i];
+    const double mean = sum / (double)n;
+    double var = 0.0;
+    for (uint32_t i = 0; i < n; ++i) var += ((double)y[i] - mean) * ((double)y[i] - mean);
+    var /= (double)n;
+    const double scale = 1.0 / std::sqrt(var + eps);
+    for (uint32_t i = 0; i < n; ++i) y[i] = (float)(((double)y[i] - mean) * scale * (double)w[i] + (double)b[i]);
+}
+
+// The relative row of a signed distance (core/src/deberta/math.rs:30-40,
+// transformers' make_log_bucket_position): distances within half the
+// buckets are their own row; beyond, ceil(ln(|d| / mid) / ln((max - 1) / mid)
+// * (mid - 1)) + mid with F32 logarithms, signed, offset by the buckets and
+// clamped to the table.
+uint32_t deberta_bucket(int64_t distance, uint32_t buckets, uint32_t maximum) {
+    const int64_t mid = buckets / 2;
+    const int64_t mag0 = distance < 0 ? -distance : distance;
+    int64_t mag = mag0;
+    if (mag0 > mid) {
+        const float a = std::log((float)mag0 / (float)mid), c = std::log((float)(maximum - 1) / (float)mid);
+        mag = (int64_t)std::ceil(a / c * (float)(mid - 1)) + mid;
+    }
+    const int64_t signed_mag = distance < 0 ? -mag : mag;
+    return (uint32_t)std::min<int64_t>(std::max<int64_t>(signed_mag + buckets, 0), 2 * (int64_t)buckets - 1);
+}
+
 // ---- Threads ----------------------------------------------------------------
 
 // Runs fn(task) for task in [0, tasks) on `threads` threads. A task computes
@@ -205,6 +237,14 @@ struct Layer {
 
 struct Model {
     uint32_t family, layers, hidden, heads, d, inter, vocab, positions, types, position_offset;
+    // DeBERTa-v2: the relative table's half rows and the distance the log
+    // buckets reach; the normalized relative rows [2 buckets, H], and each
+    // layer's shared-key projections of them, query then key [2 buckets][2 H].
+    bool deberta = false;
+    uint32_t buckets = 0, max_rel = 0;
+    double eps64 = 0.0;
+    std::vector<float> reln;
+    std::vector<std::vector<float>> pos_qk;
     float eps;
     uint32_t ahead;       // keys past a query it reads; UINT32_MAX for the whole row
     bool rotary = false, modern = false, silu_act = false;
@@ -232,7 +272,7 @@ const float *tensor_f32(Model &m, const turbo_backend_tensor &t, uint32_t dtype)
 void load(Model &m, const turbo_backend_model *d) {
     m.family = d->family;
     if (d->family != TURBO_FAMILY_BERT && d->family != TURBO_FAMILY_ROBERTA && d->family != TURBO_FAMILY_MODERNBERT &&
-        d->family != TURBO_FAMILY_NOMIC_BERT)
+        d->family != TURBO_FAMILY_NOMIC_BERT && d->family != TURBO_FAMILY_DEBERTA_V2)
         throw Failure(TURBO_E_UNSUPPORTED, "family " + std::to_string(d->family) + " is not an encoder the oracle runs");
     if (d->dtype != TURBO_DTYPE_F32 && d->dtype != TURBO_DTYPE_F16 && d->dtype != TURBO_DTYPE_BF16)
         throw Failure(TURBO_E_UNSUPPORTED, "dtype " + std::to_string(d->dtype));
@@ -252,16 +292,36 @@ void load(Model &m, const turbo_backend_model *d) {
     const uint32_t H = m.hidden, I = m.inter;
     m.t.resize(d->tensor_count);
     for (uint32_t i = 0; i < d->tensor_count; ++i) m.t[i] = tensor_f32(m, d->tensors[i], d->dtype);
+    m.deberta = d->family == TURBO_FAMILY_DEBERTA_V2;
     if (!m.rotary) {
-        const uint32_t need = TURBO_BERT_EMBEDDING_TENSORS + m.layers * TURBO_BERT_LAYER_TENSORS;
+        const uint32_t emb = m.deberta ? TURBO_DEBERTA_EMBEDDING_TENSORS : TURBO_BERT_EMBEDDING_TENSORS;
+        const uint32_t need = emb + m.layers * TURBO_BERT_LAYER_TENSORS;
         if (d->tensor_count != need) throw Failure(TURBO_E_INVALID_ARGUMENT, "tensor_count");
-        m.word = m.t[TURBO_BERT_WORD_EMBEDDINGS];
-        m.pos = m.t[TURBO_BERT_POSITION_EMBEDDINGS];
-        m.type = m.t[TURBO_BERT_TOKEN_TYPE_EMBEDDINGS];
-        m.emb_w = m.t[TURBO_BERT_EMBEDDINGS_LN_WEIGHT];
-        m.emb_b = m.t[TURBO_BERT_EMBEDDINGS_LN_BIAS];
+        if (m.deberta) {
+            if (d->struct_size < offsetof(turbo_backend_model, max_relative_positions) + 4 || d->position_buckets < 2 ||
+                d->max_relative_positions < 2)
+                throw Failure(TURBO_E_INVALID_ARGUMENT, "a DeBERTa-v2 model needs position_buckets and max_relative_positions");
+            m.buckets = d->position_buckets;
+            m.max_rel = d->max_relative_positions;
+            m.eps64 = d->layer_norm_eps;
+            m.word = m.t[TURBO_DEBERTA_WORD_EMBEDDINGS];
+            m.emb_w = m.t[TURBO_DEBERTA_EMBEDDINGS_LN_WEIGHT];
+            m.emb_b = m.t[TURBO_DEBERTA_EMBEDDINGS_LN_BIAS];
+            // The relative rows through their own LayerNorm (core/src/deberta/weights.rs:91-92).
+            const float *rel = m.t[TURBO_DEBERTA_RELATIVE_EMBEDDINGS];
+            m.reln.assign(rel, rel + (size_t)2 * m.buckets * H);
+            for (uint32_t r = 0; r < 2 * m.buckets; ++r)
+                deberta_norm(&m.reln[(size_t)r * H], m.t[TURBO_DEBERTA_RELATIVE_LN_WEIGHT],
+                             m.t[TURBO_DEBERTA_RELATIVE_LN_BIAS], H, d->layer_norm_eps);
+        } else {
+            m.word = m.t[TURBO_BERT_WORD_EMBEDDINGS];
+            m.pos = m.t[TURBO_BERT_POSITION_EMBEDDINGS];
+            m.type = m.t[TURBO_BERT_TOKEN_TYPE_EMBEDDINGS];
+            m.emb_w = m.t[TURBO_BERT_EMBEDDINGS_LN_WEIGHT];
+            m.emb_b = m.t[TURBO_BERT_EMBEDDINGS_LN_BIAS];
+        }
         for (uint32_t l = 0; l < m.layers; ++l) {
-            auto w = [&](uint32_t r) { return m.t[TURBO_BERT_EMBEDDING_TENSORS + l * TURBO_BERT_LAYER_TENSORS + r]; };
+            auto w = [&](uint32_t r) { return m.t[emb + l * TURBO_BERT_LAYER_TENSORS + r]; };
             Layer L;
             std::vector<const float *> rows;
             for (uint32_t part : {TURBO_BERT_Q_WEIGHT, TURBO_BERT_K_WEIGHT, TURBO_BERT_V_WEIGHT})
@@ -286,6 +346,20 @@ void load(Model &m, const turbo_backend_model *d) {
             L.attn_ln_b = w(TURBO_BERT_ATTN_LN_BIAS);
             L.ffn_ln_w = w(TURBO_BERT_FFN_LN_WEIGHT);
             L.ffn_ln_b = w(TURBO_BERT_FFN_LN_BIAS);
+            if (m.deberta) {
+                // Shared keys: the layer's query and key projections of every
+                // normalized relative row, an in-order FMA chain then the bias
+                // (core/src/deberta/weights.rs:98-106).
+                std::vector<float> pq((size_t)2 * m.buckets * 2 * H);
+                for (uint32_t r = 0; r < 2 * m.buckets; ++r)
+                    for (uint32_t o = 0; o < 2 * H; ++o) {
+                        float acc = 0.0f;
+                        for (uint32_t k = 0; k < H; ++k)
+                            acc = __builtin_fmaf(m.reln[(size_t)r * H + k], L.qkv.wt[(size_t)k * L.qkv.n + o], acc);
+                        pq[(size_t)r * 2 * H + o] = acc + L.qkv.bias[o];
+                    }
+                m.pos_qk.push_back(std::move(pq));
+            }
             m.ls.push_back(std::move(L));
         }
         return;
@@ -453,6 +527,17 @@ struct Run {
                 const uint32_t at = pk.at[t];
                 float *dst = &x[(size_t)t * H];
                 const float *w = m.word + (size_t)ids[at] * H;
+                if (m.deberta) {
+                    // A masked position is zero after the embedding; a live one
+                    // its row through the embedding norm (core/src/deberta/mod.rs:245-252).
+                    if (!mask[at]) {
+                        std::fill(dst, dst + H, 0.0f);
+                    } else {
+                        std::copy(w, w + H, dst);
+                        deberta_norm(dst, m.emb_w, m.emb_b, H, m.eps64);
+                    }
+                    continue;
+                }
                 if (!m.rotary) {
                     const float *ps = m.pos + (size_t)(at % seq + m.position_offset) * H;
                     const float *tt = m.type + (size_t)types[at] * H;
@@ -472,8 +557,80 @@ struct Run {
     void norm(float *buf, const float *w, const float *b) {
         const uint32_t H = m.hidden;
         parallel(threads, (T() + 15) / 16, [&](size_t c) {
-            for (uint32_t t = (uint32_t)c * 16; t < std::min<uint32_t>(T(), (uint32_t)c * 16 + 16); ++t)
-                layer_norm(&buf[(size_t)t * H], w, b, H, m.eps);
+            for (uint32_t t = (uint32_t)c * 16; t < std::min<uint32_t>(T(), (uint32_t)c * 16 + 16); ++t) {
+                if (m.deberta) deberta_norm(&buf[(size_t)t * H], w, b, H, m.eps64);
+                else layer_norm(&buf[(size_t)t * H], w, b, H, m.eps);
+            }
+        });
+    }
+
+    // DeBERTa's disentangled attention of layer l (core/src/deberta/attention.rs:207-315):
+    // for each live query i and live key j, the score
+    // (q_i . k_j + q_i . pos_k[b] + k_j . pos_q[b]) / sqrt(3 d), b the bucket of
+    // the columns' distance, each dot an in-order FMA chain; the row's
+    // softmax over the live keys, and the context as an in-order FMA chain
+    // over them. A masked position attends uniformly to every position
+    // through the row's last live one: the mean of their values in F64.
+    void attention_deberta(uint32_t l) {
+        const uint32_t H = m.hidden, d = m.d, ld = 3 * H;
+        const float inv = (float)(1.0 / std::sqrt(3.0 * (double)d));
+        const float *pq = m.pos_qk[l].data();
+        parallel(threads, (size_t)batch * m.heads, [&](size_t task) {
+            const uint32_t r = (uint32_t)(task / m.heads), head = (uint32_t)(task % m.heads);
+            const uint32_t start = pk.start[r], len = pk.len[r];
+            if (len == 0) return;
+            const uint8_t *mk = &mask[(size_t)r * seq];
+            std::vector<uint32_t> live;
+            for (uint32_t p = 0; p < len; ++p)
+                if (mk[p]) live.push_back(p);
+            const uint32_t nv = (uint32_t)live.size();
+            const float *qv = &qkv[(size_t)start * ld];
+            auto dot = [&](const float *a, const float *b) {
+                float acc = 0.0f;
+                for (uint32_t c = 0; c < d; ++c) acc = __builtin_fmaf(a[c], b[c], acc);
+                return acc;
+            };
+            std::vector<float> sc(nv);
+            for (uint32_t ii = 0; ii < nv; ++ii) {
+                const uint32_t pi = live[ii];
+                const float *q = qv + (size_t)pi * ld + head * d;
+                for (uint32_t jj = 0; jj < nv; ++jj) {
+                    const uint32_t pj = live[jj];
+                    const float *k = qv + (size_t)pj * ld + H + head * d;
+                    const uint32_t bk = deberta_bucket((int64_t)pi - (int64_t)pj, m.buckets, m.max_rel);
+                    const float *row = pq + (size_t)bk * 2 * H;
+                    sc[jj] = (dot(q, k) + dot(q, row + H + head * d) + dot(k, row + head * d)) * inv;
+                }
+                float mx = kNegInf;
+                for (uint32_t jj = 0; jj < nv; ++jj)
+                    if (sc[jj] > mx) mx = sc[jj];
+                float lanes[kLanes];
+                for (uint32_t w = 0; w < kLanes; ++w) lanes[w] = 0.0f;
+                for (uint32_t jj = 0; jj < nv; ++jj) {
+                    sc[jj] = cephes_exp(sc[jj] - mx);
+                    lanes[jj % kLanes] += sc[jj];
+                }
+                for (uint32_t w = kLanes / 2; w > 0; w /= 2)
+                    for (uint32_t x = 0; x < w; ++x) lanes[x] += lanes[x + w];
+                const float rinv = 1.0f / lanes[0];
+                for (uint32_t jj = 0; jj < nv; ++jj) sc[jj] *= rinv;
+                float *out = &ctx[(size_t)(start + pi) * H + head * d];
+                for (uint32_t c = 0; c < d; ++c) {
+                    float acc = 0.0f;
+                    for (uint32_t jj = 0; jj < nv; ++jj)
+                        acc = __builtin_fmaf(sc[jj], qv[(size_t)live[jj] * ld + 2 * H + head * d + c], acc);
+                    out[c] = acc;
+                }
+            }
+            for (uint32_t p = 0; p < len; ++p) {
+                if (mk[p]) continue;
+                float *out = &ctx[(size_t)(start + p) * H + head * d];
+                for (uint32_t c = 0; c < d; ++c) {
+                    double sum = 0.0;
+                    for (uint32_t j = 0; j < len; ++j) sum += (double)qv[(size_t)j * ld + 2 * H + head * d + c];
+                    out[c] = (float)(sum / (double)len);
+                }
+            }
         });
     }
 
@@ -648,7 +805,8 @@ void encode(const Model &m, const turbo_backend_embed_rows *rows, const turbo_to
                 float *y = &run.qkv[(size_t)t * 3 * H + c0];
                 for (uint32_t j = 0; j < cols; ++j) y[j] = acc[j] + L.qkv.bias[c0 + j];
             });
-            run.attention(UINT32_MAX);
+            if (m.deberta) run.attention_deberta(l);
+            else run.attention(UINT32_MAX);
             run.linear(run.ctx.data(), H, L.out,
                        [&](uint32_t t, uint32_t c0, uint32_t cols, const float *acc) { residual(t, c0, cols, acc, L.out); });
             run.norm(x, L.attn_ln_w, L.attn_ln_b);
@@ -793,6 +951,9 @@ uint32_t oracle_pack(const int32_t *mask, uint32_t batch, uint32_t seq, uint32_t
 }
 
 float oracle_exp(float x) { return cephes_exp(x); }
+uint32_t oracle_deberta_bucket(int64_t distance, uint32_t buckets, uint32_t maximum) {
+    return deberta_bucket(distance, buckets, maximum);
+}
 float oracle_gelu(float x) { return gelu_erf(x); }
 float oracle_silu(float x) { return silu(x); }
 void oracle_layer_norm(float *y, const float *w, const float *b, uint32_t n, float eps) { layer_norm(y, w, b, n, eps); }

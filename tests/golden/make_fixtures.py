@@ -3,7 +3,7 @@
 Run here, where the reference tree is mounted; the fixtures it writes are
 committed, and nothing at test time reads the reference.
 
-For each sealed tiny bundle (testdata/tiny-bert-bundle, tiny-modernbert-bundle,
+For each sealed tiny bundle (testdata/tiny-bert-bundle, tiny-modernbert-bundle, tiny-deberta-bundle,
 tiny-nomic-bundle) it keeps the upstream reference cases (token ids, lengths
 and the fp32 vectors upstream sentence-transformers produced) and the bundle's
 weights. To keep the files small, the word-embedding table keeps only the rows
@@ -36,6 +36,11 @@ def modernbert_order():
             ["attn_ln_weight", "qkv_weight", "attn_out_weight", "ffn_ln_weight", "ffn_in_weight", "ffn_out_weight"])
 
 
+def deberta_order():
+    return (["word_embeddings", "embeddings_ln_weight", "embeddings_ln_bias", "relative_embeddings", "relative_ln_weight",
+             "relative_ln_bias"], bert_order(0)[1])
+
+
 def nomic_order():
     return (["word_embeddings", "token_type_embeddings", "embeddings_ln_weight", "embeddings_ln_bias"],
             ["qkv_weight", "attn_out_weight", "attn_ln_weight", "attn_ln_bias", "ffn_gate_weight", "ffn_up_weight",
@@ -53,7 +58,7 @@ def one(bundle, out_name):
     ids, lengths, vectors = ref["ids"], ref["lengths"], ref["embeddings"]
     family = arch["family"]
     emb, per = {"FAMILY_BERT": bert_order(arch["layers"]), "FAMILY_MODERNBERT": modernbert_order(),
-                "FAMILY_NOMIC_BERT": nomic_order()}[family]
+                "FAMILY_NOMIC_BERT": nomic_order(), "FAMILY_DEBERTA_V2": deberta_order()}[family]
     used = sorted(set(int(v) for r, n in zip(ids, lengths) for v in r[:n]) | {0})
     remap = {old: new for new, old in enumerate(used)}
     new_ids = np.zeros_like(ids)
@@ -245,6 +250,7 @@ if __name__ == "__main__":
     one("tiny-bert-bundle", "tiny_bert")
     one("tiny-modernbert-bundle", "tiny_modernbert")
     one("tiny-nomic-bundle", "tiny_nomic")
+    one("tiny-deberta-bundle", "tiny_deberta")
     rerank_fixture()
     qa_fixture()
     bundle_files()

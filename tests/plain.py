@@ -130,11 +130,71 @@ def rotary_states(desc, ids, mask, types):
     return x, live
 
 
+def log_bucket(rel, buckets, maximum):
+    """transformers' make_log_bucket_position over an array of signed
+    distances, its logarithms in float32, offset by the buckets and clamped
+    to the table."""
+    mid = buckets // 2
+    rel = np.asarray(rel, np.int64)
+    sign = np.sign(rel)
+    a = np.where((rel < mid) & (rel > -mid), mid - 1, np.abs(rel))
+    log_pos = np.ceil(np.log(a.astype(np.float32) / np.float32(mid)) /
+                      np.log(np.float32(maximum - 1) / np.float32(mid)) * np.float32(mid - 1)).astype(np.int64) + mid
+    signed = np.where(np.abs(rel) <= mid, rel, log_pos * sign)
+    return np.clip(signed + buckets, 0, 2 * buckets - 1)
+
+
+def deberta_states(desc, ids, mask, types=None, uniform_masked=True):
+    """Final hidden states of one DeBERTa-v2 row (shared keys, c2p and p2c),
+    through its last live token: embeddings LayerNorm'd and zeroed where
+    masked; scores (q k + q pos_k[b(i - j)] + k pos_q[b(i - j)]) / sqrt(3 d),
+    p2c gathered at the negated distance and transposed; masked pairs take
+    the most negative finite value, so a masked query attends uniformly."""
+    t = [_f64(x) for x in desc.tensors]
+    H, heads = desc.hidden, desc.heads
+    d = H // heads
+    buckets, maximum = desc.relative
+    n = int(np.nonzero(mask)[0].max()) + 1
+    live = mask[:n] != 0
+    x = ln(t[0][ids[:n]], t[1], t[2], desc.layer_norm_eps) * live[:, None]
+    rel = ln(t[3][: 2 * buckets], t[4], t[5], desc.layer_norm_eps)
+    pos = np.arange(n)
+    r = log_bucket(pos[:, None] - pos[None, :], buckets, maximum)            # [i, j]
+    # (uniform_masked=False plants a mistake for the tests: masked queries
+    # reading the live keys, as a visible query does.)
+    allowed = live[:, None] & live[None, :] if uniform_masked else np.broadcast_to(live[None, :], (n, n))
+    for l in range(desc.layers):
+        w = t[S.DEBERTA_EMBEDDING_TENSORS + l * S.BERT_LAYER_TENSORS:][:S.BERT_LAYER_TENSORS]
+        q = (x @ w[0].T + w[1]).reshape(n, heads, d)
+        k = (x @ w[2].T + w[3]).reshape(n, heads, d)
+        v = (x @ w[4].T + w[5]).reshape(n, heads, d)
+        pq = (rel @ w[0].T + w[1]).reshape(-1, heads, d)
+        pk = (rel @ w[2].T + w[3]).reshape(-1, heads, d)
+        c2c = np.einsum("ihd,jhd->hij", q, k)
+        c2p_all = np.einsum("ihd,rhd->hir", q, pk)
+        c2p = np.take_along_axis(c2p_all, np.broadcast_to(r[None], c2c.shape), axis=2)
+        p2c_all = np.einsum("jhd,rhd->hjr", k, pq)
+        # transformers: index with the negated distance's bucket, then transpose.
+        r_neg = log_bucket(pos[None, :] - pos[:, None], buckets, maximum)      # [i, j] -> bucket(j - i)
+        p2c_idx = 2 * buckets - r_neg                                            # -bucket(j - i) offset back
+        p2c_idx = np.clip(p2c_idx, 0, 2 * buckets - 1).T                        # as [j, i]
+        p2c = np.take_along_axis(p2c_all, np.broadcast_to(p2c_idx[None], c2c.shape), axis=2).transpose(0, 2, 1)
+        s = (c2c + c2p + p2c) / math.sqrt(3 * d)
+        s = np.where(allowed[None], s, np.finfo(np.float32).min)
+        p = np.exp(s - s.max(-1, keepdims=True))
+        p = p / p.sum(-1, keepdims=True)
+        a = np.einsum("hij,jhd->ihd", p, v).reshape(n, H)
+        x = ln(x + a @ w[6].T + w[7], w[8], w[9], desc.layer_norm_eps)
+        f = gelu(x @ w[10].T + w[11])
+        x = ln(x + f @ w[12].T + w[13], w[14], w[15], desc.layer_norm_eps)
+    return x, live
+
+
 def embed(desc, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN, normalize=S.TURBO_NORMALIZE_L2,
           output_dim=None):
     """Pooled, cut and normalized vectors of each row, float64."""
     types = np.zeros_like(ids) if types is None else types
-    states = rotary_states if desc.rotary else bert_states
+    states = rotary_states if desc.rotary else deberta_states if desc.family == S.TURBO_FAMILY_DEBERTA_V2 else bert_states
     out = []
     for r in range(ids.shape[0]):
         x, live = states(desc, ids[r], mask[r], types[r])

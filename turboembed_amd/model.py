@@ -48,7 +48,7 @@ class ModelDesc:
     def __init__(self, family, layers, hidden, heads, intermediate, vocab_size, max_positions, token_types,
                  layer_norm_eps, tensors, position_offset=0, rope=None, attention_window=0, global_every=0,
                  mlp=S.TURBO_MLP_DENSE, activation=S.TURBO_ACTIVATION_GELU_ERF, norm=S.TURBO_NORM_LAYER,
-                 names=None, compute_dtype=0, span_head=None):
+                 names=None, compute_dtype=0, span_head=None, relative=None):
         self.family, self.layers, self.hidden, self.heads = family, layers, hidden, heads
         self.intermediate, self.vocab_size, self.max_positions = intermediate, vocab_size, max_positions
         self.token_types, self.layer_norm_eps, self.position_offset = token_types, layer_norm_eps, position_offset
@@ -66,6 +66,8 @@ class ModelDesc:
         self.names = names or [f"tensor{i}" for i in range(len(self.tensors))]
         # TURBO_DTYPE_I8 asks for int8 GEMMs below EXACT; 0 leaves it to the precision.
         self.compute_dtype = compute_dtype
+        # A DeBERTa-v2 model's (position_buckets, max_relative_positions).
+        self.relative = relative
         # An extractive QA model's span head, (weight [head_out, hidden],
         # bias [head_out]) in F32, for a backend that applies it
         # (turbo_backend.h:332-337); None on every other model.
@@ -110,6 +112,8 @@ class ModelDesc:
         m.token_types, m.layer_norm_eps = self.token_types, self.layer_norm_eps
         m.tensor_count, m.position_offset = n, self.position_offset
         m.compute_dtype = self.compute_dtype
+        if self.relative is not None:
+            m.position_buckets, m.max_relative_positions = self.relative
         m.tensors = C.cast(arr, C.POINTER(S.turbo_backend_tensor))
         m.format, m.graph_input, m.graph_output = S.TURBO_FORMAT_SAFETENSORS, S.TURBO_INPUT_TOKEN_IDS, \
             S.TURBO_OUTPUT_HIDDEN_STATES
@@ -151,5 +155,5 @@ def with_dtype(desc, dtype):
                     desc.max_positions, desc.token_types, desc.layer_norm_eps,
                     [None if t is None else conv(t) for t in desc.tensors], desc.position_offset, desc.rope,
                     desc.attention_window, desc.global_every, desc.mlp, desc.activation, desc.norm, desc.names,
-                    desc.compute_dtype, desc.span_head)
+                    desc.compute_dtype, desc.span_head, desc.relative)
     return out

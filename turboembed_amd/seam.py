@@ -73,6 +73,7 @@ TURBO_CHOICES_LEN = 1024
 
 TURBO_FAMILY_BERT = 1
 TURBO_FAMILY_ROBERTA = 2
+TURBO_FAMILY_DEBERTA_V2 = 4
 TURBO_FAMILY_MODERNBERT = 5
 TURBO_FAMILY_NOMIC_BERT = 6
 TURBO_FORMAT_SAFETENSORS = 1
@@ -96,6 +97,7 @@ MODERNBERT_EMBEDDING_TENSORS = 3
 MODERNBERT_LAYER_TENSORS = 6
 NOMIC_EMBEDDING_TENSORS = 4
 NOMIC_LAYER_TENSORS = 9
+DEBERTA_EMBEDDING_TENSORS = 6
 
 
 class turbo_text(C.Structure):
