@@ -179,7 +179,7 @@ def test_a_bundle_is_refused_as_the_core_refuses_it(tmp_path):
     assert _code(lambda: b.reference()) == B.TURBO_E_BUNDLE_INVALID
     # A family the backend does not load, and a manifest that does not parse.
     m = json.load(open(os.path.join(d, "manifest.json")))
-    m["architecture"]["family"] = "FAMILY_DEBERTA_V2"
+    m["architecture"]["family"] = "FAMILY_STATIC"
     json.dump(m, open(os.path.join(d, "manifest.json"), "w"))
     assert _code(lambda: B.Bundle(d).model_desc()) == B.TURBO_E_BUNDLE_NO_ARTIFACT
     open(os.path.join(d, "manifest.json"), "w").write("{")

@@ -64,7 +64,7 @@ def test_the_mfma_probe_reports_a_rate_and_a_clock(runtime):
 
 # ---- The sealed tiny bundles ---------------------------------------------------------
 
-@pytest.mark.parametrize("name", ["tiny_bert", "tiny_modernbert", "tiny_nomic"])
+@pytest.mark.parametrize("name", ["tiny_bert", "tiny_modernbert", "tiny_nomic", "tiny_deberta"])
 @pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
 def test_tiny_bundles_meet_the_upstream_vectors(context, name, precision):
     desc, ids, lengths, vectors, info = oracle.fixture(name)
@@ -388,6 +388,49 @@ def test_rerank_refuses_what_the_core_refuses(context):
     with pytest.raises(T.TurboError) as e:
         s.rerank(pairs, h, info["start_id"], info["end_id"], query_tokens=8)
     assert e.value.code == S.TURBO_E_UNSUPPORTED_TASK
+    s.close()
+    model.close()
+
+
+# ---- DeBERTa-v2: disentangled attention over relative buckets ----------------------------
+#
+# Rows with holes and a masked column 0 (a masked token is zero after the
+# embedding, and every one shares one uniform-attention state), every pooling,
+# ranges and layer reads, against the oracle; and a run long enough to split.
+
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+def test_deberta_rows_with_masked_tokens_meet_the_oracle(context, precision):
+    from test_deberta import holed_rows, small_deberta
+    desc = small_deberta()
+    ids, mask = holed_rows(desc.vocab_size)
+    model = context.load(desc)
+    s = model.session(4, 40, precision, max_ranges=12)
+    for pooling in (S.TURBO_POOLING_MEAN, S.TURBO_POOLING_CLS, S.TURBO_POOLING_LAST):
+        got = s.embed(ids, mask, pooling=pooling)
+        assert_close(got, oracle.encode(desc, ids, mask, pooling=pooling), s.compute_dtype)
+    ranges = [(0, 0, 40), (1, 2, 13), (2, 5, 6), (1, 12, 25)]
+    s.write_layer_ranges(ids, mask, ranges, 2, normalize=S.TURBO_NORMALIZE_NONE)
+    s.run()
+    want = oracle.encode(desc, ids, mask, normalize=S.TURBO_NORMALIZE_NONE, ranges=ranges, taps=2)
+    assert_close(s.read(), want, s.compute_dtype)
+    s.close()
+    model.close()
+
+
+def test_deberta_split_runs_meet_the_oracle(context, monkeypatch):
+    from test_deberta import small_deberta
+    desc = small_deberta(seed=5, hidden=64, heads=4, inter=128, buckets=16, maximum=64)
+    g = np.random.Generator(np.random.PCG64(6))
+    ids = g.integers(0, desc.vocab_size, (80, 64)).astype(np.int32)
+    lengths = g.integers(48, 65, 80)
+    mask = (np.arange(64)[None, :] < lengths[:, None]).astype(np.int32)
+    mask[7, 3] = 0
+    assert mask.sum() >= 4096
+    model = context.load(desc)
+    monkeypatch.setenv("TURBO_ROCM_SPLIT", "4")
+    s = model.session(80, 64, S.TURBO_PRECISION_FASTEST)
+    got = s.embed(ids, mask)
+    assert_close(got, oracle.encode(desc, ids, mask), s.compute_dtype)
     s.close()
     model.close()
 

@@ -23,8 +23,8 @@ As the reference core reads one:
   (handed to model_load) or a rerank model's pooler and classifier (applied
   on the host).
 
-The rocm backend loads the BERT, RoBERTa, ModernBERT and nomic-bert
-families from raw weights (FORMAT_SAFETENSORS); a bundle of another family
+The rocm backend loads the BERT, RoBERTa, DeBERTa-v2, ModernBERT and
+nomic-bert families from raw weights (FORMAT_SAFETENSORS); a bundle of another family
 or format is TURBO_E_BUNDLE_NO_ARTIFACT here. Tokenizers are the caller's:
 nothing here reads tokenizer.json.
 """
@@ -44,7 +44,8 @@ TURBO_E_BUNDLE_INTEGRITY = 1282
 TURBO_E_BUNDLE_NO_ARTIFACT = 1283
 
 FAMILIES = {"FAMILY_BERT": S.TURBO_FAMILY_BERT, "FAMILY_ROBERTA": S.TURBO_FAMILY_ROBERTA,
-            "FAMILY_MODERNBERT": S.TURBO_FAMILY_MODERNBERT, "FAMILY_NOMIC_BERT": S.TURBO_FAMILY_NOMIC_BERT}
+            "FAMILY_DEBERTA_V2": S.TURBO_FAMILY_DEBERTA_V2, "FAMILY_MODERNBERT": S.TURBO_FAMILY_MODERNBERT,
+            "FAMILY_NOMIC_BERT": S.TURBO_FAMILY_NOMIC_BERT}
 
 # The tensor roles of each family in TURBO_* order: embeddings, then a layer's
 # (include/turbo/turbo_backend.h:63-153).
@@ -56,6 +57,8 @@ _BERT = (("word_embeddings", "position_embeddings", "token_type_embeddings", "em
 ROLES = {
     S.TURBO_FAMILY_BERT: _BERT,
     S.TURBO_FAMILY_ROBERTA: _BERT,
+    S.TURBO_FAMILY_DEBERTA_V2: (("word_embeddings", "embeddings_ln_weight", "embeddings_ln_bias", "relative_embeddings",
+                                 "relative_ln_weight", "relative_ln_bias"), _BERT[1]),
     S.TURBO_FAMILY_MODERNBERT: (("word_embeddings", "embeddings_ln_weight", "final_norm_weight"),
                                 ("attn_ln_weight", "qkv_weight", "attn_out_weight", "ffn_ln_weight", "ffn_in_weight",
                                  "ffn_out_weight")),
@@ -189,7 +192,7 @@ class Bundle:
         family = FAMILIES.get(a.get("family"))
         if family is None:
             raise _error(TURBO_E_BUNDLE_NO_ARTIFACT, f"family {a.get('family')}: the rocm backend loads BERT, "
-                                                     "RoBERTa, ModernBERT and nomic-bert encoders")
+                                                     "RoBERTa, DeBERTa-v2, ModernBERT and nomic-bert encoders")
         arts = self.manifest.get("artifacts", [])
         if not 0 <= artifact < len(arts):
             raise _error(S.TURBO_E_INVALID_ARGUMENT, f"artifact {artifact}: bundle has {len(arts)} artifacts")
@@ -238,6 +241,12 @@ class Bundle:
                       mlp=_ENUMS["mlp"][a.get("mlp", "MLP_DENSE")],
                       activation=_ENUMS["activation"][a.get("activation", "ACTIVATION_GELU_ERF")],
                       norm=_ENUMS["norm"][a.get("norm", "NORM_LAYER")])
+        if family == S.TURBO_FAMILY_DEBERTA_V2:
+            rel = a.get("relative") or {}
+            if "position_buckets" not in rel or "max_relative_positions" not in rel:
+                raise _error(TURBO_E_BUNDLE_INVALID, "architecture.relative: a DeBERTa-v2 model needs position_buckets "
+                                                     "and max_relative_positions")
+            kw["relative"] = (int(rel["position_buckets"]), int(rel["max_relative_positions"]))
         c = self.manifest.get("classifier")
         if self.task == "TASK_EXTRACTIVE_QA" and c is not None:
             kw["span_head"] = self._classifier(find, names, a, c)[2:]

@@ -466,4 +466,112 @@ hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads,
     }
 }
 
+// ---- DeBERTa-v2 ---------------------------------------------------------------------
+//
+// Disentangled attention (reference core/src/deberta/attention.rs:207-315):
+// one workgroup per (row, head), wave w taking the row's queries w, w + 4,
+// ... A live query's score against each live key is
+// (q . k + q . pos_k[b] + k . pos_q[b]) / sqrt(3 d), three in-order F32 FMA
+// chains over the head's d columns, b the relative row of the columns'
+// distance (buckets[i - j + positions - 1]); the scores of the row's keys
+// sit in the wave's LDS (4 x max_len floats), then the max, e^(s - max)
+// and their sum by wave reductions, and the context as an F32 FMA chain
+// over the keys, times one over the sum. A masked query attends uniformly to
+// every position through the row's last live one: the mean of their values.
+template <typename T>
+__global__ void __launch_bounds__(256) deberta_attention_kernel(const T *__restrict__ qkv, int tcap, int heads, int d,
+                                                                Packing p, const int32_t *__restrict__ mask, int seq,
+                                                                int batch, const float *__restrict__ pos,
+                                                                const int32_t *__restrict__ buckets, int positions,
+                                                                T *__restrict__ ctx, int lds_len) {
+    extern __shared__ float scores[];
+    const int r = blockIdx.x / heads, head = blockIdx.x % heads;
+    if (r >= batch) return;
+    const int len = p.len[r], start = p.start[r];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float *sc = scores + wave * lds_len;
+    const int H = heads * d;
+    const T *Q = qkv + ((size_t)head * tcap + start) * d;
+    const T *K = qkv + ((size_t)(heads + head) * tcap + start) * d;
+    const T *Vt = qkv + (size_t)2 * heads * tcap * d + (size_t)head * d * tcap + start;
+    const int32_t *mk = mask + (size_t)r * seq;
+    const float inv = (float)(1.0 / sqrt(3.0 * (double)d));
+    for (int i = wave; i < len; i += 4) {
+        T *out = ctx + (size_t)(start + i) * H + head * d;
+        if (mk[i] == 0) {
+            for (int c = lane; c < d; c += 64) {
+                float s = 0.0f;
+                for (int j = 0; j < len; ++j) s += to_f32(Vt[(size_t)c * tcap + j]);
+                out[c] = from_f32<T>(s / (float)len);
+            }
+            continue;
+        }
+        const T *q = Q + (size_t)i * d;
+        float mx = -INFINITY;
+        for (int j = lane; j < len; j += 64) {
+            float s = -INFINITY;
+            if (mk[j] != 0) {
+                const T *k = K + (size_t)j * d;
+                const float *row = pos + (size_t)buckets[i - j + positions - 1] * 2 * H;
+                const float *pq = row + head * d, *pk = row + H + head * d;
+                float a = 0.0f, b = 0.0f, e = 0.0f;
+                for (int c = 0; c < d; ++c) {
+                    const float qc = to_f32(q[c]), kc = to_f32(k[c]);
+                    a = fmaf(qc, kc, a);
+                    b = fmaf(qc, pk[c], b);
+                    e = fmaf(kc, pq[c], e);
+                }
+                s = (a + b + e) * inv;
+            }
+            sc[j] = s;
+            mx = fmaxf(mx, s);
+        }
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        float sum = 0.0f;
+        for (int j = lane; j < len; j += 64) {
+            const float e = sc[j] == -INFINITY ? 0.0f : __expf(sc[j] - mx);
+            sc[j] = e;
+            sum += e;
+        }
+        sum = wave_sum(sum);
+        // Every lane reads every key's weight: this wave's LDS writes first.
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        const float rs = 1.0f / sum;
+        for (int c = lane; c < d; c += 64) {
+            float acc = 0.0f;
+            for (int j = 0; j < len; ++j) acc = fmaf(sc[j], to_f32(Vt[(size_t)c * tcap + j]), acc);
+            out[c] = from_f32<T>(acc * rs);
+        }
+        // The next query's scores overwrite these only after every lane read them.
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+template <typename T>
+static hipError_t deberta_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
+                            const int32_t *mask, int seq, int batch, int max_len, const float *pos,
+                            const int32_t *buckets, int positions, void *ctx) {
+    const size_t lds = (size_t)4 * max_len * sizeof(float);
+    if (lds > 160 * 1024 || max_len > positions) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((deberta_attention_kernel<T>), dim3(batch * heads), dim3(256), lds, s, (const T *)qkv, tcap,
+                       heads, d, p, mask, seq, batch, pos, buckets, positions, (T *)ctx, max_len);
+    return hipGetLastError();
+}
+
+hipError_t deberta_attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
+                             const int32_t *mask, int seq, int batch, int max_len, const float *pos,
+                             const int32_t *buckets, int positions, void *ctx) {
+    if (max_len <= 0 || batch <= 0) return hipSuccess;
+    switch (dt) {
+    case Dt::F16:
+        return deberta_t<_Float16>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, pos, buckets, positions, ctx);
+    case Dt::BF16:
+        return deberta_t<__bf16>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, pos, buckets, positions, ctx);
+    default:
+        return deberta_t<float>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, pos, buckets, positions, ctx);
+    }
+}
+
 }  // namespace rocm

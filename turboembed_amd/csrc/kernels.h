@@ -31,10 +31,23 @@ hipError_t pack_rows(hipStream_t s, const int32_t *mask, int batch, int seq, Pac
 // x[t] = LN(word[id] + pos[p + offset] + type[ty]) (BERT, RoBERTa), or, with
 // pos NULL, LN(word[id] (+ type[ty] when type is not NULL)) (rotary
 // families); ln_b NULL is no bias. Writes x (F32) and, when xh is not NULL,
-// its copy in `dt`.
+// its copy in `dt`. With zero_mask (the rows' mask, DeBERTa-v2), a token
+// whose mask is 0 is zero instead.
 hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                     const Packing &p, int seq, int position_offset, const float *word, const float *pos,
-                    const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt);
+                    const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt,
+                    const int32_t *zero_mask = nullptr);
+
+// DeBERTa-v2's disentangled attention over qkv (as attention reads it) into
+// ctx: for each live query i and live key j of a row, the score
+// (q_i . k_j + q_i . pos_k[b] + k_j . pos_q[b]) / sqrt(3 d), b =
+// buckets[i - j + positions - 1]; pos is the layer's [2 position_buckets][2 H]
+// F32 shared-key projections of the relative rows, query then key. A masked
+// query (mask 0 before the row's last live token) attends uniformly to every
+// position through it.
+hipError_t deberta_attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
+                             const int32_t *mask, int seq, int batch, int max_len, const float *pos,
+                             const int32_t *buckets, int positions, void *ctx);
 
 // out = LN(in) row by row over `tokens` rows of `hidden`; out_f32 and out_h
 // (in `dt`) may each be NULL, and out_f32 may be in (in place). ln_b NULL is

@@ -125,7 +125,8 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, c
                                                        int offset, const float *__restrict__ word,
                                                        const float *__restrict__ pos, const float *__restrict__ type,
                                                        const float *__restrict__ ln_w, const float *__restrict__ ln_b,
-                                                       float eps, float *__restrict__ x, H *__restrict__ xh) {
+                                                       float eps, float *__restrict__ x, H *__restrict__ xh,
+                                                       const int32_t *__restrict__ zero_mask) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= tokens) return;
     const int lane = threadIdx.x & 63;
@@ -158,6 +159,12 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, c
         }
     }
     ln_wave<G>(v, hidden, ln_w, ln_b, eps);
+    // DeBERTa: a masked token is zero after the embedding.
+    if (zero_mask && zero_mask[at] == 0)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[g][k] = 0.0f;
     store_row<G, H>(v, hidden, x + (size_t)t * hidden, xh ? xh + (size_t)t * hidden : nullptr);
 }
 
@@ -239,9 +246,10 @@ static hipError_t add_ln_y(hipStream_t s, int tokens, int hidden, float *x, cons
 template <typename H, int G>
 static hipError_t embed_ln_v(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                              const Packing &p, int seq, int offset, const float *word, const float *pos,
-                             const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh) {
+                             const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh,
+                             const int32_t *zero_mask) {
     hipLaunchKernelGGL((embed_ln_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, ids, types, p,
-                       seq, offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh);
+                       seq, offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh, zero_mask);
     return hipGetLastError();
 }
 
@@ -271,8 +279,10 @@ static hipError_t ln_v(hipStream_t s, int tokens, int hidden, const float *in, c
 template <typename H>
 static hipError_t embed_ln_t(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                              const Packing &p, int seq, int offset, const float *word, const float *pos,
-                             const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh) {
-    ROWWISE_DISPATCH(embed_ln_v, s, tokens, hidden, ids, types, p, seq, offset, word, pos, type, ln_w, ln_b, eps, x, xh)
+                             const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh,
+                             const int32_t *zero_mask) {
+    ROWWISE_DISPATCH(embed_ln_v, s, tokens, hidden, ids, types, p, seq, offset, word, pos, type, ln_w, ln_b, eps, x, xh,
+                     zero_mask)
 }
 
 template <typename H>
@@ -289,18 +299,19 @@ static hipError_t add_ln_t(hipStream_t s, int tokens, int hidden, float *x, cons
 
 hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                     const Packing &p, int seq, int position_offset, const float *word, const float *pos,
-                    const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt) {
+                    const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt,
+                    const int32_t *zero_mask) {
     if (tokens <= 0) return hipSuccess;
     switch (dt) {
     case Dt::F16:
         return embed_ln_t<_Float16>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w,
-                                    ln_b, eps, x, xh);
+                                    ln_b, eps, x, xh, zero_mask);
     case Dt::BF16:
         return embed_ln_t<__bf16>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w, ln_b,
-                                  eps, x, xh);
+                                  eps, x, xh, zero_mask);
     default:
         return embed_ln_t<float>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w, ln_b,
-                                 eps, x, xh);
+                                 eps, x, xh, zero_mask);
     }
 }
 

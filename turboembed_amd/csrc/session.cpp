@@ -89,14 +89,32 @@ void widen(const turbo_backend_model *d, uint32_t i, size_t n, float *dst, const
 
 }  // namespace
 
+// DeBERTa-v2's relative row of a signed distance (reference
+// core/src/deberta/math.rs:30-40, transformers' make_log_bucket_position):
+// within half the buckets the distance itself; beyond,
+// ceil(ln(|d| / mid) / ln((max - 1) / mid) * (mid - 1)) + mid with F32
+// logarithms, signed; offset by the buckets and clamped to the table.
+static uint32_t deberta_bucket(int64_t distance, uint32_t buckets, uint32_t maximum) {
+    const int64_t mid = buckets / 2, mag0 = distance < 0 ? -distance : distance;
+    int64_t mag = mag0;
+    if (mag0 > mid) {
+        const float a = std::log((float)mag0 / (float)mid), c = std::log((float)(maximum - 1) / (float)mid);
+        mag = (int64_t)std::ceil(a / c * (float)(mid - 1)) + mid;
+    }
+    const int64_t v = (distance < 0 ? -mag : mag) + buckets;
+    return (uint32_t)std::min<int64_t>(std::max<int64_t>(v, 0), 2 * (int64_t)buckets - 1);
+}
+
 Model *model_load(Context *c, const turbo_backend_model *d) {
     if (d->struct_size < offsetof(turbo_backend_model, tensors) + sizeof(void *))
         fail(TURBO_E_INVALID_STRUCT_SIZE, "rocm: turbo_backend_model of " + std::to_string(d->struct_size) + " bytes");
-    const bool bert = d->family == TURBO_FAMILY_BERT || d->family == TURBO_FAMILY_ROBERTA;
+    const bool deberta = d->family == TURBO_FAMILY_DEBERTA_V2;
+    const bool bert = d->family == TURBO_FAMILY_BERT || d->family == TURBO_FAMILY_ROBERTA || deberta;
     const bool modern = d->family == TURBO_FAMILY_MODERNBERT, nomic = d->family == TURBO_FAMILY_NOMIC_BERT;
     if (!bert && !modern && !nomic)
         fail(TURBO_E_UNSUPPORTED, "rocm: family " + std::to_string(d->family) +
-                                      ": the rocm backend runs BERT, RoBERTa, ModernBERT and nomic-bert encoders");
+                                      ": the rocm backend runs BERT, RoBERTa, DeBERTa-v2, ModernBERT and nomic-bert "
+                                      "encoders");
     if (d->format != TURBO_FORMAT_SAFETENSORS) fail(TURBO_E_UNSUPPORTED, "rocm: only raw weights (safetensors) load");
     if (d->dtype != TURBO_DTYPE_F32 && d->dtype != TURBO_DTYPE_F16 && d->dtype != TURBO_DTYPE_BF16)
         fail(TURBO_E_UNSUPPORTED, "rocm: weights of dtype " + std::to_string(d->dtype));
@@ -163,16 +181,48 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
         widen(d, i, n, &img.data[at], what);
         return at;
     };
+    std::vector<float> reln;   // DeBERTa-v2: the normalized relative rows
+    uint32_t rel_buckets = 0, rel_max = 0;
     if (bert) {
-        if (d->tensor_count != TURBO_BERT_EMBEDDING_TENSORS + d->layers * TURBO_BERT_LAYER_TENSORS)
+        const uint32_t emb = deberta ? TURBO_DEBERTA_EMBEDDING_TENSORS : TURBO_BERT_EMBEDDING_TENSORS;
+        if (d->tensor_count != emb + d->layers * TURBO_BERT_LAYER_TENSORS)
             fail(TURBO_E_INVALID_ARGUMENT, "rocm: tensor_count " + std::to_string(d->tensor_count));
-        off.word = put(TURBO_BERT_WORD_EMBEDDINGS, (size_t)d->vocab_size * H, "word");
-        off.pos = put(TURBO_BERT_POSITION_EMBEDDINGS, (size_t)d->max_positions * H, "position");
-        off.type = put(TURBO_BERT_TOKEN_TYPE_EMBEDDINGS, (size_t)std::max(1u, d->token_types) * H, "type");
-        off.emb_w = put(TURBO_BERT_EMBEDDINGS_LN_WEIGHT, H, "ln");
-        off.emb_b = put(TURBO_BERT_EMBEDDINGS_LN_BIAS, H, "ln");
+        if (deberta) {
+            if (d->struct_size < offsetof(turbo_backend_model, max_relative_positions) + 4 ||
+                d->position_buckets < 2 || d->max_relative_positions < 2 || d->token_types > 1)
+                fail(TURBO_E_INVALID_ARGUMENT, "rocm: a DeBERTa-v2 model has position_buckets and "
+                                               "max_relative_positions of 2 or more, and no token types");
+            rel_buckets = d->position_buckets;
+            rel_max = d->max_relative_positions;
+            off.word = put(TURBO_DEBERTA_WORD_EMBEDDINGS, (size_t)d->vocab_size * H, "word");
+            off.emb_w = put(TURBO_DEBERTA_EMBEDDINGS_LN_WEIGHT, H, "ln");
+            off.emb_b = put(TURBO_DEBERTA_EMBEDDINGS_LN_BIAS, H, "ln");
+            // The relative rows through their own LayerNorm, in F64 (reference
+            // core/src/deberta/weights.rs:91-92, math.rs:9-27).
+            const size_t rows = (size_t)2 * rel_buckets;
+            reln.resize(rows * H);
+            std::vector<float> w(H), bb(H);
+            widen(d, TURBO_DEBERTA_RELATIVE_EMBEDDINGS, rows * H, reln.data(), "relative");
+            widen(d, TURBO_DEBERTA_RELATIVE_LN_WEIGHT, H, w.data(), "relative ln");
+            widen(d, TURBO_DEBERTA_RELATIVE_LN_BIAS, H, bb.data(), "relative ln");
+            for (size_t r = 0; r < rows; ++r) {
+                float *y = &reln[r * H];
+                double sum = 0.0, var = 0.0;
+                for (uint32_t i = 0; i < H; ++i) sum += (double)y[i];
+                const double mean = sum / H;
+                for (uint32_t i = 0; i < H; ++i) var += ((double)y[i] - mean) * ((double)y[i] - mean);
+                const double scale = 1.0 / std::sqrt(var / H + d->layer_norm_eps);
+                for (uint32_t i = 0; i < H; ++i) y[i] = (float)(((double)y[i] - mean) * scale * w[i] + bb[i]);
+            }
+        } else {
+            off.word = put(TURBO_BERT_WORD_EMBEDDINGS, (size_t)d->vocab_size * H, "word");
+            off.pos = put(TURBO_BERT_POSITION_EMBEDDINGS, (size_t)d->max_positions * H, "position");
+            off.type = put(TURBO_BERT_TOKEN_TYPE_EMBEDDINGS, (size_t)std::max(1u, d->token_types) * H, "type");
+            off.emb_w = put(TURBO_BERT_EMBEDDINGS_LN_WEIGHT, H, "ln");
+            off.emb_b = put(TURBO_BERT_EMBEDDINGS_LN_BIAS, H, "ln");
+        }
         for (uint32_t l = 0; l < d->layers; ++l) {
-            const uint32_t b = TURBO_BERT_EMBEDDING_TENSORS + l * TURBO_BERT_LAYER_TENSORS;
+            const uint32_t b = emb + l * TURBO_BERT_LAYER_TENSORS;
             LOff &o = loff[l];
             // Q, K and V back to back: one [3H, H] product.
             o.wqkv = img.add((size_t)3 * H * H);
@@ -312,6 +362,34 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
         L.n_qkv = (size_t)3 * H;
         L.n_in = o.n_in;
         m->ls.push_back(L);
+    }
+    if (deberta) {
+        // Each layer's query and key projections of the normalized relative
+        // rows (shared keys): the first 2 H rows of its QKV product and bias,
+        // one F32 product a layer on the device; and the relative row of each
+        // distance a session can reach.
+        m->deberta = true;
+        const size_t rows = (size_t)2 * rel_buckets;
+        DevPtr rel(dev_alloc(rows * H * 4, "relative rows"));
+        check(hipMemcpy(rel.get(), reln.data(), rows * H * 4, hipMemcpyHostToDevice), "relative rows");
+        m->rel_pos.reset(dev_alloc((size_t)d->layers * rows * 2 * H * 4, "relative projections"));
+        float *pos = static_cast<float *>(m->rel_pos.get());
+        for (uint32_t l = 0; l < d->layers; ++l) {
+            EpiArgs e;
+            e.kind = Epi::Plain;
+            e.bias = m->ls[l].bqkv;
+            e.out = pos + (size_t)l * rows * 2 * H;
+            e.ldo = (int)(2 * H);
+            check(gemm(nullptr, Dt::F32, (int)rows, (int)(2 * H), (int)H, rel.get(), (int)H, m->ls[l].wqkv, e, 0),
+                  "relative projections");
+            m->ls[l].pos_qk = pos + (size_t)l * rows * 2 * H;
+        }
+        std::vector<int32_t> table((size_t)2 * m->positions - 1);
+        for (int64_t dist = -(int64_t)m->positions + 1; dist < (int64_t)m->positions; ++dist)
+            table[(size_t)(dist + m->positions - 1)] = (int32_t)deberta_bucket(dist, rel_buckets, rel_max);
+        m->rel_table.reset(dev_alloc(table.size() * 4, "relative buckets"));
+        check(hipMemcpy(m->rel_table.get(), table.data(), table.size() * 4, hipMemcpyHostToDevice), "relative buckets");
+        check(hipDeviceSynchronize(), "relative projections");
     }
     // The F32 weights serve the F32 tier as they are.
     for (const Model::Layer &L : m->ls) m->gemm_w[(int)Dt::F32].push_back({L.wqkv, L.wo, L.w1, L.w2});
@@ -927,8 +1005,14 @@ static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) 
             if (!global) window = (int)m.window;
         }
         mm(l, G_QKV);
-        LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, pk, mask, (int)s.seq, (int)part.rows,
-                                      (int)part.max_len, window, s.ctxb, bc.simple_attention));
+        if (m.deberta)
+            LAUNCH("attention", deberta_attention(st, dt, s.qkv, (int)s.tcap, heads, dh, pk, mask, (int)s.seq,
+                                                  (int)part.rows, (int)part.max_len, L.pos_qk,
+                                                  static_cast<const int32_t *>(m.rel_table.get()), (int)m.positions,
+                                                  s.ctxb));
+        else
+            LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, pk, mask, (int)s.seq, (int)part.rows,
+                                          (int)part.max_len, window, s.ctxb, bc.simple_attention));
         mm(l, G_OUT);
         // Post-norm: x = LN1(x + y). Pre-norm: x += y, xh = LN_mlp(x).
         if (m.modern)
@@ -977,7 +1061,8 @@ void encode(Session &s) {
     } while (0)
     LAUNCH("pack_rows", pack_rows(st, s.mask, (int)s.batch, (int)s.seq, s.pk));
     LAUNCH("embed_ln", embed_ln(st, T, H, s.ids, s.types, s.pk, (int)s.seq, (int)m.position_offset, m.word, m.pos,
-                                m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt));
+                                m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt,
+                                m.deberta ? s.mask : nullptr));
     // ModernBERT's first layer reads the embeddings' rows as they are (no
     // attention norm); on the F32 tier xh is the pre-norm rows' F32 copy.
     if (m.modern && f32) LAUNCH("copy", copy_bytes(st, s.x, s.xh, (size_t)T * H * 4));

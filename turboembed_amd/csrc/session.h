@@ -117,7 +117,12 @@ struct Model {
     struct Layer {
         const float *wqkv, *bqkv, *wo, *bo, *ln1_w, *ln1_b, *w1, *b1, *w2, *b2, *ln2_w, *ln2_b;
         size_t n_qkv, n_in;   // output rows of the QKV and FFN-in products
+        const float *pos_qk;  // DeBERTa-v2: [2 buckets][2 H] query then key projections of the relative rows
     };
+    // DeBERTa-v2: every layer's relative projections, and the relative row
+    // of each distance d in [-(positions - 1), positions - 1] at d + positions - 1.
+    bool deberta = false;
+    DevPtr rel_pos, rel_table;
     std::vector<Layer> ls;
     // Narrowed GEMM weights, per dtype (index Dt), made on first need.
     std::mutex lock;
