@@ -44,6 +44,38 @@ def kernel_flops(shape, tokens, lengths):
     return f
 
 
+HBM_PEAK = 8.0e12   # MI355X HBM3E, bytes/s (published)
+
+
+def tail_bytes(shape, dtype, tokens, rows, od):
+    """Algorithmic HBM bytes of the memory-bound kernels' launches in one
+    run, by the timing hook's names: each operand read once and each result
+    written once (a table row once per token that reads it).
+
+    embed_ln per token: the word row (and, off the rotary families, the
+    position and type rows) in F32, the ids, x written in F32 and its
+    16-bit operand copy. add_layer_norm per token: x and the product y read,
+    x written, and the normalized operand copy (16-bit, or F32 on a
+    pre-norm F32 session) except on post-norm F32 sessions and after a
+    pre-norm model's last layer. pool: each pooled token's F32 row (one per
+    output row for CLS and LAST), then the output rows."""
+    H = shape.hidden
+    modern = shape.family == S.TURBO_FAMILY_MODERNBERT
+    act = 4 if dtype == "f32" else 2
+    ysz = 2 if dtype == "f16" and shape.rope is None else 4
+    tables, ids = (1, 4) if shape.rope is not None else (3, 8)
+    out = {"embed_ln": tokens * (tables * 4 * H + ids + 4 * H + (0 if dtype == "f32" else act * H))}
+    L = shape.layers
+    if modern:
+        out["add_layer_norm"] = tokens * ((2 * L - 1) * (8 * H + ysz * H + act * H) + (8 * H + ysz * H))
+    else:
+        out["add_layer_norm"] = tokens * 2 * L * (8 * H + ysz * H + (0 if dtype == "f32" else act * H))
+    pooled = rows if shape.pooling in (S.TURBO_POOLING_CLS, S.TURBO_POOLING_LAST) and not shape.ranges_per_row \
+        else tokens
+    out["pool"] = pooled * 4 * H + rows * 4 * od
+    return out
+
+
 COPY_PROBE_BYTES = 256 << 20   # the traffic counters' reference copy: read and write this much
 
 
@@ -165,6 +197,7 @@ def main():
     sess.set_timing(True)
     sess.replay(1)
     times = sess.times()
+    counts = sess.launches()
     sess.set_timing(False)
     per = kernel_flops(shape, tokens, lens)
     gemm_names = [k for k in times if k.startswith("gemm_")]
@@ -200,6 +233,15 @@ def main():
                 "unit": "TFLOP/s", "frac": achieved / PEAK[dtype], "traffic": traffic,
                 "launches_per_step": dom_launches, "avg_launch_us": dom_ms / dom_launches * 1e3,
                 "flops_per_launch": dom_flops / dom_launches}
+
+    # The memory-bound kernels against HBM's published rate.
+    n_out = len(rngs) if rngs else shape.batch
+    tail = {}
+    for k, b in tail_bytes(shape, dtype, tokens, n_out, shape.hidden).items():
+        if times.get(k):
+            gbps = b / (times[k] / 1e3) / 1e9
+            tail[k] = {"launches": counts[k], "avg_launch_us": times[k] / counts[k] * 1e3,
+                       "bytes_per_launch": b / counts[k], "achieved_GBps": gbps, "frac": gbps * 1e9 / HBM_PEAK}
 
     # The same session on variable-length rows under the mask (the second
     # run of the workload), timed the same way.
@@ -267,6 +309,7 @@ def main():
         "ranges": len(rngs) if rngs else 0,
         "tune_ms": sess.tuning.tune_ms,
         "roofline": roofline,
+        "hbm_tail": tail,
         "cpu_baseline": cpu,
         "mfma_ceiling_measured": ceiling,
     }

@@ -107,9 +107,9 @@ int32_t turbo_rocm_session_packing(void *session, int32_t *start, int32_t *len, 
 int32_t turbo_rocm_session_hidden(void *session, float *out, uint64_t floats, turbo_error *err);
 
 /* Times every kernel of the session's later runs with HIP events on the
- * context's stream; turbo_rocm_session_times then writes "<kernel> <ms>"
- * lines, the milliseconds summed over the last run's launches of that
- * kernel. */
+ * context's stream; turbo_rocm_session_times then writes
+ * "<kernel> <ms> <launches>" lines: the milliseconds summed over the last
+ * run's launches of that kernel, and how many there were. */
 int32_t turbo_rocm_session_timing(void *session, uint32_t on, turbo_error *err);
 int32_t turbo_rocm_session_times(void *session, char *out, uint32_t len, turbo_error *err);
 

@@ -453,9 +453,16 @@ class Session:
         _ok(self.lib.turbo_rocm_session_times(self.h, buf, 8192, C.byref(err)), err)
         out = {}
         for line in buf.value.decode().splitlines():
-            name, ms = line.split()
+            name, ms, _ = line.split()
             out[name] = float(ms)
         return out
+
+    def launches(self):
+        """The last timed run's launch count of each kernel, by name."""
+        buf = C.create_string_buffer(8192)
+        err = S.new_error()
+        _ok(self.lib.turbo_rocm_session_times(self.h, buf, 8192, C.byref(err)), err)
+        return {name: int(n) for name, _, n in (line.split() for line in buf.value.decode().splitlines())}
 
     def replay(self, runs):
         """Run the written rows `runs` more times on the device, then wait."""

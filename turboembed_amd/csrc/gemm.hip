@@ -20,6 +20,7 @@
 // blocks are renumbered so that each XCD takes a contiguous run of output
 // tiles, along N first: the run shares its A rows, which then stay in that
 // XCD's L2.
+#include <atomic>
 #include <cstring>
 #include <type_traits>
 
@@ -302,13 +303,133 @@ __device__ __forceinline__ void store8(T *dst, const float (&v)[8]) {
     *(vec4 *)dst = *(const vec4 *)tmp;
 }
 
+// Stores through a buffer resource: a lane whose row lies past the output
+// gets an offset past the resource's end and the hardware drops its store, so
+// the store loop has no per-lane branches and the compiler can overlap each
+// store's LDS reads with the previous store.
+constexpr int OOB = 0x7fffffff;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// An int8 product's output: the int32 sum times both scales, plus the bias,
+// each step rounded on its own (no contraction), so every store path of the
+// epilogue gives the same bits.
+__device__ __forceinline__ float dequant(float acc, float as, float ws, float bias) {
+    return __fadd_rn(__fmul_rn(__fmul_rn(acc, as), ws), bias);
+}
+
+template <typename T>
+__device__ __forceinline__ u32x4_t pack8(const float (&v)[8]) {
+    T tmp[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) tmp[q] = from_f32<T>(v[q]);
+    return __builtin_bit_cast(u32x4_t, tmp);
+}
+
+template <typename T>
+__device__ __forceinline__ u32x2_t pack4(const float (&v)[4]) {
+    T tmp[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) tmp[q] = from_f32<T>(v[q]);
+    return __builtin_bit_cast(u32x2_t, tmp);
+}
+
+// The per-column constants a lane's epilogue stores use (the bias, and the
+// int8 weight scales), read before the main loop. A global load issued among
+// the stores would make the wait for its value wait for every store before it
+// too (the vector memory counter retires in order), so the epilogue reads
+// nothing from global memory once its first store is out. Row-wise stores: 8
+// consecutive columns of each of the lane's PH chunks; V^T stores: the one
+// column of each of the lane's KV items.
+template <int TN, int PASS, bool SCALED>
+struct EpiCols {
+    static constexpr int COLS = TN * 32, CH = COLS / 8, PH = CH / gcd_c(64, CH);
+    static constexpr int KV = COLS * (PASS / 8) / 64;
+    float b[PH][8], w[PH][8];
+    float bv[KV], wv[KV];
+};
+
+template <Epi KIND, int TN, int PASS, bool SCALED>
+__device__ __forceinline__ void load_cols(EpiCols<TN, PASS, SCALED> &c, const EpiArgs &e, int N, int nw) {
+    using C = EpiCols<TN, PASS, SCALED>;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int p = 0; p < C::PH; ++p)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) c.b[p][q] = 0.0f, c.w[p][q] = 1.0f;
+#pragma unroll
+    for (int k = 0; k < C::KV; ++k) c.bv[k] = 0.0f, c.wv[k] = 1.0f;
+#if defined(__HIP_DEVICE_COMPILE__)
+    // Buffer reads: columns at or past N read as 0 (their outputs are never stored).
+    auto rsrc = [&](const float *p) {
+        return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, N * 4, 0x00020000);
+    };
+    auto at = [&](const __amdgpu_buffer_rsrc_t &r, int n) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, n * 4, 0, 0));
+    };
+    const bool vt = (KIND == Epi::Qkv || KIND == Epi::QkvRope) && nw / e.hidden == 2;
+    if (e.bias) {
+        const __amdgpu_buffer_rsrc_t r = rsrc(e.bias);
+        if (vt) {
+#pragma unroll
+            for (int k = 0; k < C::KV; ++k) c.bv[k] = at(r, nw + (lane + 64 * k) / (PASS / 8));
+        } else {
+#pragma unroll
+            for (int p = 0; p < C::PH; ++p)
+#pragma unroll
+                for (int q = 0; q < 8; ++q) c.b[p][q] = at(r, nw + ((lane + 64 * p) % C::CH) * 8 + q);
+        }
+    }
+    if constexpr (SCALED) {
+        const __amdgpu_buffer_rsrc_t r = rsrc(e.w_scale);
+        if (vt) {
+#pragma unroll
+            for (int k = 0; k < C::KV; ++k) c.wv[k] = at(r, nw + (lane + 64 * k) / (PASS / 8));
+        } else {
+#pragma unroll
+            for (int p = 0; p < C::PH; ++p)
+#pragma unroll
+                for (int q = 0; q < 8; ++q) c.w[p][q] = at(r, nw + ((lane + 64 * p) % C::CH) * 8 + q);
+        }
+    }
+#else
+    (void)e;
+    (void)N;
+    (void)nw;
+    (void)lane;
+#endif
+}
+
+// `ascale` (int8 operands): the activation scales of this wave's rows,
+// staged in LDS before the first store.
 template <typename T, Epi KIND, int TM, int TN, int PASS, bool SCALED, typename ACC>
 __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int mw, int nw, float *scratch,
+                                             const float *ascale, const EpiCols<TN, PASS, SCALED> &cols,
                                              const ACC (&acc)[TM][TN]) {
     typedef float float4_t __attribute__((ext_vector_type(4)));
     constexpr int COLS = TN * 32, SROW = COLS + 4, CH = COLS / 8;   // 8-column chunks per row
     static_assert(PASS == 32 || PASS == 16, "32 or 16 rows a pass");
     const int lane = threadIdx.x & 63, h = lane >> 5, ql = lane & 31;
+    constexpr bool QKV = KIND == Epi::Qkv || KIND == Epi::QkvRope;
+    // The branch-free path: whole 8-column chunks, and an output region the
+    // 32-bit buffer offsets reach (row-major from this wave's first row, or
+    // one of the Q, K and V blocks).
+    const int64_t region = QKV ? (int64_t)e.heads * e.tcap * e.d * (int64_t)sizeof(T)
+                               : (int64_t)(M - mw) * e.ldo * (int64_t)((KIND == Epi::Plain || e.out_f32) ? 4 : sizeof(T));
+    const bool fast = KIND != Epi::Residual && (N & 7) == 0 && region < OOB && (!QKV || (e.d & 7) == 0);
+    const bool fast_v = fast && ((e.tcap | e.tok0) & 7) == 0;   // V^T: 8 tokens in 16 aligned bytes
+#if defined(__HIP_DEVICE_COMPILE__)
+    __amdgpu_buffer_rsrc_t rs;
+    if constexpr (QKV) {
+        const int which = nw / e.hidden;
+        rs = __builtin_amdgcn_make_buffer_rsrc((T *)e.out + (size_t)which * e.heads * e.tcap * e.d, (short)0,
+                                               (int)region, 0x00020000);
+    } else if constexpr (KIND != Epi::Residual) {
+        void *base = (KIND == Epi::Plain || e.out_f32) ? (void *)((float *)e.out + (size_t)mw * e.ldo)
+                                                       : (void *)((T *)e.out + (size_t)mw * e.ldo);
+        rs = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)(region > 0 && region < OOB ? region : 0), 0x00020000);
+    }
+#endif
 #pragma unroll
     for (int pi = 0; pi < TM * (32 / PASS); ++pi) {
         const int i = pi / (32 / PASS), half = pi % (32 / PASS);
@@ -336,18 +457,29 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                     if (n >= N) continue;
                     const int rem = n - 2 * e.hidden, head = rem / e.d, c = rem - head * e.d;
                     float v[8];
-                    const float bias = e.bias ? e.bias[n] : 0.0f;
+                    const float bias = cols.bv[k];
                     const int m = mt + g;
                     if constexpr (SCALED) {
-                        const float ws = e.w_scale[n];
+                        const float ws = cols.wv[k];
 #pragma unroll
-                        for (int q = 0; q < 8; ++q)
-                            v[q] = scratch[(g + q) * SROW + col] * (m + q < M ? e.a_scale[m + q] : 0.0f) * ws + bias;
+                        for (int q = 0; q < 8; ++q) v[q] = dequant(scratch[(g + q) * SROW + col], ascale[m + q - mw], ws, bias);
                     } else {
 #pragma unroll
                         for (int q = 0; q < 8; ++q) v[q] = scratch[(g + q) * SROW + col] + bias;
                     }
                     T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + ((size_t)head * e.d + c) * e.tcap + e.tok0;
+#if defined(__HIP_DEVICE_COMPILE__)
+                    if (fast_v) {
+                        // From the V block: rows past M, and a tail of fewer than 8, are dropped.
+                        const int off = m + 8 <= M ? (int)((((size_t)head * e.d + c) * e.tcap + e.tok0 + m) * sizeof(T)) : OOB;
+                        __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs, off, 0, 0);
+                        if (m + 8 > M && m < M) {
+#pragma unroll
+                            for (int q = 0; q < 8; ++q)
+                                if (m + q < M) out[m + q] = from_f32<T>(v[q]);
+                        }
+                    } else
+#endif
                     if (m + 8 <= M && ((e.tcap | e.tok0) & 7) == 0) {
                         store8<T>(out + m, v);
                     } else {
@@ -364,25 +496,91 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
         // 64 k taking chunk u % CH of row u / CH. A lane's chunk repeats every
         // PH items (64 PH is a multiple of CH), so its biases and scales are
         // read once per phase.
-        constexpr int PH = CH / gcd_c(64, CH);
+        constexpr int PH = EpiCols<TN, PASS, SCALED>::PH;
         static_assert((PASS * CH) % 64 == 0 && ((PASS * CH) / 64) % PH == 0, "whole items per lane");
-        int ccs[PH];
-        float biases[PH][8], wscs[PH][8];
+#if defined(__HIP_DEVICE_COMPILE__)
+        if constexpr (KIND != Epi::Residual) {
+            if (fast) {
+                const bool f32 = KIND == Epi::Plain || e.out_f32;
 #pragma unroll
-        for (int p = 0; p < PH; ++p) {
-            ccs[p] = ((lane + 64 * p) % CH) * 8;
-            const int n = nw + ccs[p];
+                for (int k = 0; k < PASS * CH / 64; ++k) {
+                    const int cc = ((lane + 64 * (k % PH)) % CH) * 8, n = nw + cc;
+                    const float(&bias)[8] = cols.b[k % PH];
+                    const float(&wsc)[8] = cols.w[k % PH];
+                    const int row = (lane + 64 * k) / CH, m = mt + row;
+                    const bool ok = m < M && n < N;
+                    const float4_t lo = *(const float4_t *)&scratch[row * SROW + cc];
+                    const float4_t hi = *(const float4_t *)&scratch[row * SROW + cc + 4];
+                    const float as = SCALED ? ascale[m - mw] : 1.0f;
+                    float v[8];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                biases[p][q] = (e.bias && n + q < N) ? e.bias[n + q] : 0.0f;
-                wscs[p][q] = (SCALED && n + q < N) ? e.w_scale[n + q] : 1.0f;
+                    for (int q = 0; q < 4; ++q) {
+                        if constexpr (SCALED) {
+                            v[q] = dequant(lo[q], as, wsc[q], bias[q]);
+                            v[4 + q] = dequant(hi[q], as, wsc[4 + q], bias[4 + q]);
+                        } else {
+                            v[q] = lo[q] + bias[q];
+                            v[4 + q] = hi[q] + bias[4 + q];
+                        }
+                    }
+                    const int rm = m - mw;   // row within the wave's region
+                    if constexpr (KIND == Epi::Plain || KIND == Epi::Bias) {
+                        if (f32) {
+                            const int off = ok ? (rm * e.ldo + n) * 4 : OOB;
+                            __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                                          __float_as_uint(v[2]), __float_as_uint(v[3])},
+                                                                  rs, off, 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{__float_as_uint(v[4]), __float_as_uint(v[5]),
+                                                                          __float_as_uint(v[6]), __float_as_uint(v[7])},
+                                                                  rs, ok ? off + 16 : OOB, 0, 0);
+                        } else {
+                            __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs,
+                                                                  ok ? (rm * e.ldo + n) * (int)sizeof(T) : OOB, 0, 0);
+                        }
+                    } else if constexpr (KIND == Epi::Gelu) {
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) v[q] = sizeof(T) == 2 ? dev_gelu_fast(v[q]) : dev_gelu(v[q]);
+                        __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs,
+                                                              ok ? (rm * e.ldo + n) * (int)sizeof(T) : OOB, 0, 0);
+                    } else if constexpr (KIND == Epi::Gated) {
+                        // Columns (2p, 2p + 1) are gate and up of output column n / 2 + p.
+                        float g4[4];
+#pragma unroll
+                        for (int p = 0; p < 4; ++p) {
+                            const float g = e.silu ? dev_silu(v[2 * p])
+                                                   : sizeof(T) == 2 ? dev_gelu_fast(v[2 * p]) : dev_gelu(v[2 * p]);
+                            g4[p] = __fmul_rn(g, v[2 * p + 1]);
+                        }
+                        __builtin_amdgcn_raw_buffer_store_b64(pack4<T>(g4), rs,
+                                                             ok ? (rm * e.ldo + (n >> 1)) * (int)sizeof(T) : OOB, 0, 0);
+                    } else {   // Qkv, QkvRope: Q or K, token-major per head
+                        const int which = n / e.hidden, rem = n - which * e.hidden;
+                        const int head = rem / e.d, c = rem - head * e.d;
+                        if constexpr (KIND == Epi::QkvRope) {
+                            const int pos = e.at[e.tok0 + min(m, M - 1)] % e.seq, hd = e.d >> 1;
+#pragma unroll
+                            for (int p = 0; p < 4; ++p) {
+                                const int pr = (c >> 1) + p;
+                                const float cs = e.cos[(size_t)pos * hd + pr], sn = e.sin[(size_t)pos * hd + pr];
+                                const float x1 = v[2 * p], x2 = v[2 * p + 1];
+                                v[2 * p] = __fsub_rn(__fmul_rn(x1, cs), __fmul_rn(x2, sn));
+                                v[2 * p + 1] = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
+                            }
+                        }
+                        const int off = ok ? (int)((((size_t)head * e.tcap + e.tok0 + m) * e.d + c) * sizeof(T)) : OOB;
+                        __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs, off, 0, 0);
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+                continue;
             }
         }
+#endif
 #pragma unroll
         for (int k = 0; k < PASS * CH / 64; ++k) {
-            const int cc = ccs[k % PH], n = nw + cc;
-            const float(&bias)[8] = biases[k % PH];
-            const float(&wsc)[8] = wscs[k % PH];
+            const int cc = ((lane + 64 * (k % PH)) % CH) * 8, n = nw + cc;
+            const float(&bias)[8] = cols.b[k % PH];
+            const float(&wsc)[8] = cols.w[k % PH];
             const int row = (lane + 64 * k) / CH;
             const int m = mt + row;
             if (m >= M || n >= N) continue;
@@ -390,12 +588,12 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
             float v[8];
             const float4_t lo = *(const float4_t *)&scratch[row * SROW + cc];
             const float4_t hi = *(const float4_t *)&scratch[row * SROW + cc + 4];
-            const float as = SCALED ? e.a_scale[m] : 1.0f;
+            const float as = SCALED ? ascale[m - mw] : 1.0f;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 if constexpr (SCALED) {
-                    v[q] = lo[q] * as * wsc[q] + bias[q];
-                    v[4 + q] = hi[q] * as * wsc[4 + q] + bias[4 + q];
+                    v[q] = dequant(lo[q], as, wsc[q], bias[q]);
+                    v[4 + q] = dequant(hi[q], as, wsc[4 + q], bias[4 + q]);
                 } else {
                     v[q] = lo[q] + bias[q];
                     v[4 + q] = hi[q] + bias[4 + q];
@@ -492,7 +690,9 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
     if (b < per * 8) b = (b % 8) * per + b / 8;
     const int tile_n = b % grid_n, tile_m = b / grid_n;
     const int m0 = tile_m * BM, n0 = tile_n * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // The wave index is uniform: kept in scalar registers, the LDS bases of
+    // the direct loads (M0) need no per-load readfirstlane.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
 
     // The operands are read through buffer resources based at the tile's
@@ -540,6 +740,14 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
         (void)k0;
 #endif
     };
+
+    // 16 rows a pass: half the staging LDS of 32, and the same stores.
+    constexpr int PASS = 16;
+    static_assert(WAVES * PASS * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <= STAGES * TILE,
+                  "epilogue staging fits the stages");
+    const int mw = m0 + wm * (BM / WM), nw = n0 + wn * (BN / WN);
+    EpiCols<TN, PASS, sizeof(T) == 1> cols;
+    load_cols<KIND>(cols, e, N, nw);
 
     acc_t acc[TM][TN];
 #pragma unroll
@@ -595,13 +803,19 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
     }
 
     // Every wave is done with the stages: their LDS becomes each wave's
-    // staging area for the stores.
+    // staging area for the stores (and, for int8 operands, for its rows'
+    // activation scales, read before the first store).
     __syncthreads();
-    constexpr int PASS = WAVES * 32 * (TN * 32 + 4) * 4 <= STAGES * TILE ? 32 : 16;
-    static_assert(WAVES * PASS * (TN * 32 + 4) * 4 <= STAGES * TILE, "epilogue staging fits the stages");
-    epilogue_lds<OT, KIND, TM, TN, PASS, sizeof(T) == 1>(e, M, N, m0 + wm * (BM / WM), n0 + wn * (BN / WN),
+    float *ascale = reinterpret_cast<float *>(smem + STAGES * TILE) - (WAVES - wave) * (BM / WM);
+    if constexpr (sizeof(T) == 1) {
+#pragma unroll
+        for (int r = lane; r < BM / WM; r += 64) ascale[r] = mw + r < M ? e.a_scale[mw + r] : 0.0f;
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's scales are in LDS
+        __builtin_amdgcn_wave_barrier();
+    }
+    epilogue_lds<OT, KIND, TM, TN, PASS, sizeof(T) == 1>(e, M, N, mw, nw,
                                                          reinterpret_cast<float *>(smem) + wave * PASS * (TN * 32 + 4),
-                                                         acc);
+                                                         ascale, cols, acc);
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK, int OCC, Epi KIND>
@@ -689,11 +903,15 @@ int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap) 
 }
 
 // The device's compute units, for the launch-shape choice.
+// (Read once per device: an attribute query on every launch costs host time
+// the device then spends idle between eagerly launched products.)
 static int cu_count() {
+    static std::atomic<int> cached[64];
     int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-        return 256;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (dev >= 0 && dev < 64 && (n = cached[dev].load(std::memory_order_relaxed)) > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+    if (dev >= 0 && dev < 64) cached[dev].store(n, std::memory_order_relaxed);
     return n;
 }
 

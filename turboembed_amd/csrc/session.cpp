@@ -1242,17 +1242,18 @@ bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
 // After a synchronized run: each kernel's milliseconds, summed by name.
 void collect_times(Session &s) {
     if (!s.timing) return;
-    std::map<std::string, double> by;
+    std::map<std::string, std::pair<double, uint32_t>> by;
     std::vector<std::string> order;
     for (size_t i = 0; i + 1 < s.ev_used; i += 2) {
         float ms = 0;
         (void)hipEventElapsedTime(&ms, s.ev[i], s.ev[i + 1]);
         const std::string &n = s.ev_name[i / 2];
         if (!by.count(n)) order.push_back(n);
-        by[n] += ms;
+        by[n].first += ms;
+        by[n].second += 1;
     }
     s.last_times.clear();
-    for (auto &n : order) s.last_times.emplace_back(n, by[n]);
+    for (auto &n : order) s.last_times.push_back({n, by[n].first, by[n].second});
 }
 
 void session_run(Session *s, turbo_backend_run *out) {
@@ -1345,7 +1346,7 @@ int32_t turbo_rocm_session_times(void *session, char *out, uint32_t len, turbo_e
         std::string t;
         for (auto &p : s->last_times) {
             char line[128];
-            std::snprintf(line, sizeof line, "%s %.6f\n", p.first.c_str(), p.second);
+            std::snprintf(line, sizeof line, "%s %.6f %u\n", p.name.c_str(), p.ms, p.launches);
             t += line;
         }
         if (len) std::snprintf(out, len, "%s", t.c_str());

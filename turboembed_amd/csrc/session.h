@@ -196,7 +196,12 @@ struct Session {
     std::vector<hipEvent_t> ev;
     std::vector<std::string> ev_name;
     size_t ev_used = 0;
-    std::vector<std::pair<std::string, double>> last_times;
+    struct Timed {
+        std::string name;
+        double ms;
+        uint32_t launches;
+    };
+    std::vector<Timed> last_times;
 };
 
 Model *model_load(Context *c, const turbo_backend_model *desc);
