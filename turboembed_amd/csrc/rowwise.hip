@@ -18,12 +18,20 @@ namespace rocm {
 __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restrict__ mask, int batch, int seq,
                                                          Packing p) {
     extern __shared__ int32_t lens[];
-    for (int r = threadIdx.x; r < batch; r += blockDim.x) lens[r] = 0;
+    // Each wave takes whole rows: every lane's last live column among its
+    // strided ones, then the wave's maximum (no atomics on a few shared words).
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    for (int r = wave; r < batch; r += waves) {
+        const int32_t *row = mask + (size_t)r * seq;
+        int last = 0;
+        for (int c = lane; c < seq; c += 64)
+            if (row[c] != 0) last = c + 1;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o, 64));
+        if (lane == 0) lens[r] = last;
+    }
     __syncthreads();
     const int n = batch * seq;
-    for (int i = threadIdx.x; i < n; i += blockDim.x)
-        if (mask[i] != 0) atomicMax(&lens[i / seq], i % seq + 1);
-    __syncthreads();
     if (threadIdx.x == 0) {
         int t = 0;
         for (int r = 0; r < batch; ++r) {
