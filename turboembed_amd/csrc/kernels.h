@@ -114,11 +114,23 @@ hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads,
                      const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx,
                      bool simple = false);
 
+// A mean's tokens are summed in chunks of POOL_CHUNK, each chunk in token
+// order by its own workgroup, then the chunks' sums in chunk order: `part`
+// holds [count][chunks][output_dim] F32 sums and `cnt` [count][chunks]
+// token counts, chunks >= ceil(seq / POOL_CHUNK).
+constexpr int POOL_CHUNK = 256;
+struct PoolScratch {
+    float *part = nullptr;
+    int32_t *cnt = nullptr;
+    int chunks = 0;
+};
+
 // One vector per row (mode 0: MEAN/CLS/LAST as pooling says) or per range
 // (mode 1: the mean over the range's live tokens), cut to output_dim, L2
 // normalized when l2, into out [count, output_dim] F32.
 hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
-                int count, const uint32_t *ranges, int pooling, int output_dim, int l2, float *out);
+                int count, const uint32_t *ranges, int pooling, int output_dim, int l2, const PoolScratch &ps,
+                float *out);
 
 // The MFMA rate probe: `blocks` workgroups of 4 waves, each wave 8 chains of
 // 32x32x16 F16 products for `iters` rounds, fixed or random operands; out
@@ -131,7 +143,8 @@ constexpr int HEAD_MAX = 16;
 // Range i's mean over all `hidden` values (as pool's mode 1) through a linear
 // head, w [hout, hidden] and b [hout] F32, its sums in F64: out [count, hout].
 hipError_t pool_head(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
-                     int count, const uint32_t *ranges, const float *hw, const float *hb, int hout, float *out);
+                     int count, const uint32_t *ranges, const float *hw, const float *hb, int hout,
+                     const PoolScratch &ps, float *out);
 
 // Symmetric int8 rows: for each of `rows` rows of `cols` values (row stride
 // ld, F32 or F16 per src_dt), scale = max |x| / 127 and q = round(x / scale)

@@ -359,18 +359,9 @@ hipError_t layer_norm(hipStream_t s, int tokens, int hidden, const float *in, co
 // the core's host head, core/src/qa/session.rs:268-276, sums the same terms).
 constexpr int POOL_THREADS = 256;
 
-template <bool HEAD>
-__global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const float *__restrict__ x, int hidden, Packing p,
-                                                            const int32_t *__restrict__ mask, int seq, int mode,
-                                                            const uint32_t *__restrict__ ranges, int pooling, int od,
-                                                            int l2, float *__restrict__ out,
-                                                            const float *__restrict__ hw,
-                                                            const float *__restrict__ hb, int hout) {
-    __shared__ double part[POOL_THREADS / 64];
-    __shared__ double hpart[HEAD ? HEAD_MAX : 1][POOL_THREADS / 64];
-    __shared__ int flag;
-    const int i = blockIdx.x;
-    int r, c0, c1;
+// Item i's tokens: a row's live extent (mode 0) or a range within it.
+__device__ __forceinline__ void pool_span(int i, int mode, const Packing &p, const uint32_t *__restrict__ ranges, int &r,
+                                          int &c0, int &c1) {
     if (mode == 0) {
         r = i;
         c0 = 0;
@@ -380,8 +371,80 @@ __global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const float *__restr
         c0 = (int)ranges[3 * i + 1];
         c1 = min((int)ranges[3 * i + 2], p.len[r]);
     }
-    const int start = p.start[r];
+}
+
+// Workgroup (i, k): the F32 sum, in token order, of chunk k of item i's
+// tokens (its live ones, when the item has any live token; else all of
+// them), and how many it summed. Tokens are read 8 at a time (their loads in
+// flight together), and added in order.
+__global__ void __launch_bounds__(POOL_THREADS) pool_part_kernel(const float *__restrict__ x, int hidden, Packing p,
+                                                                 const int32_t *__restrict__ mask, int seq, int mode,
+                                                                 const uint32_t *__restrict__ ranges, int od,
+                                                                 float *__restrict__ part, int32_t *__restrict__ cnt,
+                                                                 int chunks) {
+    const int i = blockIdx.x, k = blockIdx.y;
+    int r, c0, c1;
+    pool_span(i, mode, p, ranges, r, c0, c1);
+    const int cs = c0 + k * POOL_CHUNK;
+    if (cs >= c1) return;   // past the item: the finish reads only its own chunks
+    const int ce = min(cs + POOL_CHUNK, c1), start = p.start[r];
     const int32_t *mk = mask + (size_t)r * seq;
+    int any = 0;
+    for (int q = c0 + (int)threadIdx.x; q < c1 && !any; q += POOL_THREADS) any = mk[q] != 0;
+    const bool live_only = __syncthreads_or(any) != 0;
+    constexpr int MAXV = 8;
+    float acc[MAXV];
+#pragma unroll
+    for (int v = 0; v < MAXV; ++v) acc[v] = 0.0f;
+    int n = 0;
+    for (int q0 = cs; q0 < ce; q0 += 8) {
+        bool use[8];
+        float val[8][MAXV];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int q = q0 + j;
+            use[j] = q < ce && (!live_only || mk[q] != 0);
+            const float *row = x + (size_t)(start + (use[j] ? q : cs)) * hidden;
+#pragma unroll
+            for (int v = 0; v < MAXV; ++v) {
+                const int c = threadIdx.x + POOL_THREADS * v;
+                val[j][v] = (use[j] && c < od) ? row[c] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (!use[j]) continue;
+#pragma unroll
+            for (int v = 0; v < MAXV; ++v) acc[v] = __fadd_rn(acc[v], val[j][v]);
+            ++n;
+        }
+    }
+    float *dst = part + ((size_t)i * chunks + k) * od;
+#pragma unroll
+    for (int v = 0; v < MAXV; ++v) {
+        const int c = threadIdx.x + POOL_THREADS * v;
+        if (c < od) dst[c] = acc[v];
+    }
+    if (threadIdx.x == 0) cnt[(size_t)i * chunks + k] = n;
+}
+
+template <bool HEAD>
+__global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const float *__restrict__ x, int hidden, Packing p,
+                                                            const int32_t *__restrict__ mask, int seq, int mode,
+                                                            const uint32_t *__restrict__ ranges, int pooling, int od,
+                                                            int l2, float *__restrict__ out,
+                                                            const float *__restrict__ hw,
+                                                            const float *__restrict__ hb, int hout,
+                                                            const float *__restrict__ sums,
+                                                            const int32_t *__restrict__ cnt, int chunks) {
+    __shared__ double part[POOL_THREADS / 64];
+    __shared__ double hpart[HEAD ? HEAD_MAX : 1][POOL_THREADS / 64];
+    const int i = blockIdx.x;
+    int r, c0, c1;
+    pool_span(i, mode, p, ranges, r, c0, c1);
+    const int start = p.start[r];
+    (void)mask;
+    (void)seq;
     constexpr int MAXV = 8;   // output_dim up to 2048
     float acc[MAXV];
 #pragma unroll
@@ -394,23 +457,17 @@ __global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const float *__restr
             if (c < od) acc[v] = x[(size_t)tok * hidden + c];
         }
     } else {
-        if (threadIdx.x == 0) {
-            int any = 0;
-            for (int q = c0; q < c1 && !any; ++q) any = mk[q] != 0;
-            flag = any;
-        }
-        __syncthreads();
-        const bool live_only = flag != 0;
+        // The chunks' sums in chunk order (one chunk: its sum exactly).
+        const int nch = (c1 - c0 + POOL_CHUNK - 1) / POOL_CHUNK;
         int n = 0;
-        for (int q = c0; q < c1; ++q) {
-            if (live_only && mk[q] == 0) continue;
-            const float *row = x + (size_t)(start + q) * hidden;
+        for (int k = 0; k < nch; ++k) {
+            const float *src = sums + ((size_t)i * chunks + k) * od;
 #pragma unroll
             for (int v = 0; v < MAXV; ++v) {
                 const int c = threadIdx.x + POOL_THREADS * v;
-                if (c < od) acc[v] = __fadd_rn(acc[v], row[c]);
+                if (c < od) acc[v] = __fadd_rn(acc[v], src[c]);
             }
-            ++n;
+            n += cnt[(size_t)i * chunks + k];
         }
         const float inv = __fdiv_rn(1.0f, (float)n);
 #pragma unroll
@@ -462,21 +519,36 @@ __global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const float *__restr
     }
 }
 
+// The chunks a span of up to `seq` tokens takes.
+static bool pool_fits(const PoolScratch &ps, int seq) {
+    return ps.part && ps.cnt && ps.chunks >= (seq + POOL_CHUNK - 1) / POOL_CHUNK;
+}
+
 hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq, int count,
-                const uint32_t *ranges, int pooling, int output_dim, int l2, float *out) {
+                const uint32_t *ranges, int pooling, int output_dim, int l2, const PoolScratch &ps, float *out) {
     if (output_dim > 8 * POOL_THREADS) return hipErrorInvalidValue;
     if (count <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pool_kernel<false>, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq,
-                       ranges ? 1 : 0, ranges, pooling, output_dim, l2, out, nullptr, nullptr, 0);
+    const int mode = ranges ? 1 : 0;
+    if (mode == 1 || pooling == 1) {
+        if (!pool_fits(ps, seq)) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(pool_part_kernel, dim3(count, ps.chunks), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq,
+                           mode, ranges, output_dim, ps.part, ps.cnt, ps.chunks);
+    }
+    hipLaunchKernelGGL(pool_kernel<false>, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq, mode, ranges,
+                       pooling, output_dim, l2, out, nullptr, nullptr, 0, ps.part, ps.cnt, ps.chunks);
     return hipGetLastError();
 }
 
 hipError_t pool_head(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
-                     int count, const uint32_t *ranges, const float *hw, const float *hb, int hout, float *out) {
+                     int count, const uint32_t *ranges, const float *hw, const float *hb, int hout,
+                     const PoolScratch &ps, float *out) {
     if (hidden > 8 * POOL_THREADS || hout < 1 || hout > HEAD_MAX || !ranges) return hipErrorInvalidValue;
     if (count <= 0) return hipSuccess;
+    if (!pool_fits(ps, seq)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pool_part_kernel, dim3(count, ps.chunks), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq, 1,
+                       ranges, hidden, ps.part, ps.cnt, ps.chunks);
     hipLaunchKernelGGL(pool_kernel<true>, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq, 1, ranges,
-                       1 /* the mean */, hidden, 0, out, hw, hb, hout);
+                       1 /* the mean */, hidden, 0, out, hw, hb, hout, ps.part, ps.cnt, ps.chunks);
     return hipGetLastError();
 }
 

@@ -638,6 +638,9 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     }
     const size_t outs = std::max<size_t>(B, s->max_ranges);
     s->out = static_cast<float *>(alloc(outs * H * 4, "session output"));
+    s->pool_scratch.chunks = (int)((S + POOL_CHUNK - 1) / POOL_CHUNK);
+    s->pool_scratch.part = static_cast<float *>(alloc(outs * s->pool_scratch.chunks * H * 4, "session pooling"));
+    s->pool_scratch.cnt = static_cast<int32_t *>(alloc(outs * s->pool_scratch.chunks * 4, "session pooling"));
     s->output.ctx = m->ctx;
     s->output.placement = TURBO_PLACE_DEVICE;
     s->output.dev = s->out;
@@ -1038,7 +1041,7 @@ static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) 
             }
             float *block = s.out + (size_t)(l + reads - nl) * s.count * od;
             LAUNCH("pool", pool(st, src, H, s.pk, s.mask, (int)s.seq, (int)s.count, s.ranges, (int)s.pooling, od, l2,
-                                block));
+                                s.pool_scratch, block));
         }
     }
 #undef LAUNCH
@@ -1090,10 +1093,10 @@ void encode(Session &s) {
     const int n_out = s.count ? (int)s.count : (int)s.batch;
     if (s.head)
         LAUNCH("pool_head", pool_head(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.ranges, m.head_w, m.head_b,
-                                      (int)m.head_out, s.out));
+                                      (int)m.head_out, s.pool_scratch, s.out));
     else
         LAUNCH("pool", pool(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.count ? s.ranges : nullptr,
-                            (int)s.pooling, od, l2, s.out + (size_t)(reads - 1) * s.count * od));
+                            (int)s.pooling, od, l2, s.pool_scratch, s.out + (size_t)(reads - 1) * s.count * od));
 #undef LAUNCH
 }
 

@@ -153,6 +153,7 @@ struct Session {
     int8_t *aq = nullptr;    // I8: a GEMM's quantized operand [tcap, max(H, I)]
     float *ascale = nullptr; // I8: its per-token scales [tcap]
     float *out = nullptr;    // [max(max_batch, max_ranges), H] F32
+    PoolScratch pool_scratch;   // the means' chunk sums
     Buffer output;
     int32_t *staging = nullptr;   // pinned: ids, mask, types planes then ranges
     size_t staging_ints = 0;
