@@ -171,6 +171,33 @@ def test_ranges(context, precision):
     model.close()
 
 
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
+def test_means_over_many_chunks(context, precision):
+    # Rows of up to 1100 tokens with holes: a mean sums 256-token chunks on
+    # their own, then the chunk sums in order. Rows and ranges that cross
+    # chunk boundaries (or hold a whole chunk of masked tokens) meet the
+    # oracle; a whole-row range is the row bit for bit.
+    desc = small.bert(seed=17, positions=1200)
+    ids, mask, types = small.ragged_rows(17, 4, 1100, desc.vocab_size)
+    mask[1] = 0
+    mask[1, :1000] = 1
+    mask[1, 300:600] = 0
+    model = context.load(desc)
+    s = model.session(4, 1100, precision, max_ranges=16)
+    rows = s.embed(ids, mask, types, pooling=S.TURBO_POOLING_MEAN)
+    assert_close(rows, oracle.encode(desc, ids, mask, types, pooling=S.TURBO_POOLING_MEAN), s.compute_dtype)
+    lens = [int(np.flatnonzero(m)[-1]) + 1 for m in mask]
+    s.write_ranges(ids, mask, [(r, 0, lens[r]) for r in range(4)], types)
+    s.run()
+    assert np.array_equal(s.read(), rows)
+    ranges = [(0, 10, 1000), (1, 250, 650), (1, 290, 610), (1, 255, 257), (3, 0, lens[3]), (0, 511, 513)]
+    s.write_ranges(ids, mask, ranges, types)
+    s.run()
+    assert_close(s.read(), oracle.encode(desc, ids, mask, types, ranges=ranges), s.compute_dtype)
+    s.close()
+    model.close()
+
+
 def test_same_rows_same_bits(context):
     desc = small.bert(seed=14)
     ids, mask, types = small.ragged_rows(14, 8, 64, desc.vocab_size)
