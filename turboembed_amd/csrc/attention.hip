@@ -12,25 +12,36 @@
 
 namespace rocm {
 
-// The scalar path: one workgroup of 64 lanes per (64-query block, head, row),
-// a lane per query, the keys staged through LDS 64 at a time, an online
-// softmax in F32 with Cephes' exp. Every tier's reference path.
+// The scalar path: one workgroup of SW waves per (64-query block, head, row),
+// a lane per query; the keys are staged through LDS 64 at a time (32 at
+// d = 128) and wave w takes keys w, w + SW, ... of each stage, with its own
+// online softmax in F32 on Cephes' exp (a key's dot product in column order,
+// one FMA chain). The waves' states then merge: each rescales its context and
+// sum to the largest of their maxima, and wave 0 adds the contexts and sums in
+// wave order. Every tier's reference path.
+constexpr int SW = 4;
 template <typename T, int D>
-__global__ void __launch_bounds__(64) attention_simple_kernel(const T *__restrict__ qkv, int tcap, int heads,
-                                                              Packing p, const int32_t *__restrict__ mask, int seq,
-                                                              int window, T *__restrict__ ctx) {
+__global__ void __launch_bounds__(64 * SW) attention_simple_kernel(const T *__restrict__ qkv, int tcap, int heads,
+                                                                   Packing p, const int32_t *__restrict__ mask,
+                                                                   int seq, int window, T *__restrict__ ctx) {
     const int r = blockIdx.z, head = blockIdx.y, q0 = blockIdx.x * 64;
     const int len = p.len[r];
     if (q0 >= len) return;
     const int start = p.start[r];
-    const int lane = threadIdx.x, i = q0 + lane;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i = q0 + lane;
     const T *Q = qkv + ((size_t)head * tcap + start) * D;
     const T *K = qkv + ((size_t)(heads + head) * tcap + start) * D;
     const T *Vt = qkv + (size_t)2 * heads * tcap * D + (size_t)head * D * tcap + start;
     const int32_t *mk = mask + (size_t)r * seq;
     constexpr int KC = D <= 64 ? 64 : 32;   // keys staged a step
-    __shared__ float ks[KC][D + 1], vs[KC][D + 1];
+    constexpr int CH = D < 32 ? D : 32;     // context columns merged a round
+    constexpr int KV = 2 * KC * (D + 1), RED = SW * 64 * CH;
+    // K and V of the staged keys; after the loop, the merge's scratch.
+    __shared__ float buf[KV > RED ? KV : RED];
     __shared__ float live[KC];
+    __shared__ float mst[SW][64], lst[SW][64];
+    float(*ks)[D + 1] = reinterpret_cast<float(*)[D + 1]>(buf);
+    float(*vs)[D + 1] = reinterpret_cast<float(*)[D + 1]>(buf + KC * (D + 1));
     float q[D], acc[D];
     const float scale = 1.0f / sqrtf((float)D);
 #pragma unroll
@@ -41,16 +52,16 @@ __global__ void __launch_bounds__(64) attention_simple_kernel(const T *__restric
     float mx = -INFINITY, l = 0.0f;
     for (int j0 = 0; j0 < len; j0 += KC) {
         __syncthreads();
-        for (int x = lane; x < KC * D; x += 64) {
+        for (int x = threadIdx.x; x < KC * D; x += 64 * SW) {
             const int j = x / D, c = x % D;
             const bool in = j0 + j < len;
             ks[j][c] = in ? to_f32(K[(size_t)(j0 + j) * D + c]) : 0.0f;
             vs[j][c] = in ? to_f32(Vt[(size_t)c * tcap + j0 + j]) : 0.0f;
         }
-        if (lane < KC) live[lane] = (j0 + lane < len && mk[j0 + lane] != 0) ? 1.0f : 0.0f;
+        if (threadIdx.x < KC) live[threadIdx.x] = (j0 + (int)threadIdx.x < len && mk[j0 + threadIdx.x] != 0) ? 1.0f : 0.0f;
         __syncthreads();
         const int nj = min(KC, len - j0);
-        for (int j = 0; j < nj; ++j) {
+        for (int j = wave; j < nj; j += SW) {
             const int key = j0 + j;
             if (live[j] == 0.0f) continue;
             if (window < INT32_MAX && (key + window < i || key > i + window)) continue;
@@ -71,11 +82,40 @@ __global__ void __launch_bounds__(64) attention_simple_kernel(const T *__restric
             for (int c = 0; c < D; ++c) acc[c] = fmaf(pj, vs[j][c], acc[c]);
         }
     }
-    if (i >= len) return;
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    // Merge: every wave's state to the largest max (a wave that saw no key
+    // weighs 0), then the contexts and sums in wave order.
+    __syncthreads();
+    mst[wave][lane] = mx;
+    lst[wave][lane] = l;
+    __syncthreads();
+    float big = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < SW; ++w) big = fmaxf(big, mst[w][lane]);
+    const float f = mx == -INFINITY ? 0.0f : dev_exp(mx - big);
+    float tot_l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < SW; ++w) {
+        const float mw = mst[w][lane];
+        tot_l += (mw == -INFINITY ? 0.0f : dev_exp(mw - big)) * lst[w][lane];
+    }
+    const float inv = tot_l > 0.0f ? 1.0f / tot_l : 0.0f;
     T *out = ctx + (size_t)(start + i) * heads * D + head * D;
 #pragma unroll
-    for (int c = 0; c < D; ++c) out[c] = from_f32<T>(acc[c] * inv);
+    for (int c0 = 0; c0 < D; c0 += CH) {
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < CH; ++c) buf[(wave * CH + c) * 64 + lane] = acc[c0 + c] * f;
+        __syncthreads();
+        if (wave == 0 && i < len) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                float t = 0.0f;
+#pragma unroll
+                for (int w = 0; w < SW; ++w) t += buf[(w * CH + c) * 64 + lane];
+                out[c0 + c] = from_f32<T>(t * inv);
+            }
+        }
+    }
 }
 
 template <typename T>
@@ -84,8 +124,8 @@ static hipError_t attention_t(hipStream_t s, const void *qkv, int tcap, int head
     const dim3 grid((max_len + 63) / 64, heads, batch);
 #define ATT_CASE(D)                                                                                             \
     case D:                                                                                                     \
-        hipLaunchKernelGGL((attention_simple_kernel<T, D>), grid, dim3(64), 0, s, (const T *)qkv, tcap, heads, p, \
-                           mask, seq, window, (T *)ctx);                                                        \
+        hipLaunchKernelGGL((attention_simple_kernel<T, D>), grid, dim3(64 * SW), 0, s, (const T *)qkv, tcap,     \
+                           heads, p, mask, seq, window, (T *)ctx);                                              \
         break;
     switch (d) {
         ATT_CASE(8)
