@@ -831,7 +831,7 @@ def test_autotune_measures_caches_and_reuses(context, tmp_path):
     model.close()
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x192", "128x128", "256x128k32", "r128x128"])
+@pytest.mark.parametrize("tile", ["256x256", "256x192", "128x128", "256x128k32", "r128x128", "r64x64"])
 def test_forced_tiles_meet_the_oracle(context, tile, monkeypatch):
     desc = small.bert(seed=32, hidden=192, heads=3, inter=384, positions=320, std=0.1)
     ids, mask, types = small.ragged_rows(32, 6, 300, desc.vocab_size)

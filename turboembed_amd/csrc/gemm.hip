@@ -849,19 +849,19 @@ static hipError_t launch_lds(hipStream_t s, int M, int N, int K, const void *A, 
     return hipErrorInvalidValue;
 }
 
-int gemm_tiles() { return 13; }
+int gemm_tiles() { return 14; }
 
 // Names of the block shapes, as a choices string spells them: output tile,
 // then what sets it apart (r: operands staged through registers; k32: 32
 // columns of k a stage; s<n>: n stages).
-static const char *const TILE_NAME[14] = {"auto",      "r128x128",   "r256x128",   "r64x128",    "256x128",
+static const char *const TILE_NAME[15] = {"auto",      "r128x128",   "r256x128",   "r64x128",    "256x128",
                                           "128x128",   "128x256",    "256x256",    "128x128s2",  "256x128k32",
-                                          "128x256k32", "256x128k32s3", "256x256k32", "256x192"};
+                                          "128x256k32", "256x128k32s3", "256x256k32", "256x192",    "r64x64"};
 
-const char *gemm_tile_name(int tile) { return tile >= 0 && tile <= 13 ? TILE_NAME[tile] : "?"; }
+const char *gemm_tile_name(int tile) { return tile >= 0 && tile <= 14 ? TILE_NAME[tile] : "?"; }
 
 int gemm_tile_by_name(const char *s, size_t n) {
-    for (int t = 0; t <= 13; ++t)
+    for (int t = 0; t <= 14; ++t)
         if (std::strlen(TILE_NAME[t]) == n && std::strncmp(TILE_NAME[t], s, n) == 0) return t;
     // A bare number names a tile too.
     int v = 0;
@@ -870,7 +870,7 @@ int gemm_tile_by_name(const char *s, size_t n) {
         if (s[i] < '0' || s[i] > '9') return -1;
         v = v * 10 + (s[i] - '0');
     }
-    return v <= 13 ? v : -1;
+    return v <= 14 ? v : -1;
 }
 
 // The tiles worth timing for a product of this type and shape: every
@@ -890,6 +890,7 @@ int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap) 
         add(1);
         add(2);
         add(3);
+        add(14);
         return n;
     }
     add(7);
@@ -934,22 +935,24 @@ static int wide_tile(int M, int N, int K, const EpiArgs &e) {
     return 7;
 }
 
-// Block shapes by number: 1-3 stage operands through registers (any K a
-// multiple of 8, and the F32 tier); 4-13 are the pipelined kernel, for 16-bit
-// operands with K a multiple of 64 (every encoder shape here).
+// Block shapes by number: 1-3 and 14 stage operands through registers (any K
+// a multiple of 8, and the F32 tier); 4-13 are the pipelined kernel, for
+// 16-bit operands with K a multiple of 64 (every encoder shape here).
 template <typename T, int BK>
 static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
                          int tile) {
     const bool pipelined = sizeof(T) == 2 && K % 64 == 0 && lda % 8 == 0;
     if (tile == 0) tile = pipelined ? (M >= 2048 ? wide_tile(M, N, K, e) : 5) : 1;
     // A pipelined shape asked of an operand it cannot take runs the staged kernel.
-    if (tile >= 4 && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
+    if (tile >= 4 && tile <= 13 && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
     // 96-column wave tiles need Q, K and V to start on their boundaries.
     if (tile == 13 && (e.kind == Epi::Qkv || e.kind == Epi::QkvRope) && e.hidden % 96 != 0) tile = 7;
     switch (tile) {
     case 1: return launch<T, 128, 128, BK>(s, M, N, K, A, lda, W, e);
     case 2: return launch<T, 256, 128, BK>(s, M, N, K, A, lda, W, e);
     case 3: return launch<T, 64, 128, BK>(s, M, N, K, A, lda, W, e);
+    // 64 x 64: four times the workgroups of 128 x 128, for products too small to fill the chip.
+    case 14: return launch<T, 64, 64, BK>(s, M, N, K, A, lda, W, e);
     }
     if constexpr (sizeof(T) == 2) {
         switch (tile) {
