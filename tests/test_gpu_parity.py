@@ -33,8 +33,9 @@ def assert_close(got, want, compute_dtype):
 # ---- The GEMM kernel alone ------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [S.TURBO_DTYPE_F32, S.TURBO_DTYPE_F16, S.TURBO_DTYPE_BF16])
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13])
-@pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 200, 96), (33, 96, 32), (1000, 768, 768), (517, 2304, 1152)])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14])
+@pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 200, 96), (33, 96, 32), (1000, 768, 768), (517, 2304, 1152),
+                                 (70, 100, 64)])
 def test_gemm_matches_numpy(runtime, dtype, tile, mnk):
     m, n, k = mnk
     g = np.random.Generator(np.random.PCG64(m * 7 + n + k))
