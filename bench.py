@@ -25,8 +25,7 @@ import turboembed_amd as T  # noqa: E402
 from turboembed_amd import seam as S  # noqa: E402
 from turboembed_amd import workloads as W  # noqa: E402
 
-PEAK = {"f16": 2.5e15, "bf16": 2.5e15, "f32": 157.3e12}   # dense MFMA, MI355X
-HBM_PEAK = 8.0e12
+PEAK = {"f16": 2.5e15, "bf16": 2.5e15, "f32": 157.3e12, "i8": 5.0e15}   # dense MFMA, MI355X (int8: ops/s)
 
 
 def kernel_flops(shape, tokens, lengths):
@@ -161,7 +160,21 @@ def main():
         lengths = tuple(int(v) for v in args.lengths.split(","))
     t0 = time.time()
     desc = W.model(shape)
-    ids, mask, types = W.rows(shape, lengths=lengths)
+    if shape.task == S.TURBO_TASK_RERANK:
+        # The cross-encoder's encoder: every pair's window ([CLS] query [SEP]
+        # passage [SEP], types 0/1) as a row, CLS states unnormalized; the
+        # head, applied on the host in F64, is outside the timed steps.
+        from turboembed_amd.rerank import pair_windows
+        qt = shape.extra["query_tokens"]
+        wins = [pair_windows(q, p, shape.cls_id, shape.sep_id, query_tokens=qt, max_tokens=shape.seq)
+                for q, p in W.rerank_pairs(shape)]
+        ids = np.concatenate([w[0] for w in wins]).astype(np.int32)
+        types = np.concatenate([w[1] for w in wins]).astype(np.int32)
+        wl = np.concatenate([w[2] for w in wins])
+        mask = (np.arange(shape.seq)[None, :] < wl[:, None]).astype(np.int32)
+        assert ids.shape[0] == shape.batch, "one window a pair"
+    else:
+        ids, mask, types = W.rows(shape, lengths=lengths)
     print(f"# model and rows ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
     rt = T.Runtime()
@@ -174,7 +187,8 @@ def main():
     rngs = W.ranges(shape, mask) if shape.ranges_per_row else None
     sess = model.session(shape.batch, shape.seq, shape.precision, autotune=mode, budget_ms=args.budget_ms,
                          max_ranges=len(rngs) if rngs else 0)
-    dtype = {S.TURBO_DTYPE_F16: "f16", S.TURBO_DTYPE_BF16: "bf16", S.TURBO_DTYPE_F32: "f32"}[sess.compute_dtype]
+    dtype = {S.TURBO_DTYPE_F16: "f16", S.TURBO_DTYPE_BF16: "bf16", S.TURBO_DTYPE_F32: "f32",
+             S.TURBO_DTYPE_I8: "i8"}[sess.compute_dtype]
     if rngs:
         sess.write_ranges(ids, mask, rngs, types, normalize=shape.normalize)
     else:
@@ -230,7 +244,7 @@ def main():
     if args.copy_probe:
         T.copy_probe(COPY_PROBE_BYTES, iters=3)
     roofline = {"kernel": dom, "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[dtype] / 1e12,
-                "unit": "TFLOP/s", "frac": achieved / PEAK[dtype], "traffic": traffic,
+                "unit": "TOP/s" if dtype == "i8" else "TFLOP/s", "frac": achieved / PEAK[dtype], "traffic": traffic,
                 "launches_per_step": dom_launches, "avg_launch_us": dom_ms / dom_launches * 1e3,
                 "flops_per_launch": dom_flops / dom_launches}
 
@@ -296,8 +310,11 @@ def main():
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic",
         "config": {"workload": f"{args.workload}: {shape.layers} layers, hidden {shape.hidden}, {shape.heads} heads, "
-                               f"FFN {shape.intermediate}, {shape.batch} rows x {shape.seq}, "
-                               f"{'all live' if lengths is None else 'lengths ' + str(shape.lengths if lengths == 'default' else lengths)}",
+                               f"FFN {shape.intermediate}, {shape.batch} rows x {shape.seq}, " +
+                               (f"{shape.batch} query/passage pairs, query {shape.extra['query']} and passage "
+                                f"{shape.extra['passage']} tokens, one [CLS] q [SEP] p [SEP] window each"
+                                if shape.task == S.TURBO_TASK_RERANK else
+                                f"{'all live' if lengths is None else 'lengths ' + str(shape.lengths if lengths == 'default' else lengths)}"),
                    "global_batch": shape.batch, "seq_len": shape.seq, "live_tokens": tokens, "parallelism": "none"},
         "tokens_per_s": tokens / (ms / 1e3),
         "mfma_util_pct": 100.0 * total_flops / (ms / 1e3) / PEAK[dtype],
