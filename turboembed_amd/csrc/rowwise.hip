@@ -16,7 +16,7 @@ namespace rocm {
 // integer maxima in LDS, then an exclusive scan in row order, then each
 // token's place. Integer work only, so the result is exact.
 __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restrict__ mask, int batch, int seq,
-                                                         Packing p) {
+                                                         Packing p, int starts_in_lds) {
     extern __shared__ int32_t lens[];
     // Each wave takes whole rows: every lane's last live column among its
     // strided ones, then the wave's maximum (no atomics on a few shared words).
@@ -32,13 +32,15 @@ __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restri
     }
     __syncthreads();
     const int n = batch * seq;
+    // Each row's start after its length (lens[batch + r]), both in LDS for
+    // the placement below.
     if (threadIdx.x == 0) {
         int t = 0;
         for (int r = 0; r < batch; ++r) {
             const int l = lens[r];
             p.start[r] = t;
             p.len[r] = l;
-            lens[r] = t;   // now each row's start
+            if (starts_in_lds) lens[batch + r] = t;
             t += l;
         }
         p.tokens[0] = t;
@@ -46,15 +48,19 @@ __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restri
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const int r = i / seq, c = i % seq;
-        if (c < p.len[r]) {
-            p.at[lens[r] + c] = i;
-            p.row[lens[r] + c] = r;
+        if (c < lens[r]) {
+            const int at = (starts_in_lds ? lens[batch + r] : p.start[r]) + c;
+            p.at[at] = i;
+            p.row[at] = r;
         }
     }
 }
 
 hipError_t pack_rows(hipStream_t s, const int32_t *mask, int batch, int seq, Packing p) {
-    hipLaunchKernelGGL(pack_rows_kernel, dim3(1), dim3(1024), batch * sizeof(int32_t), s, mask, batch, seq, p);
+    // The starts go to LDS beside the lengths when both fit.
+    const int in_lds = 2 * (size_t)batch * sizeof(int32_t) <= 64 * 1024 ? 1 : 0;
+    hipLaunchKernelGGL(pack_rows_kernel, dim3(1), dim3(1024), (1 + in_lds) * batch * sizeof(int32_t), s, mask, batch,
+                       seq, p, in_lds);
     return hipGetLastError();
 }
 
