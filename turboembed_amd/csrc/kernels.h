@@ -28,6 +28,14 @@ struct Packing {
 
 hipError_t pack_rows(hipStream_t s, const int32_t *mask, int batch, int seq, Packing p);
 
+// Int8 operand rows a LayerNorm can write beside its 16-bit output (the next
+// product's operand): the codes of each row's values as rounded to the 16-bit
+// type, with its scale, exactly as quantize_rows makes them from that output.
+struct QuantOut {
+    int8_t *q = nullptr;   // [tokens][hidden]
+    float *scale = nullptr;   // [tokens]
+};
+
 // x[t] = LN(word[id] + pos[p + offset] + type[ty]) (BERT, RoBERTa), or, with
 // pos NULL, LN(word[id] (+ type[ty] when type is not NULL)) (rotary
 // families); ln_b NULL is no bias. Writes x (F32) and, when xh is not NULL,
@@ -36,7 +44,7 @@ hipError_t pack_rows(hipStream_t s, const int32_t *mask, int batch, int seq, Pac
 hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                     const Packing &p, int seq, int position_offset, const float *word, const float *pos,
                     const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt,
-                    const int32_t *zero_mask = nullptr);
+                    const int32_t *zero_mask = nullptr, const QuantOut &qo = QuantOut());
 
 // DeBERTa-v2's disentangled attention over qkv (as attention reads it) into
 // ctx: for each live query i and live key j of a row, the score
@@ -60,7 +68,8 @@ hipError_t layer_norm(hipStream_t s, int tokens, int hidden, const float *in, co
 // LN(v) in `dt` when not NULL. Pre-norm (pre_norm 1): x = v, and out_h =
 // LN(v) in `dt` (out_h F32 on the F32 tier). ln_b NULL is no bias.
 hipError_t add_layer_norm(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
-                          const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt);
+                          const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt,
+                          const QuantOut &qo = QuantOut());
 
 // What a GEMM does with each output once its sum is done.
 enum class Epi : int {

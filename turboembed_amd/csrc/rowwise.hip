@@ -133,6 +133,38 @@ __device__ __forceinline__ void store_row(const float (&v)[G][4], int hidden, fl
     }
 }
 
+// The row's int8 codes and scale from its values as rounded to H (what a
+// 16-bit output holds), as quantize_rows makes them: scale = max |v| / 127,
+// code = clamp(rint(v * 127 / max), -127, 127).
+template <int G, typename H>
+__device__ __forceinline__ void quant_row(const float (&v)[G][4], int hidden, int8_t *q, float *scale) {
+    const int lane = threadIdx.x & 63;
+    float r[G][4], mx = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            r[g][k] = 4 * (lane + 64 * g) < hidden ? to_f32(from_f32<H>(v[g][k])) : 0.0f;
+            mx = fmaxf(mx, fabsf(r[g][k]));
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int c = 4 * (lane + 64 * g);
+        if (c >= hidden) continue;
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int code = (int)fminf(fmaxf(rintf(r[g][k] * inv), -127.0f), 127.0f);
+            w |= (uint32_t)(uint8_t)(int8_t)code << (8 * k);
+        }
+        *(uint32_t *)(q + c) = w;
+    }
+    if (lane == 0) *scale = mx / 127.0f;
+}
+
 template <int G, typename H>
 __global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, const int32_t *__restrict__ ids,
                                                        const int32_t *__restrict__ types, Packing p, int seq,
@@ -140,7 +172,7 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, c
                                                        const float *__restrict__ pos, const float *__restrict__ type,
                                                        const float *__restrict__ ln_w, const float *__restrict__ ln_b,
                                                        float eps, float *__restrict__ x, H *__restrict__ xh,
-                                                       const int32_t *__restrict__ zero_mask) {
+                                                       const int32_t *__restrict__ zero_mask, QuantOut qo) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= tokens) return;
     const int lane = threadIdx.x & 63;
@@ -180,6 +212,7 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, c
 #pragma unroll
             for (int k = 0; k < 4; ++k) v[g][k] = 0.0f;
     store_row<G, H>(v, hidden, x + (size_t)t * hidden, xh ? xh + (size_t)t * hidden : nullptr);
+    if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)t * hidden, qo.scale + t);
 }
 
 template <int G, typename H>
@@ -212,7 +245,7 @@ template <int G, typename Y, typename H>
 __global__ void __launch_bounds__(256) add_layer_norm_kernel(int tokens, int hidden, float *__restrict__ x,
                                                              const Y *__restrict__ y, const float *__restrict__ ln_w,
                                                              const float *__restrict__ ln_b, float eps, int pre_norm,
-                                                             H *__restrict__ out_h) {
+                                                             H *__restrict__ out_h, QuantOut qo) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= tokens) return;
     const int lane = threadIdx.x & 63;
@@ -236,23 +269,24 @@ __global__ void __launch_bounds__(256) add_layer_norm_kernel(int tokens, int hid
     if (pre_norm) store_row<G, H>(v, hidden, row, nullptr);
     ln_wave<G>(v, hidden, ln_w, ln_b, eps);
     store_row<G, H>(v, hidden, pre_norm ? nullptr : row, out_h ? out_h + (size_t)t * hidden : nullptr);
+    if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)t * hidden, qo.scale + t);
 }
 
 template <typename H, int G, typename Y>
 static hipError_t add_ln_v(hipStream_t s, int tokens, int hidden, float *x, const void *y, const float *ln_w,
-                           const float *ln_b, float eps, int pre_norm, void *out_h) {
+                           const float *ln_b, float eps, int pre_norm, void *out_h, const QuantOut &qo) {
     hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, x,
-                       (const Y *)y, ln_w, ln_b, eps, pre_norm, (H *)out_h);
+                       (const Y *)y, ln_w, ln_b, eps, pre_norm, (H *)out_h, qo);
     return hipGetLastError();
 }
 
 template <typename H, int G>
 static hipError_t add_ln_y(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
-                           const float *ln_b, float eps, int pre_norm, void *out_h) {
+                           const float *ln_b, float eps, int pre_norm, void *out_h, const QuantOut &qo) {
     switch (ydt) {
-    case Dt::F16: return add_ln_v<H, G, _Float16>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h);
-    case Dt::BF16: return add_ln_v<H, G, __bf16>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h);
-    case Dt::F32: return add_ln_v<H, G, float>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h);
+    case Dt::F16: return add_ln_v<H, G, _Float16>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::BF16: return add_ln_v<H, G, __bf16>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::F32: return add_ln_v<H, G, float>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
     default: return hipErrorInvalidValue;
     }
 }
@@ -261,9 +295,9 @@ template <typename H, int G>
 static hipError_t embed_ln_v(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                              const Packing &p, int seq, int offset, const float *word, const float *pos,
                              const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh,
-                             const int32_t *zero_mask) {
+                             const int32_t *zero_mask, const QuantOut &qo) {
     hipLaunchKernelGGL((embed_ln_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, ids, types, p,
-                       seq, offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh, zero_mask);
+                       seq, offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh, zero_mask, qo);
     return hipGetLastError();
 }
 
@@ -294,9 +328,9 @@ template <typename H>
 static hipError_t embed_ln_t(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                              const Packing &p, int seq, int offset, const float *word, const float *pos,
                              const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh,
-                             const int32_t *zero_mask) {
+                             const int32_t *zero_mask, const QuantOut &qo) {
     ROWWISE_DISPATCH(embed_ln_v, s, tokens, hidden, ids, types, p, seq, offset, word, pos, type, ln_w, ln_b, eps, x, xh,
-                     zero_mask)
+                     zero_mask, qo)
 }
 
 template <typename H>
@@ -307,35 +341,37 @@ static hipError_t ln_t(hipStream_t s, int tokens, int hidden, const float *in, c
 
 template <typename H>
 static hipError_t add_ln_t(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
-                           const float *ln_b, float eps, int pre_norm, void *out_h) {
-    ROWWISE_DISPATCH(add_ln_y, s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h)
+                           const float *ln_b, float eps, int pre_norm, void *out_h, const QuantOut &qo) {
+    ROWWISE_DISPATCH(add_ln_y, s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo)
 }
 
 hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
                     const Packing &p, int seq, int position_offset, const float *word, const float *pos,
                     const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt,
-                    const int32_t *zero_mask) {
+                    const int32_t *zero_mask, const QuantOut &qo) {
     if (tokens <= 0) return hipSuccess;
+    if (qo.q && (dt != Dt::F16 || !xh || hidden % 4 != 0)) return hipErrorInvalidValue;
     switch (dt) {
     case Dt::F16:
         return embed_ln_t<_Float16>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w,
-                                    ln_b, eps, x, xh, zero_mask);
+                                    ln_b, eps, x, xh, zero_mask, qo);
     case Dt::BF16:
         return embed_ln_t<__bf16>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w, ln_b,
-                                  eps, x, xh, zero_mask);
+                                  eps, x, xh, zero_mask, qo);
     default:
         return embed_ln_t<float>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w, ln_b,
-                                 eps, x, xh, zero_mask);
+                                 eps, x, xh, zero_mask, qo);
     }
 }
 
 hipError_t add_layer_norm(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
-                          const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt) {
+                          const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt, const QuantOut &qo) {
     if (tokens <= 0) return hipSuccess;
+    if (qo.q && (dt != Dt::F16 || !out_h || hidden % 4 != 0)) return hipErrorInvalidValue;
     switch (dt) {
-    case Dt::F16: return add_ln_t<_Float16>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h);
-    case Dt::BF16: return add_ln_t<__bf16>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h);
-    default: return add_ln_t<float>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h);
+    case Dt::F16: return add_ln_t<_Float16>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::BF16: return add_ln_t<__bf16>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    default: return add_ln_t<float>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
     }
 }
 

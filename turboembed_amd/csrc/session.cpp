@@ -965,6 +965,15 @@ static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) 
     // first (per token; each part's rows at its own tokens of the operand
     // buffer, whose rows are max(H, I) wide), and the epilogue takes both scales.
     static const char *const NAMES[G_COUNT] = {"gemm_qkv", "gemm_out", "gemm_ffn_in", "gemm_ffn_out"};
+    // On the I8 tier the LayerNorms that make the QKV and FFN-in operands
+    // write their int8 rows too (the codes quantize_rows would make of their
+    // 16-bit output); the product that follows then skips its quantize.
+    QuantOut qo;
+    if (i8) {
+        qo.q = s.aq + t0 * std::max(H, I);
+        qo.scale = s.ascale + t0;
+    }
+    bool aq_ready = false;
     auto mm = [&](uint32_t l, GemmSlot g) {
         LayerGemm lg = layer_gemm(s, l, g);
         const void *A = static_cast<const char *>(lg.A) + t0 * lg.K * (lg.A == s.x ? 4 : el);
@@ -975,7 +984,9 @@ static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) 
         }
         if (i8) {
             int8_t *aq = s.aq + t0 * std::max(H, I);
-            LAUNCH("quantize", quantize_rows(st, A, Dt::F16, T, lg.K, lg.K, aq, s.ascale + t0));
+            if (!(aq_ready && (g == G_QKV || g == G_FFN1)))
+                LAUNCH("quantize", quantize_rows(st, A, Dt::F16, T, lg.K, lg.K, aq, s.ascale + t0));
+            aq_ready = false;
             lg.e.a_scale = s.ascale + t0;
             lg.e.w_scale = lg.wscale;
             A = aq;
@@ -1019,20 +1030,26 @@ static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) 
         mm(l, G_OUT);
         // Post-norm: x = LN1(x + y). Pre-norm: x += y, xh = LN_mlp(x).
         if (m.modern)
-            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, x, y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt));
+            LAUNCH("add_layer_norm",
+                   add_layer_norm(st, T, H, x, y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt, qo));
         else
-            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, x, y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out, dt));
+            LAUNCH("add_layer_norm",
+                   add_layer_norm(st, T, H, x, y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out, dt, qo));
+        aq_ready = i8;
         mm(l, G_FFN1);
         mm(l, G_FFN2);
         // Post-norm: x = LN2(x + y). Pre-norm: x += y and the next layer's
         // attention norm into xh, or after the last layer x = LN_final(x + y).
+        const QuantOut next = l + 1 < nl ? qo : QuantOut();
         if (!m.modern)
-            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, x, y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out, dt));
+            LAUNCH("add_layer_norm",
+                   add_layer_norm(st, T, H, x, y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out, dt, next));
         else if (l + 1 < nl)
             LAUNCH("add_layer_norm",
-                   add_layer_norm(st, T, H, x, y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps, 1, norm_out, dt));
+                   add_layer_norm(st, T, H, x, y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps, 1, norm_out, dt, next));
         else
             LAUNCH("add_layer_norm", add_layer_norm(st, T, H, x, y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
+        aq_ready = i8 && l + 1 < nl;
         if (reads > 1 && l + 1 < nl && l + reads >= nl) {
             const float *src = s.x;
             if (m.modern) {
