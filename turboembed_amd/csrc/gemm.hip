@@ -741,8 +741,14 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
 #endif
     };
 
-    // 16 rows a pass: half the staging LDS of 32, and the same stores.
-    constexpr int PASS = 16;
+    // 16 rows a pass (half the staging LDS of 32, and the same row-wise
+    // stores); 32 for the QKV scatter when they fit, so each V^T column
+    // gets 64 contiguous bytes a store instead of 32.
+    constexpr bool QKV_KIND = KIND == Epi::Qkv || KIND == Epi::QkvRope;
+    constexpr int PASS = QKV_KIND && WAVES * 32 * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <=
+                                         STAGES * TILE
+                             ? 32
+                             : 16;
     static_assert(WAVES * PASS * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <= STAGES * TILE,
                   "epilogue staging fits the stages");
     const int mw = m0 + wm * (BM / WM), nw = n0 + wn * (BN / WN);
