@@ -381,10 +381,7 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
             float mx[2] = {-INFINITY, -INFINITY};
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
-                if (all_live) {
-#pragma unroll
-                    for (int rr = 0; rr < 16; rr += 2) mx[qt] = fmaxf(mx[qt], fmaxf(sc[qt][rr], sc[qt][rr + 1]));
-                } else {
+                if (!all_live) {
                     // This lane's live keys in reach as a mask over the
                     // sub-block; register rr holds key 8 h + j, j = 16 (rr / 8) + rr % 8.
                     uint32_t okm = sbits;
@@ -403,11 +400,11 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
 #pragma unroll
                     for (int rr = 0; rr < 16; ++rr) {
                         const int j = 16 * (rr >> 3) + (rr & 7);
-                        const float v = (word >> j) & 1u ? sc[qt][rr] : -INFINITY;
-                        sc[qt][rr] = v;
-                        mx[qt] = fmaxf(mx[qt], v);
+                        sc[qt][rr] = (word >> j) & 1u ? sc[qt][rr] : -INFINITY;
                     }
                 }
+#pragma unroll
+                for (int rr = 0; rr < 16; rr += 2) mx[qt] = fmaxf(mx[qt], fmaxf(sc[qt][rr], sc[qt][rr + 1]));
                 mx[qt] = fmaxf(mx[qt], __shfl_xor(mx[qt], 32, 64));
             }
             // Every lane runs the same instructions below (the matrix cores
