@@ -186,6 +186,15 @@ template <> struct AttnMma<__bf16> {
     }
 };
 
+// The max of a lane's value and the value of the lane 32 away, in every
+// lane: v_permlane32_swap exchanges the upper half of one copy with the lower
+// half of the other, so the two copies hold each lane pair's two values (a
+// vector op; a cross-lane shuffle would go through LDS).
+__device__ __forceinline__ float max_across_halves(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ int swap23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
 // LDS rows of 128 bytes (64 keys of V^T, or one key's 64 columns of K) keep
@@ -405,7 +414,7 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
                 }
 #pragma unroll
                 for (int rr = 0; rr < 16; rr += 2) mx[qt] = fmaxf(mx[qt], fmaxf(sc[qt][rr], sc[qt][rr + 1]));
-                mx[qt] = fmaxf(mx[qt], __shfl_xor(mx[qt], 32, 64));
+                mx[qt] = max_across_halves(mx[qt]);
             }
             // Every lane runs the same instructions below (the matrix cores
             // take the whole wave): a query with nothing live in reach yet adds
