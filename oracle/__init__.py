@@ -46,6 +46,8 @@ def lib():
         _lib.oracle_quantize.restype = None
         _lib.oracle_deberta_bucket.argtypes = [C.c_int64, C.c_uint32, C.c_uint32]
         _lib.oracle_deberta_bucket.restype = C.c_uint32
+        _lib.oracle_set_gated_limit.argtypes = [C.c_float]
+        _lib.oracle_set_gated_limit.restype = None
     return _lib
 
 
@@ -70,13 +72,15 @@ def ranges_array(ranges):
 
 
 def encode(desc: ModelDesc, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN, normalize=S.TURBO_NORMALIZE_L2,
-           output_dim=None, ranges=None, threads=0, hidden=False, head=False, taps=1, tap_alone=False):
+           output_dim=None, ranges=None, threads=0, hidden=False, head=False, taps=1, tap_alone=False,
+           gated_limit=0.0):
     """The oracle's vectors for the rows (and ranges); with hidden=True also
     the final hidden states of the packed tokens. head=True on a range write
     to a model with a span head: each range's row is the head's logits.
     taps > 1 on a range write: the ranges pooled from each of the last taps
     layers, [taps * count, od] block by block; with tap_alone the first of
-    those layers alone, [count, od]."""
+    those layers alone, [count, od]. gated_limit > 0 saturates the gated
+    MLP's product at that magnitude (an F16 tier's 65504), for this call."""
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     mask = np.ascontiguousarray(mask, dtype=np.int32)
     types = None if types is None else np.ascontiguousarray(types, dtype=np.int32)
@@ -90,8 +94,15 @@ def encode(desc: ModelDesc, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN,
     out = np.zeros((n_out, od), dtype=np.float32)
     hid = np.zeros((ids.shape[0] * ids.shape[1], desc.hidden), dtype=np.float32) if hidden else None
     why = C.create_string_buffer(512)
-    rc = lib().oracle_encode(C.byref(desc.struct()), C.byref(r), rr, len(ranges), threads, out.ctypes.data,
-                             None if hid is None else hid.ctypes.data, why, 512)
+    if threads == 0:
+        # The cores this process may run on (a box's share, not its count).
+        threads = len(os.sched_getaffinity(0))
+    lib().oracle_set_gated_limit(gated_limit)
+    try:
+        rc = lib().oracle_encode(C.byref(desc.struct()), C.byref(r), rr, len(ranges), threads, out.ctypes.data,
+                                 None if hid is None else hid.ctypes.data, why, 512)
+    finally:
+        lib().oracle_set_gated_limit(0.0)
     if rc != 0:
         raise RuntimeError(f"oracle: {S.STATUS_NAMES.get(rc, rc)}: {why.value.decode()}")
     if hidden:

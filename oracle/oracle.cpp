@@ -33,6 +33,11 @@
 namespace {
 
 constexpr uint32_t kLanes = 16;        // attention's vector lanes (attend.rs:23)
+// A limit on the gated product act(gate) * up (0: none). The CPU path holds
+// it in F32; a device tier that stores it in F16 saturates it at 65504 (the
+// reference's CUDA backend, core/cuda/rotary.cuh:31-45), and the tests check
+// that tier against this oracle with the same limit set.
+std::atomic<float> gated_limit{0.0f};
 constexpr float kNegInf = -std::numeric_limits<float>::infinity();
 
 struct Failure : std::runtime_error {
@@ -860,7 +865,8 @@ void encode(const Model &m, const turbo_backend_embed_rows *rows, const turbo_to
             for (uint32_t j = 0; j < cols / 2; ++j) {
                 const float g = acc[2 * j] + L.ffn_in.bias[c0 + 2 * j];
                 const float u = acc[2 * j + 1] + L.ffn_in.bias[c0 + 2 * j + 1];
-                y[j] = (m.silu_act ? silu(g) : gelu_erf(g)) * u;
+                const float v = (m.silu_act ? silu(g) : gelu_erf(g)) * u, lim = gated_limit.load();
+                y[j] = lim > 0.0f ? (v > lim ? lim : v < -lim ? -lim : v) : v;
             }
         });
         run.linear(run.ffn.data(), I, L.ffn_out,
@@ -951,6 +957,7 @@ uint32_t oracle_pack(const int32_t *mask, uint32_t batch, uint32_t seq, uint32_t
 }
 
 float oracle_exp(float x) { return cephes_exp(x); }
+void oracle_set_gated_limit(float limit) { gated_limit.store(limit); }
 uint32_t oracle_deberta_bucket(int64_t distance, uint32_t buckets, uint32_t maximum) {
     return deberta_bucket(distance, buckets, maximum);
 }

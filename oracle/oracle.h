@@ -48,6 +48,10 @@ uint32_t oracle_pack(const int32_t *mask, uint32_t batch, uint32_t seq, uint32_t
 // ubinary. out holds rows * dim or rows * ((dim + 7) / 8) bytes.
 void  oracle_quantize(const float *x, uint32_t rows, uint32_t dim, uint32_t mode, const float *ranges, uint8_t *out);
 float oracle_exp(float x);
+/* A limit on the gated MLP's product act(gate) * up, 0 for none (the
+ * default, the CPU path's F32): an F16 tier stores that product saturated at
+ * 65504, and is checked against the oracle with this limit set. */
+void  oracle_set_gated_limit(float limit);
 /* DeBERTa-v2's relative row of a signed distance (core/src/deberta/math.rs:30-40). */
 uint32_t oracle_deberta_bucket(int64_t distance, uint32_t buckets, uint32_t maximum);
 float oracle_gelu(float x);

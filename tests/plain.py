@@ -90,9 +90,11 @@ def rope(x, theta, pos):
     return x * cos + rot * sin
 
 
-def rotary_states(desc, ids, mask, types):
+def rotary_states(desc, ids, mask, types, gated_limit=0.0):
     """ModernBERT (pre-norm, alternating windows) or nomic-bert (post-norm),
-    as turbo_backend.h:107-153 describes them."""
+    as turbo_backend.h:107-153 describes them; gated_limit > 0 clips the
+    gated product act(gate) * up to that magnitude."""
+    clip = (lambda g: np.clip(g, -gated_limit, gated_limit)) if gated_limit > 0 else (lambda g: g)  # noqa: E731
     t = [_f64(x) for x in desc.tensors]
     H, heads, I = desc.hidden, desc.heads, desc.intermediate
     d = H // heads
@@ -116,7 +118,7 @@ def rotary_states(desc, ids, mask, types):
             x = x + a @ w[2].T
             h = ln(x, w[3], None, eps)
             y = h @ w[4].T
-            x = x + (act(y[:, :I]) * y[:, I:]) @ w[5].T
+            x = x + clip(act(y[:, :I]) * y[:, I:]) @ w[5].T
         return ln(x, t[2], None, eps), live
     x = ln(t[0][ids[:n]] + t[1][types[:n]], t[2], t[3], eps)
     for l in range(desc.layers):
@@ -126,7 +128,7 @@ def rotary_states(desc, ids, mask, types):
         q, k = rope(q, g_theta, pos), rope(k, g_theta, pos)
         a = attention(q, k, v, live)
         x = ln(x + a @ w[1].T, w[2], w[3], eps)
-        x = ln(x + (act(x @ w[4].T) * (x @ w[5].T)) @ w[6].T, w[7], w[8], eps)
+        x = ln(x + clip(act(x @ w[4].T) * (x @ w[5].T)) @ w[6].T, w[7], w[8], eps)
     return x, live
 
 
@@ -191,13 +193,14 @@ def deberta_states(desc, ids, mask, types=None, uniform_masked=True):
 
 
 def embed(desc, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN, normalize=S.TURBO_NORMALIZE_L2,
-          output_dim=None):
+          output_dim=None, gated_limit=0.0):
     """Pooled, cut and normalized vectors of each row, float64."""
     types = np.zeros_like(ids) if types is None else types
     states = rotary_states if desc.rotary else deberta_states if desc.family == S.TURBO_FAMILY_DEBERTA_V2 else bert_states
+    kw = dict(gated_limit=gated_limit) if desc.rotary else {}
     out = []
     for r in range(ids.shape[0]):
-        x, live = states(desc, ids[r], mask[r], types[r])
+        x, live = states(desc, ids[r], mask[r], types[r], **kw)
         if pooling == S.TURBO_POOLING_CLS:
             v = x[0]
         elif pooling == S.TURBO_POOLING_LAST:

@@ -49,6 +49,30 @@ def nomic(seed=0, layers=2, hidden=64, heads=2, inter=96, vocab=300, positions=1
                      norm=S.TURBO_NORM_LAYER)
 
 
+def gated_overflow(desc, unit=0, scale=500.0):
+    """The gated model with one FFN unit's two input rows (the activation's
+    and the multiplier's) scaled by `scale` in its last layer, so that the
+    unit's product act(gate) * up passes F16's 65504 on most tokens, and
+    its FFN-out column scaled by 1 / (6 scale), so that the product's share
+    of the residual stays a few units (the other states still count, and
+    the column's weights stay normal F16 numbers)."""
+    if desc.family == S.TURBO_FAMILY_MODERNBERT:
+        first, per, I = S.MODERNBERT_EMBEDDING_TENSORS, S.MODERNBERT_LAYER_TENSORS, desc.intermediate
+        rows, out = [(4, unit), (4, I + unit)], 5
+    else:
+        first, per = S.NOMIC_EMBEDDING_TENSORS, S.NOMIC_LAYER_TENSORS
+        rows, out = [(4, unit), (5, unit)], 6
+    base = first + (desc.layers - 1) * per
+    for k, r in rows:
+        t = desc.tensors[base + k].copy()
+        t[r] *= np.float32(scale)
+        desc.tensors[base + k] = t
+    t = desc.tensors[base + out].copy()
+    t[:, unit] *= np.float32(1.0 / (6.0 * scale))
+    desc.tensors[base + out] = t
+    return desc
+
+
 def ragged_rows(seed, batch, seq, vocab, types=2):
     """Rows of lengths 1..seq with holes (mask-0 columns before the last
     live one), one left-padded row, ids that are not the pad under mask 0,
@@ -75,3 +99,12 @@ def cosine_rows(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return (a * b).sum(1) / np.maximum(np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1), 1e-300)
+
+
+def spearman(a, b):
+    """Spearman's rank correlation of two score vectors (distinct scores)."""
+    ra = np.argsort(np.argsort(np.asarray(a))).astype(np.float64)
+    rb = np.argsort(np.argsort(np.asarray(b))).astype(np.float64)
+    ra -= ra.mean()
+    rb -= rb.mean()
+    return float((ra * rb).sum() / np.sqrt((ra * ra).sum() * (rb * rb).sum()))

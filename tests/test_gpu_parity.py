@@ -128,6 +128,31 @@ def test_ragged_rows_meet_the_oracle(context, family, precision):
     model.close()
 
 
+@pytest.mark.parametrize("family", ["modernbert", "nomic"])
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_FASTEST, "bf16", S.TURBO_PRECISION_EXACT])
+def test_a_gated_product_past_f16_saturates(context, family, precision):
+    # One FFN unit's act(gate) * up passes 65504 on most tokens. An F16
+    # product saturates there instead of rounding to infinity (the
+    # reference's CUDA backend, core/cuda/rotary.cuh:31-45), so the vectors
+    # are finite and meet the oracle with the same limit; BF16 and F32 hold
+    # the product as it is and meet the plain oracle.
+    desc = small.gated_overflow(MODELS[family](seed=41))
+    if precision == "bf16":
+        from turboembed_amd.model import with_dtype
+        desc, precision = with_dtype(desc, "bf16"), S.TURBO_PRECISION_MODEL
+    ids, mask, types = small.ragged_rows(41, 4, 40, desc.vocab_size)
+    types = None if family == "modernbert" else types
+    model = context.load(desc)
+    s = model.session(4, 40, precision)
+    got = s.embed(ids, mask, types, normalize=S.TURBO_NORMALIZE_NONE)
+    assert np.isfinite(got).all()
+    f16 = s.compute_dtype == S.TURBO_DTYPE_F16
+    want = oracle.encode(desc, ids, mask, types, normalize=S.TURBO_NORMALIZE_NONE, gated_limit=65504.0 if f16 else 0.0)
+    assert_close(got, want, s.compute_dtype)
+    s.close()
+    model.close()
+
+
 def test_packing_is_the_oracle_s_bit_for_bit(context):
     desc = small.bert(seed=12)
     ids, mask, types = small.ragged_rows(12, 9, 40, desc.vocab_size)
@@ -560,6 +585,36 @@ def test_span_head_meets_the_upstream_logits(context, precision, max_batch):
     assert dw <= SCORE_BOUND[s.compute_dtype], dw
     print(f"QA max_batch {max_batch} dtype {s.compute_dtype}: {d:.2e} of the scale from transformers, "
           f"{dw:.2e} from the oracle")
+    s.close()
+    model.close()
+
+
+@pytest.mark.parametrize("task", [S.TURBO_TASK_EMBED, S.TURBO_TASK_RERANK, S.TURBO_TASK_EXTRACTIVE_QA])
+@pytest.mark.parametrize("precision", [S.TURBO_PRECISION_MODEL, S.TURBO_PRECISION_FASTEST, S.TURBO_PRECISION_EXACT])
+def test_capability_answers_every_task_the_core_maps_to_embed(runtime, task, precision):
+    # The core asks with the model's own task (QA and rerank included) and
+    # refuses the session on UNSUPPORTED (core/src/session/create.rs:93-111).
+    st, dt, honored, reason = runtime.capability(0, task, precision)
+    assert st == S.TURBO_CAP_EXPERIMENTAL, reason
+    assert dt == (S.TURBO_DTYPE_F16 if precision == S.TURBO_PRECISION_FASTEST else S.TURBO_DTYPE_F32)
+    assert honored == 0x338 and reason == ""
+    st, _, _, reason = runtime.capability(0, 99, precision)
+    assert st == S.TURBO_CAP_UNSUPPORTED and "task 99" in reason
+
+
+def test_a_qa_session_opens_as_the_core_opens_it(context):
+    # Capability with TURBO_TASK_EXTRACTIVE_QA, then session_open with EMBED
+    # and a range per token; the span head's logits come back.
+    desc, windows, logits, info = oracle.qa_fixture()
+    st, _, _, _ = context.rt.capability(context.ordinal, S.TURBO_TASK_EXTRACTIVE_QA, S.TURBO_PRECISION_EXACT)
+    assert st == S.TURBO_CAP_EXPERIMENTAL
+    model = context.load(desc)
+    s = model.session(2, info["qa"]["max_seq"], S.TURBO_PRECISION_EXACT, task=S.TURBO_TASK_EXTRACTIVE_QA)
+    assert s.task == S.TURBO_TASK_EXTRACTIVE_QA and s.max_ranges == 2 * info["qa"]["max_seq"]
+    got = s.span_logits(windows[:2], info["pad_id"])
+    n = sum(len(w) for w, _ in windows[:2])
+    flat = np.stack([np.concatenate([a for a, _ in got]), np.concatenate([e for _, e in got])], 1)
+    assert np.abs(flat - logits[:n]).max() <= SCORE_BOUND[s.compute_dtype] * np.abs(logits).max()
     s.close()
     model.close()
 

@@ -192,3 +192,23 @@ def test_rope_table_follows_the_rope_formula():
     # The pairs past 0 turn slower under the larger base.
     small_t = rope_table(160000.0, 10000.0, 5, 3)
     assert small_t[0, 1, 4, 2] < small_t[1, 1, 4, 2]
+
+
+@pytest.mark.parametrize("family", ["modernbert", "nomic"])
+def test_the_gated_limit_meets_the_textbook_and_bites(family):
+    # The F16 tier's saturation of the gated product (65504), restated in the
+    # oracle as a limit: the oracle with it meets the f64 textbook with the
+    # same clip, the oracle without it meets the textbook without, and on a
+    # model whose unit passes 65504 the two differ.
+    make = small.modernbert if family == "modernbert" else small.nomic
+    desc = small.gated_overflow(make(seed=41))
+    ids, mask, types = small.ragged_rows(41, 4, 40, desc.vocab_size)
+    types = None if family == "modernbert" else types
+    kw = dict(normalize=S.TURBO_NORMALIZE_NONE)
+    lim = oracle.encode(desc, ids, mask, types, gated_limit=65504.0, **kw)
+    free = oracle.encode(desc, ids, mask, types, **kw)
+    _plain_close(lim, plain.embed(desc, ids, mask, types, gated_limit=65504.0, **kw))
+    _plain_close(free, plain.embed(desc, ids, mask, types, **kw))
+    assert np.abs(lim - free).max() > 1e-3
+    # A limit no product reaches changes no bit.
+    assert np.array_equal(oracle.encode(desc, ids, mask, types, gated_limit=3e38, **kw), free)

@@ -15,6 +15,8 @@ from turboembed_amd import TurboError
 from turboembed_amd import seam as S
 from turboembed_amd.rerank import PAIR_BERT, PAIR_ROBERTA, RerankHead, head_scores, pair_windows
 
+import small
+
 
 @pytest.fixture(scope="module")
 def tiny():
@@ -114,3 +116,16 @@ def test_the_head_refuses_a_non_finite_state():
     with pytest.raises(TurboError) as e:
         head_scores(states, RerankHead(classifier_weight=np.ones(8, np.float32)))
     assert e.value.code == S.TURBO_E_INTERNAL
+
+
+def test_the_rank_statistic_is_spearman_s():
+    # The rank agreement the int8 cross-encoder is held to: identical orders
+    # give 1, reversed -1, and it is scipy's Spearman rho on distinct values.
+    from scipy.stats import spearmanr
+    a = np.arange(100, dtype=np.float64)
+    assert small.spearman(a, a * 3 + 1) == pytest.approx(1.0)
+    assert small.spearman(a, -a) == pytest.approx(-1.0)
+    g = np.random.Generator(np.random.PCG64(1))
+    x, y = g.standard_normal(64), g.standard_normal(64)
+    y = x + 0.5 * y
+    assert small.spearman(x, y) == pytest.approx(spearmanr(x, y).statistic, abs=1e-12)

@@ -232,6 +232,14 @@ class Session:
         # every token a run may hold (core/src/session/create.rs:61-62,
         # core/src/qa/session.rs:138-140).
         self.task = task
+        # The core asks the backend about the model's own task first and
+        # refuses the session when the backend cannot run it
+        # (core/src/session/create.rs:93-111).
+        ctx = model.ctx
+        st, _, _, reason = ctx.rt.capability(ctx.ordinal, task, precision)
+        if st == S.TURBO_CAP_UNSUPPORTED:
+            raise TurboError(S.TURBO_E_UNSUPPORTED_TASK, 0,
+                             f"the rocm backend does not run task {task}: {reason}")
         if task == S.TURBO_TASK_EXTRACTIVE_QA:
             task, max_ranges = S.TURBO_TASK_EMBED, max_ranges or max_batch * max_seq
         d.task, d.max_batch, d.max_seq, d.precision = task, max_batch, max_seq, precision

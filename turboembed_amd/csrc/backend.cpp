@@ -160,15 +160,23 @@ int32_t device_info(uint32_t ordinal, turbo_device_info *out, turbo_error *err) 
 // is bit n - 1 (core/src/session/tokens.rs:157-162).
 constexpr uint32_t EMBED_HONORED = (1u << 3) | (1u << 4) | (1u << 5) | (1u << 8) | (1u << 9);
 
+// Every task the core maps onto the embedding encoder runs here: EMBED,
+// RERANK (CLS rows for the core's host head) and EXTRACTIVE_QA (range writes
+// through the span head, token_head = 1). The core asks with the model's own
+// task before it opens the session with EMBED (reference
+// core/src/session/create.rs:61-62, 93-111; the CUDA backend answers
+// EXPERIMENTAL whatever the task, core/cuda/backend.cpp:411-434).
 int32_t capability(uint32_t ordinal, uint32_t task, uint32_t precision, uint32_t *status, uint32_t *dtype,
                    uint32_t *options_honored, char *reason, uint32_t reason_len, turbo_error *err) {
     return guarded(err, [&] {
         if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device " + std::to_string(ordinal));
-        if (task != TURBO_TASK_EMBED && task != TURBO_TASK_RERANK) {
+        if (task != TURBO_TASK_EMBED && task != TURBO_TASK_RERANK && task != TURBO_TASK_EXTRACTIVE_QA) {
             *status = TURBO_CAP_UNSUPPORTED;
             *dtype = 0;
             *options_honored = 0;
-            if (reason_len) std::snprintf(reason, reason_len, "the rocm backend runs the embed and rerank encoders alone");
+            if (reason_len)
+                std::snprintf(reason, reason_len, "task %u: the rocm backend runs the embed, rerank and extractive QA "
+                              "encoders", task);
             return TURBO_OK;
         }
         *status = TURBO_CAP_EXPERIMENTAL;

@@ -75,6 +75,16 @@ template <> struct Mma<float> {
     }
 };
 
+// A gated unit's product act(gate) * up as stored: at an F16 output it
+// saturates at F16's largest finite magnitude instead of rounding to
+// infinity (a NaN stays NaN), as the reference's CUDA backend stores it
+// (core/cuda/rotary.cuh:31-45); BF16 and F32 outputs hold it as it is.
+template <typename T> __device__ __forceinline__ float gated_product(float g, float up) {
+    const float v = __fmul_rn(g, up);
+    if constexpr (std::is_same<T, _Float16>::value) return v > 65504.0f ? 65504.0f : v < -65504.0f ? -65504.0f : v;
+    return v;
+}
+
 // The epilogue of one 32 x 32 MFMA tile, for this lane's column n and its 16
 // rows m0 + 8 (r / 4) + 4 (lane / 32) + r % 4, v = acc + bias. The kind is a
 // template argument, so each kernel carries one small epilogue, and what
@@ -137,7 +147,7 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
             const float up = __shfl_xor(v, 1, 64);
             if (!col_ok || m >= M || (n & 1)) continue;
             const float g = e.silu ? dev_silu(v) : sizeof(T) == 2 ? dev_gelu_fast(v) : dev_gelu(v);
-            ((T *)e.out)[(size_t)m * e.ldo + (n >> 1)] = from_f32<T>(__fmul_rn(g, up));
+            ((T *)e.out)[(size_t)m * e.ldo + (n >> 1)] = from_f32<T>(gated_product<T>(g, up));
         }
     }
 }
@@ -549,7 +559,7 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                         for (int p = 0; p < 4; ++p) {
                             const float g = e.silu ? dev_silu(v[2 * p])
                                                    : sizeof(T) == 2 ? dev_gelu_fast(v[2 * p]) : dev_gelu(v[2 * p]);
-                            g4[p] = __fmul_rn(g, v[2 * p + 1]);
+                            g4[p] = gated_product<T>(g, v[2 * p + 1]);
                         }
                         __builtin_amdgcn_raw_buffer_store_b64(pack4<T>(g4), rs,
                                                              ok ? (rm * e.ldo + (n >> 1)) * (int)sizeof(T) : OOB, 0, 0);
@@ -635,7 +645,7 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                 for (int p = 0; p < 4; ++p) {
                     if (n + 2 * p + 1 >= N) break;
                     const float g = e.silu ? dev_silu(v[2 * p]) : sizeof(T) == 2 ? dev_gelu_fast(v[2 * p]) : dev_gelu(v[2 * p]);
-                    o[p] = from_f32<T>(__fmul_rn(g, v[2 * p + 1]));
+                    o[p] = from_f32<T>(gated_product<T>(g, v[2 * p + 1]));
                 }
             } else {   // Qkv, QkvRope: Q or K, token-major per head
                 const int which = n / e.hidden, rem = n - which * e.hidden;
