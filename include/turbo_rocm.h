@@ -94,6 +94,22 @@ int32_t turbo_rocm_rerank_run(void *session, const int32_t *ids, const int32_t *
                               const float *pooler_weight, const float *pooler_bias, const float *classifier_weight,
                               float classifier_bias, float *scores, turbo_error *err);
 
+/* turbo_rocm_buffer_quantize_static: buffer_quantize (the table's entry,
+ * turbo_backend.h:610-626) without an allocation. It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The same codes, byte for byte, staged in a fixed device area of
+ * 16 MiB a GPU (allocated once with the library, held until the process
+ * ends) instead of memory allocated per call: the codes, then on a 256-byte
+ * boundary the int8 ranges ([2, dim] F32), must fit it, or the call fails
+ * with TURBO_E_INVALID_ARGUMENT before any device work. It calls no
+ * allocating routine. Calls that overlap on one GPU through different
+ * contexts share the area and race; calls through one context are serialized.
+ * run, when not NULL, gets the int8 ranges' bytes in h2d_bytes and no
+ * device allocation. */
+int32_t turbo_rocm_buffer_quantize_static(void *buffer, uint32_t quantization, const float *int8_ranges, uint32_t rows,
+                                          uint32_t dim, turbo_backend_run *run, turbo_error *err);
+
 /* ---- Test and measurement hooks (no counterpart in the reference's seam; the
  * reference's CUDA backend keeps similar ones, core/src/cuda.rs:177-499) ---- */
 

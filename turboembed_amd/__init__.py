@@ -63,6 +63,8 @@ def library():
                                     C.POINTER(u32), E],
         "turbo_rocm_rerank_scores": [P, u32, u32, P, P, P, C.c_float, P, E],
         "turbo_rocm_rerank_run": [P, P, P, P, u32, u32, P, u32, P, P, P, C.c_float, P, E],
+        "turbo_rocm_buffer_quantize_static": [P, u32, C.POINTER(C.c_float), u32, u32, C.POINTER(S.turbo_backend_run),
+                                              E],
     }
     for name, args in protos.items():
         f = getattr(lib, name)
@@ -186,6 +188,17 @@ class Buffer:
         _ok(self.t.buffer_quantize(self.h, quantization,
                                    None if rr is None else rr.ctypes.data_as(C.POINTER(C.c_float)), rows, dim,
                                    None if run is None else C.byref(run), C.byref(err)), err)
+
+    def quantize_static(self, quantization, rows, dim, int8_ranges=None, run=None):
+        """turbo_rocm_buffer_quantize_static: the same codes as quantize,
+        staged in the device's fixed area instead of allocated memory."""
+        rr = None
+        if int8_ranges is not None:
+            rr = np.ascontiguousarray(int8_ranges, np.float32)
+        err = S.new_error()
+        _ok(library().turbo_rocm_buffer_quantize_static(
+            self.h, quantization, None if rr is None else rr.ctypes.data_as(C.POINTER(C.c_float)), rows, dim,
+            None if run is None else C.byref(run), C.byref(err)), err)
 
     def close(self):
         if self.h:

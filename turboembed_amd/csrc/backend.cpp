@@ -197,6 +197,9 @@ int32_t context_create(uint32_t ordinal, turbo_log_fn log, void *ud, void **out,
         c->log = log;
         c->log_user_data = ud;
         OnDevice on(c->ordinal);
+        // The device's fixed staging area (the no-allocation buffer_quantize):
+        // its address on this device, looked up with the device current.
+        check(static_scratch(c->ordinal, &c->scratch), "the device's staging area");
         // Default priority on every stream: the one stream priority every run
         // uses. The side streams carry a split run's other parts of rows; the
         // events fork them from the first and join them back.
@@ -361,6 +364,35 @@ int32_t buffer_read(void *buf, void *dst, uint64_t bytes, turbo_error *err) {
     });
 }
 
+// The checks buffer_quantize and its no-allocation variant share: the
+// codes' mode, a device-addressable buffer holding rows x dim F32 values,
+// finite int8 ranges with min <= max. Returns the codes' bytes (0: nothing
+// to do).
+uint64_t quantize_codes_bytes(const Buffer *b, uint32_t quantization, const float *int8_ranges, uint32_t rows,
+                              uint32_t dim) {
+    if (quantization != TURBO_QUANTIZE_INT8 && quantization != TURBO_QUANTIZE_UBINARY)
+        fail(TURBO_E_INVALID_ARGUMENT, "rocm: quantization " + std::to_string(quantization) +
+                                           " is not int8 or ubinary");
+    if (!b->dev || (b->placement != TURBO_PLACE_DEVICE && b->placement != TURBO_PLACE_SHARED))
+        fail(TURBO_E_INVALID_ARGUMENT, "rocm: buffer_quantize needs a device or shared buffer");
+    const uint64_t floats = (uint64_t)rows * dim;
+    if (floats * 4 > b->bytes)
+        fail(TURBO_E_INVALID_ARGUMENT, "rocm: " + std::to_string(rows) + " by " + std::to_string(dim) +
+                                           " values over the buffer's " + std::to_string(b->bytes) + " bytes");
+    if (rows == 0 || dim == 0) return 0;
+    if (rows > (uint32_t)INT32_MAX || dim > (uint32_t)INT32_MAX)
+        fail(TURBO_E_INVALID_ARGUMENT, "rocm: rows and dim must fit in 31 bits");
+    const bool i8 = quantization == TURBO_QUANTIZE_INT8;
+    if (i8) {
+        if (!int8_ranges) fail(TURBO_E_INVALID_ARGUMENT, "rocm: int8 codes need the [2, dim] ranges");
+        for (uint32_t d = 0; d < dim; ++d)
+            if (!std::isfinite(int8_ranges[d]) || !std::isfinite(int8_ranges[dim + d]) ||
+                int8_ranges[d] > int8_ranges[dim + d])
+                fail(TURBO_E_INVALID_ARGUMENT, "rocm: int8 ranges of dimension " + std::to_string(d));
+    }
+    return i8 ? floats : (uint64_t)rows * ((dim + 7) / 8);
+}
+
 // On-device vector codes (turbo_backend.h:610-626): the first rows x dim F32
 // values of a device buffer as int8 or ubinary codes, written over the
 // buffer's leading bytes. The codes go to a temporary device buffer first,
@@ -370,27 +402,9 @@ int32_t buffer_quantize(void *buf, uint32_t quantization, const float *int8_rang
                         turbo_backend_run *run, turbo_error *err) {
     return guarded(err, [&] {
         Buffer *b = static_cast<Buffer *>(buf);
-        if (quantization != TURBO_QUANTIZE_INT8 && quantization != TURBO_QUANTIZE_UBINARY)
-            fail(TURBO_E_INVALID_ARGUMENT, "rocm: quantization " + std::to_string(quantization) +
-                                               " is not int8 or ubinary");
-        if (!b->dev || (b->placement != TURBO_PLACE_DEVICE && b->placement != TURBO_PLACE_SHARED))
-            fail(TURBO_E_INVALID_ARGUMENT, "rocm: buffer_quantize needs a device or shared buffer");
-        const uint64_t floats = (uint64_t)rows * dim;
-        if (floats * 4 > b->bytes)
-            fail(TURBO_E_INVALID_ARGUMENT, "rocm: " + std::to_string(rows) + " by " + std::to_string(dim) +
-                                               " values over the buffer's " + std::to_string(b->bytes) + " bytes");
-        if (rows == 0 || dim == 0) return TURBO_OK;
-        if (rows > (uint32_t)INT32_MAX || dim > (uint32_t)INT32_MAX)
-            fail(TURBO_E_INVALID_ARGUMENT, "rocm: rows and dim must fit in 31 bits");
+        const uint64_t code_bytes = quantize_codes_bytes(b, quantization, int8_ranges, rows, dim);
+        if (code_bytes == 0) return TURBO_OK;
         const bool i8 = quantization == TURBO_QUANTIZE_INT8;
-        if (i8) {
-            if (!int8_ranges) fail(TURBO_E_INVALID_ARGUMENT, "rocm: int8 codes need the [2, dim] ranges");
-            for (uint32_t d = 0; d < dim; ++d)
-                if (!std::isfinite(int8_ranges[d]) || !std::isfinite(int8_ranges[dim + d]) ||
-                    int8_ranges[d] > int8_ranges[dim + d])
-                    fail(TURBO_E_INVALID_ARGUMENT, "rocm: int8 ranges of dimension " + std::to_string(d));
-        }
-        const uint64_t code_bytes = i8 ? floats : (uint64_t)rows * ((dim + 7) / 8);
         std::lock_guard<std::mutex> g(b->ctx->lock);
         OnDevice on(b->ctx->ordinal);
         const uint64_t dev0 = device_allocs.load();
@@ -514,5 +528,46 @@ const turbo_backend turbo_rocm_backend = {
     0,
     buffer_quantize,
 };
+
+// buffer_quantize without an allocation: the same codes, staged in the
+// device's fixed staging area (STATIC_SCRATCH_BYTES: the codes, then the
+// int8 ranges on a 256-byte boundary) instead of memory allocated per call.
+// Calls whose codes and ranges exceed it are refused before any device work.
+// Every call on one GPU shares the area, so calls that overlap on one GPU
+// (through two contexts) race; calls through one context are serialized by
+// its lock. Nothing in the area needs clearing: every code byte is written.
+int32_t turbo_rocm_buffer_quantize_static(void *buf, uint32_t quantization, const float *int8_ranges, uint32_t rows,
+                                          uint32_t dim, turbo_backend_run *run, turbo_error *err) {
+    return guarded(err, [&] {
+        Buffer *b = static_cast<Buffer *>(buf);
+        const uint64_t code_bytes = quantize_codes_bytes(b, quantization, int8_ranges, rows, dim);
+        if (code_bytes == 0) return TURBO_OK;
+        const bool i8 = quantization == TURBO_QUANTIZE_INT8;
+        const uint64_t ranges_at = (code_bytes + 255) & ~(uint64_t)255;
+        const uint64_t need = i8 ? ranges_at + (uint64_t)2 * dim * 4 : code_bytes;
+        if (need > STATIC_SCRATCH_BYTES)
+            fail(TURBO_E_INVALID_ARGUMENT, "rocm: buffer_quantize_static stages at most " +
+                                               std::to_string(STATIC_SCRATCH_BYTES) + " bytes (the codes, then the "
+                                               "int8 ranges); " + std::to_string(rows) + " by " + std::to_string(dim) +
+                                               " values need " + std::to_string(need));
+        std::lock_guard<std::mutex> g(b->ctx->lock);
+        OnDevice on(b->ctx->ordinal);
+        void *area = b->ctx->scratch;
+        if (!area) fail(TURBO_E_RUNTIME, "rocm: the device's staging area was not found at context creation");
+        uint8_t *codes = static_cast<uint8_t *>(area);
+        const float *ranges = i8 ? reinterpret_cast<const float *>(codes + ranges_at) : nullptr;
+        hipStream_t st = b->ctx->stream;
+        if (i8)
+            check(hipMemcpyAsync(codes + ranges_at, int8_ranges, (size_t)2 * dim * 4, hipMemcpyHostToDevice, st),
+                  "int8 ranges");
+        check(quantize_codes(st, static_cast<const float *>(b->dev), (int)rows, (int)dim, (int)quantization, ranges,
+                             codes),
+              "buffer_quantize_static");
+        check(hipMemcpyAsync(b->dev, codes, code_bytes, hipMemcpyDeviceToDevice, st), "buffer_quantize_static");
+        check(hipStreamSynchronize(st), "buffer_quantize_static");
+        if (run && i8) run->h2d_bytes += (uint64_t)2 * dim * 4;
+        return TURBO_OK;
+    });
+}
 
 }  // extern "C"

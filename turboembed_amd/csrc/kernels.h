@@ -172,6 +172,15 @@ hipError_t quantize_rows(hipStream_t s, const void *src, Dt src_dt, int rows, in
 hipError_t quantize_codes(hipStream_t s, const float *x, int rows, int dim, int mode, const float *ranges,
                           uint8_t *out);
 
+// The fixed staging area of the no-allocation buffer_quantize: a device
+// array of STATIC_SCRATCH_BYTES on each GPU, alive until the process ends.
+// static_scratch gives its address on `device`, which must be the current
+// device (looked up once a device, then kept). Every caller on one GPU shares
+// it: calls that overlap on one GPU race.
+constexpr size_t STATIC_SCRATCH_BYTES = (size_t)16 << 20;
+constexpr int MAX_DEVICES = 64;
+hipError_t static_scratch(int device, void **ptr);
+
 // dst = src over `bytes` (a multiple of 16), 16-byte vectors, one pass.
 hipError_t copy_bytes(hipStream_t s, const void *src, void *dst, size_t bytes);
 

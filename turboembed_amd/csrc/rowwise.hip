@@ -3,6 +3,7 @@
 // All are HBM-bound; each reads its input once, coalesced, with wave64
 // shuffle reductions and no atomics on floats.
 #include <algorithm>
+#include <mutex>
 
 #include "kernels.h"
 #include "devmath.h"
@@ -761,6 +762,35 @@ hipError_t quantize_codes(hipStream_t s, const float *x, int rows, int dim, int 
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
+}
+
+// ---- A fixed staging area for callers that cannot allocate ------------------------------
+//
+// buffer_quantize stages its codes in device memory it allocates per call;
+// its no-allocation variant stages them (and the int8 ranges) here instead:
+// one file-scope array a GPU, held until the process ends. On the host the
+// array's name stands for a host-side stand-in, not a device address, so its
+// address on each device is looked up once, with that device current, and
+// kept; host code passes that address to kernels and copies, never the name.
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
+hipError_t static_scratch(int device, void **ptr) {
+    static std::mutex lock;
+    static void *addr[MAX_DEVICES] = {};
+    if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> g(lock);
+    if (!addr[device]) {
+        int current = -1;
+        hipError_t e = hipGetDevice(&current);
+        if (e != hipSuccess) return e;
+        if (current != device) return hipErrorInvalidDevice;
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[device] = p;
+    }
+    *ptr = addr[device];
+    return hipSuccess;
 }
 
 // ---- Plain copy (the traffic counters' reference) ---------------------------------------

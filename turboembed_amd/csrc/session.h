@@ -80,6 +80,7 @@ struct Context {
     turbo_log_fn log = nullptr;
     void *log_user_data = nullptr;
     std::mutex lock;                 // a launch through its sync, and reads
+    void *scratch = nullptr;         // the device's fixed staging area (static_scratch)
     void say(uint32_t level, const std::string &m) const;
 };
 
