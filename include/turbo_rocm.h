@@ -113,6 +113,15 @@ int32_t turbo_rocm_buffer_quantize_static(void *buffer, uint32_t quantization, c
 /* ---- Test and measurement hooks (no counterpart in the reference's seam; the
  * reference's CUDA backend keeps similar ones, core/src/cuda.rs:177-499) ---- */
 
+/* Makes the GEMM block shape `name` (as a choices string spells it, e.g.
+ * "256x256"; NULL or "" for none) fail to launch from now on, in place of a
+ * device that cannot take it: the launcher's rule picks another shape, the
+ * tuner skips it, a cached choice naming it is not taken, and a session that
+ * forces it is refused with TURBO_E_UNSUPPORTED (the reference's
+ * turbo_cuda_fail_variant, core/src/cuda.rs:461-469,
+ * core/cuda/backend.cpp:2430-2440, 3006-3010). Process-wide. */
+int32_t turbo_rocm_fail_variant(const char *name, turbo_error *err);
+
 /* The last run's packing, read back from the device: each row's first packed
  * token and length ([batch] each), each packed token's r * seq + p ([tokens]),
  * and the packed token count. */

@@ -887,6 +887,59 @@ def test_autotune_measures_caches_and_reuses(context, tmp_path):
     model.close()
 
 
+def test_a_block_shape_that_cannot_launch_is_skipped_and_refused(context, tmp_path, monkeypatch):
+    # The fail-variant hook stands in for a device that cannot take a block
+    # shape (reference core/src/cuda.rs:461-469, core/cuda/backend.cpp:
+    # 2430-2440, 3006-3010): a session forcing it is refused, the tuner
+    # never times it, a cached choice naming it is not taken, and the rule
+    # runs another shape whose vectors meet the oracle.
+    from turboembed_amd import tuning as TU
+    desc = small.bert(seed=33, hidden=128, heads=2, inter=256, positions=320, std=0.1)
+    ids, mask, types = small.ragged_rows(33, 16, 300, desc.vocab_size)
+    want = oracle.encode(desc, ids, mask, types)
+    model = context.load(desc)
+    cache = TU.TuneCache(str(tmp_path))
+    with pytest.raises(T.TurboError):
+        T.fail_variant("no-such-shape")
+    T.fail_variant("256x256")
+    try:
+        monkeypatch.setenv("TURBO_ROCM_CHOICES", "le16k:qkv=256x256")
+        with pytest.raises(T.TurboError) as e:
+            model.session(16, 320, S.TURBO_PRECISION_FASTEST)
+        assert e.value.code == S.TURBO_E_UNSUPPORTED and "le16k:qkv=256x256" in e.value.message, e.value
+        monkeypatch.delenv("TURBO_ROCM_CHOICES")
+        s = model.session(16, 320, S.TURBO_PRECISION_FASTEST, autotune=S.TURBO_AUTOTUNE_ON, cache=cache,
+                          budget_ms=3000)
+        assert s.tuned == S.TURBO_TUNED_MEASURED
+        assert s.timings and not any(k.endswith("/256x256") for k in s.timings), s.timings
+        assert "=256x256" not in s.choices()
+        assert_close(s.embed(ids, mask, types), want, s.compute_dtype)
+        s.close()
+        # The rule's own shape for these products is 256x256; it runs another.
+        s = model.session(16, 320, S.TURBO_PRECISION_FASTEST)
+        assert_close(s.embed(ids, mask, types), want, s.compute_dtype)
+        s.close()
+        # A cached choice that names it is measured again, not taken.
+        key_cache = TU.TuneCache(str(tmp_path / "named"))
+        s = model.session(16, 320, S.TURBO_PRECISION_FASTEST, autotune=S.TURBO_AUTOTUNE_ON, cache=key_cache,
+                          budget_ms=100)
+        key = s.key
+        s.close()
+        key_cache.put(key, "all:qkv=256x256,out=auto,ffn1=auto,ffn2=auto,attn=mfma;forced=none", {"x": 1.0})
+        s = model.session(16, 320, S.TURBO_PRECISION_FASTEST, autotune=S.TURBO_AUTOTUNE_ON, cache=key_cache,
+                          budget_ms=100)
+        assert s.tuned != S.TURBO_TUNED_CACHE and "=256x256" not in s.choices()
+        s.close()
+    finally:
+        T.fail_variant(None)
+    # Launchable again once the hook is cleared.
+    monkeypatch.setenv("TURBO_ROCM_CHOICES", "le16k:qkv=256x256")
+    s = model.session(16, 320, S.TURBO_PRECISION_FASTEST)
+    assert_close(s.embed(ids, mask, types), want, s.compute_dtype)
+    s.close()
+    model.close()
+
+
 @pytest.mark.parametrize("tile", ["256x256", "256x192", "128x128", "256x128k32", "r128x128", "r64x64"])
 def test_forced_tiles_meet_the_oracle(context, tile, monkeypatch):
     desc = small.bert(seed=32, hidden=192, heads=3, inter=384, positions=320, std=0.1)

@@ -63,6 +63,7 @@ def library():
                                     C.POINTER(u32), E],
         "turbo_rocm_rerank_scores": [P, u32, u32, P, P, P, C.c_float, P, E],
         "turbo_rocm_rerank_run": [P, P, P, P, u32, u32, P, u32, P, P, P, C.c_float, P, E],
+        "turbo_rocm_fail_variant": [C.c_char_p, E],
         "turbo_rocm_buffer_quantize_static": [P, u32, C.POINTER(C.c_float), u32, u32, C.POINTER(S.turbo_backend_run),
                                               E],
     }
@@ -555,3 +556,10 @@ def copy_probe(nbytes, iters=5, ordinal=0):
     err = S.new_error()
     _ok(library().turbo_rocm_copy_probe(ordinal, nbytes, iters, C.byref(ms), C.byref(err)), err)
     return ms.value
+
+
+def fail_variant(name=None):
+    """Makes the GEMM block shape `name` fail to launch from now on, as on
+    a device that cannot take it (None for none); a test hook."""
+    err = S.new_error()
+    _ok(library().turbo_rocm_fail_variant(name.encode() if name else None, C.byref(err)), err)

@@ -21,6 +21,7 @@
 // tiles, along N first: the run shares its A rows, which then stay in that
 // XCD's L2.
 #include <atomic>
+#include <mutex>
 #include <cstring>
 #include <type_traits>
 
@@ -867,6 +868,25 @@ static hipError_t launch_lds(hipStream_t s, int M, int N, int K, const void *A, 
 
 int gemm_tiles() { return 14; }
 
+// The block shape made to fail to launch, as on a device that cannot take
+// it (a test hook; -1 for none): an explicit launch of it fails, the rule
+// picks another, the tuner skips it and a session forcing it is refused.
+static std::mutex fail_lock;
+static int fail_tile = -1;
+
+bool gemm_fail_variant(const char *name) {
+    const int t = name && *name ? gemm_tile_by_name(name, std::strlen(name)) : -1;
+    if (name && *name && t <= 0) return false;
+    std::lock_guard<std::mutex> g(fail_lock);
+    fail_tile = t;
+    return true;
+}
+
+bool gemm_made_to_fail(int tile) {
+    std::lock_guard<std::mutex> g(fail_lock);
+    return tile > 0 && tile == fail_tile;
+}
+
 // Names of the block shapes, as a choices string spells them: output tile,
 // then what sets it apart (r: operands staged through registers; k32: 32
 // columns of k a stage; s<n>: n stages).
@@ -958,7 +978,14 @@ template <typename T, int BK>
 static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
                          int tile) {
     const bool pipelined = sizeof(T) == 2 && K % 64 == 0 && lda % 8 == 0;
-    if (tile == 0) tile = pipelined ? (M >= 2048 ? wide_tile(M, N, K, e) : 5) : 1;
+    if (tile == 0) {
+        tile = pipelined ? (M >= 2048 ? wide_tile(M, N, K, e) : 5) : 1;
+        // The rule's next choices when its own cannot launch here.
+        static const int PIPELINED[] = {7, 4, 5, 6, 8}, STAGED[] = {1, 2, 3, 14, 0};
+        const int *next = pipelined ? PIPELINED : STAGED;
+        for (int i = 0; gemm_made_to_fail(tile) && i < 5 && next[i]; ++i) tile = next[i];
+    }
+    if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
     // A pipelined shape asked of an operand it cannot take runs the staged kernel.
     if (tile >= 4 && tile <= 13 && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
     // 96-column wave tiles need Q, K and V to start on their boundaries.
@@ -994,8 +1021,12 @@ static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int 
 static hipError_t gemm_i8(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
                           int tile) {
     if (K % 64 != 0 || lda % 16 != 0 || !e.a_scale || !e.w_scale) return hipErrorInvalidValue;
-    if (tile == 0) tile = K % 128 == 0 ? 7 : 9;
+    if (tile == 0) {
+        tile = K % 128 == 0 ? 7 : 9;
+        if (gemm_made_to_fail(tile)) tile = tile == 7 ? 9 : 7;
+    }
     if (tile == 7 && K % 128 != 0) tile = 9;
+    if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
     switch (tile) {
     case 7: return launch_lds<int8_t, 256, 256, 2, 4, 2, 128, 1>(s, M, N, K, A, lda, W, e);
     default: return launch_lds<int8_t, 256, 128, 2, 2, 2, 64, 2>(s, M, N, K, A, lda, W, e);

@@ -113,6 +113,12 @@ int gemm_tile_by_name(const char *s, size_t n);
 // shape (K, lda and the epilogue decide which kernels take them) into out:
 // how many.
 int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap);
+// A test hook standing in for a device that cannot launch one block shape:
+// the shape a name spells (NULL or "" for none) fails to launch from now on.
+// False for a name that spells no shape. gemm_made_to_fail says whether a
+// shape is the one.
+bool gemm_fail_variant(const char *name);
+bool gemm_made_to_fail(int tile);
 
 // Softmax attention within each row and head over Q and K ([heads][tcap][d]
 // each) and V transposed ([heads][d][tcap]), in `dt`, one after another in

@@ -574,7 +574,17 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     if (tuned_mode && tuning->cached && *tuning->cached) {
         std::string why;
         Choices c = kc;
-        if (parse_choices(tuning->cached, &c, false, &why)) {
+        // A cached choice of a block shape that cannot launch here is not taken.
+        bool launchable = true;
+        if (parse_choices(tuning->cached, &c, false, &why))
+            for (int b = 0; b < c.bins; ++b)
+                for (int g = 0; g < G_COUNT; ++g)
+                    if (gemm_made_to_fail(c.bin[b].tile[g])) {
+                        launchable = false;
+                        why = std::string(BIN_NAME[b]) + ":" + GEMM_NAME[g] + "=" + gemm_tile_name(c.bin[b].tile[g]) +
+                              " cannot launch on this device";
+                    }
+        if (launchable && why.empty()) {
             kc = c;
             cached = true;
             m->ctx->say(LOG_DEBUG, "rocm: kernels from the cache: " + std::string(tuning->cached));
@@ -587,6 +597,14 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         if (!parse_choices(env, &kc, true, &why))
             fail(TURBO_E_INVALID_ARGUMENT, "rocm: TURBO_ROCM_CHOICES " + std::string(env) + ": " + why);
     }
+    // A forced block shape that cannot launch on this device refuses the
+    // session (reference core/cuda/backend.cpp:3006-3010).
+    for (int b = 0; b < kc.bins; ++b)
+        for (int g = 0; g < G_COUNT; ++g)
+            if (kc.bin[b].tile_forced[g] && gemm_made_to_fail(kc.bin[b].tile[g]))
+                fail(TURBO_E_UNSUPPORTED, std::string("rocm: ") + BIN_NAME[b] + ":" + GEMM_NAME[g] + "=" +
+                                              gemm_tile_name(kc.bin[b].tile[g]) +
+                                              ": the GEMM kernel cannot launch on this device");
     // The scalar path is the only one some sessions have.
     for (int b = 0; b < kc.bins; ++b)
         if (!mfma_attn) kc.bin[b].simple_attention = true;
@@ -1226,6 +1244,8 @@ bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
             int best = -1;
             for (int i = 0; i < n; ++i) {
                 if (i > 0 && cand[i] == cand[0]) continue;
+                // A block shape that cannot launch here is not timed.
+                if (gemm_made_to_fail(cand[i])) continue;
                 if (Clock::now() >= deadline) break;
                 auto launch = [&]() { return gemm(st, s.dt, M, lg.N, lg.K, A, lg.K, lg.W, lg.e, cand[i]); };
                 check(launch(), "the tuner's GEMM");
@@ -1317,6 +1337,14 @@ void session_run(Session *s, turbo_backend_run *out) {
 using namespace rocm;
 
 extern "C" {
+
+int32_t turbo_rocm_fail_variant(const char *name, turbo_error *err) {
+    return guarded(err, [&] {
+        if (!gemm_fail_variant(name))
+            fail(TURBO_E_INVALID_ARGUMENT, std::string("rocm: '") + name + "' names no GEMM block shape");
+        return TURBO_OK;
+    });
+}
 
 int32_t turbo_rocm_session_packing(void *session, int32_t *start, int32_t *len, int32_t *at, uint32_t *tokens,
                                    turbo_error *err) {
