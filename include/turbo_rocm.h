@@ -143,6 +143,10 @@ int32_t turbo_rocm_session_times(void *session, char *out, uint32_t len, turbo_e
  * this is the device's throughput on them, for measurement. */
 int32_t turbo_rocm_session_replay(void *session, uint32_t runs, turbo_error *err);
 
+/* How many graphs the session has captured (one per bin of packed tokens, at
+ * session_open) and how many runs replayed one since. */
+int32_t turbo_rocm_session_graphs(void *session, uint64_t *captured, uint64_t *launched, turbo_error *err);
+
 /* The session's kernel choices, as TURBO_ROCM_CHOICES takes them. */
 int32_t turbo_rocm_session_choices(void *session, char *out, uint32_t len, turbo_error *err);
 

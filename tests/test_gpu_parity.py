@@ -997,6 +997,57 @@ def test_graph_replays_are_the_eager_runs(context, family, precision, monkeypatc
     model.close()
 
 
+@pytest.mark.parametrize("family", ["bert", "modernbert"])
+def test_fresh_ragged_batches_replay_their_bin_s_graph(context, family, monkeypatch):
+    # Every bin's graph is captured at session_open (reference
+    # core/cuda/backend.cpp:2366-2417); a run of new rows of any shape in a
+    # bin replays that bin's graph with no capture, its kernels reading the
+    # run's extent from the device, bit for bit the directly launched
+    # kernels, with no host or device allocation. 16 rows of up to 320
+    # tokens reach four bins, the largest split into four parts.
+    desc = small.bert(seed=43, hidden=128, heads=2, inter=256, positions=320, std=0.1) if family == "bert" else \
+        small.modernbert(seed=43, hidden=128, heads=2, inter=192, positions=320, window=32, std=0.1)
+    model = context.load(desc)
+    batches = []
+    g = np.random.Generator(np.random.PCG64(43))
+    # (rows, columns, every column live): 5120, 4800 and 4100 live tokens
+    # take the split bin (four parts, then four of one and three rows).
+    shapes = [(16, 320, True), (3, 40, False), (9, 300, False), (16, 300, True), (2, 256, False), (12, 320, False),
+              (1, 5, False), (13, 316, True), (4, 320, True)]
+    for k, (rows, seq, full) in enumerate(shapes):
+        ids, mask, types = small.ragged_rows(100 + k, rows, seq, desc.vocab_size)
+        if full:
+            mask[:] = 1
+        batches.append((ids, mask, None if family == "modernbert" else types))
+    monkeypatch.setenv("TURBO_ROCM_GRAPHS", "0")
+    eager = model.session(16, 320, S.TURBO_PRECISION_FASTEST)
+    want = [eager.embed(*b) for b in batches]
+    assert eager.graphs() == (0, 0)
+    eager.close()
+    monkeypatch.delenv("TURBO_ROCM_GRAPHS")
+    s = model.session(16, 320, S.TURBO_PRECISION_FASTEST)
+    captured, launched = s.graphs()
+    assert captured == 4 and launched == 0, (captured, launched)
+    for i, b in enumerate(batches):
+        got = s.embed(*b)
+        assert np.array_equal(got, want[i]), i
+        assert s.run_info.host_allocs == 0 and s.run_info.device_allocs == 0
+        assert_close(got, oracle.encode(desc, *b), s.compute_dtype)
+    assert s.graphs() == (4, len(batches))
+    # Range writes, and a span-free MEAN/CLS switch, take the same graphs.
+    ids, mask, types = batches[3]
+    rr = [(r, 0, int(mask[r].nonzero()[0].max()) + 1) for r in range(ids.shape[0])]
+    s.write_ranges(ids, mask, rr, types)
+    s.run()
+    assert np.array_equal(s.read(), want[3])
+    cls = s.embed(ids, mask, types, pooling=S.TURBO_POOLING_CLS, output_dim=100)
+    assert_close(cls, oracle.encode(desc, ids, mask, types, pooling=S.TURBO_POOLING_CLS, output_dim=100),
+                 s.compute_dtype)
+    assert s.graphs() == (4, len(batches) + 2)
+    s.close()
+    model.close()
+
+
 # ---- Vector codes on the device (buffer_quantize) --------------------------------------------
 #
 # Byte-exact against the reference's golden codes (testdata/quantize, copied

@@ -55,6 +55,7 @@ def library():
         "turbo_rocm_session_times": [P, C.c_char_p, u32, E],
         "turbo_rocm_session_choices": [P, C.c_char_p, u32, E],
         "turbo_rocm_session_replay": [P, u32, E],
+        "turbo_rocm_session_graphs": [P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), E],
         "turbo_rocm_gemm_check": [u32, u32, u32, u32, u32, P, P, P, P, u32, E],
         "turbo_rocm_gemm_time": [u32, u32, u32, u32, u32, u32, u32, C.POINTER(C.c_float), E],
         "turbo_rocm_copy_probe": [u32, C.c_uint64, u32, C.POINTER(C.c_float), E],
@@ -446,6 +447,13 @@ class Session:
         return span_logits(self, windows, fill_id)
 
     # -- hooks ---------------------------------------------------------------------
+    def graphs(self):
+        """(graphs captured, runs that replayed one) of this session."""
+        c, l = C.c_uint64(), C.c_uint64()
+        err = S.new_error()
+        _ok(self.lib.turbo_rocm_session_graphs(self.h, C.byref(c), C.byref(l), C.byref(err)), err)
+        return c.value, l.value
+
     def packing(self):
         b = self._keep[0].shape[0]
         start = np.zeros(b, np.int32)

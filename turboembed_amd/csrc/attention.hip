@@ -23,8 +23,10 @@ constexpr int SW = 4;
 template <typename T, int D>
 __global__ void __launch_bounds__(64 * SW) attention_simple_kernel(const T *__restrict__ qkv, int tcap, int heads,
                                                                    Packing p, const int32_t *__restrict__ mask,
-                                                                   int seq, int window, T *__restrict__ ctx) {
-    const int r = blockIdx.z, head = blockIdx.y, q0 = blockIdx.x * 64;
+                                                                   Span sp, int window, T *__restrict__ ctx) {
+    const Live lv = live_of(sp);
+    if ((int)blockIdx.z >= lv.rows) return;
+    const int r = lv.row0 + blockIdx.z, head = blockIdx.y, q0 = blockIdx.x * 64, seq = lv.seq;
     const int len = p.len[r];
     if (q0 >= len) return;
     const int start = p.start[r];
@@ -120,12 +122,12 @@ __global__ void __launch_bounds__(64 * SW) attention_simple_kernel(const T *__re
 
 template <typename T>
 static hipError_t attention_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
-                              const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx) {
-    const dim3 grid((max_len + 63) / 64, heads, batch);
+                              const int32_t *mask, const Span &sp, int max_rows, int max_len, int window, void *ctx) {
+    const dim3 grid((max_len + 63) / 64, heads, max_rows);
 #define ATT_CASE(D)                                                                                             \
     case D:                                                                                                     \
         hipLaunchKernelGGL((attention_simple_kernel<T, D>), grid, dim3(64 * SW), 0, s, (const T *)qkv, tcap,     \
-                           heads, p, mask, seq, window, (T *)ctx);                                              \
+                           heads, p, mask, sp, window, (T *)ctx);                                               \
         break;
     switch (d) {
         ATT_CASE(8)
@@ -217,8 +219,8 @@ template <int N> __device__ __forceinline__ void att_wait_vmcnt() {
 // finite). Each block's live keys are a 64-bit mask, the same for the whole
 // workgroup.
 template <typename T, int D>
-__global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads, int batch,
-                                                             int nqb, Packing p, const int32_t *__restrict__ mask, int seq,
+__global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads, Span sp,
+                                                             int nqb, Packing p, const int32_t *__restrict__ mask,
                                                              int window, T *__restrict__ ctx) {
     constexpr int WQ = 64, QB = 4 * WQ, KB = 64, STAGES = 3;
     constexpr int KBYTES = KB * D * 2, VBYTES = D * KB * 2, SBYTES = KBYTES + VBYTES;
@@ -238,8 +240,9 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
     // XCD's L2. Pairs go 8 to a group of 8 nqb blocks.
     const int L = blockIdx.x;
     const int pair = (L / (8 * nqb)) * 8 + L % 8, qb = (L / 8) % nqb;
-    if (pair >= heads * batch) return;
-    const int r = pair / heads, head = pair % heads, q0 = qb * QB;
+    const Live lv = live_of(sp);
+    if (pair >= heads * lv.rows) return;
+    const int r = lv.row0 + pair / heads, head = pair % heads, q0 = qb * QB, seq = lv.seq;
     const int len = p.len[r];
     if (q0 >= len) return;
     const int start = p.start[r];
@@ -482,9 +485,10 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
 
 template <typename T>
 static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
-                                   const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx) {
+                                   const int32_t *mask, const Span &sp, int max_rows, int max_len, int window,
+                                   void *ctx) {
     // A 1-D grid of groups of 8 (row, head) pairs times nqb query blocks.
-    const int nqb = (max_len + 255) / 256, pairs = heads * batch;
+    const int nqb = (max_len + 255) / 256, pairs = heads * max_rows;
     const int blocks = ((pairs + 7) / 8) * 8 * nqb;
     if (d != 64) return hipErrorInvalidValue;
     // Three stages of K (64 x 64) and V^T (64 x 64) blocks, then a live mask
@@ -493,22 +497,23 @@ static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int
     const int bytes = 3 * 2 * 64 * 64 * 2 + ((max_len + 127) / 64) * 8;
     if (bytes > 160 * 1024) return hipErrorInvalidValue;
     hipLaunchKernelGGL((attention_mfma_kernel<T, 64>), dim3(blocks), dim3(256), bytes, s, (const T *)qkv, tcap, heads,
-                       batch, nqb, p, mask, seq, window, (T *)ctx);
+                       sp, nqb, p, mask, window, (T *)ctx);
     return hipGetLastError();
 }
 
 hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
-                     const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx, bool simple) {
-    if (max_len <= 0) return hipSuccess;
+                     const int32_t *mask, const Span &sp, int max_rows, int max_len, int window, void *ctx,
+                     bool simple) {
+    if (max_len <= 0 || max_rows <= 0) return hipSuccess;
     const bool mfma = d == 64 && !simple;
     switch (dt) {
     case Dt::F16:
-        return mfma ? attention_mfma_t<_Float16>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, window, ctx)
-                    : attention_t<_Float16>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, window, ctx);
+        return mfma ? attention_mfma_t<_Float16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx)
+                    : attention_t<_Float16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx);
     case Dt::BF16:
-        return mfma ? attention_mfma_t<__bf16>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, window, ctx)
-                    : attention_t<__bf16>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, window, ctx);
-    default: return attention_t<float>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, window, ctx);
+        return mfma ? attention_mfma_t<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx)
+                    : attention_t<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx);
+    default: return attention_t<float>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx);
     }
 }
 
@@ -526,13 +531,15 @@ hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads,
 // every position through the row's last live one: the mean of their values.
 template <typename T>
 __global__ void __launch_bounds__(256) deberta_attention_kernel(const T *__restrict__ qkv, int tcap, int heads, int d,
-                                                                Packing p, const int32_t *__restrict__ mask, int seq,
-                                                                int batch, const float *__restrict__ pos,
+                                                                Packing p, const int32_t *__restrict__ mask, Span sp,
+                                                                const float *__restrict__ pos,
                                                                 const int32_t *__restrict__ buckets, int positions,
                                                                 T *__restrict__ ctx, int lds_len) {
     extern __shared__ float scores[];
-    const int r = blockIdx.x / heads, head = blockIdx.x % heads;
-    if (r >= batch) return;
+    const Live lv = live_of(sp);
+    const int head = blockIdx.x % heads, seq = lv.seq;
+    if ((int)blockIdx.x / heads >= lv.rows) return;
+    const int r = lv.row0 + (int)blockIdx.x / heads;
     const int len = p.len[r], start = p.start[r];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float *sc = scores + wave * lds_len;
@@ -597,26 +604,27 @@ __global__ void __launch_bounds__(256) deberta_attention_kernel(const T *__restr
 
 template <typename T>
 static hipError_t deberta_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
-                            const int32_t *mask, int seq, int batch, int max_len, const float *pos,
+                            const int32_t *mask, const Span &sp, int max_rows, int max_len, const float *pos,
                             const int32_t *buckets, int positions, void *ctx) {
     const size_t lds = (size_t)4 * max_len * sizeof(float);
     if (lds > 160 * 1024 || max_len > positions) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((deberta_attention_kernel<T>), dim3(batch * heads), dim3(256), lds, s, (const T *)qkv, tcap,
-                       heads, d, p, mask, seq, batch, pos, buckets, positions, (T *)ctx, max_len);
+    hipLaunchKernelGGL((deberta_attention_kernel<T>), dim3(max_rows * heads), dim3(256), lds, s, (const T *)qkv, tcap,
+                       heads, d, p, mask, sp, pos, buckets, positions, (T *)ctx, max_len);
     return hipGetLastError();
 }
 
 hipError_t deberta_attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
-                             const int32_t *mask, int seq, int batch, int max_len, const float *pos,
+                             const int32_t *mask, const Span &sp, int max_rows, int max_len, const float *pos,
                              const int32_t *buckets, int positions, void *ctx) {
-    if (max_len <= 0 || batch <= 0) return hipSuccess;
+    if (max_len <= 0 || max_rows <= 0) return hipSuccess;
     switch (dt) {
     case Dt::F16:
-        return deberta_t<_Float16>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, pos, buckets, positions, ctx);
+        return deberta_t<_Float16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions,
+                                   ctx);
     case Dt::BF16:
-        return deberta_t<__bf16>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, pos, buckets, positions, ctx);
+        return deberta_t<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions, ctx);
     default:
-        return deberta_t<float>(s, qkv, tcap, heads, d, p, mask, seq, batch, max_len, pos, buckets, positions, ctx);
+        return deberta_t<float>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions, ctx);
     }
 }
 

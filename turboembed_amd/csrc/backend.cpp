@@ -52,6 +52,14 @@ void fill(turbo_error *err, int32_t code, uint32_t field, const std::string &m) 
 
 std::atomic<uint64_t> device_allocs{0};
 std::atomic<uint64_t> host_allocs{0};
+static thread_local uint64_t host_allocs_here = 0;
+
+void counted_host_alloc() {
+    host_allocs.fetch_add(1, std::memory_order_relaxed);
+    ++host_allocs_here;
+}
+
+uint64_t host_allocs_on_thread() { return host_allocs_here; }
 
 void *dev_alloc(size_t bytes, const char *what) {
     void *p = nullptr;
@@ -193,6 +201,7 @@ int32_t context_create(uint32_t ordinal, turbo_log_fn log, void *ud, void **out,
     return guarded(err, [&] {
         if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device " + std::to_string(ordinal));
         auto c = std::make_unique<Context>();
+        counted_host_alloc();
         c->ordinal = devices()[ordinal];
         c->log = log;
         c->log_user_data = ud;
@@ -265,6 +274,7 @@ int32_t buffer_alloc(void *ctx, const turbo_buffer_desc *desc, void **out, void 
         b->placement = desc->placement;
         b->bytes = desc_bytes(desc);
         b->owned = true;
+        counted_host_alloc();
         switch (desc->placement) {
         case TURBO_PLACE_DEVICE: b->dev = dev_alloc(b->bytes, "buffer_alloc"); break;
         case TURBO_PLACE_PINNED:
@@ -279,6 +289,7 @@ int32_t buffer_alloc(void *ctx, const turbo_buffer_desc *desc, void **out, void 
             b->dev = b->host;
             break;
         case TURBO_PLACE_HOST:
+            counted_host_alloc();
             b->host = std::malloc(b->bytes ? b->bytes : 1);
             if (!b->host) fail(TURBO_E_OUT_OF_MEMORY, "rocm: host buffer");
             break;
@@ -299,6 +310,7 @@ int32_t buffer_import(void *ctx, const turbo_buffer_desc *desc, const turbo_nati
         b->placement = desc->placement;
         b->bytes = desc_bytes(desc);
         b->owned = false;
+        counted_host_alloc();
         char *p = reinterpret_cast<char *>(handle->handle) + handle->offset;
         if (handle->kind == TURBO_HANDLE_CUDA_PTR && desc->placement == TURBO_PLACE_DEVICE) {
             b->dev = p;

@@ -10,7 +10,25 @@
 #include <hip/hip_bf16.h>
 #include <stdint.h>
 
+#include "kernels.h"
+
 namespace rocm {
+
+// A launch's extent on the device: the rows and packed tokens of its span,
+// from the run's dimensions (scalar loads, made uniform) or as given.
+struct Live {
+    int row0, rows, tok0, tokens, max_len, seq;
+};
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ Live live_of(const Span &s) {
+    if (!s.dims) return Live{s.row0, s.rows, s.tok0, s.tokens, s.max_len, s.seq};
+    const RunDims *d = s.dims;
+    if (s.part < 0)
+        return Live{0, uniform(d->batch), 0, uniform(d->tokens), uniform(d->max_len), uniform(d->seq)};
+    const PartDims *p = &d->part[s.part];
+    return Live{uniform(p->row0), uniform(p->rows), uniform(p->tok0), uniform(p->tokens), uniform(p->max_len),
+                uniform(d->seq)};
+}
 
 __device__ __forceinline__ float dev_exp(float x) {
     const float lo = -80.0f;

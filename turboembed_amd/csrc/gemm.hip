@@ -86,6 +86,30 @@ template <typename T> __device__ __forceinline__ float gated_product(float g, fl
     return v;
 }
 
+// The rows a GEMM launch multiplies: its span, and how far apart A's token
+// rows are for the span's first token (the run's operand rows may be wider
+// than the product's K).
+struct GemmRows {
+    Span sp;
+    int a_tok;
+};
+
+// The span's first token moves the epilogue's row-major output (and the int8
+// activation scales) down to it; the Q, K and V scatter takes it as the
+// token of row 0, and the rotary epilogue reads the rows' stride from the
+// run's dimensions.
+template <Epi KIND, typename OT>
+__device__ __forceinline__ void place_epilogue(EpiArgs &e, const Live &lv, bool dims) {
+    e.tok0 = lv.tok0;
+    if (dims) e.seq = lv.seq;
+    if (e.a_scale) e.a_scale += lv.tok0;
+    const size_t rows = (size_t)lv.tok0 * e.ldo;
+    if constexpr (KIND == Epi::Plain) e.out = (float *)e.out + rows;
+    else if constexpr (KIND == Epi::Bias) e.out = e.out_f32 ? (void *)((float *)e.out + rows) : (void *)((OT *)e.out + rows);
+    else if constexpr (KIND == Epi::Gelu || KIND == Epi::Gated) e.out = (OT *)e.out + rows;
+    else if constexpr (KIND == Epi::Residual) e.x += rows;
+}
+
 // The epilogue of one 32 x 32 MFMA tile, for this lane's column n and its 16
 // rows m0 + 8 (r / 4) + 4 (lane / 32) + r % 4, v = acc + bias. The kind is a
 // template argument, so each kernel carries one small epilogue, and what
@@ -154,7 +178,7 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
 }
 
 template <typename T, int BM, int BN, int BK, Epi KIND>
-__global__ void __launch_bounds__(256) gemm_kernel(int M, int N, int K, const T *__restrict__ A, int lda,
+__global__ void __launch_bounds__(256) gemm_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int lda,
                                                    const T *__restrict__ W, EpiArgs e, int grid_n) {
     constexpr int VEC = 16 / sizeof(T);          // elements in 16 bytes
     constexpr int STRIDE = BK + VEC;             // LDS row, padded by 16 bytes
@@ -169,8 +193,15 @@ __global__ void __launch_bounds__(256) gemm_kernel(int M, int N, int K, const T 
 
     __shared__ __attribute__((aligned(16))) T lds[2][(BM + BN) * STRIDE];
 
-    // XCD-aware renumbering of the block.
-    const int nb = gridDim.x, per = nb / 8;
+    const Live lv = live_of(sp);
+    const int M = lv.tokens;
+    // XCD-aware renumbering of the block over the span's own tiles (the grid
+    // may be sized for more rows: the blocks past them leave).
+    const int live = (M + BM - 1) / BM * grid_n;
+    if ((int)blockIdx.x >= live) return;
+    A += (size_t)lv.tok0 * a_tok;
+    place_epilogue<KIND, T>(e, lv, sp.dims != nullptr);
+    const int per = live / 8;
     int b = blockIdx.x;
     if (b < per * 8) b = (b % 8) * per + b / 8;
     const int tile_n = b % grid_n, tile_m = b / grid_n;
@@ -249,24 +280,25 @@ __global__ void __launch_bounds__(256) gemm_kernel(int M, int N, int K, const T 
 }
 
 template <typename T, int BM, int BN, int BK, Epi KIND>
-static hipError_t launch_k(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W,
-                           const EpiArgs &e) {
+static hipError_t launch_k(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda,
+                           const void *W, const EpiArgs &e) {
     const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM;
-    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, BK, KIND>), dim3(gn * gm), dim3(256), 0, s, M, N, K, (const T *)A,
-                       lda, (const T *)W, e, gn);
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, BK, KIND>), dim3(gn * gm), dim3(256), 0, s, gr.sp, gr.a_tok, N, K,
+                       (const T *)A, lda, (const T *)W, e, gn);
     return hipGetLastError();
 }
 
 template <typename T, int BM, int BN, int BK>
-static hipError_t launch(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e) {
+static hipError_t launch(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda, const void *W,
+                         const EpiArgs &e) {
     switch (e.kind) {
-    case Epi::Plain: return launch_k<T, BM, BN, BK, Epi::Plain>(s, M, N, K, A, lda, W, e);
-    case Epi::Qkv: return launch_k<T, BM, BN, BK, Epi::Qkv>(s, M, N, K, A, lda, W, e);
-    case Epi::Gelu: return launch_k<T, BM, BN, BK, Epi::Gelu>(s, M, N, K, A, lda, W, e);
-    case Epi::Residual: return launch_k<T, BM, BN, BK, Epi::Residual>(s, M, N, K, A, lda, W, e);
-    case Epi::QkvRope: return launch_k<T, BM, BN, BK, Epi::QkvRope>(s, M, N, K, A, lda, W, e);
-    case Epi::Gated: return launch_k<T, BM, BN, BK, Epi::Gated>(s, M, N, K, A, lda, W, e);
-    case Epi::Bias: return launch_k<T, BM, BN, BK, Epi::Bias>(s, M, N, K, A, lda, W, e);
+    case Epi::Plain: return launch_k<T, BM, BN, BK, Epi::Plain>(s, gr, M, N, K, A, lda, W, e);
+    case Epi::Qkv: return launch_k<T, BM, BN, BK, Epi::Qkv>(s, gr, M, N, K, A, lda, W, e);
+    case Epi::Gelu: return launch_k<T, BM, BN, BK, Epi::Gelu>(s, gr, M, N, K, A, lda, W, e);
+    case Epi::Residual: return launch_k<T, BM, BN, BK, Epi::Residual>(s, gr, M, N, K, A, lda, W, e);
+    case Epi::QkvRope: return launch_k<T, BM, BN, BK, Epi::QkvRope>(s, gr, M, N, K, A, lda, W, e);
+    case Epi::Gated: return launch_k<T, BM, BN, BK, Epi::Gated>(s, gr, M, N, K, A, lda, W, e);
+    case Epi::Bias: return launch_k<T, BM, BN, BK, Epi::Bias>(s, gr, M, N, K, A, lda, W, e);
     }
     return hipErrorInvalidValue;
 }
@@ -678,7 +710,7 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
 
 template <typename T, typename OT, int BM, int BN, int WM, int WN, int STAGES, int BK, int OCC, Epi KIND>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
-gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *__restrict__ W, EpiArgs e,
+gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int lda, const T *__restrict__ W, EpiArgs e,
                 int grid_n) {
     constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
     constexpr int EPC = 16 / (int)sizeof(T);                 // elements in a 16-byte chunk
@@ -696,7 +728,14 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
     typedef typename Mma<T>::acc acc_t;
     extern __shared__ __attribute__((aligned(1024))) char smem[];
 
-    const int nb = gridDim.x, per = nb / 8;
+    const Live lv = live_of(sp);
+    const int M = lv.tokens;
+    // XCD-aware renumbering over the span's own tiles; blocks past them leave.
+    const int live = (M + BM - 1) / BM * grid_n;
+    if ((int)blockIdx.x >= live) return;
+    A += (size_t)lv.tok0 * a_tok;
+    place_epilogue<KIND, OT>(e, lv, sp.dims != nullptr);
+    const int per = live / 8;
     int b = blockIdx.x;
     if (b < per * 8) b = (b % 8) * per + b / 8;
     const int tile_n = b % grid_n, tile_m = b / grid_n;
@@ -836,23 +875,23 @@ gemm_lds_kernel(int M, int N, int K, const T *__restrict__ A, int lda, const T *
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK, int OCC, Epi KIND>
-static hipError_t launch_lds_k(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W,
-                               const EpiArgs &e) {
+static hipError_t launch_lds_k(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda,
+                               const void *W, const EpiArgs &e) {
     // int8 operands write F16 activations.
     typedef typename std::conditional<sizeof(T) == 1, _Float16, T>::type OT;
     constexpr int bytes = STAGES * (BM + BN) * BK * (int)sizeof(T);
     // Dynamic LDS up to the device's 160 KB per workgroup needs no attribute on gfx950.
     const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM;
     hipLaunchKernelGGL((gemm_lds_kernel<T, OT, BM, BN, WM, WN, STAGES, BK, OCC, KIND>), dim3(gn * gm),
-                       dim3(64 * WM * WN), bytes, s, M, N, K, (const T *)A, lda, (const T *)W, e, gn);
+                       dim3(64 * WM * WN), bytes, s, gr.sp, gr.a_tok, N, K, (const T *)A, lda, (const T *)W, e, gn);
     return hipGetLastError();
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK = 64, int OCC = 1>
-static hipError_t launch_lds(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W,
-                             const EpiArgs &e) {
+static hipError_t launch_lds(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda,
+                             const void *W, const EpiArgs &e) {
 #define LDS_CASE(E) \
-    case Epi::E: return launch_lds_k<T, BM, BN, WM, WN, STAGES, BK, OCC, Epi::E>(s, M, N, K, A, lda, W, e);
+    case Epi::E: return launch_lds_k<T, BM, BN, WM, WN, STAGES, BK, OCC, Epi::E>(s, gr, M, N, K, A, lda, W, e);
     switch (e.kind) {
         LDS_CASE(Plain)
         LDS_CASE(Qkv)
@@ -975,7 +1014,8 @@ static int wide_tile(int M, int N, int K, const EpiArgs &e) {
 // a multiple of 8, and the F32 tier); 4-13 are the pipelined kernel, for
 // 16-bit operands with K a multiple of 64 (every encoder shape here).
 template <typename T, int BK>
-static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
+static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda, const void *W,
+                         const EpiArgs &e,
                          int tile) {
     const bool pipelined = sizeof(T) == 2 && K % 64 == 0 && lda % 8 == 0;
     if (tile == 0) {
@@ -991,26 +1031,26 @@ static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int 
     // 96-column wave tiles need Q, K and V to start on their boundaries.
     if (tile == 13 && (e.kind == Epi::Qkv || e.kind == Epi::QkvRope) && e.hidden % 96 != 0) tile = 7;
     switch (tile) {
-    case 1: return launch<T, 128, 128, BK>(s, M, N, K, A, lda, W, e);
-    case 2: return launch<T, 256, 128, BK>(s, M, N, K, A, lda, W, e);
-    case 3: return launch<T, 64, 128, BK>(s, M, N, K, A, lda, W, e);
+    case 1: return launch<T, 128, 128, BK>(s, gr, M, N, K, A, lda, W, e);
+    case 2: return launch<T, 256, 128, BK>(s, gr, M, N, K, A, lda, W, e);
+    case 3: return launch<T, 64, 128, BK>(s, gr, M, N, K, A, lda, W, e);
     // 64 x 64: four times the workgroups of 128 x 128, for products too small to fill the chip.
-    case 14: return launch<T, 64, 64, BK>(s, M, N, K, A, lda, W, e);
+    case 14: return launch<T, 64, 64, BK>(s, gr, M, N, K, A, lda, W, e);
     }
     if constexpr (sizeof(T) == 2) {
         switch (tile) {
-        case 4: return launch_lds<T, 256, 128, 2, 2, 3>(s, M, N, K, A, lda, W, e);
-        case 5: return launch_lds<T, 128, 128, 2, 2, 4>(s, M, N, K, A, lda, W, e);
-        case 6: return launch_lds<T, 128, 256, 2, 2, 3>(s, M, N, K, A, lda, W, e);
-        case 7: return launch_lds<T, 256, 256, 2, 4, 2>(s, M, N, K, A, lda, W, e);
-        case 8: return launch_lds<T, 128, 128, 2, 2, 2>(s, M, N, K, A, lda, W, e);
+        case 4: return launch_lds<T, 256, 128, 2, 2, 3>(s, gr, M, N, K, A, lda, W, e);
+        case 5: return launch_lds<T, 128, 128, 2, 2, 4>(s, gr, M, N, K, A, lda, W, e);
+        case 6: return launch_lds<T, 128, 256, 2, 2, 3>(s, gr, M, N, K, A, lda, W, e);
+        case 7: return launch_lds<T, 256, 256, 2, 4, 2>(s, gr, M, N, K, A, lda, W, e);
+        case 8: return launch_lds<T, 128, 128, 2, 2, 2>(s, gr, M, N, K, A, lda, W, e);
         // BK 32 with two workgroups a CU, so one's epilogue overlaps the other's products.
-        case 9: return launch_lds<T, 256, 128, 2, 2, 2, 32, 2>(s, M, N, K, A, lda, W, e);
-        case 10: return launch_lds<T, 128, 256, 2, 2, 2, 32, 2>(s, M, N, K, A, lda, W, e);
-        case 11: return launch_lds<T, 256, 128, 2, 2, 3, 32, 2>(s, M, N, K, A, lda, W, e);
-        case 12: return launch_lds<T, 256, 256, 2, 4, 3, 32, 1>(s, M, N, K, A, lda, W, e);
+        case 9: return launch_lds<T, 256, 128, 2, 2, 2, 32, 2>(s, gr, M, N, K, A, lda, W, e);
+        case 10: return launch_lds<T, 128, 256, 2, 2, 2, 32, 2>(s, gr, M, N, K, A, lda, W, e);
+        case 11: return launch_lds<T, 256, 128, 2, 2, 3, 32, 2>(s, gr, M, N, K, A, lda, W, e);
+        case 12: return launch_lds<T, 256, 256, 2, 4, 3, 32, 1>(s, gr, M, N, K, A, lda, W, e);
         // 8 waves as 4 x 2 of 64 x 96: N = 768, 2304 and 3072 in whole rounds of tiles.
-        case 13: return launch_lds<T, 256, 192, 4, 2, 2>(s, M, N, K, A, lda, W, e);
+        case 13: return launch_lds<T, 256, 192, 4, 2, 2>(s, gr, M, N, K, A, lda, W, e);
         }
     }
     return hipErrorInvalidValue;
@@ -1018,7 +1058,8 @@ static hipError_t gemm_t(hipStream_t s, int M, int N, int K, const void *A, int 
 
 // The int8 tier: the pipelined kernel alone, on 128-byte rows (K a multiple
 // of 128) or 64-byte rows (K a multiple of 64).
-static hipError_t gemm_i8(hipStream_t s, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
+static hipError_t gemm_i8(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda, const void *W,
+                          const EpiArgs &e,
                           int tile) {
     if (K % 64 != 0 || lda % 16 != 0 || !e.a_scale || !e.w_scale) return hipErrorInvalidValue;
     if (tile == 0) {
@@ -1028,21 +1069,22 @@ static hipError_t gemm_i8(hipStream_t s, int M, int N, int K, const void *A, int
     if (tile == 7 && K % 128 != 0) tile = 9;
     if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
     switch (tile) {
-    case 7: return launch_lds<int8_t, 256, 256, 2, 4, 2, 128, 1>(s, M, N, K, A, lda, W, e);
-    default: return launch_lds<int8_t, 256, 128, 2, 2, 2, 64, 2>(s, M, N, K, A, lda, W, e);
+    case 7: return launch_lds<int8_t, 256, 256, 2, 4, 2, 128, 1>(s, gr, M, N, K, A, lda, W, e);
+    default: return launch_lds<int8_t, 256, 128, 2, 2, 2, 64, 2>(s, gr, M, N, K, A, lda, W, e);
     }
 }
 
-hipError_t gemm(hipStream_t s, Dt dt, int M, int N, int K, const void *A, int lda, const void *W, const EpiArgs &e,
-                int tile) {
+hipError_t gemm(hipStream_t s, Dt dt, const Span &sp, int M, int N, int K, const void *A, int lda, int a_tok,
+                const void *W, const EpiArgs &e, int tile) {
     if (M <= 0) return hipSuccess;
-    if (dt == Dt::I8) return gemm_i8(s, M, N, K, A, lda, W, e, tile);
+    const GemmRows gr{sp, a_tok ? a_tok : lda};
+    if (dt == Dt::I8) return gemm_i8(s, gr, M, N, K, A, lda, W, e, tile);
     if (K % (16 / (int)dt_bytes(dt)) != 0 || lda % (16 / (int)dt_bytes(dt)) != 0) return hipErrorInvalidValue;
     if ((e.kind == Epi::QkvRope || e.kind == Epi::Gated) && N % 2 != 0) return hipErrorInvalidValue;
     switch (dt) {
-    case Dt::F16: return gemm_t<_Float16, 32>(s, M, N, K, A, lda, W, e, tile);
-    case Dt::BF16: return gemm_t<__bf16, 32>(s, M, N, K, A, lda, W, e, tile);
-    default: return gemm_t<float, 16>(s, M, N, K, A, lda, W, e, tile);
+    case Dt::F16: return gemm_t<_Float16, 32>(s, gr, M, N, K, A, lda, W, e, tile);
+    case Dt::BF16: return gemm_t<__bf16, 32>(s, gr, M, N, K, A, lda, W, e, tile);
+    default: return gemm_t<float, 16>(s, gr, M, N, K, A, lda, W, e, tile);
     }
 }
 

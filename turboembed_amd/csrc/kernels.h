@@ -26,14 +26,54 @@ struct Packing {
     int32_t *tokens;    // [1] packed tokens of the run
 };
 
-hipError_t pack_rows(hipStream_t s, const int32_t *mask, int batch, int seq, Packing p);
+// The dimensions of a run, written by the host beside the rows and read on
+// the device by every kernel of the run, so one captured graph serves every
+// batch of a token bin: grids are sized for the bin's bounds, and a
+// workgroup past the run's own extent leaves at once. A split run's parts
+// each have their rows, packed tokens and longest row (an unused part has
+// none). Options the pooling reads are here too.
+constexpr int MAX_PARTS = 4;
+struct PartDims {
+    int32_t row0, rows, tok0, tokens, max_len, pad[3];
+};
+struct RunDims {
+    int32_t batch, seq, tokens, max_len;    // rows, their stride, packed tokens, longest row
+    int32_t count, pooling, output_dim, l2; // ranges (0: one vector a row), pooling, width, L2 normalize
+    int32_t head, pad[7];                   // 1: ranges through the span head
+    PartDims part[MAX_PARTS];
+};
+
+// The rows and packed tokens one launch works on: part `part` of the run
+// whose dimensions `dims` points to (-1: the whole run), read on the device;
+// or, with dims NULL, the values given here (kernel tests and the tuner).
+struct Span {
+    const RunDims *dims = nullptr;
+    int part = -1;
+    int row0 = 0, rows = 0, tok0 = 0, tokens = 0, max_len = 0, seq = 0;
+};
+inline Span span_of(const RunDims *dims, int part) {
+    Span s;
+    s.dims = dims;
+    s.part = part;
+    return s;
+}
+inline Span span_tokens(int tokens) {
+    Span s;
+    s.tokens = tokens;
+    return s;
+}
+
+// Packs the run's rows (batch and seq from the dimensions; batch at most
+// max_batch).
+hipError_t pack_rows(hipStream_t s, const int32_t *mask, const RunDims *dims, int max_batch, Packing p);
 
 // Int8 operand rows a LayerNorm can write beside its 16-bit output (the next
 // product's operand): the codes of each row's values as rounded to the 16-bit
 // type, with its scale, exactly as quantize_rows makes them from that output.
 struct QuantOut {
-    int8_t *q = nullptr;   // [tokens][hidden]
+    int8_t *q = nullptr;   // [tokens][hidden] from token 0 of the run...
     float *scale = nullptr;   // [tokens]
+    int tok_stride = 0;    // ...a part's rows starting tok0 * tok_stride bytes in
 };
 
 // x[t] = LN(word[id] + pos[p + offset] + type[ty]) (BERT, RoBERTa), or, with
@@ -41,8 +81,9 @@ struct QuantOut {
 // families); ln_b NULL is no bias. Writes x (F32) and, when xh is not NULL,
 // its copy in `dt`. With zero_mask (the rows' mask, DeBERTa-v2), a token
 // whose mask is 0 is zero instead.
-hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
-                    const Packing &p, int seq, int position_offset, const float *word, const float *pos,
+// Over the whole run's tokens (span part -1); max_tokens bounds the grid.
+hipError_t embed_ln(hipStream_t s, const Span &sp, int max_tokens, int hidden, const int32_t *ids,
+                    const int32_t *types, const Packing &p, int position_offset, const float *word, const float *pos,
                     const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt,
                     const int32_t *zero_mask = nullptr, const QuantOut &qo = QuantOut());
 
@@ -53,22 +94,25 @@ hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, c
 // F32 shared-key projections of the relative rows, query then key. A masked
 // query (mask 0 before the row's last live token) attends uniformly to every
 // position through it.
+// The span's rows; max_rows and max_len bound the grid and the LDS.
 hipError_t deberta_attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
-                             const int32_t *mask, int seq, int batch, int max_len, const float *pos,
+                             const int32_t *mask, const Span &sp, int max_rows, int max_len, const float *pos,
                              const int32_t *buckets, int positions, void *ctx);
 
 // out = LN(in) row by row over `tokens` rows of `hidden`; out_f32 and out_h
 // (in `dt`) may each be NULL, and out_f32 may be in (in place). ln_b NULL is
 // no bias.
-hipError_t layer_norm(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
-                      float eps, float *out_f32, void *out_h, Dt dt);
+// Row pointers are the run's token 0; the span's tokens are normed.
+hipError_t layer_norm(hipStream_t s, const Span &sp, int max_tokens, int hidden, const float *in, const float *ln_w,
+                      const float *ln_b, float eps, float *out_f32, void *out_h, Dt dt);
 
 // The residual add and a LayerNorm in one pass, row by row: v = x + y (y in
 // ydt: F32, F16 or BF16). Post-norm (pre_norm 0): x = LN(v), and out_h =
 // LN(v) in `dt` when not NULL. Pre-norm (pre_norm 1): x = v, and out_h =
 // LN(v) in `dt` (out_h F32 on the F32 tier). ln_b NULL is no bias.
-hipError_t add_layer_norm(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
-                          const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt,
+// Over the span's tokens; x, y and out_h point at the run's token 0.
+hipError_t add_layer_norm(hipStream_t s, const Span &sp, int max_tokens, int hidden, float *x, const void *y, Dt ydt,
+                          const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt,
                           const QuantOut &qo = QuantOut());
 
 // What a GEMM does with each output once its sum is done.
@@ -89,21 +133,29 @@ struct EpiArgs {
     int ldo = 0;                   // row stride of out (elements)
     float *x = nullptr;            // Residual: [m, ldo] F32
     int tcap = 0, heads = 0, d = 0, hidden = 0;   // Qkv scatter
-    int tok0 = 0;                  // Qkv, QkvRope: the packed token of row 0 of A (of at, and of the scatter)
+    int tok0 = 0;                  // set on the device: the packed token of row 0 of A (of at, and of the scatter)
     const float *cos = nullptr, *sin = nullptr;   // QkvRope: [positions][d / 2]
     const int32_t *at = nullptr;   // QkvRope: each token's r * seq + p
-    int seq = 0;
+    int seq = 0;                   // QkvRope: the rows' stride (read from the span's dimensions when it has them)
     int silu = 0;                  // Gated: SiLU instead of GELU
     int out_f32 = 0;               // Bias: F32 outputs (else the operand type; F16 for int8 operands)
     // I8 operands: output (m, n) is the int32 sum times a_scale[m] * w_scale[n].
     const float *a_scale = nullptr, *w_scale = nullptr;
 };
 
-// C[m, n] = sum_k A[m, k] W[n, k] over m < M (rows of A, ld lda), n < N, k < K,
-// operands in `dt`, F32 accumulation on MFMA, then the epilogue. `tile`
-// picks the block shape (0 = the launcher's choice for the shape).
-hipError_t gemm(hipStream_t s, Dt dt, int M, int N, int K, const void *A, int lda, const void *W,
-                const EpiArgs &e, int tile = 0);
+// C[m, n] = sum_k A[m, k] W[n, k] over the span's tokens m (rows of A, ld
+// lda), n < N, k < K, operands in `dt`, F32 accumulation on MFMA, then the
+// epilogue. A, a row-major output and the int8 activation scales point at
+// the run's token 0; the span's rows start tok0 * a_tok rows of A in (a_tok
+// 0: lda) and tok0 rows of the output in; max_m bounds the grid. `tile`
+// picks the block shape (0 = the launcher's choice for max_m).
+hipError_t gemm(hipStream_t s, Dt dt, const Span &sp, int max_m, int N, int K, const void *A, int lda, int a_tok,
+                const void *W, const EpiArgs &e, int tile = 0);
+// The same with explicit rows M from token 0 (kernel tests and the tuner).
+inline hipError_t gemm(hipStream_t s, Dt dt, int M, int N, int K, const void *A, int lda, const void *W,
+                       const EpiArgs &e, int tile = 0) {
+    return gemm(s, dt, span_tokens(M), M, N, K, A, lda, 0, W, e, tile);
+}
 int gemm_tiles();   // how many block shapes `tile` may name (1..n)
 // A block shape's name in a choices string ("auto" for 0, the launcher's
 // rule), and the shape a name (or a bare number) spells, -1 for none.
@@ -125,8 +177,9 @@ bool gemm_made_to_fail(int tile);
 // qkv, into ctx [tokens, heads * d] in `dt`. window: keys within `window` of
 // the query (|i - j| <= window), or INT32_MAX. F16 and BF16 run on the matrix
 // cores unless `simple`; F32 runs the scalar path.
+// The span's rows; max_rows and max_len bound the grid.
 hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
-                     const int32_t *mask, int seq, int batch, int max_len, int window, void *ctx,
+                     const int32_t *mask, const Span &sp, int max_rows, int max_len, int window, void *ctx,
                      bool simple = false);
 
 // A mean's tokens are summed in chunks of POOL_CHUNK, each chunk in token
@@ -140,12 +193,15 @@ struct PoolScratch {
     int chunks = 0;
 };
 
-// One vector per row (mode 0: MEAN/CLS/LAST as pooling says) or per range
-// (mode 1: the mean over the range's live tokens), cut to output_dim, L2
-// normalized when l2, into out [count, output_dim] F32.
-hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
-                int count, const uint32_t *ranges, int pooling, int output_dim, int l2, const PoolScratch &ps,
-                float *out);
+// The run's vectors, as its dimensions say: one a row (count 0: MEAN, CLS
+// or LAST as pooling says) or one a range (the mean over the range's live
+// tokens), cut to output_dim, L2 normalized when l2, into out
+// [items, output_dim] F32; with head set, each range's mean over all
+// `hidden` values through the span head (hw [hout, hidden], hb [hout] F32,
+// F64 sums) into out [count, hout]. max_items bounds the grid.
+hipError_t pool(hipStream_t s, const RunDims *dims, int max_items, const float *x, int hidden, const Packing &p,
+                const int32_t *mask, const uint32_t *ranges, const PoolScratch &ps, float *out,
+                const float *hw = nullptr, const float *hb = nullptr, int hout = 0);
 
 // The MFMA rate probe: `blocks` workgroups of 4 waves, each wave 8 chains of
 // 32x32x16 F16 products for `iters` rounds, fixed or random operands; out
@@ -155,11 +211,6 @@ hipError_t mfma_probe(hipStream_t s, int blocks, int iters, int random, float *o
 // The span head's outputs at most (2 for start and end).
 constexpr int HEAD_MAX = 16;
 
-// Range i's mean over all `hidden` values (as pool's mode 1) through a linear
-// head, w [hout, hidden] and b [hout] F32, its sums in F64: out [count, hout].
-hipError_t pool_head(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
-                     int count, const uint32_t *ranges, const float *hw, const float *hb, int hout,
-                     const PoolScratch &ps, float *out);
 
 // Symmetric int8 rows: for each of `rows` rows of `cols` values (row stride
 // ld, F32 or F16 per src_dt), scale = max |x| / 127 and q = round(x / scale)
@@ -167,6 +218,12 @@ hipError_t pool_head(hipStream_t s, const float *x, int hidden, const Packing &p
 // Per output channel for weights, per token for activations.
 hipError_t quantize_rows(hipStream_t s, const void *src, Dt src_dt, int rows, int cols, int ld, int8_t *dst,
                          float *scale);
+// The same over a span's tokens: src, dst and scale point at the run's token
+// 0; the span's rows start tok0 * ld values of src, tok0 * dst_tok bytes of
+// dst (rows of cols bytes from there) and tok0 scales in. max_rows bounds
+// the grid.
+hipError_t quantize_span(hipStream_t s, const Span &sp, int max_rows, const void *src, Dt src_dt, int cols, int ld,
+                         int8_t *dst, int dst_tok, float *scale);
 
 // Vector codes of rows x dim F32 values (reference core/src/quantize.rs:48-80,
 // sentence-transformers' quantize_embeddings layout): mode 2 (int8) with
@@ -189,6 +246,9 @@ hipError_t static_scratch(int device, void **ptr);
 
 // dst = src over `bytes` (a multiple of 16), 16-byte vectors, one pass.
 hipError_t copy_bytes(hipStream_t s, const void *src, void *dst, size_t bytes);
+// dst = src over the span's tokens, rows of row_bytes (a multiple of 16)
+// from the run's token 0; max_tokens bounds the grid.
+hipError_t copy_rows(hipStream_t s, const Span &sp, int max_tokens, const void *src, void *dst, size_t row_bytes);
 
 // n values uniform in [-amp, amp) from a counter hash of (seed, index).
 hipError_t fill_uniform(hipStream_t s, float *dst, size_t n, float amp, uint32_t seed);

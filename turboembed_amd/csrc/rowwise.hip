@@ -16,9 +16,11 @@ namespace rocm {
 // (reference core/src/cpu/encoder/mod.rs:395-405; core/cuda/kernels.cu:290-381):
 // integer maxima in LDS, then an exclusive scan in row order, then each
 // token's place. Integer work only, so the result is exact.
-__global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restrict__ mask, int batch, int seq,
-                                                         Packing p, int starts_in_lds) {
+__global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restrict__ mask,
+                                                         const RunDims *__restrict__ dims, Packing p,
+                                                         int starts_in_lds) {
     extern __shared__ int32_t lens[];
+    const int batch = uniform(dims->batch), seq = uniform(dims->seq);
     // Each wave takes whole rows: every lane's last live column among its
     // strided ones, then the wave's maximum (no atomics on a few shared words).
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
@@ -57,11 +59,11 @@ __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restri
     }
 }
 
-hipError_t pack_rows(hipStream_t s, const int32_t *mask, int batch, int seq, Packing p) {
+hipError_t pack_rows(hipStream_t s, const int32_t *mask, const RunDims *dims, int max_batch, Packing p) {
     // The starts go to LDS beside the lengths when both fit.
-    const int in_lds = 2 * (size_t)batch * sizeof(int32_t) <= 64 * 1024 ? 1 : 0;
-    hipLaunchKernelGGL(pack_rows_kernel, dim3(1), dim3(1024), (1 + in_lds) * batch * sizeof(int32_t), s, mask, batch,
-                       seq, p, in_lds);
+    const int in_lds = 2 * (size_t)max_batch * sizeof(int32_t) <= 64 * 1024 ? 1 : 0;
+    hipLaunchKernelGGL(pack_rows_kernel, dim3(1), dim3(1024), (1 + in_lds) * max_batch * sizeof(int32_t), s, mask,
+                       dims, p, in_lds);
     return hipGetLastError();
 }
 
@@ -167,15 +169,17 @@ __device__ __forceinline__ void quant_row(const float (&v)[G][4], int hidden, in
 }
 
 template <int G, typename H>
-__global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, const int32_t *__restrict__ ids,
-                                                       const int32_t *__restrict__ types, Packing p, int seq,
+__global__ void __launch_bounds__(256) embed_ln_kernel(Span sp, int hidden, const int32_t *__restrict__ ids,
+                                                       const int32_t *__restrict__ types, Packing p,
                                                        int offset, const float *__restrict__ word,
                                                        const float *__restrict__ pos, const float *__restrict__ type,
                                                        const float *__restrict__ ln_w, const float *__restrict__ ln_b,
                                                        float eps, float *__restrict__ x, H *__restrict__ xh,
                                                        const int32_t *__restrict__ zero_mask, QuantOut qo) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= tokens) return;
+    const Live lv = live_of(sp);
+    const int local = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (local >= lv.tokens) return;
+    const int t = lv.tok0 + local, seq = lv.seq;
     const int lane = threadIdx.x & 63;
     const int at = p.at[t];
     const int id = ids[at];
@@ -213,16 +217,18 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(int tokens, int hidden, c
 #pragma unroll
             for (int k = 0; k < 4; ++k) v[g][k] = 0.0f;
     store_row<G, H>(v, hidden, x + (size_t)t * hidden, xh ? xh + (size_t)t * hidden : nullptr);
-    if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)t * hidden, qo.scale + t);
+    if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden, qo.scale + t);
 }
 
 template <int G, typename H>
-__global__ void __launch_bounds__(256) layer_norm_kernel(int tokens, int hidden, const float *__restrict__ in,
+__global__ void __launch_bounds__(256) layer_norm_kernel(Span sp, int hidden, const float *__restrict__ in,
                                                          const float *__restrict__ ln_w,
                                                          const float *__restrict__ ln_b, float eps, float *out_f32,
                                                          H *__restrict__ out_h) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= tokens) return;
+    const Live lv = live_of(sp);
+    const int local = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (local >= lv.tokens) return;
+    const int t = lv.tok0 + local;
     const int lane = threadIdx.x & 63;
     const float *row = in + (size_t)t * hidden;
     float v[G][4];
@@ -243,12 +249,14 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(int tokens, int hidden,
 // then x = LN(v) (post-norm) or x = v (pre-norm), and out_h = LN(v). One
 // read of x and of the product, one write of x and of the operand copy.
 template <int G, typename Y, typename H>
-__global__ void __launch_bounds__(256) add_layer_norm_kernel(int tokens, int hidden, float *__restrict__ x,
+__global__ void __launch_bounds__(256) add_layer_norm_kernel(Span sp, int hidden, float *__restrict__ x,
                                                              const Y *__restrict__ y, const float *__restrict__ ln_w,
                                                              const float *__restrict__ ln_b, float eps, int pre_norm,
                                                              H *__restrict__ out_h, QuantOut qo) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= tokens) return;
+    const Live lv = live_of(sp);
+    const int local = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (local >= lv.tokens) return;
+    const int t = lv.tok0 + local;
     const int lane = threadIdx.x & 63;
     float *row = x + (size_t)t * hidden;
     const Y *yr = y + (size_t)t * hidden;
@@ -270,42 +278,44 @@ __global__ void __launch_bounds__(256) add_layer_norm_kernel(int tokens, int hid
     if (pre_norm) store_row<G, H>(v, hidden, row, nullptr);
     ln_wave<G>(v, hidden, ln_w, ln_b, eps);
     store_row<G, H>(v, hidden, pre_norm ? nullptr : row, out_h ? out_h + (size_t)t * hidden : nullptr);
-    if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)t * hidden, qo.scale + t);
+    if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden, qo.scale + t);
 }
 
 template <typename H, int G, typename Y>
-static hipError_t add_ln_v(hipStream_t s, int tokens, int hidden, float *x, const void *y, const float *ln_w,
-                           const float *ln_b, float eps, int pre_norm, void *out_h, const QuantOut &qo) {
-    hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, x,
+static hipError_t add_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y,
+                           const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h,
+                           const QuantOut &qo) {
+    hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp, hidden, x,
                        (const Y *)y, ln_w, ln_b, eps, pre_norm, (H *)out_h, qo);
     return hipGetLastError();
 }
 
 template <typename H, int G>
-static hipError_t add_ln_y(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
-                           const float *ln_b, float eps, int pre_norm, void *out_h, const QuantOut &qo) {
+static hipError_t add_ln_y(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y, Dt ydt,
+                           const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h,
+                           const QuantOut &qo) {
     switch (ydt) {
-    case Dt::F16: return add_ln_v<H, G, _Float16>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
-    case Dt::BF16: return add_ln_v<H, G, __bf16>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
-    case Dt::F32: return add_ln_v<H, G, float>(s, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::F16: return add_ln_v<H, G, _Float16>(s, sp, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::BF16: return add_ln_v<H, G, __bf16>(s, sp, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::F32: return add_ln_v<H, G, float>(s, sp, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
     default: return hipErrorInvalidValue;
     }
 }
 
 template <typename H, int G>
-static hipError_t embed_ln_v(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
-                             const Packing &p, int seq, int offset, const float *word, const float *pos,
+static hipError_t embed_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, const int32_t *ids,
+                             const int32_t *types, const Packing &p, int offset, const float *word, const float *pos,
                              const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh,
                              const int32_t *zero_mask, const QuantOut &qo) {
-    hipLaunchKernelGGL((embed_ln_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, ids, types, p,
-                       seq, offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh, zero_mask, qo);
+    hipLaunchKernelGGL((embed_ln_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp, hidden, ids, types, p,
+                       offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh, zero_mask, qo);
     return hipGetLastError();
 }
 
 template <typename H, int G>
-static hipError_t ln_v(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
-                       float eps, float *out_f32, void *out_h) {
-    hipLaunchKernelGGL((layer_norm_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, tokens, hidden, in, ln_w,
+static hipError_t ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, const float *in, const float *ln_w,
+                       const float *ln_b, float eps, float *out_f32, void *out_h) {
+    hipLaunchKernelGGL((layer_norm_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp, hidden, in, ln_w,
                        ln_b, eps, out_f32, (H *)out_h);
     return hipGetLastError();
 }
@@ -326,63 +336,65 @@ static hipError_t ln_v(hipStream_t s, int tokens, int hidden, const float *in, c
     }
 
 template <typename H>
-static hipError_t embed_ln_t(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
-                             const Packing &p, int seq, int offset, const float *word, const float *pos,
+static hipError_t embed_ln_t(hipStream_t s, const Span &sp, int tokens, int hidden, const int32_t *ids,
+                             const int32_t *types, const Packing &p, int offset, const float *word, const float *pos,
                              const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh,
                              const int32_t *zero_mask, const QuantOut &qo) {
-    ROWWISE_DISPATCH(embed_ln_v, s, tokens, hidden, ids, types, p, seq, offset, word, pos, type, ln_w, ln_b, eps, x, xh,
+    ROWWISE_DISPATCH(embed_ln_v, s, sp, tokens, hidden, ids, types, p, offset, word, pos, type, ln_w, ln_b, eps, x, xh,
                      zero_mask, qo)
 }
 
 template <typename H>
-static hipError_t ln_t(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
-                       float eps, float *out_f32, void *out_h) {
-    ROWWISE_DISPATCH(ln_v, s, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h)
+static hipError_t ln_t(hipStream_t s, const Span &sp, int tokens, int hidden, const float *in, const float *ln_w,
+                       const float *ln_b, float eps, float *out_f32, void *out_h) {
+    ROWWISE_DISPATCH(ln_v, s, sp, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h)
 }
 
 template <typename H>
-static hipError_t add_ln_t(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
-                           const float *ln_b, float eps, int pre_norm, void *out_h, const QuantOut &qo) {
-    ROWWISE_DISPATCH(add_ln_y, s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo)
+static hipError_t add_ln_t(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y, Dt ydt,
+                           const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h,
+                           const QuantOut &qo) {
+    ROWWISE_DISPATCH(add_ln_y, s, sp, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo)
 }
 
-hipError_t embed_ln(hipStream_t s, int tokens, int hidden, const int32_t *ids, const int32_t *types,
-                    const Packing &p, int seq, int position_offset, const float *word, const float *pos,
+hipError_t embed_ln(hipStream_t s, const Span &sp, int max_tokens, int hidden, const int32_t *ids,
+                    const int32_t *types, const Packing &p, int position_offset, const float *word, const float *pos,
                     const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh, Dt dt,
                     const int32_t *zero_mask, const QuantOut &qo) {
-    if (tokens <= 0) return hipSuccess;
+    if (max_tokens <= 0) return hipSuccess;
     if (qo.q && (dt != Dt::F16 || !xh || hidden % 4 != 0)) return hipErrorInvalidValue;
     switch (dt) {
     case Dt::F16:
-        return embed_ln_t<_Float16>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w,
+        return embed_ln_t<_Float16>(s, sp, max_tokens, hidden, ids, types, p, position_offset, word, pos, type, ln_w,
                                     ln_b, eps, x, xh, zero_mask, qo);
     case Dt::BF16:
-        return embed_ln_t<__bf16>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w, ln_b,
-                                  eps, x, xh, zero_mask, qo);
+        return embed_ln_t<__bf16>(s, sp, max_tokens, hidden, ids, types, p, position_offset, word, pos, type, ln_w,
+                                  ln_b, eps, x, xh, zero_mask, qo);
     default:
-        return embed_ln_t<float>(s, tokens, hidden, ids, types, p, seq, position_offset, word, pos, type, ln_w, ln_b,
-                                 eps, x, xh, zero_mask, qo);
+        return embed_ln_t<float>(s, sp, max_tokens, hidden, ids, types, p, position_offset, word, pos, type, ln_w,
+                                 ln_b, eps, x, xh, zero_mask, qo);
     }
 }
 
-hipError_t add_layer_norm(hipStream_t s, int tokens, int hidden, float *x, const void *y, Dt ydt, const float *ln_w,
-                          const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt, const QuantOut &qo) {
-    if (tokens <= 0) return hipSuccess;
+hipError_t add_layer_norm(hipStream_t s, const Span &sp, int max_tokens, int hidden, float *x, const void *y, Dt ydt,
+                          const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt,
+                          const QuantOut &qo) {
+    if (max_tokens <= 0) return hipSuccess;
     if (qo.q && (dt != Dt::F16 || !out_h || hidden % 4 != 0)) return hipErrorInvalidValue;
     switch (dt) {
-    case Dt::F16: return add_ln_t<_Float16>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
-    case Dt::BF16: return add_ln_t<__bf16>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
-    default: return add_ln_t<float>(s, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::F16: return add_ln_t<_Float16>(s, sp, max_tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::BF16: return add_ln_t<__bf16>(s, sp, max_tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    default: return add_ln_t<float>(s, sp, max_tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
     }
 }
 
-hipError_t layer_norm(hipStream_t s, int tokens, int hidden, const float *in, const float *ln_w, const float *ln_b,
-                      float eps, float *out_f32, void *out_h, Dt dt) {
-    if (tokens <= 0) return hipSuccess;
+hipError_t layer_norm(hipStream_t s, const Span &sp, int max_tokens, int hidden, const float *in, const float *ln_w,
+                      const float *ln_b, float eps, float *out_f32, void *out_h, Dt dt) {
+    if (max_tokens <= 0) return hipSuccess;
     switch (dt) {
-    case Dt::F16: return ln_t<_Float16>(s, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h);
-    case Dt::BF16: return ln_t<__bf16>(s, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h);
-    default: return ln_t<float>(s, tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h);
+    case Dt::F16: return ln_t<_Float16>(s, sp, max_tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h);
+    case Dt::BF16: return ln_t<__bf16>(s, sp, max_tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h);
+    default: return ln_t<float>(s, sp, max_tokens, hidden, in, ln_w, ln_b, eps, out_f32, out_h);
     }
 }
 
@@ -416,182 +428,188 @@ __device__ __forceinline__ void pool_span(int i, int mode, const Packing &p, con
     }
 }
 
-// Workgroup (i, k): the F32 sum, in token order, of chunk k of item i's
-// tokens (its live ones, when the item has any live token; else all of
-// them), and how many it summed. Tokens are read 8 at a time (their loads in
-// flight together), and added in order.
-__global__ void __launch_bounds__(POOL_THREADS) pool_part_kernel(const float *__restrict__ x, int hidden, Packing p,
-                                                                 const int32_t *__restrict__ mask, int seq, int mode,
-                                                                 const uint32_t *__restrict__ ranges, int od,
-                                                                 float *__restrict__ part, int32_t *__restrict__ cnt,
-                                                                 int chunks) {
-    const int i = blockIdx.x, k = blockIdx.y;
-    int r, c0, c1;
-    pool_span(i, mode, p, ranges, r, c0, c1);
-    const int cs = c0 + k * POOL_CHUNK;
-    if (cs >= c1) return;   // past the item: the finish reads only its own chunks
-    const int ce = min(cs + POOL_CHUNK, c1), start = p.start[r];
-    const int32_t *mk = mask + (size_t)r * seq;
-    int any = 0;
-    for (int q = c0 + (int)threadIdx.x; q < c1 && !any; q += POOL_THREADS) any = mk[q] != 0;
-    const bool live_only = __syncthreads_or(any) != 0;
-    constexpr int MAXV = 8;
-    float acc[MAXV];
-#pragma unroll
-    for (int v = 0; v < MAXV; ++v) acc[v] = 0.0f;
-    int n = 0;
-    for (int q0 = cs; q0 < ce; q0 += 8) {
-        bool use[8];
-        float val[8][MAXV];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int q = q0 + j;
-            use[j] = q < ce && (!live_only || mk[q] != 0);
-            const float *row = x + (size_t)(start + (use[j] ? q : cs)) * hidden;
-#pragma unroll
-            for (int v = 0; v < MAXV; ++v) {
-                const int c = threadIdx.x + POOL_THREADS * v;
-                val[j][v] = (use[j] && c < od) ? row[c] : 0.0f;
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (!use[j]) continue;
-#pragma unroll
-            for (int v = 0; v < MAXV; ++v) acc[v] = __fadd_rn(acc[v], val[j][v]);
-            ++n;
-        }
-    }
-    float *dst = part + ((size_t)i * chunks + k) * od;
-#pragma unroll
-    for (int v = 0; v < MAXV; ++v) {
-        const int c = threadIdx.x + POOL_THREADS * v;
-        if (c < od) dst[c] = acc[v];
-    }
-    if (threadIdx.x == 0) cnt[(size_t)i * chunks + k] = n;
+// The run's pooling as its dimensions give it: item count and mode (ranges
+// when count > 0, else the rows), the pooling of a row, the output width, L2
+// and the span head.
+struct PoolRun {
+    int items, mode, pooling, od, l2, head;
+};
+__device__ __forceinline__ PoolRun pool_run(const RunDims *__restrict__ d, int hidden) {
+    const int count = uniform(d->count), head = uniform(d->head);
+    return PoolRun{count ? count : uniform(d->batch), count ? 1 : 0, uniform(d->pooling),
+                   head ? hidden : uniform(d->output_dim), uniform(d->l2), head};
 }
 
-template <bool HEAD>
-__global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const float *__restrict__ x, int hidden, Packing p,
-                                                            const int32_t *__restrict__ mask, int seq, int mode,
-                                                            const uint32_t *__restrict__ ranges, int pooling, int od,
-                                                            int l2, float *__restrict__ out,
-                                                            const float *__restrict__ hw,
+// Work item w = (item i, chunk k), over a grid-stride loop: the F32 sum, in
+// token order, of chunk k of item i's tokens (its live ones, when the item
+// has any live token; else all of them), and how many it summed. Tokens are
+// read 8 at a time (their loads in flight together), and added in order. A
+// row's CLS or LAST vector needs no sums.
+__global__ void __launch_bounds__(POOL_THREADS) pool_part_kernel(const RunDims *__restrict__ dims,
+                                                                 const float *__restrict__ x, int hidden, Packing p,
+                                                                 const int32_t *__restrict__ mask,
+                                                                 const uint32_t *__restrict__ ranges,
+                                                                 float *__restrict__ part, int32_t *__restrict__ cnt,
+                                                                 int chunks) {
+    const PoolRun pr = pool_run(dims, hidden);
+    if (pr.mode == 0 && pr.pooling != 1) return;
+    const int seq = uniform(dims->seq), od = pr.od;
+    for (int w = blockIdx.x; w < pr.items * chunks; w += gridDim.x) {
+        const int i = w / chunks, k = w % chunks;
+        int r, c0, c1;
+        pool_span(i, pr.mode, p, ranges, r, c0, c1);
+        const int cs = c0 + k * POOL_CHUNK;
+        if (cs >= c1) continue;   // past the item: the finish reads only its own chunks
+        const int ce = min(cs + POOL_CHUNK, c1), start = p.start[r];
+        const int32_t *mk = mask + (size_t)r * seq;
+        int any = 0;
+        for (int q = c0 + (int)threadIdx.x; q < c1 && !any; q += POOL_THREADS) any = mk[q] != 0;
+        const bool live_only = __syncthreads_or(any) != 0;
+        constexpr int MAXV = 8;
+        float acc[MAXV];
+#pragma unroll
+        for (int v = 0; v < MAXV; ++v) acc[v] = 0.0f;
+        int n = 0;
+        for (int q0 = cs; q0 < ce; q0 += 8) {
+            bool use[8];
+            float val[8][MAXV];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int q = q0 + j;
+                use[j] = q < ce && (!live_only || mk[q] != 0);
+                const float *row = x + (size_t)(start + (use[j] ? q : cs)) * hidden;
+#pragma unroll
+                for (int v = 0; v < MAXV; ++v) {
+                    const int c = threadIdx.x + POOL_THREADS * v;
+                    val[j][v] = (use[j] && c < od) ? row[c] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (!use[j]) continue;
+#pragma unroll
+                for (int v = 0; v < MAXV; ++v) acc[v] = __fadd_rn(acc[v], val[j][v]);
+                ++n;
+            }
+        }
+        float *dst = part + ((size_t)i * chunks + k) * od;
+#pragma unroll
+        for (int v = 0; v < MAXV; ++v) {
+            const int c = threadIdx.x + POOL_THREADS * v;
+            if (c < od) dst[c] = acc[v];
+        }
+        if (threadIdx.x == 0) cnt[(size_t)i * chunks + k] = n;
+    }
+}
+
+// Item i over a grid-stride loop: its vector from the chunk sums (or its
+// CLS or LAST row), then the cut and L2, or the span head.
+__global__ void __launch_bounds__(POOL_THREADS) pool_kernel(const RunDims *__restrict__ dims,
+                                                            const float *__restrict__ x, int hidden, Packing p,
+                                                            const uint32_t *__restrict__ ranges,
+                                                            float *__restrict__ out, const float *__restrict__ hw,
                                                             const float *__restrict__ hb, int hout,
                                                             const float *__restrict__ sums,
                                                             const int32_t *__restrict__ cnt, int chunks) {
     __shared__ double part[POOL_THREADS / 64];
-    __shared__ double hpart[HEAD ? HEAD_MAX : 1][POOL_THREADS / 64];
-    const int i = blockIdx.x;
-    int r, c0, c1;
-    pool_span(i, mode, p, ranges, r, c0, c1);
-    const int start = p.start[r];
-    (void)mask;
-    (void)seq;
+    __shared__ double hpart[HEAD_MAX][POOL_THREADS / 64];
+    const PoolRun pr = pool_run(dims, hidden);
+    const int od = pr.od;
     constexpr int MAXV = 8;   // output_dim up to 2048
-    float acc[MAXV];
+    for (int i = blockIdx.x; i < pr.items; i += gridDim.x) {
+        int r, c0, c1;
+        pool_span(i, pr.mode, p, ranges, r, c0, c1);
+        const int start = p.start[r];
+        float acc[MAXV];
 #pragma unroll
-    for (int v = 0; v < MAXV; ++v) acc[v] = 0.0f;
-    if (mode == 0 && pooling != 1) {
-        const int tok = pooling == 2 ? start : start + p.len[r] - 1;   // CLS: column 0; LAST: last live
-#pragma unroll
-        for (int v = 0; v < MAXV; ++v) {
-            const int c = threadIdx.x + POOL_THREADS * v;
-            if (c < od) acc[v] = x[(size_t)tok * hidden + c];
-        }
-    } else {
-        // The chunks' sums in chunk order (one chunk: its sum exactly).
-        const int nch = (c1 - c0 + POOL_CHUNK - 1) / POOL_CHUNK;
-        int n = 0;
-        for (int k = 0; k < nch; ++k) {
-            const float *src = sums + ((size_t)i * chunks + k) * od;
+        for (int v = 0; v < MAXV; ++v) acc[v] = 0.0f;
+        if (pr.mode == 0 && pr.pooling != 1) {
+            const int tok = pr.pooling == 2 ? start : start + p.len[r] - 1;   // CLS: column 0; LAST: last live
 #pragma unroll
             for (int v = 0; v < MAXV; ++v) {
                 const int c = threadIdx.x + POOL_THREADS * v;
-                if (c < od) acc[v] = __fadd_rn(acc[v], src[c]);
+                if (c < od) acc[v] = x[(size_t)tok * hidden + c];
             }
-            n += cnt[(size_t)i * chunks + k];
-        }
-        const float inv = __fdiv_rn(1.0f, (float)n);
+        } else {
+            // The chunks' sums in chunk order (one chunk: its sum exactly).
+            const int nch = (c1 - c0 + POOL_CHUNK - 1) / POOL_CHUNK;
+            int n = 0;
+            for (int k = 0; k < nch; ++k) {
+                const float *src = sums + ((size_t)i * chunks + k) * od;
 #pragma unroll
-        for (int v = 0; v < MAXV; ++v) acc[v] = __fmul_rn(acc[v], inv);
-    }
-    if constexpr (HEAD) {
-        // od is hidden here: every value of the mean meets the head.
-        for (int o = 0; o < hout; ++o) {
-            double t = 0.0;
+                for (int v = 0; v < MAXV; ++v) {
+                    const int c = threadIdx.x + POOL_THREADS * v;
+                    if (c < od) acc[v] = __fadd_rn(acc[v], src[c]);
+                }
+                n += cnt[(size_t)i * chunks + k];
+            }
+            const float inv = __fdiv_rn(1.0f, (float)n);
+#pragma unroll
+            for (int v = 0; v < MAXV; ++v) acc[v] = __fmul_rn(acc[v], inv);
+        }
+        if (pr.head) {
+            // od is hidden here: every value of the mean meets the head.
+            for (int o = 0; o < hout; ++o) {
+                double t = 0.0;
+#pragma unroll
+                for (int v = 0; v < MAXV; ++v) {
+                    const int c = threadIdx.x + POOL_THREADS * v;
+                    if (c < od) t = fma((double)hw[(size_t)o * hidden + c], (double)acc[v], t);
+                }
+                t = wave_sum(t);
+                if ((threadIdx.x & 63) == 0) hpart[o][threadIdx.x >> 6] = t;
+            }
+            __syncthreads();
+            if ((int)threadIdx.x < hout) {
+                double tot = (double)hb[threadIdx.x];
+#pragma unroll
+                for (int w = 0; w < POOL_THREADS / 64; ++w) tot += hpart[threadIdx.x][w];
+                out[(size_t)i * hout + threadIdx.x] = (float)tot;
+            }
+            __syncthreads();   // hpart is read before the next item writes it
+            continue;
+        }
+        if (pr.l2) {
+            double s = 0.0;
 #pragma unroll
             for (int v = 0; v < MAXV; ++v) {
                 const int c = threadIdx.x + POOL_THREADS * v;
-                if (c < od) t = fma((double)hw[(size_t)o * hidden + c], (double)acc[v], t);
+                if (c < od) s += (double)acc[v] * (double)acc[v];
             }
-            t = wave_sum(t);
-            if ((threadIdx.x & 63) == 0) hpart[o][threadIdx.x >> 6] = t;
-        }
-        __syncthreads();
-        if ((int)threadIdx.x < hout) {
-            double tot = (double)hb[threadIdx.x];
+            s = wave_sum(s);
+            if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+            __syncthreads();
+            double tot = 0.0;
 #pragma unroll
-            for (int w = 0; w < POOL_THREADS / 64; ++w) tot += hpart[threadIdx.x][w];
-            out[(size_t)i * hout + threadIdx.x] = (float)tot;
+            for (int w = 0; w < POOL_THREADS / 64; ++w) tot += part[w];
+            __syncthreads();   // part is read before the next item writes it
+            const double norm = fmax(sqrt(tot), 1e-12);
+            const float inv = (float)(1.0 / norm);
+#pragma unroll
+            for (int v = 0; v < MAXV; ++v) acc[v] = __fmul_rn(acc[v], inv);
         }
-        return;
-    }
-    if (l2) {
-        double s = 0.0;
 #pragma unroll
         for (int v = 0; v < MAXV; ++v) {
             const int c = threadIdx.x + POOL_THREADS * v;
-            if (c < od) s += (double)acc[v] * (double)acc[v];
+            if (c < od) out[(size_t)i * od + c] = acc[v];
         }
-        s = wave_sum(s);
-        if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
-        __syncthreads();
-        double tot = 0.0;
-#pragma unroll
-        for (int w = 0; w < POOL_THREADS / 64; ++w) tot += part[w];
-        const double norm = fmax(sqrt(tot), 1e-12);
-        const float inv = (float)(1.0 / norm);
-#pragma unroll
-        for (int v = 0; v < MAXV; ++v) acc[v] = __fmul_rn(acc[v], inv);
-    }
-#pragma unroll
-    for (int v = 0; v < MAXV; ++v) {
-        const int c = threadIdx.x + POOL_THREADS * v;
-        if (c < od) out[(size_t)i * od + c] = acc[v];
     }
 }
 
-// The chunks a span of up to `seq` tokens takes.
-static bool pool_fits(const PoolScratch &ps, int seq) {
-    return ps.part && ps.cnt && ps.chunks >= (seq + POOL_CHUNK - 1) / POOL_CHUNK;
-}
+// Workgroups a pooling launch takes at most: items beyond them loop.
+constexpr int POOL_GRID = 2048;
 
-hipError_t pool(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq, int count,
-                const uint32_t *ranges, int pooling, int output_dim, int l2, const PoolScratch &ps, float *out) {
-    if (output_dim > 8 * POOL_THREADS) return hipErrorInvalidValue;
-    if (count <= 0) return hipSuccess;
-    const int mode = ranges ? 1 : 0;
-    if (mode == 1 || pooling == 1) {
-        if (!pool_fits(ps, seq)) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(pool_part_kernel, dim3(count, ps.chunks), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq,
-                           mode, ranges, output_dim, ps.part, ps.cnt, ps.chunks);
-    }
-    hipLaunchKernelGGL(pool_kernel<false>, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq, mode, ranges,
-                       pooling, output_dim, l2, out, nullptr, nullptr, 0, ps.part, ps.cnt, ps.chunks);
-    return hipGetLastError();
-}
-
-hipError_t pool_head(hipStream_t s, const float *x, int hidden, const Packing &p, const int32_t *mask, int seq,
-                     int count, const uint32_t *ranges, const float *hw, const float *hb, int hout,
-                     const PoolScratch &ps, float *out) {
-    if (hidden > 8 * POOL_THREADS || hout < 1 || hout > HEAD_MAX || !ranges) return hipErrorInvalidValue;
-    if (count <= 0) return hipSuccess;
-    if (!pool_fits(ps, seq)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(pool_part_kernel, dim3(count, ps.chunks), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq, 1,
-                       ranges, hidden, ps.part, ps.cnt, ps.chunks);
-    hipLaunchKernelGGL(pool_kernel<true>, dim3(count), dim3(POOL_THREADS), 0, s, x, hidden, p, mask, seq, 1, ranges,
-                       1 /* the mean */, hidden, 0, out, hw, hb, hout, ps.part, ps.cnt, ps.chunks);
+hipError_t pool(hipStream_t s, const RunDims *dims, int max_items, const float *x, int hidden, const Packing &p,
+                const int32_t *mask, const uint32_t *ranges, const PoolScratch &ps, float *out, const float *hw,
+                const float *hb, int hout) {
+    if (hidden > 8 * POOL_THREADS || hout < 0 || hout > HEAD_MAX) return hipErrorInvalidValue;
+    if (max_items <= 0) return hipSuccess;
+    if (!ps.part || !ps.cnt || ps.chunks <= 0) return hipErrorInvalidValue;
+    const int part_blocks = (int)std::min<long>((long)max_items * ps.chunks, POOL_GRID);
+    hipLaunchKernelGGL(pool_part_kernel, dim3(part_blocks), dim3(POOL_THREADS), 0, s, dims, x, hidden, p, mask, ranges,
+                       ps.part, ps.cnt, ps.chunks);
+    hipLaunchKernelGGL(pool_kernel, dim3(std::min(max_items, POOL_GRID)), dim3(POOL_THREADS), 0, s, dims, x, hidden, p,
+                       ranges, out, hw, hb, hout, ps.part, ps.cnt, ps.chunks);
     return hipGetLastError();
 }
 
@@ -688,6 +706,70 @@ hipError_t quantize_rows(hipStream_t s, const void *src, Dt src_dt, int rows, in
                            ld, dst, scale);
     else
         return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// A span's rows: src row t at src + t * ld, dst row t at dst + tok0 *
+// dst_tok + (t - tok0) * cols (bytes), scale t at scale + t.
+template <typename S>
+__global__ void __launch_bounds__(256) quantize_span_kernel(Span sp, const S *__restrict__ src, int cols, int ld,
+                                                            int8_t *__restrict__ dst, int dst_tok,
+                                                            float *__restrict__ scale) {
+    const Live lv = live_of(sp);
+    const int local = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (local >= lv.tokens) return;
+    const int t = lv.tok0 + local, lane = threadIdx.x & 63;
+    const S *row = src + (size_t)t * ld;
+    float v[QMAXK][8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < QMAXK; ++k) {
+        const int c = 8 * (lane + 64 * k);
+        if (c < cols) {
+            float a[4], b[4];
+            load4(row + c, a);
+            load4(row + c + 4, b);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[k][q] = a[q];
+                v[k][4 + q] = b[q];
+                mx = fmaxf(mx, fmaxf(fabsf(a[q]), fabsf(b[q])));
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+    int8_t *out = dst + (size_t)lv.tok0 * dst_tok + (size_t)local * cols;
+#pragma unroll
+    for (int k = 0; k < QMAXK; ++k) {
+        const int c = 8 * (lane + 64 * k);
+        if (c < cols) {
+            uint32_t w[2] = {0, 0};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int code = (int)fminf(fmaxf(rintf(v[k][q] * inv), -127.0f), 127.0f);
+                w[q >> 2] |= (uint32_t)(uint8_t)(int8_t)code << (8 * (q & 3));
+            }
+            *(uint2 *)(out + c) = make_uint2(w[0], w[1]);
+        }
+    }
+    if (lane == 0) scale[t] = mx / 127.0f;
+}
+
+hipError_t quantize_span(hipStream_t s, const Span &sp, int max_rows, const void *src, Dt src_dt, int cols, int ld,
+                         int8_t *dst, int dst_tok, float *scale) {
+    if (max_rows <= 0) return hipSuccess;
+    // The codes of a row are the ones quantize_rows makes (same arithmetic).
+    if (cols % 8 != 0 || ld % 8 != 0 || cols > 8 * 64 * QMAXK || (src_dt != Dt::F32 && src_dt != Dt::F16))
+        return hipErrorInvalidValue;
+    const dim3 grid((max_rows + 3) / 4);
+    if (src_dt == Dt::F32)
+        hipLaunchKernelGGL(quantize_span_kernel<float>, grid, dim3(256), 0, s, sp, (const float *)src, cols, ld, dst,
+                           dst_tok, scale);
+    else
+        hipLaunchKernelGGL(quantize_span_kernel<_Float16>, grid, dim3(256), 0, s, sp, (const _Float16 *)src, cols, ld,
+                           dst, dst_tok, scale);
     return hipGetLastError();
 }
 
@@ -805,6 +887,24 @@ hipError_t copy_bytes(hipStream_t s, const void *src, void *dst, size_t bytes) {
     if (n == 0) return hipSuccess;
     const size_t blocks = std::min<size_t>((n + 255) / 256, 256 * 32);
     hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const uint4 *)src, (uint4 *)dst, n);
+    return hipGetLastError();
+}
+
+__global__ void __launch_bounds__(256) copy_rows_kernel(Span sp, const uint4 *__restrict__ src,
+                                                        uint4 *__restrict__ dst, int row_vecs) {
+    const Live lv = live_of(sp);
+    const size_t n = (size_t)lv.tokens * row_vecs, base = (size_t)lv.tok0 * row_vecs;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[base + i] = src[base + i];
+}
+
+hipError_t copy_rows(hipStream_t s, const Span &sp, int max_tokens, const void *src, void *dst, size_t row_bytes) {
+    if (row_bytes % 16 != 0) return hipErrorInvalidValue;
+    const size_t n = (size_t)max_tokens * (row_bytes / 16);
+    if (n == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 256 * 32);
+    hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, sp, (const uint4 *)src, (uint4 *)dst,
+                       (int)(row_bytes / 16));
     return hipGetLastError();
 }
 

@@ -149,6 +149,7 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
         fail(TURBO_E_UNSUPPORTED, "rocm: compute_dtype " + std::to_string(fixed));
 
     auto m = std::make_unique<Model>();
+    counted_host_alloc();
     m->ctx = c;
     m->int8 = fixed == TURBO_DTYPE_I8;
     m->family = d->family;
@@ -535,6 +536,7 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         dt = Dt::I8;
     }
     auto s = std::make_unique<Session>();
+    counted_host_alloc();
     s->model = m;
     s->ctx = m->ctx;
     s->task = desc->task;
@@ -621,13 +623,20 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         s->owned.emplace_back(dev_alloc(bytes, what));
         return s->owned.back().get();
     };
-    // Rows and ranges in one allocation, in the staging buffer's order.
-    s->staging_ints = 3 * B * S + 3 * (size_t)s->max_ranges;
+    // Rows, the run's dimensions and the ranges in one allocation, in the
+    // staging buffer's order: the ids, mask and types planes, then (on a
+    // 64-byte boundary) the dimensions, the ranges right after them.
+    const size_t dims_at = (3 * B * S + 15) / 16 * 16;
+    s->staging_ints = dims_at + sizeof(RunDims) / 4 + 3 * (size_t)s->max_ranges;
     int32_t *rows = static_cast<int32_t *>(alloc(s->staging_ints * 4, "session rows"));
     s->ids = rows;
     s->mask = rows + B * S;
     s->types = rows + 2 * B * S;
-    s->ranges = reinterpret_cast<uint32_t *>(rows + 3 * B * S);
+    s->dims_dev = reinterpret_cast<RunDims *>(rows + dims_at);
+    s->ranges = reinterpret_cast<uint32_t *>(s->dims_dev + 1);
+    check(hipMemset(s->dims_dev, 0, sizeof(RunDims)), "session rows");
+    s->row_lens.assign(B, 0);
+    counted_host_alloc();
     int32_t *pk = static_cast<int32_t *>(alloc((2 * B + 2 * s->tcap + 64) * 4, "session packing"));
     s->pk.start = pk;
     s->pk.len = pk + B;
@@ -665,6 +674,7 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     s->output.bytes = outs * H * 4;
     s->output.owned = false;
     check(hipHostMalloc((void **)&s->staging, s->staging_ints * 4, hipHostMallocDefault), "session staging");
+    s->dims_host = reinterpret_cast<RunDims *>(s->staging + dims_at);
 
     const auto t0 = std::chrono::steady_clock::now();
     std::string timings;
@@ -677,6 +687,8 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         check(hipStreamSynchronize(m->ctx->stream), "session qkv");
     }
     s->choices = format_choices(kc);
+    // Each bin's graph, with the bin's choices (after the tuner's timing).
+    capture_graphs(*s);
     if (tuning) {
         const uint32_t k = forced_knobs(kc);
         tuning->tuned = all_forced(kc) ? TURBO_TUNED_FORCED
@@ -710,15 +722,24 @@ void session_release(Session *s) {
         OnDevice on(s->ctx->ordinal);
         (void)hipStreamSynchronize(s->ctx->stream);
         if (s->staging) (void)hipHostFree(s->staging);
-        for (auto &g : s->graph_of) (void)hipGraphExecDestroy(g.second);
+        for (hipGraphExec_t g : s->graph)
+            if (g) (void)hipGraphExecDestroy(g);
         for (hipEvent_t e : s->ev) (void)hipEventDestroy(e);
         s->owned.clear();
     }
     delete s;
 }
 
-// Runs of at least this many packed tokens split their rows over two streams.
+// Runs of more than this many packed tokens split their rows over the
+// context's streams: the bins above it (le16k, gt16k) capture their graphs
+// with parts, the ones at or below it without.
 constexpr uint32_t SPLIT_MIN_TOKENS = 4096;
+
+// The parts a bin's runs take at most.
+static uint32_t parts_of_bin(const Session &s, int b) {
+    const bool splits = b > 0 && (uint32_t)BIN_EDGE[b - 1] >= SPLIT_MIN_TOKENS;
+    return splits && s.split_parts > 1 && s.max_batch >= 2 ? std::min(s.split_parts, s.max_batch) : 1;
+}
 
 void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_token_range *ranges, uint32_t count) {
     if (r->batch == 0 || r->seq == 0) fail(TURBO_E_INVALID_SHAPE, "rocm: batch and seq may not be 0");
@@ -768,10 +789,11 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     OnDevice on(s->ctx->ordinal);
     // The staging buffer may still feed the last write's copy.
     check(hipStreamSynchronize(s->ctx->stream), "embed_write");
-    int32_t *ids = s->staging, *mask = ids + (size_t)B * S, *types = mask + (size_t)B * S;
-    uint32_t *rg = reinterpret_cast<uint32_t *>(types + (size_t)B * S);
+    const size_t plane = (size_t)s->max_batch * s->max_seq;
+    int32_t *ids = s->staging, *mask = ids + plane, *types = mask + plane;
+    uint32_t *rg = reinterpret_cast<uint32_t *>(s->dims_host + 1);
     uint32_t tokens = 0, max_len = 0;
-    std::vector<uint32_t> lens(B);
+    uint32_t *lens = s->row_lens.data();   // each row's packed length (sized at session_open)
     const Model &m = *s->model;
     const int32_t ntypes = (int32_t)std::max(1u, m.types);
     for (uint32_t row = 0; row < B; ++row) {
@@ -806,16 +828,67 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
         rg[3 * i + 1] = g2.start;
         rg[3 * i + 2] = g2.end;
     }
-    const size_t plane = (size_t)s->max_batch * s->max_seq;
+    // Split the rows into parts of about equal packed tokens (rows in
+    // order: part i ends at the first row where the tokens reach i + 1
+    // parts' share), on runs of the bins that split; not when ranges are
+    // read from layers before the last (each read pools every row). A run
+    // takes its bin's parts (or one row a part when it has fewer rows), so
+    // each part stays within a share of the bin plus one row: the bounds its
+    // graph's grids were sized for.
+    uint32_t parts = 1;
+    if (B >= 2 && tokens > SPLIT_MIN_TOKENS && (alone || taps == 1)) parts = std::min(s->split_parts, B);
+    parts = std::max(parts, 1u);
+    uint32_t part_row[MAX_PARTS + 1], part_tok[MAX_PARTS + 1], part_len[MAX_PARTS];
+    {
+        uint32_t row = 0, t = 0;
+        for (uint32_t i = 0; i < parts; ++i) {
+            part_row[i] = row;
+            part_tok[i] = t;
+            part_len[i] = 0;
+            const uint64_t share = (uint64_t)tokens * (i + 1) / parts;
+            // At least one row a part, and one left for each part after it.
+            do {
+                part_len[i] = std::max(part_len[i], lens[row]);
+                t += lens[row++];
+            } while (row < B - (parts - 1 - i) && (i + 1 == parts || t < share));
+        }
+        part_row[parts] = row;
+        part_tok[parts] = t;
+    }
+    // The run's dimensions, beside the ranges: what every kernel of the run
+    // reads on the device. A part past the run's is empty.
+    RunDims &d = *s->dims_host;
+    std::memset(&d, 0, sizeof d);
+    d.batch = (int32_t)B;
+    d.seq = (int32_t)S;
+    d.tokens = (int32_t)tokens;
+    d.max_len = (int32_t)max_len;
+    d.count = (int32_t)count;
+    d.pooling = (int32_t)r->pooling;
+    d.output_dim = (int32_t)r->output_dim;
+    d.l2 = r->normalize == TURBO_NORMALIZE_L2 ? 1 : 0;
+    d.head = head ? 1 : 0;
+    for (uint32_t i = 0; i < MAX_PARTS; ++i) {
+        PartDims &pd = d.part[i];
+        if (i < parts) {
+            pd.row0 = (int32_t)part_row[i];
+            pd.rows = (int32_t)(part_row[i + 1] - part_row[i]);
+            pd.tok0 = (int32_t)part_tok[i];
+            pd.tokens = (int32_t)(part_tok[i + 1] - part_tok[i]);
+            pd.max_len = (int32_t)part_len[i];
+        } else {
+            pd.row0 = (int32_t)B;
+            pd.tok0 = (int32_t)tokens;
+        }
+    }
     // Planes are B*S long here but the device keeps them max_batch*max_seq
-    // apart: three copies, plus the ranges.
-    const size_t n = (size_t)B * S * 4;
+    // apart: three copies, then the dimensions and the ranges in one.
+    const size_t n = (size_t)B * S * 4, tail = sizeof(RunDims) + (size_t)count * 12;
     check(hipMemcpyAsync(s->ids, ids, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
     check(hipMemcpyAsync(s->mask, mask, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
     check(hipMemcpyAsync(s->types, types, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
-    if (count) check(hipMemcpyAsync(s->ranges, rg, (size_t)count * 12, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
-    (void)plane;
-    s->h2d = 3 * n + (size_t)count * 12;
+    check(hipMemcpyAsync(s->dims_dev, s->dims_host, tail, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+    s->h2d = 3 * n + tail;
     s->batch = B;
     s->seq = S;
     s->pooling = r->pooling;
@@ -824,31 +897,10 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     s->head = head;
     s->taps = taps;
     s->tap_alone = alone;
-    // Split the rows into parts of about equal packed tokens (rows in
-    // order: part i ends at the first row where the tokens reach i + 1
-    // parts' share), on runs large enough to fill the device once a part;
-    // not when ranges are read from layers before the last (each read pools
-    // every row).
-    uint32_t parts = 1;
-    if (B >= 2 && tokens >= SPLIT_MIN_TOKENS && (alone || taps == 1))
-        parts = std::min(s->split_parts, std::min(B, tokens / (SPLIT_MIN_TOKENS / 2)));
-    s->parts = std::max(parts, 1u);
-    {
-        uint32_t r = 0, t = 0;
-        for (uint32_t i = 0; i < s->parts; ++i) {
-            s->part_row[i] = r;
-            s->part_tok[i] = t;
-            s->part_len[i] = 0;
-            const uint64_t share = (uint64_t)tokens * (i + 1) / s->parts;
-            // At least one row a part, and one left for each part after it.
-            do {
-                s->part_len[i] = std::max(s->part_len[i], lens[r]);
-                t += lens[r++];
-            } while (r < B - (s->parts - 1 - i) && (i + 1 == s->parts || t < share));
-        }
-        s->part_row[s->parts] = r;
-        s->part_tok[s->parts] = t;
-    }
+    s->parts = parts;
+    std::copy(part_row, part_row + parts + 1, s->part_row);
+    std::copy(part_tok, part_tok + parts + 1, s->part_tok);
+    std::copy(part_len, part_len + parts, s->part_len);
     s->count = count;
     s->tokens = tokens;
     s->max_len = max_len;
@@ -888,6 +940,8 @@ static const void *layer_input(const Session &s) {
     return s.act == Dt::F32 && !m.modern ? (const void *)s.x : s.xh;
 }
 
+// Product g of layer l, its operand and outputs at the run's token 0 (a
+// launch's span moves them to its own first token on the device).
 static LayerGemm layer_gemm(Session &s, uint32_t l, GemmSlot g) {
     Model &m = *s.model;
     const Model::Layer &L = m.ls[l];
@@ -949,29 +1003,40 @@ static LayerGemm layer_gemm(Session &s, uint32_t l, GemmSlot g) {
     return r;
 }
 
-namespace {
-
-// Rows [row0, row0 + rows) of a run and their packed tokens [tok0, tok0 + tokens).
-struct Part {
-    uint32_t row0, rows, tok0, tokens, max_len;
+// How large a run's launches are: every grid covers the largest run of the
+// bin (whose kernel choices they take), so the launches of a bin are the same
+// whether captured into its graph or launched directly, and give the same
+// bits. A part's tokens are at most a share of the bin's plus one row (its
+// last row crosses the share) plus one (the share's rounding).
+struct Bounds {
+    int bin = 0;
+    uint32_t tokens = 0, rows = 0, max_len = 0, parts = 1, part_tokens = 0, items = 0;
 };
 
-}  // namespace
+static Bounds bounds_of(const Session &s, int b, uint32_t parts) {
+    Bounds o;
+    o.bin = b;
+    o.tokens = bin_tokens(b, s.tcap);
+    o.rows = std::min<uint32_t>(s.max_batch, o.tokens);
+    o.max_len = std::min<uint32_t>(s.max_seq, o.tokens);
+    o.parts = std::max(parts, 1u);
+    const uint32_t bp = o.parts;
+    o.part_tokens = bp == 1 ? o.tokens : std::min(o.tokens, (o.tokens + bp - 1) / bp + 1 + o.max_len);
+    o.items = std::max(o.rows, s.max_ranges);
+    return o;
+}
 
-// The layers over one part of the run's rows, on stream st: every product,
-// norm and attention launch reads and writes that part's tokens alone.
-static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) {
+// The layers over part `part` of the run's rows, on stream st: every
+// product, norm and attention launch reads that part's rows and tokens from
+// the run's dimensions. Layer reads pool their ranges as they pass.
+static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, Timer &tm) {
     Model &m = *s.model;
-    const int T = (int)part.tokens, H = (int)m.hidden, I = (int)m.inter, heads = (int)m.heads, dh = H / heads;
+    const int H = (int)m.hidden, I = (int)m.inter, heads = (int)m.heads, dh = H / heads;
     const Dt dt = s.act;   // activations; the GEMMs take s.dt
     const bool f32 = dt == Dt::F32, i8 = s.dt == Dt::I8;
-    const size_t el = dt_bytes(dt), t0 = part.tok0;
-    const BinChoice &bc = s.kc.bin[bin_of(part.tokens, s.kc.bins)];
-    auto at = [&](void *base, size_t width, size_t bytes) -> void * {
-        return base ? static_cast<char *>(base) + t0 * width * bytes : nullptr;
-    };
-    float *x = s.x + t0 * H;
-    void *xh = at(s.xh, H, el), *y = at(s.y, H, dt_bytes(s.ydt));
+    const BinChoice &bc = s.kc.bin[bd.bin];
+    const Span sp = span_of(s.dims_dev, part), whole = span_of(s.dims_dev, -1);
+    const int T = (int)bd.part_tokens;   // the grids' rows
     auto run = [&](const char *name, hipError_t e) { check(e, name); };
 #define LAUNCH(NAME, CALL) \
     do {                   \
@@ -986,38 +1051,32 @@ static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) 
     // On the I8 tier the LayerNorms that make the QKV and FFN-in operands
     // write their int8 rows too (the codes quantize_rows would make of their
     // 16-bit output); the product that follows then skips its quantize.
+    const int qrow = std::max(H, I);
     QuantOut qo;
     if (i8) {
-        qo.q = s.aq + t0 * std::max(H, I);
-        qo.scale = s.ascale + t0;
+        qo.q = s.aq;
+        qo.scale = s.ascale;
+        qo.tok_stride = qrow;
     }
     bool aq_ready = false;
     auto mm = [&](uint32_t l, GemmSlot g) {
         LayerGemm lg = layer_gemm(s, l, g);
-        const void *A = static_cast<const char *>(lg.A) + t0 * lg.K * (lg.A == s.x ? 4 : el);
-        switch (g) {
-        case G_QKV: lg.e.tok0 = (int)t0; break;
-        case G_FFN1: lg.e.out = at(lg.e.out, I, el); break;
-        default: lg.e.out = y; break;
-        }
+        const void *A = lg.A;
+        int a_tok = 0;
         if (i8) {
-            int8_t *aq = s.aq + t0 * std::max(H, I);
             if (!(aq_ready && (g == G_QKV || g == G_FFN1)))
-                LAUNCH("quantize", quantize_rows(st, A, Dt::F16, T, lg.K, lg.K, aq, s.ascale + t0));
+                LAUNCH("quantize", quantize_span(st, sp, T, A, Dt::F16, lg.K, lg.K, s.aq, qrow, s.ascale));
             aq_ready = false;
-            lg.e.a_scale = s.ascale + t0;
+            lg.e.a_scale = s.ascale;
             lg.e.w_scale = lg.wscale;
-            A = aq;
+            A = s.aq;
+            a_tok = qrow;
         }
-        LAUNCH(NAMES[g], gemm(st, s.dt, T, lg.N, lg.K, A, lg.K, lg.W, lg.e, bc.tile[g]));
+        LAUNCH(NAMES[g], gemm(st, s.dt, sp, T, lg.N, lg.K, A, lg.K, a_tok, lg.W, lg.e, bc.tile[g]));
     };
-    Packing pk = s.pk;
-    pk.start += part.row0;
-    pk.len += part.row0;
-    const int32_t *mask = s.mask + (size_t)part.row0 * s.seq;
     // The GEMM operand copy of x after an add + LayerNorm: xh, or on the F32
     // tier x itself (post-norm) or xh as F32 (pre-norm).
-    void *norm_out = f32 && !m.modern ? nullptr : xh;
+    void *norm_out = f32 && !m.modern ? nullptr : s.xh;
     // Layers run: every one, or through the one read alone (a model cut
     // after it). Ranges are pooled after each of the last `reads` layers run
     // into block k of the output, [reads, count, output_dim], the final
@@ -1028,7 +1087,7 @@ static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) 
     // which is free between a layer's last add and the next layer's out product.
     const uint32_t nl = s.tap_alone ? m.layers + 1 - s.taps : m.layers;
     const uint32_t reads = s.tap_alone ? 1 : s.taps;
-    const int od = (int)s.output_dim, l2 = s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0;
+    const int od = (int)s.output_dim;
     for (uint32_t l = 0; l < nl; ++l) {
         const Model::Layer &L = m.ls[l];
         int window = INT32_MAX;
@@ -1038,21 +1097,21 @@ static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) 
         }
         mm(l, G_QKV);
         if (m.deberta)
-            LAUNCH("attention", deberta_attention(st, dt, s.qkv, (int)s.tcap, heads, dh, pk, mask, (int)s.seq,
-                                                  (int)part.rows, (int)part.max_len, L.pos_qk,
+            LAUNCH("attention", deberta_attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, sp,
+                                                  (int)bd.rows, (int)bd.max_len, L.pos_qk,
                                                   static_cast<const int32_t *>(m.rel_table.get()), (int)m.positions,
                                                   s.ctxb));
         else
-            LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, pk, mask, (int)s.seq, (int)part.rows,
-                                          (int)part.max_len, window, s.ctxb, bc.simple_attention));
+            LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, sp, (int)bd.rows,
+                                          (int)bd.max_len, window, s.ctxb, bc.simple_attention));
         mm(l, G_OUT);
         // Post-norm: x = LN1(x + y). Pre-norm: x += y, xh = LN_mlp(x).
         if (m.modern)
             LAUNCH("add_layer_norm",
-                   add_layer_norm(st, T, H, x, y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt, qo));
+                   add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt, qo));
         else
             LAUNCH("add_layer_norm",
-                   add_layer_norm(st, T, H, x, y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out, dt, qo));
+                   add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out, dt, qo));
         aq_ready = i8;
         mm(l, G_FFN1);
         mm(l, G_FFN2);
@@ -1061,34 +1120,40 @@ static void run_layers(Session &s, hipStream_t st, const Part &part, Timer &tm) 
         const QuantOut next = l + 1 < nl ? qo : QuantOut();
         if (!m.modern)
             LAUNCH("add_layer_norm",
-                   add_layer_norm(st, T, H, x, y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out, dt, next));
+                   add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out, dt, next));
         else if (l + 1 < nl)
-            LAUNCH("add_layer_norm",
-                   add_layer_norm(st, T, H, x, y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps, 1, norm_out, dt, next));
+            LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps,
+                                                    1, norm_out, dt, next));
         else
-            LAUNCH("add_layer_norm", add_layer_norm(st, T, H, x, y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
+            LAUNCH("add_layer_norm",
+                   add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
         aq_ready = i8 && l + 1 < nl;
         if (reads > 1 && l + 1 < nl && l + reads >= nl) {
             const float *src = s.x;
             if (m.modern) {
-                LAUNCH("layer_norm", layer_norm(st, T, H, s.x, m.final_w, nullptr, m.eps, (float *)s.y, nullptr, Dt::F32));
+                LAUNCH("layer_norm", layer_norm(st, whole, (int)bd.tokens, H, s.x, m.final_w, nullptr, m.eps,
+                                                (float *)s.y, nullptr, Dt::F32));
                 src = (const float *)s.y;
             }
             float *block = s.out + (size_t)(l + reads - nl) * s.count * od;
-            LAUNCH("pool", pool(st, src, H, s.pk, s.mask, (int)s.seq, (int)s.count, s.ranges, (int)s.pooling, od, l2,
-                                s.pool_scratch, block));
+            LAUNCH("pool", pool(st, s.dims_dev, (int)bd.items, src, H, s.pk, s.mask, s.ranges, s.pool_scratch, block));
         }
     }
 #undef LAUNCH
 }
 
-void encode(Session &s) {
+// A run's launches on the context's streams: the whole run's embedding,
+// each part's layers (forked onto the side streams and joined back), the
+// pooling. With `sequential`, every part on the first stream in turn (a
+// timed run: its events are on the first stream).
+static void encode(Session &s, const Bounds &bd, bool sequential) {
     Model &m = *s.model;
     Context &c = *s.ctx;
     hipStream_t st = c.stream;
-    const int T = (int)s.tokens, H = (int)m.hidden;
+    const int H = (int)m.hidden;
     const Dt dt = s.act;
     const bool f32 = dt == Dt::F32;
+    const Span whole = span_of(s.dims_dev, -1);
     Timer tm(s);
     auto run = [&](const char *name, hipError_t e) { check(e, name); };
 #define LAUNCH(NAME, CALL) \
@@ -1097,83 +1162,98 @@ void encode(Session &s) {
         run(NAME, CALL);   \
         tm.end();          \
     } while (0)
-    LAUNCH("pack_rows", pack_rows(st, s.mask, (int)s.batch, (int)s.seq, s.pk));
-    LAUNCH("embed_ln", embed_ln(st, T, H, s.ids, s.types, s.pk, (int)s.seq, (int)m.position_offset, m.word, m.pos,
-                                m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt,
+    LAUNCH("pack_rows", pack_rows(st, s.mask, s.dims_dev, (int)s.max_batch, s.pk));
+    LAUNCH("embed_ln", embed_ln(st, whole, (int)bd.tokens, H, s.ids, s.types, s.pk, (int)m.position_offset, m.word,
+                                m.pos, m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt,
                                 m.deberta ? s.mask : nullptr));
     // ModernBERT's first layer reads the embeddings' rows as they are (no
     // attention norm); on the F32 tier xh is the pre-norm rows' F32 copy.
-    if (m.modern && f32) LAUNCH("copy", copy_bytes(st, s.x, s.xh, (size_t)T * H * 4));
+    if (m.modern && f32) LAUNCH("copy", copy_rows(st, whole, (int)bd.tokens, s.x, s.xh, (size_t)H * 4));
     // A split run: the rows' parts run their layers on the context's
     // streams, forked here and joined before the pooling, so one part's
     // memory-bound and latency-bound launches overlap another's products.
-    // (Not while timing launches: their events are on the first stream.)
-    if (s.parts > 1 && !s.timing) {
+    if (bd.parts > 1 && !sequential) {
         check(hipEventRecord(c.fork, st), "forking the run");
-        for (uint32_t i = 1; i < s.parts; ++i) check(hipStreamWaitEvent(c.side[i - 1], c.fork, 0), "forking the run");
-        for (uint32_t i = 0; i < s.parts; ++i) {
-            const Part p{s.part_row[i], s.part_row[i + 1] - s.part_row[i], s.part_tok[i],
-                         s.part_tok[i + 1] - s.part_tok[i], s.part_len[i]};
-            run_layers(s, i == 0 ? st : c.side[i - 1], p, tm);
-        }
-        for (uint32_t i = 1; i < s.parts; ++i) {
+        for (uint32_t i = 1; i < bd.parts; ++i) check(hipStreamWaitEvent(c.side[i - 1], c.fork, 0), "forking the run");
+        for (uint32_t i = 0; i < bd.parts; ++i) run_layers(s, i == 0 ? st : c.side[i - 1], (int)i, bd, tm);
+        for (uint32_t i = 1; i < bd.parts; ++i) {
             check(hipEventRecord(c.join[i - 1], c.side[i - 1]), "joining the run");
             check(hipStreamWaitEvent(st, c.join[i - 1], 0), "joining the run");
         }
     } else {
-        run_layers(s, st, Part{0, s.batch, 0, s.tokens, s.max_len}, tm);
+        for (uint32_t i = 0; i < bd.parts; ++i) run_layers(s, st, (int)i, bd, tm);
     }
     const uint32_t reads = s.tap_alone ? 1 : s.taps;
-    const int od = (int)s.output_dim, l2 = s.normalize == TURBO_NORMALIZE_L2 ? 1 : 0;
-    const int n_out = s.count ? (int)s.count : (int)s.batch;
-    if (s.head)
-        LAUNCH("pool_head", pool_head(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.ranges, m.head_w, m.head_b,
-                                      (int)m.head_out, s.pool_scratch, s.out));
-    else
-        LAUNCH("pool", pool(st, s.x, H, s.pk, s.mask, (int)s.seq, n_out, s.count ? s.ranges : nullptr,
-                            (int)s.pooling, od, l2, s.pool_scratch, s.out + (size_t)(reads - 1) * s.count * od));
+    LAUNCH("pool", pool(st, s.dims_dev, (int)bd.items, s.x, H, s.pk, s.mask, s.ranges, s.pool_scratch,
+                        s.out + (size_t)(reads - 1) * s.count * s.output_dim, m.head_w, m.head_b, (int)m.head_out));
 #undef LAUNCH
 }
 
+// Captures bin b's graph: its launches with the bin's bounds and choices,
+// forked over the parts its runs may take.
+static void capture_bin(Session &s, int b) {
+    hipStream_t st = s.ctx->stream;
+    s.bin_parts[b] = parts_of_bin(s, b);
+    // Capture sees no rows: the run's options that change which kernels
+    // launch (layer reads) take no graph, so the capture is a plain run's.
+    const uint32_t taps = s.taps, count = s.count, od = s.output_dim;
+    const bool alone = s.tap_alone;
+    s.taps = 1;
+    s.tap_alone = false;
+    s.count = 0;
+    s.output_dim = s.model->hidden;
+    struct Restore {
+        Session &s;
+        uint32_t taps, count, od;
+        bool alone;
+        ~Restore() {
+            s.taps = taps;
+            s.tap_alone = alone;
+            s.count = count;
+            s.output_dim = od;
+        }
+    } restore{s, taps, count, od, alone};
+    check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capturing a bin's graph");
+    hipGraph_t g = nullptr;
+    try {
+        encode(s, bounds_of(s, b, s.bin_parts[b]), false);
+    } catch (...) {
+        (void)hipStreamEndCapture(st, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    check(hipStreamEndCapture(st, &g), "capturing a bin's graph");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    check(e, "instantiating a bin's graph");
+    s.graph[b] = exec;
+    ++s.captures;
+}
+
+void capture_graphs(Session &s) {
+    if (!s.graphs) return;
+    for (int b = 0; b < s.kc.bins; ++b) capture_bin(s, b);
+}
+
 void launch_run(Session &s) {
-    if (s.timing || !s.graphs) {
-        encode(s);
-        return;
-    }
-    Session::RunShape key{s.tokens, s.batch, s.seq,  s.max_len, s.count,     s.pooling,
-                          s.normalize, s.output_dim, s.head, s.taps, s.tap_alone, s.parts};
-    for (uint32_t i = 0; i < s.parts; ++i) {
-        key[12 + 3 * i] = s.part_row[i];
-        key[13 + 3 * i] = s.part_tok[i];
-        key[14 + 3 * i] = s.part_len[i];
-    }
-    auto it = s.graph_of.find(key);
-    if (it == s.graph_of.end()) {
-        constexpr size_t KEEP = 16;
-        if (s.graph_of.size() >= KEEP) {
-            (void)hipGraphExecDestroy(s.graph_of[s.graph_order.front()]);
-            s.graph_of.erase(s.graph_order.front());
-            s.graph_order.erase(s.graph_order.begin());
+    const int b = bin_of(s.tokens, s.kc.bins);
+    if (s.graphs && !s.timing && s.taps == 1 && !s.tap_alone && s.graph[b]) {
+        // The written parts fit the bin's graph by the split rule; checked
+        // anyway (a graph past its bounds would drop tokens), and a run that
+        // did not fit would launch its kernels directly.
+        const Bounds gb = bounds_of(s, b, s.bin_parts[b]);
+        bool fits = s.parts <= gb.parts;
+        for (uint32_t i = 0; i < s.parts; ++i)
+            fits = fits && s.part_tok[i + 1] - s.part_tok[i] <= gb.part_tokens && s.part_len[i] <= gb.max_len &&
+                   s.part_row[i + 1] - s.part_row[i] <= gb.rows;
+        if (fits) {
+            check(hipGraphLaunch(s.graph[b], s.ctx->stream), "launching the run's graph");
+            ++s.graph_launches;
+            return;
         }
-        hipStream_t st = s.ctx->stream;
-        check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capturing the run");
-        hipGraph_t g = nullptr;
-        try {
-            encode(s);
-        } catch (...) {
-            (void)hipStreamEndCapture(st, &g);
-            if (g) (void)hipGraphDestroy(g);
-            throw;
-        }
-        check(hipStreamEndCapture(st, &g), "capturing the run");
-        hipGraphExec_t exec = nullptr;
-        const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(g);
-        check(e, "instantiating the run's graph");
-        it = s.graph_of.emplace(key, exec).first;
-        s.graph_order.push_back(key);
     }
-    check(hipGraphLaunch(it->second, s.ctx->stream), "launching the run's graph");
+    encode(s, bounds_of(s, b, s.parts), s.timing);
 }
 
 // The tuner: each bin's four products timed at the bin's token count with
@@ -1225,7 +1305,8 @@ bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
     bool any = false;
     char line[160];
     for (int b = s.kc.bins - 1; b >= 0; --b) {
-        const int M = (int)bin_tokens(b, tcap);
+        // The rows a launch of the bin takes at most: the bin's, or a part's.
+        const int M = (int)bounds_of(s, b, parts_of_bin(s, b)).part_tokens;
         BinChoice &bc = s.kc.bin[b];
         for (int g = 0; g < G_COUNT; ++g) {
             if (bc.tile_forced[g]) continue;
@@ -1279,27 +1360,10 @@ bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
     return any;
 }
 
-// After a synchronized run: each kernel's milliseconds, summed by name.
-void collect_times(Session &s) {
-    if (!s.timing) return;
-    std::map<std::string, std::pair<double, uint32_t>> by;
-    std::vector<std::string> order;
-    for (size_t i = 0; i + 1 < s.ev_used; i += 2) {
-        float ms = 0;
-        (void)hipEventElapsedTime(&ms, s.ev[i], s.ev[i + 1]);
-        const std::string &n = s.ev_name[i / 2];
-        if (!by.count(n)) order.push_back(n);
-        by[n].first += ms;
-        by[n].second += 1;
-    }
-    s.last_times.clear();
-    for (auto &n : order) s.last_times.push_back({n, by[n].first, by[n].second});
-}
-
 void session_run(Session *s, turbo_backend_run *out) {
     if (!s->written) fail(TURBO_E_INVALID_STATE, "rocm: the session has no rows written since its last run");
     s->written = false;
-    const uint64_t dev0 = device_allocs.load();
+    const uint64_t dev0 = device_allocs.load(), host0 = host_allocs_on_thread();
     {
         std::lock_guard<std::mutex> g(s->ctx->lock);
         OnDevice on(s->ctx->ordinal);
@@ -1310,7 +1374,6 @@ void session_run(Session *s, turbo_backend_run *out) {
             throw;
         }
         check(hipStreamSynchronize(s->ctx->stream), "the run");
-        collect_times(*s);
     }
     const uint32_t n_out = s->count ? s->count * (s->tap_alone ? 1 : s->taps) : s->batch;
     s->output.bytes = (uint64_t)n_out * s->output_dim * 4;
@@ -1319,7 +1382,7 @@ void session_run(Session *s, turbo_backend_run *out) {
     out->host = nullptr;
     out->h2d_bytes = s->h2d;
     out->d2h_bytes = 0;
-    out->host_allocs = 0;
+    out->host_allocs = host_allocs_on_thread() - host0;
     out->device_allocs = device_allocs.load() - dev0;
     uint32_t *st = out->stage;
     st[TURBO_EMBED_STAGE_UPLOAD] = TURBO_STAGE_DEVICE;
@@ -1379,9 +1442,10 @@ int32_t turbo_rocm_session_timing(void *session, uint32_t on_, turbo_error *err)
         Session *s = static_cast<Session *>(session);
         OnDevice on(s->ctx->ordinal);
         if (on_ && s->ev.empty()) {
-            s->ev.resize(2 * (16 + 16 * s->model->layers));
+            counted_host_alloc();
+            s->ev.resize(2 * (16 + 16 * s->model->layers * Session::MAX_PARTS));
             for (auto &e : s->ev) check(hipEventCreate(&e), "hipEventCreate");
-            s->ev_name.resize(s->ev.size() / 2);
+            s->ev_name.assign(s->ev.size() / 2, nullptr);
         }
         s->timing = on_ != 0;
         return TURBO_OK;
@@ -1391,10 +1455,23 @@ int32_t turbo_rocm_session_timing(void *session, uint32_t on_, turbo_error *err)
 int32_t turbo_rocm_session_times(void *session, char *out, uint32_t len, turbo_error *err) {
     return guarded(err, [&] {
         Session *s = static_cast<Session *>(session);
+        // The last timed run's events (it has synchronized), summed by
+        // kernel name in first-launch order.
+        std::vector<std::string> order;
+        std::map<std::string, std::pair<double, uint32_t>> by;
+        OnDevice on(s->ctx->ordinal);
+        for (size_t i = 0; s->timing && i + 1 < s->ev_used; i += 2) {
+            float ms = 0;
+            (void)hipEventElapsedTime(&ms, s->ev[i], s->ev[i + 1]);
+            const std::string n = s->ev_name[i / 2];
+            if (!by.count(n)) order.push_back(n);
+            by[n].first += ms;
+            by[n].second += 1;
+        }
         std::string t;
-        for (auto &p : s->last_times) {
+        for (auto &n : order) {
             char line[128];
-            std::snprintf(line, sizeof line, "%s %.6f %u\n", p.name.c_str(), p.ms, p.launches);
+            std::snprintf(line, sizeof line, "%s %.6f %u\n", n.c_str(), by[n].first, by[n].second);
             t += line;
         }
         if (len) std::snprintf(out, len, "%s", t.c_str());
@@ -1410,7 +1487,15 @@ int32_t turbo_rocm_session_replay(void *session, uint32_t runs, turbo_error *err
         OnDevice on(s->ctx->ordinal);
         for (uint32_t i = 0; i < runs; ++i) launch_run(*s);
         check(hipStreamSynchronize(s->ctx->stream), "replay");
-        collect_times(*s);
+        return TURBO_OK;
+    });
+}
+
+int32_t turbo_rocm_session_graphs(void *session, uint64_t *captured, uint64_t *launched, turbo_error *err) {
+    return guarded(err, [&] {
+        Session *s = static_cast<Session *>(session);
+        *captured = s->captures;
+        *launched = s->graph_launches;
         return TURBO_OK;
     });
 }

@@ -34,7 +34,12 @@ void *dev_alloc(size_t bytes, const char *what);
 const std::vector<int> &devices();
 
 extern std::atomic<uint64_t> device_allocs;
+// The backend's own heap allocations (its handles and host buffers), on
+// every thread and on the calling thread: a run reports the change of the
+// calling thread's count across it (reference core/cuda/backend.cpp:150-175).
 extern std::atomic<uint64_t> host_allocs;
+void counted_host_alloc();
+uint64_t host_allocs_on_thread();
 
 // Every entry point: a status, the caller's turbo_error filled, nothing
 // thrown across the boundary (reference include/turbo/turbo_backend.h:10-12).
@@ -173,37 +178,33 @@ struct Session {
     // [part_row[i], part_row[i + 1]), tokens [part_tok[i], part_tok[i + 1]),
     // its longest row part_len[i]. TURBO_ROCM_SPLIT=n asks for n parts (0 or
     // 1: none).
-    static constexpr int MAX_PARTS = 4;
+    static constexpr int MAX_PARTS = rocm::MAX_PARTS;
     uint32_t split_parts = MAX_PARTS;
     uint32_t parts = 1, part_row[MAX_PARTS + 1] = {}, part_tok[MAX_PARTS + 1] = {}, part_len[MAX_PARTS] = {};
     uint64_t h2d = 0;
+    // The run's dimensions: staged with the rows (pinned) and on the device,
+    // where every kernel of a run reads them.
+    RunDims *dims_host = nullptr, *dims_dev = nullptr;
+    std::vector<uint32_t> row_lens;   // the write's row lengths (host, sized at open)
     std::vector<LayerWeights> *w = nullptr;
     Choices kc;            // kernel choices per bin of packed tokens
     std::string choices;   // kc as a choices string
-    // A run's launches captured as a graph, per run shape (tokens, rows,
-    // columns, longest row, ranges, pooling, normalize, output width, head,
-    // layer reads): a run
-    // of a shape seen before is one graph launch. Off while timing, or with
+    // One graph per bin of packed tokens, captured at session_open with the
+    // bin's kernel choices and grids sized for its largest run, and replayed
+    // for every run of that bin whatever its rows (the kernels read the run's
+    // extent from dims_dev). Runs that read layers before the last, and runs
+    // timed launch by launch, launch their kernels directly. Off with
     // TURBO_ROCM_GRAPHS=0.
-    // tokens, batch, seq, max_len, count, pooling, normalize, output_dim,
-    // head, taps, tap_alone, parts, then each part's first row, first token
-    // and longest row.
-    using RunShape = std::array<uint32_t, 12 + 3 * MAX_PARTS>;
     bool graphs = true;
-    std::map<RunShape, hipGraphExec_t> graph_of;
-    std::vector<RunShape> graph_order;   // oldest first, for eviction
+    hipGraphExec_t graph[BINS] = {};
+    uint32_t bin_parts[BINS] = {};   // parts a bin's graph runs (its runs use as many or fewer)
+    uint64_t captures = 0, graph_launches = 0;   // counted for the graphs hook
     // Per-launch timing (a test and benchmark hook): events around each
     // kernel of a run, by name.
     bool timing = false;
     std::vector<hipEvent_t> ev;
-    std::vector<std::string> ev_name;
+    std::vector<const char *> ev_name;
     size_t ev_used = 0;
-    struct Timed {
-        std::string name;
-        double ms;
-        uint32_t launches;
-    };
-    std::vector<Timed> last_times;
 };
 
 Model *model_load(Context *c, const turbo_backend_model *desc);
@@ -215,8 +216,10 @@ void session_run(Session *s, turbo_backend_run *out);
 // Times the session's candidate kernels within budget_ms and keeps the
 // fastest in s.kc; timing lines into *timings. Whether anything was timed.
 bool tune(Session &s, uint32_t budget_ms, std::string *timings);
-// One run's launches on the session's stream: replayed from its graph when
-// the shape was captured before, else captured (or launched directly).
+// One run's launches on the session's stream: its bin's graph, or the
+// kernels launched directly.
 void launch_run(Session &s);
+// Captures each bin's graph (with TURBO_ROCM_GRAPHS not 0).
+void capture_graphs(Session &s);
 
 }  // namespace rocm
