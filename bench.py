@@ -51,9 +51,9 @@ def tail_bytes(shape, dtype, tokens, rows, od):
     run, by the timing hook's names: each operand read once and each result
     written once (a table row once per token that reads it).
 
-    embed_ln per token: the word row (and, off the rotary families, the
-    position and type rows) in F32, the ids, x written in F32 and its
-    16-bit operand copy. add_layer_norm per token: x and the product y read,
+    embed_ln per token: the word row in F32, the ids (and types), x written
+    in F32 and its 16-bit operand copy; off the rotary families the position
+    and type rows once a run (they stay in L2). add_layer_norm per token: x and the product y read,
     x written, and the normalized operand copy (16-bit, or F32 on a
     pre-norm F32 session) except on post-norm F32 sessions and after a
     pre-norm model's last layer. pool: each pooled token's F32 row (one per
@@ -62,8 +62,12 @@ def tail_bytes(shape, dtype, tokens, rows, od):
     modern = shape.family == S.TURBO_FAMILY_MODERNBERT
     act = 4 if dtype == "f32" else 2
     ysz = 2 if dtype == "f16" and shape.rope is None else 4
-    tables, ids = (1, 4) if shape.rope is not None else (3, 8)
-    out = {"embed_ln": tokens * (tables * 4 * H + ids + 4 * H + (0 if dtype == "f32" else act * H))}
+    # The word row comes from HBM once a token; the position and type rows
+    # are few and stay in L2 (counted once a run).
+    rotary = shape.rope is not None
+    ids = 4 if rotary else 8
+    shared = 0 if rotary else (min(shape.seq, shape.positions) + shape.token_types) * 4 * H
+    out = {"embed_ln": tokens * (4 * H + ids + 4 * H + (0 if dtype == "f32" else act * H)) + shared}
     L = shape.layers
     if modern:
         out["add_layer_norm"] = tokens * ((2 * L - 1) * (8 * H + ysz * H + act * H) + (8 * H + ysz * H))
@@ -207,6 +211,29 @@ def main():
     tokens = int(lens.sum())
     seq_per_s = shape.batch / (ms / 1e3)
 
+    # The same rows written, run and read back each step (the reference's
+    # p50 measures this, bench/src/measure/mod.rs:292-321): PCIe both ways
+    # included, beside the device-resident figure.
+    def write_run_read(batches, steps):
+        for b in batches[:2]:
+            put(*b)
+            sess.run()
+            sess.read()
+        w0 = time.perf_counter()
+        for i in range(steps):
+            put(*batches[i % len(batches)])
+            sess.run()
+            sess.read()
+        return (time.perf_counter() - w0) / steps * 1e3
+
+    def put(i, m, t):
+        if rngs:
+            sess.write_ranges(i, m, rngs, t, normalize=shape.normalize)
+        else:
+            sess.write_tokens(i, m, t, pooling=shape.pooling, normalize=shape.normalize)
+
+    wrr_ms = write_run_read([(ids, mask, types)], args.steps)
+
     # Per-kernel times from HIP events on the session's stream, one run.
     sess.set_timing(True)
     sess.replay(1)
@@ -217,15 +244,14 @@ def main():
     gemm_names = [k for k in times if k.startswith("gemm_")]
     gemm_ms = sum(times[k] for k in gemm_names)
     gemm_flops = sum(per[k] for k in gemm_names) * shape.layers
-    launches = {k: shape.layers for k in per}
     total_flops = W.gemm_flops_per_token(shape) * tokens + W.attention_flops(shape, lens)
     # The dominant kernel: the GEMM kernel (every linear layer's launches),
     # or attention when it takes longer.
     if times.get("attention", 0.0) > gemm_ms:
         dom, dom_ms, dom_flops, dom_launches = "attention", times["attention"], per["attention"] * shape.layers, \
-            launches["attention"]
+            counts["attention"]
     else:
-        dom, dom_ms, dom_flops, dom_launches = "gemm", gemm_ms, gemm_flops, len(gemm_names) * shape.layers
+        dom, dom_ms, dom_flops, dom_launches = "gemm", gemm_ms, gemm_flops, sum(counts[k] for k in gemm_names)
     achieved = dom_flops / (dom_ms / 1e3)
     traffic = None
     if dom == "gemm" and os.path.exists(traffic_file(args.workload)):
@@ -258,8 +284,11 @@ def main():
                        "bytes_per_launch": b / counts[k], "achieved_GBps": gbps, "frac": gbps * 1e9 / HBM_PEAK}
 
     # The same session on variable-length rows under the mask (the second
-    # run of the workload), timed the same way.
-    extra_runs = {}
+    # run of the workload): one batch replayed on the device, then a fresh
+    # batch every step written, run and read back (each replays its bin's
+    # graph; none is captured in the run).
+    extra_runs = {"write_run_read": {"ms_per_step": wrr_ms, "sequences_per_s": shape.batch / (wrr_ms / 1e3),
+                                     "note": "the headline rows written, run and read back each step"}}
     also = ("64,512" if args.workload == "bert-base" else "") if args.also_lengths == "auto" else args.also_lengths
     if also and not rngs:
         lo, hi = (int(v) for v in also.split(","))
@@ -271,9 +300,18 @@ def main():
         vms = (time.perf_counter() - v0) / args.steps * 1e3
         vt = int(vmask.sum())
         vflops = W.gemm_flops_per_token(shape) * vt + W.attention_flops(shape, vmask.sum(1))
+        fresh = [W.rows(shape, lengths=(lo, hi), seed=100 + k) for k in range(args.steps)]
+        c0, _ = sess.graphs()
+        fms = write_run_read(fresh, args.steps)
+        c1, _ = sess.graphs()
+        ft = sum(int(b[1].sum()) for b in fresh) / len(fresh)
         extra_runs[f"lengths_{lo}_{hi}"] = {"ms_per_step": vms, "sequences_per_s": shape.batch / (vms / 1e3),
                                             "tokens_per_s": vt / (vms / 1e3), "live_tokens": vt,
-                                            "mfma_util_pct": 100.0 * vflops / (vms / 1e3) / PEAK[dtype]}
+                                            "mfma_util_pct": 100.0 * vflops / (vms / 1e3) / PEAK[dtype],
+                                            "fresh_write_run_read": {
+                                                "ms_per_step": fms, "sequences_per_s": shape.batch / (fms / 1e3),
+                                                "tokens_per_s": ft / (fms / 1e3), "batches": len(fresh),
+                                                "captures_during_runs": c1 - c0}}
 
     cpu = None
     min_cos = None
@@ -281,12 +319,18 @@ def main():
         import oracle
         # A bounded sample (about 10-30 s of CPU work): 4 rows, or on rows
         # over 1024 tokens the batch's shortest row; its ranges with it.
-        n = args.cpu_rows or (1 if shape.seq > 1024 else 4)
+        n = args.cpu_rows or (1 if shape.seq > 1024 else 8)
         n = min(n, shape.batch)
         pick = np.argsort(lens, kind="stable")[:n] if shape.seq > 1024 else np.arange(n)
-        threads = min(16, os.cpu_count() or 1)
-        print(f"# timed; CPU baseline on rows {pick.tolist()} ({int(lens[pick].sum())} tokens) on {threads} threads",
-              file=sys.stderr, flush=True)
+        # Every core this process may run on, one pinned thread each.
+        threads = len(os.sched_getaffinity(0))
+        oracle.set_pinning(True)
+        model_name = oracle.cpu_model()
+        print(f"# timed; CPU baseline on rows {pick.tolist()} ({int(lens[pick].sum())} tokens) on {threads} threads "
+              f"({model_name})", file=sys.stderr, flush=True)
+        # A one-row pass first: pages the code and the model's tables in.
+        oracle.encode(desc, ids[pick[:1]], mask[pick[:1]], types[pick[:1]], pooling=shape.pooling,
+                      normalize=shape.normalize, threads=threads)
         sample_ranges, got_idx = None, pick
         if rngs:
             where = {int(r): i for i, r in enumerate(pick)}
@@ -300,10 +344,14 @@ def main():
         cos = (got * want).sum(1) / np.linalg.norm(got, axis=1) / np.linalg.norm(want, axis=1)
         min_cos = float(cos.min())
         what = f", {len(sample_ranges)} ranges" if sample_ranges else ""
+        oracle.set_pinning(False)
         cpu = {"value": n / cpu_s, "unit": "sequences/s", "cores": threads, "kind": "port",
+               "cpu_model": model_name,
                "sample": f"{n} of the {shape.batch} rows ({int(lens[pick].sum())} tokens{what}), all {shape.layers} "
-                         f"layers, one pass, {cpu_s:.1f} s on {threads} threads"}
+                         f"layers, one pass after a one-row warm-up, {cpu_s:.1f} s on {threads} pinned threads "
+                         f"({model_name})"}
 
+    eff_lengths = shape.lengths if lengths == "default" else lengths
     line = {
         "metric": f"sequences/s ({args.workload}, {dtype}, {shape.batch}x{shape.seq})",
         "value": seq_per_s, "unit": "sequences/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -314,7 +362,7 @@ def main():
                                (f"{shape.batch} query/passage pairs, query {shape.extra['query']} and passage "
                                 f"{shape.extra['passage']} tokens, one [CLS] q [SEP] p [SEP] window each"
                                 if shape.task == S.TURBO_TASK_RERANK else
-                                f"{'all live' if lengths is None else 'lengths ' + str(shape.lengths if lengths == 'default' else lengths)}"),
+                                ("all live" if eff_lengths is None else f"lengths uniform in {list(eff_lengths)}")),
                    "global_batch": shape.batch, "seq_len": shape.seq, "live_tokens": tokens, "parallelism": "none"},
         "tokens_per_s": tokens / (ms / 1e3),
         "mfma_util_pct": 100.0 * total_flops / (ms / 1e3) / PEAK[dtype],

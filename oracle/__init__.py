@@ -48,6 +48,8 @@ def lib():
         _lib.oracle_deberta_bucket.restype = C.c_uint32
         _lib.oracle_set_gated_limit.argtypes = [C.c_float]
         _lib.oracle_set_gated_limit.restype = None
+        _lib.oracle_set_pinning.argtypes = [C.c_int32]
+        _lib.oracle_set_pinning.restype = None
     return _lib
 
 
@@ -291,3 +293,20 @@ def rerank_fixture():
     ref = dict(first_ids=t["case.first_ids"], first_types=t["case.first_types"],
                first_lengths=t["case.first_lengths"], scores=t["case.scores"])
     return desc, pairs, head, info, ref
+
+
+def set_pinning(on):
+    """Worker threads pin themselves to this process's CPUs, one each."""
+    lib().oracle_set_pinning(1 if on else 0)
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None

@@ -28,6 +28,9 @@
 #include <stdexcept>
 #include <string>
 #include <thread>
+
+#include <pthread.h>
+#include <sched.h>
 #include <vector>
 
 namespace {
@@ -174,6 +177,26 @@ uint32_t deberta_bucket(int64_t distance, uint32_t buckets, uint32_t maximum) {
 
 // ---- Threads ----------------------------------------------------------------
 
+// Whether worker threads pin themselves, thread i to the i-th CPU this
+// process may run on (a timing baseline's threads then do not migrate).
+std::atomic<int> pin_threads{0};
+
+void pin_to(uint32_t i) {
+    cpu_set_t allowed;
+    if (sched_getaffinity(0, sizeof allowed, &allowed) != 0) return;
+    const int n = CPU_COUNT(&allowed);
+    if (n <= 0) return;
+    int want = (int)(i % (uint32_t)n);
+    for (int c = 0; c < CPU_SETSIZE; ++c)
+        if (CPU_ISSET(c, &allowed) && want-- == 0) {
+            cpu_set_t one;
+            CPU_ZERO(&one);
+            CPU_SET(c, &one);
+            (void)pthread_setaffinity_np(pthread_self(), sizeof one, &one);
+            return;
+        }
+}
+
 // Runs fn(task) for task in [0, tasks) on `threads` threads. A task computes
 // each of its outputs whole, so the bits never depend on the thread count.
 void parallel(uint32_t threads, size_t tasks, const std::function<void(size_t)> &fn) {
@@ -186,8 +209,10 @@ void parallel(uint32_t threads, size_t tasks, const std::function<void(size_t)> 
     std::atomic<size_t> next{0};
     std::vector<std::thread> pool;
     pool.reserve(n);
+    const bool pin = pin_threads.load() != 0;
     for (uint32_t i = 0; i < n; ++i)
-        pool.emplace_back([&] {
+        pool.emplace_back([&, i] {
+            if (pin) pin_to(i);
             for (size_t t; (t = next.fetch_add(1)) < tasks;) fn(t);
         });
     for (auto &th : pool) th.join();
@@ -958,6 +983,7 @@ uint32_t oracle_pack(const int32_t *mask, uint32_t batch, uint32_t seq, uint32_t
 
 float oracle_exp(float x) { return cephes_exp(x); }
 void oracle_set_gated_limit(float limit) { gated_limit.store(limit); }
+void oracle_set_pinning(int32_t on) { pin_threads.store(on ? 1 : 0); }
 uint32_t oracle_deberta_bucket(int64_t distance, uint32_t buckets, uint32_t maximum) {
     return deberta_bucket(distance, buckets, maximum);
 }

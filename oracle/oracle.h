@@ -52,6 +52,9 @@ float oracle_exp(float x);
  * default, the CPU path's F32): an F16 tier stores that product saturated at
  * 65504, and is checked against the oracle with this limit set. */
 void  oracle_set_gated_limit(float limit);
+/* Worker threads pin themselves to the process's CPUs, one each (for a
+ * timed CPU baseline), when on is not 0. */
+void  oracle_set_pinning(int32_t on);
 /* DeBERTa-v2's relative row of a signed distance (core/src/deberta/math.rs:30-40). */
 uint32_t oracle_deberta_bucket(int64_t distance, uint32_t buckets, uint32_t maximum);
 float oracle_gelu(float x);

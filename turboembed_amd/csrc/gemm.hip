@@ -802,8 +802,6 @@ gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int l
     static_assert(WAVES * PASS * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <= STAGES * TILE,
                   "epilogue staging fits the stages");
     const int mw = m0 + wm * (BM / WM), nw = n0 + wn * (BN / WN);
-    EpiCols<TN, PASS, sizeof(T) == 1> cols;
-    load_cols<KIND>(cols, e, N, nw);
 
     acc_t acc[TM][TN];
 #pragma unroll
@@ -824,11 +822,20 @@ gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int l
 #pragma unroll
     for (int j = 0; j < TN; ++j) off_b[j] = BM * ROWB + (rb + j * 32) * ROWB;
     const int sw_a = swz_of<ROWB>(ra), sw_b = swz_of<ROWB>(rb);   // rows 32 apart share the swizzle
-    frag fa[2][TM], fb[2][TN];
+    // The fragments: both operands double-buffered (the next k-step's read
+    // while this one's products run), or, when the accumulators leave too few
+    // registers for that, A's held once and each of its rows read again for
+    // the next k-step as soon as this step's products of that row are out.
+    constexpr bool SINGLE_A = TM * TN * 16 + 2 * (TM + TN) * 4 > 216;
+    frag fa[SINGLE_A ? 1 : 2][TM], fb[2][TN];
+    auto fetch_a = [&](const char *base, int s, int set, int i) {
+        fa[set][i] = *(const frag *)(base + off_a[i] + 16 * ((2 * s + h) ^ sw_a));
+    };
     auto fetch = [&](const char *base, int s, int set) {
         const int c = 2 * s + h;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa[set][i] = *(const frag *)(base + off_a[i] + 16 * (c ^ sw_a));
+        for (int i = 0; i < TM; ++i)
+            if (!SINGLE_A || set == 0) fetch_a(base, s, SINGLE_A ? 0 : set, i);
 #pragma unroll
         for (int j = 0; j < TN; ++j) fb[set][j] = *(const frag *)(base + off_b[j] + 16 * (c ^ sw_b));
     };
@@ -848,16 +855,36 @@ gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int l
         fetch(base, 0, 0);
 #pragma unroll
         for (int s = 0; s < ROWB / 32; ++s) {
-            if (s + 1 < ROWB / 32) fetch(base, s + 1, (s + 1) & 1);
-            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (SINGLE_A) {
+                if (s + 1 < ROWB / 32) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                    for (int j = 0; j < TN; ++j)
+                        fb[(s + 1) & 1][j] = *(const frag *)(base + off_b[j] + 16 * ((2 * (s + 1) + h) ^ sw_b));
+                }
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int j = 0; j < TN; ++j) acc[i][j] = Mma<T>::run(fa[s & 1][i], fb[s & 1][j], acc[i][j]);
-            __builtin_amdgcn_sched_barrier(0);
+                for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) acc[i][j] = Mma<T>::run(fa[0][i], fb[s & 1][j], acc[i][j]);
+                    if (s + 1 < ROWB / 32) fetch_a(base, s + 1, 0, i);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                if (s + 1 < ROWB / 32) fetch(base, s + 1, (s + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) acc[i][j] = Mma<T>::run(fa[s & 1][i], fb[s & 1][j], acc[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
 
+    // The epilogue's per-column constants, read now (not held through the
+    // main loop) and before the first store, so no store waits behind them.
+    EpiCols<TN, PASS, sizeof(T) == 1> cols;
+    load_cols<KIND>(cols, e, N, nw);
     // Every wave is done with the stages: their LDS becomes each wave's
     // staging area for the stores (and, for int8 operands, for its rows'
     // activation scales, read before the first store).
@@ -905,7 +932,7 @@ static hipError_t launch_lds(hipStream_t s, const GemmRows &gr, int M, int N, in
     return hipErrorInvalidValue;
 }
 
-int gemm_tiles() { return 14; }
+int gemm_tiles() { return 15; }
 
 // The block shape made to fail to launch, as on a device that cannot take
 // it (a test hook; -1 for none): an explicit launch of it fails, the rule
@@ -929,14 +956,15 @@ bool gemm_made_to_fail(int tile) {
 // Names of the block shapes, as a choices string spells them: output tile,
 // then what sets it apart (r: operands staged through registers; k32: 32
 // columns of k a stage; s<n>: n stages).
-static const char *const TILE_NAME[15] = {"auto",      "r128x128",   "r256x128",   "r64x128",    "256x128",
+static const char *const TILE_NAME[16] = {"auto",      "r128x128",   "r256x128",   "r64x128",    "256x128",
                                           "128x128",   "128x256",    "256x256",    "128x128s2",  "256x128k32",
-                                          "128x256k32", "256x128k32s3", "256x256k32", "256x192",    "r64x64"};
+                                          "128x256k32", "256x128k32s3", "256x256k32", "256x192",    "r64x64",
+                                          "256x384"};
 
-const char *gemm_tile_name(int tile) { return tile >= 0 && tile <= 14 ? TILE_NAME[tile] : "?"; }
+const char *gemm_tile_name(int tile) { return tile >= 0 && tile <= 15 ? TILE_NAME[tile] : "?"; }
 
 int gemm_tile_by_name(const char *s, size_t n) {
-    for (int t = 0; t <= 14; ++t)
+    for (int t = 0; t <= 15; ++t)
         if (std::strlen(TILE_NAME[t]) == n && std::strncmp(TILE_NAME[t], s, n) == 0) return t;
     // A bare number names a tile too.
     int v = 0;
@@ -945,7 +973,7 @@ int gemm_tile_by_name(const char *s, size_t n) {
         if (s[i] < '0' || s[i] > '9') return -1;
         v = v * 10 + (s[i] - '0');
     }
-    return v <= 14 ? v : -1;
+    return v <= 15 ? v : -1;
 }
 
 // The tiles worth timing for a product of this type and shape: every
@@ -970,6 +998,7 @@ int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap) 
     }
     add(7);
     if (!qkv || e.hidden % 96 == 0) add(13);
+    if (!qkv || e.hidden % 96 == 0) add(15);
     add(4);
     add(6);
     add(5);
@@ -1027,9 +1056,9 @@ static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K,
     }
     if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
     // A pipelined shape asked of an operand it cannot take runs the staged kernel.
-    if (tile >= 4 && tile <= 13 && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
+    if (((tile >= 4 && tile <= 13) || tile == 15) && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
     // 96-column wave tiles need Q, K and V to start on their boundaries.
-    if (tile == 13 && (e.kind == Epi::Qkv || e.kind == Epi::QkvRope) && e.hidden % 96 != 0) tile = 7;
+    if ((tile == 13 || tile == 15) && (e.kind == Epi::Qkv || e.kind == Epi::QkvRope) && e.hidden % 96 != 0) tile = 7;
     switch (tile) {
     case 1: return launch<T, 128, 128, BK>(s, gr, M, N, K, A, lda, W, e);
     case 2: return launch<T, 256, 128, BK>(s, gr, M, N, K, A, lda, W, e);
@@ -1051,6 +1080,9 @@ static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K,
         case 12: return launch_lds<T, 256, 256, 2, 4, 3, 32, 1>(s, gr, M, N, K, A, lda, W, e);
         // 8 waves as 4 x 2 of 64 x 96: N = 768, 2304 and 3072 in whole rounds of tiles.
         case 13: return launch_lds<T, 256, 192, 4, 2, 2>(s, gr, M, N, K, A, lda, W, e);
+        // 8 waves as 2 x 4 of 128 x 96: a third less LDS reading per product than
+        // 128 x 64 waves, and N = 768, 2304 and 3072 in whole rounds at 32768 rows.
+        case 15: return launch_lds<T, 256, 384, 2, 4, 2>(s, gr, M, N, K, A, lda, W, e);
         }
     }
     return hipErrorInvalidValue;
