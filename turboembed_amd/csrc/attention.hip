@@ -218,11 +218,17 @@ template <int N> __device__ __forceinline__ void att_wait_vmcnt() {
 // exactly 0 (the session zeroes Q, K and V once, so every value read is
 // finite). Each block's live keys are a 64-bit mask, the same for the whole
 // workgroup.
-template <typename T, int D>
-__global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads, Span sp,
-                                                             int nqb, Packing p, const int32_t *__restrict__ mask,
-                                                             int window, T *__restrict__ ctx) {
-    constexpr int WQ = 64, QB = 4 * WQ, KB = 64, STAGES = 3;
+template <typename T, int D, int QT>
+__global__ void __launch_bounds__(64 * (256 / (32 * QT))) attention_mfma_kernel(const T *__restrict__ qkv, int tcap,
+                                                                               int heads, Span sp, int nqb, Packing p,
+                                                                               const int32_t *__restrict__ mask,
+                                                                               int window, T *__restrict__ ctx) {
+    // QT query tiles of 32 a wave, WAVES waves over a block of QB = 256 queries.
+    constexpr int WQ = 32 * QT, QB = 256, WAVES = QB / WQ, KB = 64, STAGES = 3;
+    // Each block's K and V^T take 8 load instructions each (8 rows of 128
+    // bytes an instruction), shared among the waves.
+    constexpr int LPW = 8 / WAVES;
+    static_assert(LPW * WAVES == 8, "the waves share a block's loads evenly");
     constexpr int KBYTES = KB * D * 2, VBYTES = D * KB * 2, SBYTES = KBYTES + VBYTES;
     constexpr int KROW = D * 2;   // bytes of one K row
     typedef typename AttnMma<T>::frag frag;
@@ -257,9 +263,9 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
     const int32_t *mk = mask + (size_t)r * seq;
     const bool wave_live = qw < len;   // a wave past the row's end loads and syncs but computes nothing
 
-    frag qf[2][D / 16];
+    frag qf[QT][D / 16];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const T *qrow = Q + (size_t)min(qw + 32 * qt + ql, len - 1) * D + h * 8;
 #pragma unroll
         for (int s = 0; s < D / 16; ++s) {
@@ -272,9 +278,9 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
     // its softmax sums, as the product of an all-ones V^T tile with P^T (every
     // row of it is the sum of the p values the context used, summed in F32 by
     // the matrix core).
-    floatx16_t o[2][D / 32 + 1];
+    floatx16_t o[QT][D / 32 + 1];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
         for (int t = 0; t <= D / 32; ++t) o[qt][t] = floatx16_t{};
     frag ones;
@@ -286,7 +292,9 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
     // a wave rescales its context rarely; every p and the sums share the max
     // in use, so the quotient is the softmax whatever that max is.
     constexpr float RESCALE = 8.0f;
-    float m_run[2] = {-INFINITY, -INFINITY};
+    float m_run[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) m_run[qt] = -INFINITY;
 
     int k_lo = 0, k_hi = len;
     if (window < INT32_MAX) {
@@ -306,23 +314,23 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
         char *base = ring + stage * SBYTES;
 #if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int row = (wave * 2 + i) * 8 + lrow;               // key within the block
+        for (int i = 0; i < LPW; ++i) {
+            const int row = (wave * LPW + i) * 8 + lrow;             // key within the block
             const int key = min(kb + row, len - 1);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rk, (__attribute__((address_space(3))) void *)(base + (wave * 2 + i) * 8 * KROW), 16,
+                rk, (__attribute__((address_space(3))) void *)(base + (wave * LPW + i) * 8 * KROW), 16,
                 key * KROW + 16 * (lchunk ^ att_swz(row)), 0, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = (wave * 2 + i) * 8 + lrow;                 // column of d
+        for (int i = 0; i < LPW; ++i) {
+            const int c = (wave * LPW + i) * 8 + lrow;               // column of d
             // Keys kb + 8 slot .. + 7 of column c; a chunk wholly past the
             // row reads the row's last chunk instead (it weighs 0).
             const int slot = lchunk ^ att_swz(c);
             int k0 = kb + 8 * slot;
             if (k0 >= len) k0 = max(0, (len - 1) & ~7);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rv, (__attribute__((address_space(3))) void *)(base + KBYTES + (wave * 2 + i) * 8 * 128), 16,
+                rv, (__attribute__((address_space(3))) void *)(base + KBYTES + (wave * LPW + i) * 8 * 128), 16,
                 (c * tcap + start + k0) * 2, 0, 0, 0);
         }
 #else
@@ -335,8 +343,8 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
         if (st < nb) issue(st, k_lo + st * KB);
     // Every block's live keys, once, before the loop (a mask read inside it
     // would make its wave wait on the prefetch loads too): block b's 64 keys
-    // as one 64-bit word, by wave b % 4.
-    for (int b = wave; b < nb; b += 4) {
+    // as one 64-bit word, by wave b % WAVES.
+    for (int b = wave; b < nb; b += WAVES) {
         const int key = k_lo + b * KB + lane;
         const uint64_t bits = __ballot(key < len && mk[key] != 0);
         if (lane == 0) live_bits[b] = bits;
@@ -345,7 +353,7 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
     for (int bi = 0; bi < nb; ++bi) {
         const int kb = k_lo + bi * KB;
         const int later = min(STAGES - 2, nb - 1 - bi);
-        if (later >= 1) att_wait_vmcnt<4>();
+        if (later >= 1) att_wait_vmcnt<2 * LPW>();
         else att_wait_vmcnt<0>();
         __syncthreads();
         if (bi + STAGES - 1 < nb) issue((bi + STAGES - 1) % STAGES, kb + (STAGES - 1) * KB);
@@ -360,39 +368,42 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
         // nothing past the row's end or outside its queries' windows
         // (wave-uniform).
         bool work[2];
-        floatx16_t scs[2][2];
+        floatx16_t scs[2][QT];
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             const int ks = kb + sub * 32;
             work[sub] = wave_live && !(window < INT32_MAX && (ks + 31 < qw - window || ks > qw + WQ - 1 + window));
-            floatx16_t a0 = floatx16_t{}, a1 = floatx16_t{};
+            floatx16_t a[QT];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) a[qt] = floatx16_t{};
             if (work[sub]) {
                 const int row = sub * 32 + swap23(ql);
 #pragma unroll
                 for (int s = 0; s < D / 16; ++s) {
                     const int c = 2 * s + h;
                     const frag kf = *(const frag *)(kbase + row * KROW + 16 * (c ^ att_swz(row)));
-                    a0 = AttnMma<T>::run(kf, qf[0][s], a0);
-                    a1 = AttnMma<T>::run(kf, qf[1][s], a1);
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) a[qt] = AttnMma<T>::run(kf, qf[qt][s], a[qt]);
                 }
             }
-            scs[sub][0] = a0;
-            scs[sub][1] = a1;
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) scs[sub][qt] = a[qt];
         }
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             const int ks = kb + sub * 32;   // the sub-block's first key
             if (!work[sub]) continue;
-            floatx16_t (&sc)[2] = scs[sub];
+            floatx16_t (&sc)[QT] = scs[sub];
             // Mask (a sub-block wholly live and in every query's window skips
             // the per-key tests) and take each tile's max of the raw scores
             // for this lane's query (the scale is positive, so it keeps their
             // order).
             const uint32_t sbits = (uint32_t)(bits >> (32 * sub));
             const bool all_live = sbits == ~0u && (window == INT32_MAX || (ks >= qw + WQ - 1 - window && ks + 31 <= qw + window));
-            float mx[2] = {-INFINITY, -INFINITY};
+            float mx[QT];
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < QT; ++qt) {
+                mx[qt] = -INFINITY;
                 if (!all_live) {
                     // This lane's live keys in reach as a mask over the
                     // sub-block; register rr holds key 8 h + j, j = 16 (rr / 8) + rr % 8.
@@ -422,22 +433,26 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
             // Every lane runs the same instructions below (the matrix cores
             // take the whole wave): a query with nothing live in reach yet adds
             // zeros and keeps its state (-inf > -inf + RESCALE is false).
-            const float mxs0 = mx[0] * scale, mxs1 = mx[1] * scale;
-            const bool grow0 = mxs0 > m_run[0] + RESCALE, grow1 = mxs1 > m_run[1] + RESCALE;
-            if (__ballot(grow0 || grow1) != 0) {
-                const float a0 = grow0 ? __builtin_amdgcn_exp2f(m_run[0] - mxs0) : 1.0f;   // 0 from -inf
-                const float a1 = grow1 ? __builtin_amdgcn_exp2f(m_run[1] - mxs1) : 1.0f;
+            float mxs[QT];
+            bool grow[QT], any = false;
 #pragma unroll
-                for (int t = 0; t <= D / 32; ++t) {
-                    o[0][t] *= a0;
-                    o[1][t] *= a1;
-                }
-                m_run[0] = grow0 ? mxs0 : m_run[0];
-                m_run[1] = grow1 ? mxs1 : m_run[1];
+            for (int qt = 0; qt < QT; ++qt) {
+                mxs[qt] = mx[qt] * scale;
+                grow[qt] = mxs[qt] > m_run[qt] + RESCALE;
+                any = any || grow[qt];
             }
-            frag pf[2][2];
+            if (__ballot(any) != 0) {
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+                for (int qt = 0; qt < QT; ++qt) {
+                    const float f = grow[qt] ? __builtin_amdgcn_exp2f(m_run[qt] - mxs[qt]) : 1.0f;   // 0 from -inf
+#pragma unroll
+                    for (int t = 0; t <= D / 32; ++t) o[qt][t] *= f;
+                    m_run[qt] = grow[qt] ? mxs[qt] : m_run[qt];
+                }
+            }
+            frag pf[QT][2];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
                 const float neg = m_run[qt] == -INFINITY ? 0.0f : -m_run[qt];
 #pragma unroll
                 for (int step = 0; step < 2; ++step) {
@@ -455,16 +470,16 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
                     const int row = 32 * t + ql;
                     const int c = sub * 4 + step * 2 + h;
                     const frag vf = *(const frag *)(vbase + row * 128 + 16 * (c ^ att_swz(row)));
-                    o[0][t] = AttnMma<T>::run(vf, pf[0][step], o[0][t]);
-                    o[1][t] = AttnMma<T>::run(vf, pf[1][step], o[1][t]);
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) o[qt][t] = AttnMma<T>::run(vf, pf[qt][step], o[qt][t]);
                 }
-                o[0][D / 32] = AttnMma<T>::run(ones, pf[0][step], o[0][D / 32]);
-                o[1][D / 32] = AttnMma<T>::run(ones, pf[1][step], o[1][D / 32]);
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) o[qt][D / 32] = AttnMma<T>::run(ones, pf[qt][step], o[qt][D / 32]);
             }
         }
     }
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int query = qw + 32 * qt + ql;
         if (query >= len) continue;
         const float l_tot = o[qt][D / 32][0];
@@ -483,6 +498,13 @@ __global__ void __launch_bounds__(256) attention_mfma_kernel(const T *__restrict
     }
 }
 
+// Query tiles of 32 a wave (1: eight waves of 32 queries, the registers for
+// four waves a SIMD; 2: four waves of 64, each K and V fragment read from LDS
+// feeding two tiles).
+#ifndef ATT_QT
+#define ATT_QT 1
+#endif
+
 template <typename T>
 static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
                                    const int32_t *mask, const Span &sp, int max_rows, int max_len, int window,
@@ -496,8 +518,8 @@ static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int
     // 64 at most 63 before the row's, so ceil(max_len / 64) + 1 blocks).
     const int bytes = 3 * 2 * 64 * 64 * 2 + ((max_len + 127) / 64) * 8;
     if (bytes > 160 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attention_mfma_kernel<T, 64>), dim3(blocks), dim3(256), bytes, s, (const T *)qkv, tcap, heads,
-                       sp, nqb, p, mask, window, (T *)ctx);
+    hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT>), dim3(blocks), dim3(64 * (256 / (32 * ATT_QT))), bytes, s,
+                       (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
     return hipGetLastError();
 }
 
