@@ -128,6 +128,37 @@ def summarize_pmc(fetch_dir, write_dir, workload, command):
     print(json.dumps(out))
 
 
+def summarize_stats(stats_dir, workload, command):
+    """profiles/kernels_<workload>.md from a rocprofv3 --kernel-trace --stats
+    run of this script: each kernel's calls, total and average duration, and
+    the GEMM kernel's launches over all its instantiations."""
+    import csv
+    import glob
+
+    rows = []
+    for f in glob.glob(os.path.join(stats_dir, "**", "*kernel_stats.csv"), recursive=True):
+        rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+    lines = [f"# rocprofv3 kernel stats: {workload}", "", "Command (from the repository root, one MI355X):", "", "```",
+             *command, "```", "", "| kernel (symbol) | calls | total ms | average µs | % |", "|---|---|---|---|---|"]
+    for r in rows:
+        ns = float(r["TotalDurationNs"])
+        lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {ns / 1e6:.3f} | {float(r['AverageNs']) / 1e3:.1f} | "
+                     f"{100 * ns / total:.2f} |")
+    for tag, pat in (("GEMM kernel (`gemm_lds_kernel` and `gemm_kernel`, every instantiation)", "gemm_"),
+                     ("attention kernel", "attention"), ("add + LayerNorm kernel", "add_layer_norm")):
+        sel = [r for r in rows if pat in r["Name"]]
+        if sel:
+            calls = sum(int(r["Calls"]) for r in sel)
+            ns = sum(float(r["TotalDurationNs"]) for r in sel)
+            lines.append(f"\nThe {tag}: {calls} launches, {ns / 1e6:.3f} ms, average {ns / calls / 1e3:.1f} µs a launch.")
+    out = os.path.join(ROOT, "profiles", f"kernels_{workload}.md")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,6 +180,8 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic_<workload>.json from two rocprofv3 --pmc runs and exit")
     ap.add_argument("--pmc-command", action="append", default=[], help="the profiling commands, for the summary")
+    ap.add_argument("--summarize-stats", metavar="STATS_DIR",
+                    help="write profiles/kernels_<workload>.md from a rocprofv3 --kernel-trace --stats run and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run (each row's encoder is "
@@ -157,6 +190,9 @@ def main():
 
     if args.summarize_pmc:
         summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.workload, args.pmc_command)
+        return
+    if args.summarize_stats:
+        summarize_stats(args.summarize_stats, args.workload, args.pmc_command)
         return
     shape = W.SHAPES[args.workload]
     lengths = {"default": "default", "full": None}.get(args.lengths)
