@@ -940,7 +940,10 @@ def test_a_block_shape_that_cannot_launch_is_skipped_and_refused(context, tmp_pa
     model.close()
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x192", "256x384", "128x128", "256x128k32", "r128x128", "r64x64"])
+# hidden 192: Q, K and V start inside the 128-column waves of 128x256 and
+# 128x256k32, which must then run 64-column waves for the QKV product.
+@pytest.mark.parametrize("tile", ["256x256", "256x192", "256x384", "128x128", "256x128k32", "r128x128", "r64x64",
+                                  "128x256", "128x256k32"])
 def test_forced_tiles_meet_the_oracle(context, tile, monkeypatch):
     desc = small.bert(seed=32, hidden=192, heads=3, inter=384, positions=320, std=0.1)
     ids, mask, types = small.ragged_rows(32, 6, 300, desc.vocab_size)

@@ -95,13 +95,11 @@ struct GemmRows {
 };
 
 // The span's first token moves the epilogue's row-major output (and the int8
-// activation scales) down to it; the Q, K and V scatter takes it as the
-// token of row 0, and the rotary epilogue reads the rows' stride from the
-// run's dimensions.
+// activation scales) down to it; the Q, K and V scatter (and the rotary
+// epilogue's positions) take it as the token of row 0.
 template <Epi KIND, typename OT>
-__device__ __forceinline__ void place_epilogue(EpiArgs &e, const Live &lv, bool dims) {
+__device__ __forceinline__ void place_epilogue(EpiArgs &e, const Live &lv) {
     e.tok0 = lv.tok0;
-    if (dims) e.seq = lv.seq;
     if (e.a_scale) e.a_scale += lv.tok0;
     const size_t rows = (size_t)lv.tok0 * e.ldo;
     if constexpr (KIND == Epi::Plain) e.out = (float *)e.out + rows;
@@ -151,7 +149,7 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
                 // the neighbouring lane (column n sits in lane n % 32).
                 const float w = __shfl_xor(v, 1, 64);
                 if (which < 2 && col_ok && m < M) {
-                    const int pos = e.at[e.tok0 + m] % e.seq;
+                    const int pos = e.pos[e.tok0 + m];
                     const float cs = e.cos[(size_t)pos * half + pr], sn = e.sin[(size_t)pos * half + pr];
                     // (x1, x2) -> (x1 cos - x2 sin, x2 cos + x1 sin)
                     v = (c & 1) ? __fadd_rn(__fmul_rn(v, cs), __fmul_rn(w, sn))
@@ -200,7 +198,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(Span sp, int a_tok, int N, in
     const int live = (M + BM - 1) / BM * grid_n;
     if ((int)blockIdx.x >= live) return;
     A += (size_t)lv.tok0 * a_tok;
-    place_epilogue<KIND, T>(e, lv, sp.dims != nullptr);
+    place_epilogue<KIND, T>(e, lv);
     const int per = live / 8;
     int b = blockIdx.x;
     if (b < per * 8) b = (b % 8) * per + b / 8;
@@ -377,17 +375,20 @@ __device__ __forceinline__ u32x2_t pack4(const float (&v)[4]) {
     return __builtin_bit_cast(u32x2_t, tmp);
 }
 
-// The per-column constants a lane's epilogue stores use (the bias, and the
-// int8 weight scales), read before the main loop. A global load issued among
-// the stores would make the wait for its value wait for every store before it
-// too (the vector memory counter retires in order), so the epilogue reads
-// nothing from global memory once its first store is out. Row-wise stores: 8
-// consecutive columns of each of the lane's PH chunks; V^T stores: the one
-// column of each of the lane's KV items.
+// The per-column constants a lane's epilogue uses (the bias, and the int8
+// weight scales), read after the main loop and before the first store. A
+// global load issued among the stores would make the wait for its value wait
+// for every store before it too (the vector memory counter retires in order),
+// so the epilogue reads nothing from global memory once its first store is
+// out. 16-bit operands: the bias of the lane's accumulator columns 32 j + ql,
+// added as the accumulators go to LDS (TN registers). int8 operands, whose
+// bias follows the scales: row-wise stores take 8 consecutive columns of each
+// of the lane's PH chunks, V^T stores the one column of each of its KV items.
 template <int TN, int PASS, bool SCALED>
 struct EpiCols {
     static constexpr int COLS = TN * 32, CH = COLS / 8, PH = CH / gcd_c(64, CH);
     static constexpr int KV = COLS * (PASS / 8) / 64;
+    float bl[TN];
     float b[PH][8], w[PH][8];
     float bv[KV], wv[KV];
 };
@@ -411,7 +412,13 @@ __device__ __forceinline__ void load_cols(EpiCols<TN, PASS, SCALED> &c, const Ep
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, n * 4, 0, 0));
     };
     const bool vt = (KIND == Epi::Qkv || KIND == Epi::QkvRope) && nw / e.hidden == 2;
-    if (e.bias) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) c.bl[j] = 0.0f;
+    if (!SCALED && e.bias) {
+        const __amdgpu_buffer_rsrc_t r = rsrc(e.bias);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) c.bl[j] = at(r, nw + j * 32 + (lane & 31));
+    } else if (e.bias) {
         const __amdgpu_buffer_rsrc_t r = rsrc(e.bias);
         if (vt) {
 #pragma unroll
@@ -443,6 +450,13 @@ __device__ __forceinline__ void load_cols(EpiCols<TN, PASS, SCALED> &c, const Ep
 #endif
 }
 
+// Head and column within the head of column `rem` of Q, K or V. (A lane's
+// columns repeat from pass to pass, so the compiler computes these once.)
+__device__ __forceinline__ void head_col(int rem, int d, int &head, int &c) {
+    head = rem / d;
+    c = rem - head * d;
+}
+
 // `ascale` (int8 operands): the activation scales of this wave's rows,
 // staged in LDS before the first store.
 template <typename T, Epi KIND, int TM, int TN, int PASS, bool SCALED, typename ACC>
@@ -461,10 +475,14 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                                : (int64_t)(M - mw) * e.ldo * (int64_t)((KIND == Epi::Plain || e.out_f32) ? 4 : sizeof(T));
     const bool fast = KIND != Epi::Residual && (N & 7) == 0 && region < OOB && (!QKV || (e.d & 7) == 0);
     const bool fast_v = fast && ((e.tcap | e.tok0) & 7) == 0;   // V^T: 8 tokens in 16 aligned bytes
+    // Q, K and V: a wave's columns lie in one of them (every block shape
+    // whose waves' width does not divide the hidden size is refused for
+    // these products), so the block, and its first column, are the wave's.
+    const int qkv_which = QKV ? uniform(nw / e.hidden) : 0, qkv_base = qkv_which * e.hidden;
 #if defined(__HIP_DEVICE_COMPILE__)
     __amdgpu_buffer_rsrc_t rs;
     if constexpr (QKV) {
-        const int which = nw / e.hidden;
+        const int which = qkv_which;
         rs = __builtin_amdgcn_make_buffer_rsrc((T *)e.out + (size_t)which * e.heads * e.tcap * e.d, (short)0,
                                                (int)region, 0x00020000);
     } else if constexpr (KIND != Epi::Residual) {
@@ -484,21 +502,22 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
             for (int r = 0; r < 16; ++r) {
                 if (PASS == 16 && (r >> 3) != half) continue;
                 const int row = (r >> 2) * 8 + h * 4 + (r & 3) - (PASS == 16 ? half * 16 : 0);
-                scratch[row * SROW + j * 32 + ql] = (float)acc[i][j][r];
+                // (16-bit operands: with the column's bias added.)
+                scratch[row * SROW + j * 32 + ql] = SCALED ? (float)acc[i][j][r] : (float)acc[i][j][r] + cols.bl[j];
             }
         __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
         __builtin_amdgcn_wave_barrier();
         const int mt = mw + i * 32 + half * PASS;
         if constexpr (KIND == Epi::Qkv || KIND == Epi::QkvRope) {
-            const int which = nw / e.hidden;   // a wave's 64 columns lie in one of Q, K, V
-            if (which == 2) {
+            if (qkv_which == 2) {
                 // V^T: for each column, 8 consecutive tokens a lane.
 #pragma unroll
                 for (int k = 0; k < COLS * (PASS / 8) / 64; ++k) {
                     const int u = lane + 64 * k, col = u / (PASS / 8), g = (u % (PASS / 8)) * 8;
                     const int n = nw + col;
                     if (n >= N) continue;
-                    const int rem = n - 2 * e.hidden, head = rem / e.d, c = rem - head * e.d;
+                    int head, c;
+                    head_col(n - qkv_base, e.d, head, c);
                     float v[8];
                     const float bias = cols.bv[k];
                     const int m = mt + g;
@@ -508,7 +527,7 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                         for (int q = 0; q < 8; ++q) v[q] = dequant(scratch[(g + q) * SROW + col], ascale[m + q - mw], ws, bias);
                     } else {
 #pragma unroll
-                        for (int q = 0; q < 8; ++q) v[q] = scratch[(g + q) * SROW + col] + bias;
+                        for (int q = 0; q < 8; ++q) v[q] = scratch[(g + q) * SROW + col];
                     }
                     T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + ((size_t)head * e.d + c) * e.tcap + e.tok0;
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -562,8 +581,8 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                             v[q] = dequant(lo[q], as, wsc[q], bias[q]);
                             v[4 + q] = dequant(hi[q], as, wsc[4 + q], bias[4 + q]);
                         } else {
-                            v[q] = lo[q] + bias[q];
-                            v[4 + q] = hi[q] + bias[4 + q];
+                            v[q] = lo[q];
+                            v[4 + q] = hi[q];
                         }
                     }
                     const int rm = m - mw;   // row within the wave's region
@@ -597,10 +616,10 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                         __builtin_amdgcn_raw_buffer_store_b64(pack4<T>(g4), rs,
                                                              ok ? (rm * e.ldo + (n >> 1)) * (int)sizeof(T) : OOB, 0, 0);
                     } else {   // Qkv, QkvRope: Q or K, token-major per head
-                        const int which = n / e.hidden, rem = n - which * e.hidden;
-                        const int head = rem / e.d, c = rem - head * e.d;
+                        int head, c;
+                        head_col(n - qkv_base, e.d, head, c);
                         if constexpr (KIND == Epi::QkvRope) {
-                            const int pos = e.at[e.tok0 + min(m, M - 1)] % e.seq, hd = e.d >> 1;
+                            const int pos = e.pos[e.tok0 + min(m, M - 1)], hd = e.d >> 1;
 #pragma unroll
                             for (int p = 0; p < 4; ++p) {
                                 const int pr = (c >> 1) + p;
@@ -638,8 +657,8 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                     v[q] = dequant(lo[q], as, wsc[q], bias[q]);
                     v[4 + q] = dequant(hi[q], as, wsc[4 + q], bias[4 + q]);
                 } else {
-                    v[q] = lo[q] + bias[q];
-                    v[4 + q] = hi[q] + bias[4 + q];
+                    v[q] = lo[q];
+                    v[4 + q] = hi[q];
                 }
             }
             if constexpr (KIND == Epi::Plain || KIND == Epi::Bias) {
@@ -684,7 +703,7 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                 const int which = n / e.hidden, rem = n - which * e.hidden;
                 const int head = rem / e.d, c = rem - head * e.d;
                 if constexpr (KIND == Epi::QkvRope) {
-                    const int pos = e.at[e.tok0 + m] % e.seq, half = e.d >> 1;
+                    const int pos = e.pos[e.tok0 + m], half = e.d >> 1;
 #pragma unroll
                     for (int p = 0; p < 4; ++p) {
                         const int pr = (c >> 1) + p;
@@ -734,7 +753,7 @@ gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int l
     const int live = (M + BM - 1) / BM * grid_n;
     if ((int)blockIdx.x >= live) return;
     A += (size_t)lv.tok0 * a_tok;
-    place_epilogue<KIND, OT>(e, lv, sp.dims != nullptr);
+    place_epilogue<KIND, OT>(e, lv);
     const int per = live / 8;
     int b = blockIdx.x;
     if (b < per * 8) b = (b % 8) * per + b / 8;
@@ -976,6 +995,19 @@ int gemm_tile_by_name(const char *s, size_t n) {
     return v <= 15 ? v : -1;
 }
 
+// Columns of one wave's output tile, per block shape (the staged shapes,
+// 1-3 and 14, store column by column and take any).
+static int wave_cols(int tile) {
+    switch (tile) {
+    case 6:
+    case 10: return 128;
+    case 13:
+    case 15: return 96;
+    case 4: case 5: case 7: case 8: case 9: case 11: case 12: return 64;
+    default: return 1;
+    }
+}
+
 // The tiles worth timing for a product of this type and shape: every
 // pipelined shape when the operands take it, else the staged ones.
 int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap) {
@@ -996,14 +1028,10 @@ int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap) 
         add(14);
         return n;
     }
-    add(7);
-    if (!qkv || e.hidden % 96 == 0) add(13);
-    if (!qkv || e.hidden % 96 == 0) add(15);
-    add(4);
-    add(6);
-    add(5);
-    add(9);
-    add(10);
+    // Q, K and V must each start on a wave's column boundary.
+    auto fits = [&](int t) { return !qkv || e.hidden % wave_cols(t) == 0; };
+    for (int t : {7, 13, 15, 4, 6, 5, 9, 10})
+        if (fits(t)) add(t);
     return n;
 }
 
@@ -1057,8 +1085,10 @@ static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K,
     if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
     // A pipelined shape asked of an operand it cannot take runs the staged kernel.
     if (((tile >= 4 && tile <= 13) || tile == 15) && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
-    // 96-column wave tiles need Q, K and V to start on their boundaries.
-    if ((tile == 13 || tile == 15) && (e.kind == Epi::Qkv || e.kind == Epi::QkvRope) && e.hidden % 96 != 0) tile = 7;
+    // Q, K and V must each start on a wave's column boundary: a shape whose
+    // waves are wider than 64 columns runs 64-column waves (K = hidden is a
+    // multiple of 64 on the pipelined kernel) when they do not.
+    if ((e.kind == Epi::Qkv || e.kind == Epi::QkvRope) && e.hidden % wave_cols(tile) != 0) tile = 7;
     switch (tile) {
     case 1: return launch<T, 128, 128, BK>(s, gr, M, N, K, A, lda, W, e);
     case 2: return launch<T, 256, 128, BK>(s, gr, M, N, K, A, lda, W, e);

@@ -23,6 +23,7 @@ struct Packing {
     int32_t *len;       // [max_batch] packed tokens of each row
     int32_t *at;        // [tcap] r * seq + p of each packed token
     int32_t *row;       // [tcap] the row of each packed token
+    int32_t *pos;       // [tcap] the column p of each packed token (its position in its row)
     int32_t *tokens;    // [1] packed tokens of the run
 };
 
@@ -135,8 +136,7 @@ struct EpiArgs {
     int tcap = 0, heads = 0, d = 0, hidden = 0;   // Qkv scatter
     int tok0 = 0;                  // set on the device: the packed token of row 0 of A (of at, and of the scatter)
     const float *cos = nullptr, *sin = nullptr;   // QkvRope: [positions][d / 2]
-    const int32_t *at = nullptr;   // QkvRope: each token's r * seq + p
-    int seq = 0;                   // QkvRope: the rows' stride (read from the span's dimensions when it has them)
+    const int32_t *pos = nullptr;  // QkvRope: each packed token's position in its row
     int silu = 0;                  // Gated: SiLU instead of GELU
     int out_f32 = 0;               // Bias: F32 outputs (else the operand type; F16 for int8 operands)
     // I8 operands: output (m, n) is the int32 sum times a_scale[m] * w_scale[n].

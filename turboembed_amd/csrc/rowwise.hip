@@ -55,6 +55,7 @@ __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restri
             const int at = (starts_in_lds ? lens[batch + r] : p.start[r]) + c;
             p.at[at] = i;
             p.row[at] = r;
+            p.pos[at] = c;
         }
     }
 }
@@ -185,7 +186,7 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(Span sp, int hidden, cons
     const int id = ids[at];
     const int ty = types ? types[at] : 0;
     const float *wr = word + (size_t)id * hidden;
-    const float *pr = pos ? pos + (size_t)(at % seq + offset) * hidden : nullptr;
+    const float *pr = pos ? pos + (size_t)(p.pos[t] + offset) * hidden : nullptr;
     const float *tr = type ? type + (size_t)ty * hidden : nullptr;
     float v[G][4];
 #pragma unroll

@@ -637,12 +637,13 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     check(hipMemset(s->dims_dev, 0, sizeof(RunDims)), "session rows");
     s->row_lens.assign(B, 0);
     counted_host_alloc();
-    int32_t *pk = static_cast<int32_t *>(alloc((2 * B + 2 * s->tcap + 64) * 4, "session packing"));
+    int32_t *pk = static_cast<int32_t *>(alloc((2 * B + 3 * s->tcap + 64) * 4, "session packing"));
     s->pk.start = pk;
     s->pk.len = pk + B;
     s->pk.at = pk + 2 * B;
     s->pk.row = pk + 2 * B + s->tcap;
-    s->pk.tokens = pk + 2 * B + 2 * s->tcap;
+    s->pk.pos = pk + 2 * B + 2 * s->tcap;
+    s->pk.tokens = pk + 2 * B + 3 * s->tcap;
     s->x = static_cast<float *>(alloc(s->tcap * H * 4, "session states"));
     s->xh = alloc(s->tcap * H * 4, "session states");
     // Q, K and V, plus a 256-byte tail: the attention kernel's 16-byte loads
@@ -967,8 +968,7 @@ static LayerGemm layer_gemm(Session &s, uint32_t l, GemmSlot g) {
             r.e.kind = Epi::QkvRope;
             r.e.cos = m.rope + (global ? 0 : 2 * half);
             r.e.sin = r.e.cos + half;
-            r.e.at = s.pk.at;
-            r.e.seq = (int)s.seq;
+            r.e.pos = s.pk.pos;
         } else {
             r.e.kind = Epi::Qkv;
         }
@@ -1284,16 +1284,9 @@ bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
             check(narrow(st, s.x, static_cast<char *>(s.ffn) + o * el, std::min(tcap * H, tcap * I - o), s.act, nullptr),
                   "the tuner's operands");
     }
-    // No rows are written yet: the rotary epilogue reads each token's
-    // position as pk.at % seq, so every token sits at position 0 of rows of
-    // max_seq for the tuner's products.
-    check(hipMemsetAsync(s.pk.at, 0, tcap * 4, st), "the tuner's operands");
-    struct Seq {
-        Session &s;
-        uint32_t was;
-        ~Seq() { s.seq = was; }
-    } seq_guard{s, s.seq};
-    s.seq = s.max_seq;
+    // No rows are written yet: every token sits at position 0 for the
+    // rotary epilogue of the tuner's products.
+    check(hipMemsetAsync(s.pk.pos, 0, tcap * 4, st), "the tuner's operands");
     hipEvent_t ev[2 * REPS];
     for (hipEvent_t &e : ev) check(hipEventCreate(&e), "the tuner's events");
     struct Events {
