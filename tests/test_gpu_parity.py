@@ -33,7 +33,7 @@ def assert_close(got, want, compute_dtype):
 # ---- The GEMM kernel alone ------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [S.TURBO_DTYPE_F32, S.TURBO_DTYPE_F16, S.TURBO_DTYPE_BF16])
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16])
 @pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 200, 96), (33, 96, 32), (1000, 768, 768), (517, 2304, 1152),
                                  (70, 100, 64)])
 def test_gemm_matches_numpy(runtime, dtype, tile, mnk):
@@ -943,7 +943,7 @@ def test_a_block_shape_that_cannot_launch_is_skipped_and_refused(context, tmp_pa
 # hidden 192: Q, K and V start inside the 128-column waves of 128x256 and
 # 128x256k32, which must then run 64-column waves for the QKV product.
 @pytest.mark.parametrize("tile", ["256x256", "256x192", "256x384", "128x128", "256x128k32", "r128x128", "r64x64",
-                                  "128x256", "128x256k32"])
+                                  "128x256", "128x256k32", "256x384k32s4"])
 def test_forced_tiles_meet_the_oracle(context, tile, monkeypatch):
     desc = small.bert(seed=32, hidden=192, heads=3, inter=384, positions=320, std=0.1)
     ids, mask, types = small.ragged_rows(32, 6, 300, desc.vocab_size)

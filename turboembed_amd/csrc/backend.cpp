@@ -368,7 +368,7 @@ int32_t buffer_read(void *buf, void *dst, uint64_t bytes, turbo_error *err) {
         Buffer *b = static_cast<Buffer *>(buf);
         if (bytes > b->bytes) fail(TURBO_E_INVALID_ARGUMENT, "rocm: read of " + std::to_string(bytes) +
                                                                  " bytes from a buffer of " + std::to_string(b->bytes));
-        std::lock_guard<std::mutex> g(b->ctx->lock);
+        std::lock_guard<std::recursive_mutex> g(b->ctx->lock);
         OnDevice on(b->ctx->ordinal);
         check(hipMemcpyAsync(dst, b->dev ? b->dev : b->host, bytes, hipMemcpyDefault, b->ctx->stream), "buffer_read");
         check(hipStreamSynchronize(b->ctx->stream), "buffer_read");
@@ -417,7 +417,7 @@ int32_t buffer_quantize(void *buf, uint32_t quantization, const float *int8_rang
         const uint64_t code_bytes = quantize_codes_bytes(b, quantization, int8_ranges, rows, dim);
         if (code_bytes == 0) return TURBO_OK;
         const bool i8 = quantization == TURBO_QUANTIZE_INT8;
-        std::lock_guard<std::mutex> g(b->ctx->lock);
+        std::lock_guard<std::recursive_mutex> g(b->ctx->lock);
         OnDevice on(b->ctx->ordinal);
         const uint64_t dev0 = device_allocs.load();
         DevPtr codes(dev_alloc(code_bytes, "quantized codes"));
@@ -562,7 +562,7 @@ int32_t turbo_rocm_buffer_quantize_static(void *buf, uint32_t quantization, cons
                                                std::to_string(STATIC_SCRATCH_BYTES) + " bytes (the codes, then the "
                                                "int8 ranges); " + std::to_string(rows) + " by " + std::to_string(dim) +
                                                " values need " + std::to_string(need));
-        std::lock_guard<std::mutex> g(b->ctx->lock);
+        std::lock_guard<std::recursive_mutex> g(b->ctx->lock);
         OnDevice on(b->ctx->ordinal);
         void *area = b->ctx->scratch;
         if (!area) fail(TURBO_E_RUNTIME, "rocm: the device's staging area was not found at context creation");

@@ -951,7 +951,10 @@ static hipError_t launch_lds(hipStream_t s, const GemmRows &gr, int M, int N, in
     return hipErrorInvalidValue;
 }
 
-int gemm_tiles() { return 15; }
+// The highest block-shape number.
+constexpr int TILES = 16;
+
+int gemm_tiles() { return TILES; }
 
 // The block shape made to fail to launch, as on a device that cannot take
 // it (a test hook; -1 for none): an explicit launch of it fails, the rule
@@ -975,15 +978,15 @@ bool gemm_made_to_fail(int tile) {
 // Names of the block shapes, as a choices string spells them: output tile,
 // then what sets it apart (r: operands staged through registers; k32: 32
 // columns of k a stage; s<n>: n stages).
-static const char *const TILE_NAME[16] = {"auto",      "r128x128",   "r256x128",   "r64x128",    "256x128",
-                                          "128x128",   "128x256",    "256x256",    "128x128s2",  "256x128k32",
-                                          "128x256k32", "256x128k32s3", "256x256k32", "256x192",    "r64x64",
-                                          "256x384"};
+static const char *const TILE_NAME[TILES + 1] = {
+    "auto",      "r128x128",   "r256x128",     "r64x128",    "256x128", "128x128", "128x256",
+    "256x256",   "128x128s2",  "256x128k32",   "128x256k32", "256x128k32s3", "256x256k32", "256x192",
+    "r64x64",    "256x384",    "256x384k32s4"};
 
-const char *gemm_tile_name(int tile) { return tile >= 0 && tile <= 15 ? TILE_NAME[tile] : "?"; }
+const char *gemm_tile_name(int tile) { return tile >= 0 && tile <= TILES ? TILE_NAME[tile] : "?"; }
 
 int gemm_tile_by_name(const char *s, size_t n) {
-    for (int t = 0; t <= 15; ++t)
+    for (int t = 0; t <= TILES; ++t)
         if (std::strlen(TILE_NAME[t]) == n && std::strncmp(TILE_NAME[t], s, n) == 0) return t;
     // A bare number names a tile too.
     int v = 0;
@@ -992,7 +995,7 @@ int gemm_tile_by_name(const char *s, size_t n) {
         if (s[i] < '0' || s[i] > '9') return -1;
         v = v * 10 + (s[i] - '0');
     }
-    return v <= 15 ? v : -1;
+    return v <= TILES ? v : -1;
 }
 
 // Columns of one wave's output tile, per block shape (the staged shapes,
@@ -1002,7 +1005,8 @@ static int wave_cols(int tile) {
     case 6:
     case 10: return 128;
     case 13:
-    case 15: return 96;
+    case 15:
+    case 16: return 96;
     case 4: case 5: case 7: case 8: case 9: case 11: case 12: return 64;
     default: return 1;
     }
@@ -1030,7 +1034,7 @@ int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap) 
     }
     // Q, K and V must each start on a wave's column boundary.
     auto fits = [&](int t) { return !qkv || e.hidden % wave_cols(t) == 0; };
-    for (int t : {7, 13, 15, 4, 6, 5, 9, 10})
+    for (int t : {7, 13, 15, 16, 4, 6, 5, 9, 10})
         if (fits(t)) add(t);
     return n;
 }
@@ -1068,8 +1072,9 @@ static int wide_tile(int M, int N, int K, const EpiArgs &e) {
 }
 
 // Block shapes by number: 1-3 and 14 stage operands through registers (any K
-// a multiple of 8, and the F32 tier); 4-13 are the pipelined kernel, for
-// 16-bit operands with K a multiple of 64 (every encoder shape here).
+// a multiple of 8, and the F32 tier); 4-13, 15 and 16 are the pipelined
+// kernel, for 16-bit operands with K a multiple of 64 (every encoder shape
+// here).
 template <typename T, int BK>
 static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda, const void *W,
                          const EpiArgs &e,
@@ -1084,7 +1089,7 @@ static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K,
     }
     if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
     // A pipelined shape asked of an operand it cannot take runs the staged kernel.
-    if (((tile >= 4 && tile <= 13) || tile == 15) && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
+    if (((tile >= 4 && tile <= 13) || tile >= 15) && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
     // Q, K and V must each start on a wave's column boundary: a shape whose
     // waves are wider than 64 columns runs 64-column waves (K = hidden is a
     // multiple of 64 on the pipelined kernel) when they do not.
@@ -1113,6 +1118,9 @@ static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K,
         // 8 waves as 2 x 4 of 128 x 96: a third less LDS reading per product than
         // 128 x 64 waves, and N = 768, 2304 and 3072 in whole rounds at 32768 rows.
         case 15: return launch_lds<T, 256, 384, 2, 4, 2>(s, gr, M, N, K, A, lda, W, e);
+        // The same waves on 32 columns of k a stage, four stages (all 160 KB
+        // of LDS): loads issued three steps ahead instead of one.
+        case 16: return launch_lds<T, 256, 384, 2, 4, 4, 32, 1>(s, gr, M, N, K, A, lda, W, e);
         }
     }
     return hipErrorInvalidValue;

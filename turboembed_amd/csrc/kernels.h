@@ -165,6 +165,8 @@ int gemm_tile_by_name(const char *s, size_t n);
 // shape (K, lda and the epilogue decide which kernels take them) into out:
 // how many.
 int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap);
+// The 256 x 384 block shape (8 waves of 128 x 96): a split run's products' shape.
+constexpr int WIDE_TILE = 15;
 // A test hook standing in for a device that cannot launch one block shape:
 // the shape a name spells (NULL or "" for none) fails to launch from now on.
 // False for a name that spells no shape. gemm_made_to_fail says whether a

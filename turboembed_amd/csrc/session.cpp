@@ -506,6 +506,8 @@ bool mfma_attention(Dt act, uint32_t head_width) { return act != Dt::F32 && head
 
 }  // namespace
 
+static void split_defaults(Session &s);
+
 Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_backend_tuning *tuning) {
     if (desc->task != TURBO_TASK_EMBED && desc->task != TURBO_TASK_RERANK)
         fail(TURBO_E_UNSUPPORTED_TASK, "rocm: task " + std::to_string(desc->task));
@@ -535,6 +537,11 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
             fail(TURBO_E_UNSUPPORTED, "rocm: int8 GEMMs need hidden and intermediate sizes in multiples of 64");
         dt = Dt::I8;
     }
+    // The open's launches (weights narrowed on first need, the tuner's runs,
+    // the graphs' capture) take the context's streams from its other
+    // sessions' runs until it returns: a launch of theirs would land in a
+    // capture.
+    std::lock_guard<std::recursive_mutex> on_ctx(m->ctx->lock);
     auto s = std::make_unique<Session>();
     counted_host_alloc();
     s->model = m;
@@ -568,10 +575,13 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     const uint32_t mode = tuning && tuning->struct_size >= offsetof(turbo_backend_tuning, mode) + 4 ? tuning->mode
                                                                                                      : TURBO_AUTOTUNE_OFF;
     const bool tuned_mode = mode == TURBO_AUTOTUNE_ON || mode == TURBO_AUTOTUNE_RETUNE;
+    if (const char *g = std::getenv("TURBO_ROCM_SPLIT"))
+        s->split_parts = (uint32_t)std::min<long>(std::max<long>(std::strtol(g, nullptr, 10), 1), Session::MAX_PARTS);
     Choices &kc = s->kc;
     kc.bins = bins_for((uint64_t)desc->max_batch * desc->max_seq);
     const bool mfma_attn = mfma_attention(s->act, m->hidden / m->heads);
     for (int b = 0; b < kc.bins; ++b) kc.bin[b].simple_attention = !mfma_attn;
+    split_defaults(*s);
     bool cached = false;
     if (tuned_mode && tuning->cached && *tuning->cached) {
         std::string why;
@@ -612,8 +622,6 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         if (!mfma_attn) kc.bin[b].simple_attention = true;
     const bool measure = ((mode == TURBO_AUTOTUNE_ON && !cached) || mode == TURBO_AUTOTUNE_RETUNE) && !all_forced(kc);
     if (const char *g = std::getenv("TURBO_ROCM_GRAPHS")) s->graphs = std::strcmp(g, "0") != 0;
-    if (const char *g = std::getenv("TURBO_ROCM_SPLIT"))
-        s->split_parts = (uint32_t)std::min<long>(std::max<long>(std::strtol(g, nullptr, 10), 1), Session::MAX_PARTS);
 
     const size_t H = m->hidden, I = m->inter, B = s->max_batch, S = s->max_seq;
     s->tcap = B * S;
@@ -742,6 +750,33 @@ static uint32_t parts_of_bin(const Session &s, int b) {
     return splits && s.split_parts > 1 && s.max_batch >= 2 ? std::min(s.split_parts, s.max_batch) : 1;
 }
 
+// The rule's choice in a bin whose runs split into parts: the 256 x 384
+// block shape on every product that can take it. The parts run the same
+// kernels side by side, and shapes fastest alone lose there: a 256 x 384
+// product at N = 768 fills half the compute units and the other part's the
+// rest. Measured on MI355X, a batch with it on all four products against
+// the shapes the tuner finds fastest alone: BERT-base 64 x 512 8.05 ms
+// against 8.23-8.35, ModernBERT 16 x 2048-8192 45.4-45.6 ms against
+// 45.4-46.6 (timing whole runs in the tuner could not tell them apart
+// reliably: its short bursts run at clocks a sustained run does not).
+static void split_defaults(Session &s) {
+    const Model &m = *s.model;
+    for (int b = 0; b < s.kc.bins; ++b) {
+        if (parts_of_bin(s, b) < 2) continue;
+        BinChoice &bc = s.kc.bin[b];
+        for (int g = 0; g < G_COUNT; ++g) {
+            if (bc.tile_forced[g] || gemm_made_to_fail(WIDE_TILE)) continue;
+            EpiArgs e;
+            e.kind = g == G_QKV ? Epi::Qkv : Epi::Bias;
+            e.hidden = (int)m.hidden;
+            const int K = g == G_FFN2 ? (int)m.inter : (int)m.hidden;
+            int cand[16];
+            const int n = gemm_candidates(s.dt, K, K, e, cand, 16);
+            if (std::find(cand, cand + n, WIDE_TILE) != cand + n) bc.tile[g] = WIDE_TILE;
+        }
+    }
+}
+
 void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_token_range *ranges, uint32_t count) {
     if (r->batch == 0 || r->seq == 0) fail(TURBO_E_INVALID_SHAPE, "rocm: batch and seq may not be 0");
     if (r->batch > s->max_batch || r->seq > s->max_seq)
@@ -786,7 +821,7 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     const uint32_t B = r->batch, S = r->seq, stride = r->row_stride ? r->row_stride : r->seq;
     if (stride < S) fail(TURBO_E_INVALID_SHAPE, "rocm: row_stride under seq");
     // Rows are packed with no stride, in the session's planes of B x S.
-    std::lock_guard<std::mutex> g(s->ctx->lock);
+    std::lock_guard<std::recursive_mutex> g(s->ctx->lock);
     OnDevice on(s->ctx->ordinal);
     // The staging buffer may still feed the last write's copy.
     check(hipStreamSynchronize(s->ctx->stream), "embed_write");
@@ -1260,8 +1295,9 @@ void launch_run(Session &s) {
 // each candidate block shape, on operands of uniform values in the
 // session's own buffers; a candidate replaces the bin's choice (the rule's,
 // or the cached one: the incumbent, timed first) when it is faster by the
-// margin. Largest bins first, as they cost the most; stops at the budget.
-// Returns whether anything was timed.
+// margin. In a bin whose runs split into parts, a product on the 256 x 384
+// shape (split_defaults) keeps it. Largest bins first, as they cost the
+// most; stops at the budget. Returns whether anything was timed.
 bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
     using Clock = std::chrono::steady_clock;
     const Clock::time_point deadline = Clock::now() + std::chrono::milliseconds(budget_ms);
@@ -1299,10 +1335,11 @@ bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
     char line[160];
     for (int b = s.kc.bins - 1; b >= 0; --b) {
         // The rows a launch of the bin takes at most: the bin's, or a part's.
-        const int M = (int)bounds_of(s, b, parts_of_bin(s, b)).part_tokens;
+        const uint32_t P = parts_of_bin(s, b);
+        const int M = (int)bounds_of(s, b, P).part_tokens;
         BinChoice &bc = s.kc.bin[b];
         for (int g = 0; g < G_COUNT; ++g) {
-            if (bc.tile_forced[g]) continue;
+            if (bc.tile_forced[g] || (P > 1 && bc.tile[g] == WIDE_TILE)) continue;
             LayerGemm lg = layer_gemm(s, 0, (GemmSlot)g);
             const void *A = lg.A;
             if (s.dt == Dt::I8) {
@@ -1358,7 +1395,7 @@ void session_run(Session *s, turbo_backend_run *out) {
     s->written = false;
     const uint64_t dev0 = device_allocs.load(), host0 = host_allocs_on_thread();
     {
-        std::lock_guard<std::mutex> g(s->ctx->lock);
+        std::lock_guard<std::recursive_mutex> g(s->ctx->lock);
         OnDevice on(s->ctx->ordinal);
         try {
             launch_run(*s);
@@ -1406,7 +1443,7 @@ int32_t turbo_rocm_session_packing(void *session, int32_t *start, int32_t *len, 
                                    turbo_error *err) {
     return guarded(err, [&] {
         Session *s = static_cast<Session *>(session);
-        std::lock_guard<std::mutex> g(s->ctx->lock);
+        std::lock_guard<std::recursive_mutex> g(s->ctx->lock);
         OnDevice on(s->ctx->ordinal);
         int32_t t = 0;
         check(hipMemcpy(&t, s->pk.tokens, 4, hipMemcpyDeviceToHost), "packing");
@@ -1423,7 +1460,7 @@ int32_t turbo_rocm_session_hidden(void *session, float *out, uint64_t floats, tu
         Session *s = static_cast<Session *>(session);
         const uint64_t n = (uint64_t)s->tokens * s->model->hidden;
         if (floats < n) fail(TURBO_E_INVALID_ARGUMENT, "rocm: the hidden states need " + std::to_string(n) + " floats");
-        std::lock_guard<std::mutex> g(s->ctx->lock);
+        std::lock_guard<std::recursive_mutex> g(s->ctx->lock);
         OnDevice on(s->ctx->ordinal);
         check(hipMemcpy(out, s->x, n * 4, hipMemcpyDeviceToHost), "hidden states");
         return TURBO_OK;
@@ -1476,7 +1513,7 @@ int32_t turbo_rocm_session_replay(void *session, uint32_t runs, turbo_error *err
     return guarded(err, [&] {
         Session *s = static_cast<Session *>(session);
         if (s->tokens == 0) fail(TURBO_E_INVALID_STATE, "rocm: the session has no rows written");
-        std::lock_guard<std::mutex> g(s->ctx->lock);
+        std::lock_guard<std::recursive_mutex> g(s->ctx->lock);
         OnDevice on(s->ctx->ordinal);
         for (uint32_t i = 0; i < runs; ++i) launch_run(*s);
         check(hipStreamSynchronize(s->ctx->stream), "replay");

@@ -84,7 +84,9 @@ struct Context {
     hipEvent_t fork = nullptr, join[SIDES] = {};
     turbo_log_fn log = nullptr;
     void *log_user_data = nullptr;
-    std::mutex lock;                 // a launch through its sync, and reads
+    // A launch through its sync, reads, and a session's open (whose tuner
+    // writes and runs rows under it).
+    std::recursive_mutex lock;
     void *scratch = nullptr;         // the device's fixed staging area (static_scratch)
     void say(uint32_t level, const std::string &m) const;
 };
