@@ -111,10 +111,12 @@ hipError_t layer_norm(hipStream_t s, const Span &sp, int max_tokens, int hidden,
 // ydt: F32, F16 or BF16). Post-norm (pre_norm 0): x = LN(v), and out_h =
 // LN(v) in `dt` when not NULL. Pre-norm (pre_norm 1): x = v, and out_h =
 // LN(v) in `dt` (out_h F32 on the F32 tier). ln_b NULL is no bias.
+// A post-norm on 16-bit rows may carry its residual in them (res_h): v =
+// out_h + y, and x = LN(v) only with keep_f32 (out_h = LN(v) always).
 // Over the span's tokens; x, y and out_h point at the run's token 0.
 hipError_t add_layer_norm(hipStream_t s, const Span &sp, int max_tokens, int hidden, float *x, const void *y, Dt ydt,
                           const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt,
-                          const QuantOut &qo = QuantOut());
+                          const QuantOut &qo = QuantOut(), bool res_h = false, bool keep_f32 = true);
 
 // What a GEMM does with each output once its sum is done.
 enum class Epi : int {

@@ -92,9 +92,27 @@ template <typename H> __device__ __forceinline__ void store4(H *p, const float (
     *(h4 *)p = h4{from_f32<H>(v[0]), from_f32<H>(v[1]), from_f32<H>(v[2]), from_f32<H>(v[3])};
 }
 
+// A lane's columns of a LayerNorm's weight and bias (bias 0 where absent).
 template <int G>
-__device__ __forceinline__ void ln_wave(float (&v)[G][4], int hidden, const float *__restrict__ w,
-                                        const float *__restrict__ b, float eps) {
+__device__ __forceinline__ void load_wb(const float *__restrict__ w, const float *__restrict__ b, int hidden,
+                                        float (&wv)[G][4], float (&bv)[G][4]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int c = 4 * (lane + 64 * g);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wv[g][k] = bv[g][k] = 0.0f;
+        if (c >= hidden) continue;
+        load4(w + c, wv[g]);
+        if (b) load4(b + c, bv[g]);
+    }
+}
+
+// A wave's row normalized: (v - mean) / sqrt(var + eps) * w + b, the mean
+// and variance over the row's `hidden` columns.
+template <int G>
+__device__ __forceinline__ void ln_apply(float (&v)[G][4], int hidden, const float (&wv)[G][4],
+                                         const float (&bv)[G][4], float eps) {
     const int lane = threadIdx.x & 63;
     float s = 0.0f;
 #pragma unroll
@@ -114,14 +132,18 @@ __device__ __forceinline__ void ln_wave(float (&v)[G][4], int hidden, const floa
     const float inv = 1.0f / sqrtf(var + eps);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const int c = 4 * (lane + 64 * g);
-        if (c >= hidden) continue;
-        float wv[4], bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        load4(w + c, wv);
-        if (b) load4(b + c, bv);
+        if (4 * (lane + 64 * g) >= hidden) continue;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) v[g][k] = (v[g][k] - mean) * inv * wv[k] + bv[k];
+        for (int k = 0; k < 4; ++k) v[g][k] = (v[g][k] - mean) * inv * wv[g][k] + bv[g][k];
     }
+}
+
+template <int G>
+__device__ __forceinline__ void ln_wave(float (&v)[G][4], int hidden, const float *__restrict__ w,
+                                        const float *__restrict__ b, float eps) {
+    float wv[G][4], bv[G][4];
+    load_wb<G>(w, b, hidden, wv, bv);
+    ln_apply<G>(v, hidden, wv, bv, eps);
 }
 
 template <int G, typename H>
@@ -217,7 +239,7 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(Span sp, int hidden, cons
         for (int g = 0; g < G; ++g)
 #pragma unroll
             for (int k = 0; k < 4; ++k) v[g][k] = 0.0f;
-    store_row<G, H>(v, hidden, x + (size_t)t * hidden, xh ? xh + (size_t)t * hidden : nullptr);
+    store_row<G, H>(v, hidden, x ? x + (size_t)t * hidden : nullptr, xh ? xh + (size_t)t * hidden : nullptr);
     if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden, qo.scale + t);
 }
 
@@ -249,11 +271,11 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(Span sp, int hidden, co
 // The residual add and a LayerNorm in one pass (a wave a token): v = x + y,
 // then x = LN(v) (post-norm) or x = v (pre-norm), and out_h = LN(v). One
 // read of x and of the product, one write of x and of the operand copy.
-template <int G, typename Y, typename H>
+template <int G, typename Y, typename H, bool RES_H>
 __global__ void __launch_bounds__(256) add_layer_norm_kernel(Span sp, int hidden, float *__restrict__ x,
                                                              const Y *__restrict__ y, const float *__restrict__ ln_w,
                                                              const float *__restrict__ ln_b, float eps, int pre_norm,
-                                                             H *__restrict__ out_h, QuantOut qo) {
+                                                             int keep_f32, H *__restrict__ out_h, QuantOut qo) {
     const Live lv = live_of(sp);
     const int local = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (local >= lv.tokens) return;
@@ -261,13 +283,19 @@ __global__ void __launch_bounds__(256) add_layer_norm_kernel(Span sp, int hidden
     const int lane = threadIdx.x & 63;
     float *row = x + (size_t)t * hidden;
     const Y *yr = y + (size_t)t * hidden;
+    H *hr = out_h ? out_h + (size_t)t * hidden : nullptr;
+    // The norm's weight and bias first: their reads overlap the row's.
+    float wv[G][4], bv[G][4];
+    load_wb<G>(ln_w, ln_b, hidden, wv, bv);
     float v[G][4];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const int c = 4 * (lane + 64 * g);
         if (c < hidden) {
             float a[4];
-            load4(row + c, v[g]);
+            // The residual: x, or (RES_H) the 16-bit rows the last norm wrote.
+            if constexpr (RES_H) load4(hr + c, v[g]);
+            else load4(row + c, v[g]);
             load4(yr + c, a);
 #pragma unroll
             for (int k = 0; k < 4; ++k) v[g][k] = v[g][k] + a[k];
@@ -277,28 +305,38 @@ __global__ void __launch_bounds__(256) add_layer_norm_kernel(Span sp, int hidden
         }
     }
     if (pre_norm) store_row<G, H>(v, hidden, row, nullptr);
-    ln_wave<G>(v, hidden, ln_w, ln_b, eps);
-    store_row<G, H>(v, hidden, pre_norm ? nullptr : row, out_h ? out_h + (size_t)t * hidden : nullptr);
+    ln_apply<G>(v, hidden, wv, bv, eps);
+    store_row<G, H>(v, hidden, pre_norm || !keep_f32 ? nullptr : row, hr);
     if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden, qo.scale + t);
 }
 
 template <typename H, int G, typename Y>
 static hipError_t add_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y,
                            const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h,
-                           const QuantOut &qo) {
-    hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp, hidden, x,
-                       (const Y *)y, ln_w, ln_b, eps, pre_norm, (H *)out_h, qo);
+                           const QuantOut &qo, bool res_h, bool keep_f32) {
+    if (res_h && sizeof(H) == 2)
+        hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H, sizeof(H) == 2>), dim3((tokens + 3) / 4), dim3(256), 0, s,
+                           sp, hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
+    else
+        hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H, false>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp,
+                           hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
     return hipGetLastError();
 }
 
 template <typename H, int G>
 static hipError_t add_ln_y(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y, Dt ydt,
                            const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h,
-                           const QuantOut &qo) {
+                           const QuantOut &qo, bool res_h, bool keep_f32) {
     switch (ydt) {
-    case Dt::F16: return add_ln_v<H, G, _Float16>(s, sp, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
-    case Dt::BF16: return add_ln_v<H, G, __bf16>(s, sp, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
-    case Dt::F32: return add_ln_v<H, G, float>(s, sp, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::F16:
+        return add_ln_v<H, G, _Float16>(s, sp, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo, res_h,
+                                        keep_f32);
+    case Dt::BF16:
+        return add_ln_v<H, G, __bf16>(s, sp, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo, res_h,
+                                      keep_f32);
+    case Dt::F32:
+        return add_ln_v<H, G, float>(s, sp, tokens, hidden, x, y, ln_w, ln_b, eps, pre_norm, out_h, qo, res_h,
+                                     keep_f32);
     default: return hipErrorInvalidValue;
     }
 }
@@ -354,8 +392,8 @@ static hipError_t ln_t(hipStream_t s, const Span &sp, int tokens, int hidden, co
 template <typename H>
 static hipError_t add_ln_t(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y, Dt ydt,
                            const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h,
-                           const QuantOut &qo) {
-    ROWWISE_DISPATCH(add_ln_y, s, sp, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo)
+                           const QuantOut &qo, bool res_h, bool keep_f32) {
+    ROWWISE_DISPATCH(add_ln_y, s, sp, tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo, res_h, keep_f32)
 }
 
 hipError_t embed_ln(hipStream_t s, const Span &sp, int max_tokens, int hidden, const int32_t *ids,
@@ -379,13 +417,22 @@ hipError_t embed_ln(hipStream_t s, const Span &sp, int max_tokens, int hidden, c
 
 hipError_t add_layer_norm(hipStream_t s, const Span &sp, int max_tokens, int hidden, float *x, const void *y, Dt ydt,
                           const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h, Dt dt,
-                          const QuantOut &qo) {
+                          const QuantOut &qo, bool res_h, bool keep_f32) {
     if (max_tokens <= 0) return hipSuccess;
     if (qo.q && (dt != Dt::F16 || !out_h || hidden % 4 != 0)) return hipErrorInvalidValue;
+    // A 16-bit residual is a post-norm's, read from and written to out_h.
+    if (res_h && (dt == Dt::F32 || !out_h || pre_norm)) return hipErrorInvalidValue;
+    if (!keep_f32 && !res_h) return hipErrorInvalidValue;
     switch (dt) {
-    case Dt::F16: return add_ln_t<_Float16>(s, sp, max_tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
-    case Dt::BF16: return add_ln_t<__bf16>(s, sp, max_tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
-    default: return add_ln_t<float>(s, sp, max_tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo);
+    case Dt::F16:
+        return add_ln_t<_Float16>(s, sp, max_tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo, res_h,
+                                  keep_f32);
+    case Dt::BF16:
+        return add_ln_t<__bf16>(s, sp, max_tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo, res_h,
+                                keep_f32);
+    default:
+        return add_ln_t<float>(s, sp, max_tokens, hidden, x, y, ydt, ln_w, ln_b, eps, pre_norm, out_h, qo, res_h,
+                               keep_f32);
     }
 }
 

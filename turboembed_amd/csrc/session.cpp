@@ -1061,6 +1061,16 @@ static Bounds bounds_of(const Session &s, int b, uint32_t parts) {
     return o;
 }
 
+// Post-norm F16 sessions carry the residual stream between a layer's norms
+// in the 16-bit GEMM operand rows (xh) alone: each add + LayerNorm reads 2
+// bytes of residual and writes 2 an element, where F32 rows would take 4
+// and 4 more (the products read the 16-bit rows either way; the sum x + y
+// is now taken from them too). The F32 rows are written where they are
+// read: after the last layer, and after a layer whose ranges are read.
+// BF16 keeps F32 rows (8 bits of mantissa would carry the residual too
+// coarsely), as do pre-norm models, whose residual no norm bounds.
+static bool residual_in_operand(const Session &s) { return s.act == Dt::F16 && !s.model->modern; }
+
 // The layers over part `part` of the run's rows, on stream st: every
 // product, norm and attention launch reads that part's rows and tokens from
 // the run's dimensions. Layer reads pool their ranges as they pass.
@@ -1112,6 +1122,7 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
     // The GEMM operand copy of x after an add + LayerNorm: xh, or on the F32
     // tier x itself (post-norm) or xh as F32 (pre-norm).
     void *norm_out = f32 && !m.modern ? nullptr : s.xh;
+    const bool res_h = residual_in_operand(s);
     // Layers run: every one, or through the one read alone (a model cut
     // after it). Ranges are pooled after each of the last `reads` layers run
     // into block k of the output, [reads, count, output_dim], the final
@@ -1145,17 +1156,20 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
             LAUNCH("add_layer_norm",
                    add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt, qo));
         else
-            LAUNCH("add_layer_norm",
-                   add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out, dt, qo));
+            LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out,
+                                                    dt, qo, res_h, !res_h));
         aq_ready = i8;
         mm(l, G_FFN1);
         mm(l, G_FFN2);
         // Post-norm: x = LN2(x + y). Pre-norm: x += y and the next layer's
         // attention norm into xh, or after the last layer x = LN_final(x + y).
         const QuantOut next = l + 1 < nl ? qo : QuantOut();
+        // A 16-bit residual writes the F32 rows where they are read: after
+        // the last layer, and after a layer whose ranges are read.
+        const bool keep_f32 = !res_h || l + 1 == nl || (reads > 1 && l + reads >= nl);
         if (!m.modern)
-            LAUNCH("add_layer_norm",
-                   add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out, dt, next));
+            LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out,
+                                                    dt, next, res_h, keep_f32));
         else if (l + 1 < nl)
             LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps,
                                                     1, norm_out, dt, next));
@@ -1198,8 +1212,10 @@ static void encode(Session &s, const Bounds &bd, bool sequential) {
         tm.end();          \
     } while (0)
     LAUNCH("pack_rows", pack_rows(st, s.mask, s.dims_dev, (int)s.max_batch, s.pk));
+    // (A 16-bit residual starts in xh alone.)
     LAUNCH("embed_ln", embed_ln(st, whole, (int)bd.tokens, H, s.ids, s.types, s.pk, (int)m.position_offset, m.word,
-                                m.pos, m.type, m.emb_w, m.emb_b, m.eps, s.x, f32 ? nullptr : s.xh, dt,
+                                m.pos, m.type, m.emb_w, m.emb_b, m.eps, residual_in_operand(s) ? nullptr : s.x,
+                                f32 ? nullptr : s.xh, dt,
                                 m.deberta ? s.mask : nullptr));
     // ModernBERT's first layer reads the embeddings' rows as they are (no
     // attention norm); on the F32 tier xh is the pre-norm rows' F32 copy.
