@@ -52,25 +52,36 @@ def tail_bytes(shape, dtype, tokens, rows, od):
     written once (a table row once per token that reads it).
 
     embed_ln per token: the word row in F32, the ids (and types), x written
-    in F32 and its 16-bit operand copy; off the rotary families the position
-    and type rows once a run (they stay in L2). add_layer_norm per token: x and the product y read,
-    x written, and the normalized operand copy (16-bit, or F32 on a
-    pre-norm F32 session) except on post-norm F32 sessions and after a
-    pre-norm model's last layer. pool: each pooled token's F32 row (one per
-    output row for CLS and LAST), then the output rows."""
+    in F32 (not on post-norm F16 and int8 sessions, whose residual starts in
+    the 16-bit rows) and its 16-bit operand copy; off the rotary families the
+    position and type rows once a run (they stay in L2). add_layer_norm per
+    token: the residual and the product y read, the normalized rows written.
+    Post-norm F16 and int8 sessions carry the residual in the 16-bit rows (2
+    bytes read and 2 written an element; the last layer's norm also writes F32
+    rows, and on int8 every norm feeding a product writes its int8 codes and
+    scale); others read and write x in F32 and write the normalized operand
+    copy (16-bit, or F32 on a pre-norm F32 session) except on post-norm F32
+    sessions and after a pre-norm model's last layer. pool: each pooled
+    token's F32 row (one per output row for CLS and LAST), then the output
+    rows."""
     H = shape.hidden
     modern = shape.family == S.TURBO_FAMILY_MODERNBERT
     act = 4 if dtype == "f32" else 2
-    ysz = 2 if dtype == "f16" and shape.rope is None else 4
+    ysz = 2 if dtype in ("f16", "i8") and shape.rope is None else 4
+    res16 = dtype in ("f16", "i8") and not modern
+    codes = H + 4 if dtype == "i8" else 0
     # The word row comes from HBM once a token; the position and type rows
     # are few and stay in L2 (counted once a run).
     rotary = shape.rope is not None
     ids = 4 if rotary else 8
     shared = 0 if rotary else (min(shape.seq, shape.positions) + shape.token_types) * 4 * H
-    out = {"embed_ln": tokens * (4 * H + ids + 4 * H + (0 if dtype == "f32" else act * H)) + shared}
+    out = {"embed_ln": tokens * (4 * H + ids + (0 if res16 else 4 * H) + (0 if dtype == "f32" else act * H) + codes)
+           + shared}
     L = shape.layers
     if modern:
         out["add_layer_norm"] = tokens * ((2 * L - 1) * (8 * H + ysz * H + act * H) + (8 * H + ysz * H))
+    elif res16:
+        out["add_layer_norm"] = tokens * (2 * L * (4 * H + ysz * H) + 4 * H + (2 * L - 1) * codes)
     else:
         out["add_layer_norm"] = tokens * 2 * L * (8 * H + ysz * H + (0 if dtype == "f32" else act * H))
     pooled = rows if shape.pooling in (S.TURBO_POOLING_CLS, S.TURBO_POOLING_LAST) and not shape.ranges_per_row \
