@@ -102,27 +102,39 @@ def summarize_pmc(fetch_dir, write_dir, workload, command):
     run) from two rocprofv3 --pmc runs of this script with --copy-probe
     (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
     same counter read for the plain copy of COPY_PROBE_BYTES; written to
-    profiles/traffic_<workload>.json and .md."""
+    profiles/traffic_<workload>.json and .md. Also per product: the run
+    launches each layer's products in the order QKV, out, FFN-in, FFN-out, so
+    its GEMM dispatches, in dispatch order, take those names in turn; each
+    product's algorithmic bytes (operands read once, output written once) are
+    for launches over tokens / parts rows (the default split)."""
     import csv
     import glob
 
-    def per_kernel(d, counter):
-        vals = {}
+    def per_dispatch(d, counter):
+        rows = []
         for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             for r in csv.DictReader(open(f)):
                 if r["Counter_Name"] == counter:
-                    vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
-        return vals
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+        return sorted(rows)
 
+    shape = W.SHAPES[workload]
+    H, I = shape.hidden, shape.intermediate
+    gated = shape.family == S.TURBO_FAMILY_MODERNBERT
+    el = 4 if shape.precision == S.TURBO_PRECISION_EXACT else 2
+    # Whole-row batches of the embedding task only (every launch's rows known).
+    M = shape.batch * shape.seq // 2 if shape.lengths is None and shape.task == S.TURBO_TASK_EMBED else None
+    products = [("qkv", H, 3 * H), ("out", H, H), ("ffn_in", H, (2 if gated else 1) * I), ("ffn_out", I, H)]
     out = {"workload": workload, "command": command, "copy_probe_bytes": COPY_PROBE_BYTES}
     lines = [f"# HBM traffic per launch: {workload}", "", "Commands (from the repository root, one MI355X):", "",
              "```", *command, "```", "",
              "| counter | copy probe reads (KiB/dispatch) | expected KiB | factor | GEMM kernel KiB/dispatch (mean) "
              "| scaled bytes/launch | dispatches |", "|---|---|---|---|---|---|---|"]
+    by_product = {}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
-        v = per_kernel(d, counter)
-        copy = [x for k, xs in v.items() if "copy_kernel" in k for x in xs]
-        gemm = [x for k, xs in v.items() if "gemm_lds_kernel" in k for x in xs]
+        v = per_dispatch(d, counter)
+        copy = [x for _, k, x in v if "copy_kernel" in k]
+        gemm = [x for _, k, x in v if "gemm_lds_kernel" in k]
         expected = COPY_PROBE_BYTES / 1024.0
         factor = expected / (sum(copy) / len(copy))
         mean = sum(gemm) / len(gemm)
@@ -130,8 +142,30 @@ def summarize_pmc(fetch_dir, write_dir, workload, command):
                         "gemm_bytes": mean * 1024.0 * factor, "dispatches": len(gemm)}
         lines.append(f"| {counter} | {sum(copy) / len(copy):.0f} | {expected:.0f} | {factor:.4f} | {mean:.0f} | "
                      f"{mean * 1024.0 * factor:.4g} | {len(gemm)} |")
+        for i, x in enumerate(gemm):
+            by_product.setdefault(products[i % 4][0], {}).setdefault(counter, []).append(x * 1024.0 * factor)
     out["traffic_bytes_per_launch"] = out["FETCH_SIZE"]["gemm_bytes"] + out["WRITE_SIZE"]["gemm_bytes"]
-    lines += ["", f"Traffic per GEMM launch (fetch + write, scaled): {out['traffic_bytes_per_launch']:.4g} bytes."]
+    lines += ["", f"Traffic per GEMM launch (fetch + write, scaled): {out['traffic_bytes_per_launch']:.4g} bytes.", ""]
+    if M:
+        lines += [f"Per product (launches over M = {M} rows; algorithmic: A = M·K and W = N·K read once, the "
+                  f"M·N output written once, {el}-byte operands and outputs):", "",
+                  "| product | N | K | fetched MB | algorithmic reads MB | ratio | written MB | algorithmic writes MB "
+                  "| ratio |", "|---|---|---|---|---|---|---|---|---|"]
+        out["products"] = {}
+        alg_total = 0.0
+        for name, K, N in products:
+            f = by_product.get(name, {}).get("FETCH_SIZE", [0.0])
+            w = by_product.get(name, {}).get("WRITE_SIZE", [0.0])
+            fm, wm = sum(f) / len(f), sum(w) / len(w)
+            nout = N // 2 if name == "ffn_in" and gated else N
+            ar, aw = (M * K + N * K) * el, M * nout * el
+            alg_total += ar + aw
+            out["products"][name] = {"fetch_bytes": fm, "write_bytes": wm, "alg_read_bytes": ar, "alg_write_bytes": aw}
+            lines.append(f"| {name} | {N} | {K} | {fm / 1e6:.1f} | {ar / 1e6:.1f} | {fm / ar:.2f} | {wm / 1e6:.1f} | "
+                         f"{aw / 1e6:.1f} | {wm / aw:.2f} |")
+        out["alg_bytes_per_launch"] = alg_total / 4
+        lines += ["", f"Algorithmic bytes per launch (mean of the four): {alg_total / 4:.4g}; traffic / algorithmic: "
+                  f"{out['traffic_bytes_per_launch'] / (alg_total / 4):.2f}."]
     with open(traffic_file(workload), "w") as f:
         json.dump(out, f, indent=1)
     with open(traffic_file(workload)[:-5] + ".md", "w") as f:
