@@ -218,7 +218,11 @@ template <int N> __device__ __forceinline__ void att_wait_vmcnt() {
 // exactly 0 (the session zeroes Q, K and V once, so every value read is
 // finite). Each block's live keys are a 64-bit mask, the same for the whole
 // workgroup.
-template <typename T, int D, int QT>
+// WIN: a sliding window (window < INT32_MAX). Without one, every sub-block
+// of a live wave has work, and the score products run unconditionally (a
+// wave past its row's end computes scores it never uses): with no path that
+// skips them, their registers need no zeroing for one.
+template <typename T, int D, int QT, bool WIN>
 __global__ void __launch_bounds__(64 * (256 / (32 * QT))) attention_mfma_kernel(const T *__restrict__ qkv, int tcap,
                                                                                int heads, Span sp, int nqb, Packing p,
                                                                                const int32_t *__restrict__ mask,
@@ -376,7 +380,7 @@ __global__ void __launch_bounds__(64 * (256 / (32 * QT))) attention_mfma_kernel(
             floatx16_t a[QT];
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) a[qt] = floatx16_t{};
-            if (work[sub]) {
+            if (!WIN || work[sub]) {
                 const int row = sub * 32 + swap23(ql);
 #pragma unroll
                 for (int s = 0; s < D / 16; ++s) {
@@ -403,7 +407,6 @@ __global__ void __launch_bounds__(64 * (256 / (32 * QT))) attention_mfma_kernel(
             float mx[QT];
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
-                mx[qt] = -INFINITY;
                 if (!all_live) {
                     // This lane's live keys in reach as a mask over the
                     // sub-block; register rr holds key 8 h + j, j = 16 (rr / 8) + rr % 8.
@@ -426,9 +429,11 @@ __global__ void __launch_bounds__(64 * (256 / (32 * QT))) attention_mfma_kernel(
                         sc[qt][rr] = (word >> j) & 1u ? sc[qt][rr] : -INFINITY;
                     }
                 }
+                // A chain of three-input maxima (v_max3_f32: 8 for 16 scores).
+                float m = fmaxf(fmaxf(sc[qt][0], sc[qt][1]), sc[qt][2]);
 #pragma unroll
-                for (int rr = 0; rr < 16; rr += 2) mx[qt] = fmaxf(mx[qt], fmaxf(sc[qt][rr], sc[qt][rr + 1]));
-                mx[qt] = max_across_halves(mx[qt]);
+                for (int rr = 3; rr < 16; rr += 2) m = fmaxf(fmaxf(m, sc[qt][rr]), rr + 1 < 16 ? sc[qt][rr + 1] : m);
+                mx[qt] = max_across_halves(m);
             }
             // Every lane runs the same instructions below (the matrix cores
             // take the whole wave): a query with nothing live in reach yet adds
@@ -518,8 +523,12 @@ static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int
     // 64 at most 63 before the row's, so ceil(max_len / 64) + 1 blocks).
     const int bytes = 3 * 2 * 64 * 64 * 2 + ((max_len + 127) / 64) * 8;
     if (bytes > 160 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT>), dim3(blocks), dim3(64 * (256 / (32 * ATT_QT))), bytes, s,
-                       (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
+    if (window < INT32_MAX)
+        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, true>), dim3(blocks), dim3(64 * (256 / (32 * ATT_QT))),
+                           bytes, s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
+    else
+        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, false>), dim3(blocks), dim3(64 * (256 / (32 * ATT_QT))),
+                           bytes, s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
     return hipGetLastError();
 }
 
