@@ -662,11 +662,13 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     s->ctxb = alloc(s->tcap * H * el, "session context");
     s->ffn = alloc(s->tcap * I * el, "session ffn");
     // The out and FFN-out products go to y and are added to x by the
-    // LayerNorm that follows: in F16 on F16 post-norm sessions (the
-    // reference's CUDA backend adds an F16 product, core/cuda/kernels.cu:466-509),
-    // in F32 on the other tiers and on the rotary families (the reference's
-    // ModernBERT needs the F32 product, core/cuda/backend.cpp:2319-2324).
-    s->ydt = s->act == Dt::F16 && !m->rotary ? Dt::F16 : Dt::F32;
+    // LayerNorm that follows: in the operand type on 16-bit post-norm
+    // sessions (the reference's CUDA backend adds an F16 product,
+    // core/cuda/kernels.cu:466-509; a BF16 product rounds at 2^-9 of itself,
+    // and the sum and its norm stay F32), in F32 on the F32 tier and on the
+    // rotary families (the reference's ModernBERT needs the F32 product,
+    // core/cuda/backend.cpp:2319-2324).
+    s->ydt = (s->act == Dt::F16 || s->act == Dt::BF16) && !m->rotary ? s->act : Dt::F32;
     s->y = alloc(s->tcap * H * dt_bytes(s->ydt), "session products");
     if (dt == Dt::I8) {
         s->aq = static_cast<int8_t *>(alloc(s->tcap * std::max(H, I), "session int8 operand"));
