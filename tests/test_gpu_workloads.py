@@ -2,7 +2,7 @@
 against the oracle at each tier's floor, through the C ABI.
 
 Each encoder runs at full width on a cut depth, so the oracle's share stays
-at seconds: XLM-R-large (BF16; RoBERTa positions from offset 2; 4096-token
+at seconds (BERT-base, the headline, at its full 12 layers on 10 rows): XLM-R-large (BF16; RoBERTa positions from offset 2; 4096-token
 rows with 64 ranges each), ModernBERT-base (F16; an 8192-token row, RoPE
 to position 8191, a global layer and two local ones), and the int8
 BERT-base cross-encoder at its full 12 layers, whose scores are held to the
@@ -65,6 +65,34 @@ def _sharpened(desc, qk_std=0.05, out_std=0.2, seed=0):
 
 def _whole_rows(mask):
     return [(r, 0, int(mask[r].nonzero()[0].max()) + 1) for r in range(mask.shape[0])]
+
+
+@pytest.mark.parametrize("sharp", [False, True])
+def test_bert_base_full_depth_meets_the_oracle(context, sharp):
+    # C2 at all 12 layers in the F16 tier: 8 whole 512-token rows and 2 of
+    # U[64, 512], more than 4096 tokens, so the run splits into two parts on
+    # its bin's graph and carries its residual in the 16-bit rows. CLS + L2
+    # (the benchmark's pooling) and MEAN, each within F16's floor of the
+    # oracle.
+    sh = W.SHAPES["bert-base"]
+    desc = W.model(sh)
+    if sharp:
+        desc = _sharpened(desc, seed=2)
+    a = W.rows(sh, batch=8, lengths=None, seed=7)
+    b = W.rows(sh, batch=2, lengths=(64, sh.seq), seed=8)
+    ids, mask, types = (np.concatenate([x, y]) for x, y in zip(a, b))
+    assert mask.sum() > 4096
+    print(f"bert-base rows of {mask.sum(1).tolist()} tokens, 12 layers, sharpened {sharp}", flush=True)
+    model = context.load(desc)
+    s = model.session(sh.batch, sh.seq, sh.precision)
+    assert s.compute_dtype == S.TURBO_DTYPE_F16
+    for pooling, normalize in ((sh.pooling, sh.normalize), (MEAN, NONE)):
+        got = s.embed(ids, mask, types, pooling=pooling, normalize=normalize)
+        want = oracle.encode(desc, ids, mask, types, pooling=pooling, normalize=normalize)
+        print(f"  pooling {pooling}: min cosine {small.cosine_rows(got, want).min():.7f}", flush=True)
+        assert_close(got, want, s.compute_dtype)
+    s.close()
+    model.close()
 
 
 @pytest.mark.parametrize("sharp", [False, True])
