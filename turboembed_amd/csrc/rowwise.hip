@@ -310,10 +310,178 @@ __global__ void __launch_bounds__(256) add_layer_norm_kernel(Span sp, int hidden
     if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden, qo.scale + t);
 }
 
+// Eight consecutive columns at p, as F32.
+template <typename H> __device__ __forceinline__ void load8(const H *p, float (&v)[8]) {
+    typedef H h8 __attribute__((ext_vector_type(8)));
+    const h8 q = *(const h8 *)p;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = to_f32(q[k]);
+}
+__device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
+    const float4_t a = *(const float4_t *)p, b = *(const float4_t *)(p + 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = a[k], v[4 + k] = b[k];
+}
+template <typename H> __device__ __forceinline__ void store8(H *p, const float (&v)[8]) {
+    typedef H h8 __attribute__((ext_vector_type(8)));
+    h8 q;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) q[k] = from_f32<H>(v[k]);
+    *(h8 *)p = q;
+}
+__device__ __forceinline__ void store8(float *p, const float (&v)[8]) {
+    *(float4_t *)p = float4_t{v[0], v[1], v[2], v[3]};
+    *(float4_t *)(p + 4) = float4_t{v[4], v[5], v[6], v[7]};
+}
+
+// The sum over a 32-lane half of the wave.
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// A half-wave row's norm weight and bias (0 where absent), 8 columns a lane
+// in each group of 256.
+template <int G>
+__device__ __forceinline__ void load_wb8(const float *__restrict__ w, const float *__restrict__ b, int hidden, int hl,
+                                         float (&wv)[G][8], float (&bv)[G][8]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int c = 8 * (hl + 32 * g);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) wv[g][k] = bv[g][k] = 0.0f;
+        if (c >= hidden) continue;
+        load8(w + c, wv[g]);
+        if (b) load8(b + c, bv[g]);
+    }
+}
+
+// A half-wave row normalized, (v - mean) / sqrt(var + eps) * w + b.
+template <int G>
+__device__ __forceinline__ void ln_pair_apply(float (&v)[G][8], int hidden, int hl, const float (&wv)[G][8],
+                                              const float (&bv)[G][8], float eps) {
+    float s = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) s += v[g][k] + v[g][k + 1];
+    const float mean = half_sum(s) / (float)hidden;
+    float q = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        if (8 * (hl + 32 * g) < hidden)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float c = v[g][k] - mean;
+                q = fmaf(c, c, q);
+            }
+    const float inv = 1.0f / sqrtf(half_sum(q) / (float)hidden + eps);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[g][k] = (v[g][k] - mean) * inv * wv[g][k] + bv[g][k];
+}
+
+// add_layer_norm_kernel's work two rows a wave: each 32-lane half takes a
+// row, 8 consecutive columns a lane in each group of 256 (16-byte reads and
+// writes of 16-bit rows, where a wave a row moves 8 bytes a lane), and the
+// norm's weight and bias, read first, serve both rows. Hidden a multiple
+// of 8.
+template <int G, typename Y, typename H, bool RES_H>
+__global__ void __launch_bounds__(256) add_ln_pair_kernel(Span sp, int hidden, float *__restrict__ x,
+                                                          const Y *__restrict__ y, const float *__restrict__ ln_w,
+                                                          const float *__restrict__ ln_b, float eps, int pre_norm,
+                                                          int keep_f32, H *__restrict__ out_h, QuantOut qo) {
+    const Live lv = live_of(sp);
+    const int local = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1);
+    // (A half's lanes all share its row; the sums stay within the half.)
+    if (local >= lv.tokens) return;
+    const int t = lv.tok0 + local;
+    const int hl = threadIdx.x & 31;
+    float *row = x + (size_t)t * hidden;
+    const Y *yr = y + (size_t)t * hidden;
+    H *hr = out_h ? out_h + (size_t)t * hidden : nullptr;
+    float wv[G][8], bv[G][8];
+    load_wb8<G>(ln_w, ln_b, hidden, hl, wv, bv);
+    float v[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int c = 8 * (hl + 32 * g);
+        if (c < hidden) {
+            float a[8];
+            if constexpr (RES_H) load8(hr + c, v[g]);
+            else load8(row + c, v[g]);
+            load8(yr + c, a);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[g][k] = v[g][k] + a[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[g][k] = 0.0f;
+        }
+    }
+    if (pre_norm)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            if (8 * (hl + 32 * g) < hidden) store8(row + 8 * (hl + 32 * g), v[g]);
+    ln_pair_apply<G>(v, hidden, hl, wv, bv, eps);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int c = 8 * (hl + 32 * g);
+        if (c >= hidden) continue;
+        if (!pre_norm && keep_f32) store8(row + c, v[g]);
+        if (hr) store8(hr + c, v[g]);
+    }
+    if (qo.q) {
+        // The row's int8 codes from its values as rounded to H, as quant_row.
+        int8_t *qr = qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden;
+        float r[G][8], mx = 0.0f;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                r[g][k] = 8 * (hl + 32 * g) < hidden ? to_f32(from_f32<H>(v[g][k])) : 0.0f;
+                mx = fmaxf(mx, fabsf(r[g][k]));
+            }
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        const float iv = mx > 0.0f ? 127.0f / mx : 0.0f;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int c = 8 * (hl + 32 * g);
+            if (c >= hidden) continue;
+            uint32_t w[2] = {0, 0};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int code = (int)fminf(fmaxf(rintf(r[g][k] * iv), -127.0f), 127.0f);
+                w[k >> 2] |= (uint32_t)(uint8_t)(int8_t)code << (8 * (k & 3));
+            }
+            *(uint2 *)(qr + c) = uint2{w[0], w[1]};
+        }
+        if (hl == 0) qo.scale[t] = mx / 127.0f;
+    }
+}
+
 template <typename H, int G, typename Y>
 static hipError_t add_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y,
                            const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h,
                            const QuantOut &qo, bool res_h, bool keep_f32) {
+    // Two rows a wave on 16-bit products (measured: BERT-base's norms 6%
+    // faster; on F32 products and rows, ModernBERT's, 2% slower). A run
+    // whose norms take F32 products keeps one layout for all of them, as a
+    // layer read's final norm (layer_norm) must give the bits of the fused one.
+    if constexpr (sizeof(Y) == 2) {
+        if (hidden % 8 == 0) {
+            if (res_h && sizeof(H) == 2)
+                hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, sizeof(H) == 2>), dim3((tokens + 7) / 8), dim3(256), 0,
+                                   s, sp, hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h,
+                                   qo);
+            else
+                hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, false>), dim3((tokens + 7) / 8), dim3(256), 0, s, sp,
+                                   hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
+            return hipGetLastError();
+        }
+    }
     if (res_h && sizeof(H) == 2)
         hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H, sizeof(H) == 2>), dim3((tokens + 3) / 4), dim3(256), 0, s,
                            sp, hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
