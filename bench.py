@@ -67,7 +67,7 @@ def tail_bytes(shape, dtype, tokens, rows, od):
     H = shape.hidden
     modern = shape.family == S.TURBO_FAMILY_MODERNBERT
     act = 4 if dtype == "f32" else 2
-    ysz = 2 if dtype in ("f16", "bf16", "i8") and shape.rope is None else 4
+    ysz = 2 if dtype in ("f16", "bf16", "i8") else 4
     res16 = dtype in ("f16", "i8") and not modern
     codes = H + 4 if dtype == "i8" else 0
     # The word row comes from HBM once a token; the position and type rows

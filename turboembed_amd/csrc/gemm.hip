@@ -129,6 +129,7 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
             if constexpr (KIND == Epi::Plain) ((float *)e.out)[at] = v;
             else if constexpr (KIND == Epi::Bias) {
                 if (e.out_f32) ((float *)e.out)[at] = v;
+                else if (sizeof(T) == 2 && e.out_bf16) ((__bf16 *)e.out)[at] = from_f32<__bf16>(v);
                 else ((T *)e.out)[at] = from_f32<T>(v);
             }
             else if constexpr (KIND == Epi::Gelu)
@@ -596,8 +597,12 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                                                                           __float_as_uint(v[6]), __float_as_uint(v[7])},
                                                                   rs, ok ? off + 16 : OOB, 0, 0);
                         } else {
-                            __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs,
-                                                                  ok ? (rm * e.ldo + n) * (int)sizeof(T) : OOB, 0, 0);
+                            // (out_bf16 is the launch's: a uniform branch.)
+                            const int off = ok ? (rm * e.ldo + n) * (int)sizeof(T) : OOB;
+                            if (sizeof(T) == 2 && e.out_bf16)
+                                __builtin_amdgcn_raw_buffer_store_b128(pack8<__bf16>(v), rs, off, 0, 0);
+                            else
+                                __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs, off, 0, 0);
                         }
                     } else if constexpr (KIND == Epi::Gelu) {
 #pragma unroll
@@ -670,6 +675,10 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                     } else {
                         for (int q = 0; n + q < N; ++q) o[q] = v[q];
                     }
+                } else if (sizeof(T) == 2 && e.out_bf16) {
+                    __bf16 *o = (__bf16 *)e.out + (size_t)m * e.ldo + n;
+                    if (full) store8<__bf16>(o, v);
+                    else for (int q = 0; n + q < N; ++q) o[q] = from_f32<__bf16>(v[q]);
                 } else {
                     T *o = (T *)e.out + (size_t)m * e.ldo + n;
                     if (full) store8<T>(o, v);

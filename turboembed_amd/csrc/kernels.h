@@ -141,6 +141,7 @@ struct EpiArgs {
     const int32_t *pos = nullptr;  // QkvRope: each packed token's position in its row
     int silu = 0;                  // Gated: SiLU instead of GELU
     int out_f32 = 0;               // Bias: F32 outputs (else the operand type; F16 for int8 operands)
+    int out_bf16 = 0;              // Bias on F16 operands: BF16 outputs (F32's range at half its bytes)
     // I8 operands: output (m, n) is the int32 sum times a_scale[m] * w_scale[n].
     const float *a_scale = nullptr, *w_scale = nullptr;
 };

@@ -466,19 +466,14 @@ template <typename H, int G, typename Y>
 static hipError_t add_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y,
                            const float *ln_w, const float *ln_b, float eps, int pre_norm, void *out_h,
                            const QuantOut &qo, bool res_h, bool keep_f32) {
-    // Two rows a wave on 16-bit products (measured: BERT-base's norms 6%
-    // faster; on F32 products and rows, ModernBERT's, 2% slower). A run
-    // whose norms take F32 products keeps one layout for all of them, as a
-    // layer read's final norm (layer_norm) must give the bits of the fused one.
-    if constexpr (sizeof(Y) == 2) {
-        if (hidden % 8 == 0) {
-            if (res_h && sizeof(H) == 2)
-                hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, sizeof(H) == 2>), dim3((tokens + 7) / 8), dim3(256), 0,
-                                   s, sp, hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h,
-                                   qo);
-            else
-                hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, false>), dim3((tokens + 7) / 8), dim3(256), 0, s, sp,
-                                   hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
+    // Two rows a wave on the 16-bit residual (measured: BERT-base's norms 6%
+    // faster; on F32 rows, ModernBERT's, 2% slower). Other runs keep one
+    // layout for all their norms: a layer read's final norm (layer_norm)
+    // must give the bits of the fused one.
+    if constexpr (sizeof(Y) == 2 && sizeof(H) == 2) {
+        if (res_h && hidden % 8 == 0) {
+            hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, true>), dim3((tokens + 7) / 8), dim3(256), 0, s, sp, hidden,
+                               x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
             return hipGetLastError();
         }
     }

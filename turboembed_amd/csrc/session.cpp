@@ -665,11 +665,14 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     // LayerNorm that follows: in the operand type on 16-bit post-norm
     // sessions (the reference's CUDA backend adds an F16 product,
     // core/cuda/kernels.cu:466-509; a BF16 product rounds at 2^-9 of itself,
-    // and the sum and its norm stay F32), in F32 on the F32 tier and on the
-    // rotary families (the reference's ModernBERT needs the F32 product,
-    // core/cuda/backend.cpp:2319-2324).
-    s->ydt = (s->act == Dt::F16 || s->act == Dt::BF16) && !m->rotary ? s->act : Dt::F32;
-    s->y = alloc(s->tcap * H * dt_bytes(s->ydt), "session products");
+    // and the sum and its norm stay F32); in BF16 on the 16-bit rotary
+    // families, whose gated FFN sums can pass F16's 65504 (the reference
+    // takes them in F32 for that, core/cuda/backend.cpp:2319-2324; BF16 has
+    // F32's range at half its bytes); in F32 on the F32 tier. A rotary
+    // family's y also holds a layer read's F32 final norm, so it keeps 4
+    // bytes an element.
+    s->ydt = s->act == Dt::F32 ? Dt::F32 : m->rotary ? Dt::BF16 : s->act;
+    s->y = alloc(s->tcap * H * (m->rotary ? 4 : dt_bytes(s->ydt)), "session products");
     if (dt == Dt::I8) {
         s->aq = static_cast<int8_t *>(alloc(s->tcap * std::max(H, I), "session int8 operand"));
         s->ascale = static_cast<float *>(alloc(s->tcap * 4, "session int8 scales"));
@@ -1023,6 +1026,7 @@ static LayerGemm layer_gemm(Session &s, uint32_t l, GemmSlot g) {
         r.e.out = s.y;
         r.e.ldo = H;
         r.e.out_f32 = s.ydt == Dt::F32 ? 1 : 0;
+        r.e.out_bf16 = s.ydt == Dt::BF16 && s.act == Dt::F16 ? 1 : 0;
         break;
     default:
         r.N = (int)L.n_in;
