@@ -150,11 +150,13 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
                 // the neighbouring lane (column n sits in lane n % 32).
                 const float w = __shfl_xor(v, 1, 64);
                 if (which < 2 && col_ok && m < M) {
+                    // Rounded products, then their sum or difference, in
+                    // every instantiation (no fused multiply-add).
+#pragma clang fp contract(off)
                     const int pos = e.pos[e.tok0 + m];
                     const float cs = e.cos[(size_t)pos * half + pr], sn = e.sin[(size_t)pos * half + pr];
                     // (x1, x2) -> (x1 cos - x2 sin, x2 cos + x1 sin)
-                    v = (c & 1) ? __fadd_rn(__fmul_rn(v, cs), __fmul_rn(w, sn))
-                                : __fsub_rn(__fmul_rn(v, cs), __fmul_rn(w, sn));
+                    v = (c & 1) ? v * cs + w * sn : v * cs - w * sn;
                 }
             }
             if (!col_ok || m >= M) continue;
@@ -354,10 +356,13 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // An int8 product's output: the int32 sum times both scales, plus the bias,
-// each step rounded on its own (no contraction), so every store path of the
-// epilogue gives the same bits.
+// each step rounded on its own, so every store path and block shape of the
+// epilogue gives the same bits. (The contraction pragma, with plain
+// operators: __fmul_rn and __fadd_rn still let the compiler fuse a product
+// into the add after inlining.)
 __device__ __forceinline__ float dequant(float acc, float as, float ws, float bias) {
-    return __fadd_rn(__fmul_rn(__fmul_rn(acc, as), ws), bias);
+#pragma clang fp contract(off)
+    return acc * as * ws + bias;
 }
 
 template <typename T>
@@ -625,13 +630,22 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                         head_col(n - qkv_base, e.d, head, c);
                         if constexpr (KIND == Epi::QkvRope) {
                             const int pos = e.pos[e.tok0 + min(m, M - 1)], hd = e.d >> 1;
+                            // The chunk's 4 pairs' angles: 16 aligned bytes of
+                            // each table (c is a multiple of 8, the tables' rows
+                            // of d / 2 floats start on 16 bytes).
+                            const size_t at = (size_t)pos * hd + (c >> 1);
+                            const float4_t cs4 = *(const float4_t *)(e.cos + at), sn4 = *(const float4_t *)(e.sin + at);
 #pragma unroll
                             for (int p = 0; p < 4; ++p) {
-                                const int pr = (c >> 1) + p;
-                                const float cs = e.cos[(size_t)pos * hd + pr], sn = e.sin[(size_t)pos * hd + pr];
+                                // Rounded products, then their difference or
+                                // sum, in every instantiation (no fused
+                                // multiply-add: split and unsplit runs launch
+                                // different block shapes).
+#pragma clang fp contract(off)
+                                const float cs = cs4[p], sn = sn4[p];
                                 const float x1 = v[2 * p], x2 = v[2 * p + 1];
-                                v[2 * p] = __fsub_rn(__fmul_rn(x1, cs), __fmul_rn(x2, sn));
-                                v[2 * p + 1] = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
+                                v[2 * p] = x1 * cs - x2 * sn;
+                                v[2 * p + 1] = x2 * cs + x1 * sn;
                             }
                         }
                         const int off = ok ? (int)((((size_t)head * e.tcap + e.tok0 + m) * e.d + c) * sizeof(T)) : OOB;
@@ -715,11 +729,13 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                     const int pos = e.pos[e.tok0 + m], half = e.d >> 1;
 #pragma unroll
                     for (int p = 0; p < 4; ++p) {
+                        // (Rounded products, as above.)
+#pragma clang fp contract(off)
                         const int pr = (c >> 1) + p;
                         const float cs = e.cos[(size_t)pos * half + pr], sn = e.sin[(size_t)pos * half + pr];
                         const float x1 = v[2 * p], x2 = v[2 * p + 1];
-                        v[2 * p] = __fsub_rn(__fmul_rn(x1, cs), __fmul_rn(x2, sn));
-                        v[2 * p + 1] = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
+                        v[2 * p] = x1 * cs - x2 * sn;
+                        v[2 * p + 1] = x2 * cs + x1 * sn;
                     }
                 }
                 const size_t t = (size_t)e.tok0 + m;
