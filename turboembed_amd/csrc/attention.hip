@@ -222,13 +222,13 @@ template <int N> __device__ __forceinline__ void att_wait_vmcnt() {
 // of a live wave has work, and the score products run unconditionally (a
 // wave past its row's end computes scores it never uses): with no path that
 // skips them, their registers need no zeroing for one.
-template <typename T, int D, int QT, bool WIN>
-__global__ void __launch_bounds__(64 * (256 / (32 * QT))) attention_mfma_kernel(const T *__restrict__ qkv, int tcap,
+template <typename T, int D, int QT, bool WIN, int QB, int STAGES>
+__global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(const T *__restrict__ qkv, int tcap,
                                                                                int heads, Span sp, int nqb, Packing p,
                                                                                const int32_t *__restrict__ mask,
                                                                                int window, T *__restrict__ ctx) {
-    // QT query tiles of 32 a wave, WAVES waves over a block of QB = 256 queries.
-    constexpr int WQ = 32 * QT, QB = 256, WAVES = QB / WQ, KB = 64, STAGES = 3;
+    // QT query tiles of 32 a wave, WAVES waves over a block of QB queries.
+    constexpr int WQ = 32 * QT, WAVES = QB / WQ, KB = 64;
     // Each block's K and V^T take 8 load instructions each (8 rows of 128
     // bytes an instruction), shared among the waves.
     constexpr int LPW = 8 / WAVES;
@@ -503,32 +503,40 @@ __global__ void __launch_bounds__(64 * (256 / (32 * QT))) attention_mfma_kernel(
     }
 }
 
-// Query tiles of 32 a wave (1: eight waves of 32 queries, the registers for
-// four waves a SIMD; 2: four waves of 64, each K and V fragment read from LDS
-// feeding two tiles).
+// Query tiles of 32 a wave (1: 32 queries a wave, the registers for four
+// waves a SIMD; 2: 64, each K and V fragment read from LDS feeding two
+// tiles); queries a workgroup (ATT_QB: 256, eight waves, or 128, four); LDS
+// ring stages.
 #ifndef ATT_QT
 #define ATT_QT 1
+#endif
+#ifndef ATT_QB
+#define ATT_QB 256
+#endif
+#ifndef ATT_STAGES
+#define ATT_STAGES 3
 #endif
 
 template <typename T>
 static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
                                    const int32_t *mask, const Span &sp, int max_rows, int max_len, int window,
                                    void *ctx) {
+    constexpr int QB = ATT_QB, STAGES = ATT_STAGES, THREADS = 64 * (QB / (32 * ATT_QT));
     // A 1-D grid of groups of 8 (row, head) pairs times nqb query blocks.
-    const int nqb = (max_len + 255) / 256, pairs = heads * max_rows;
+    const int nqb = (max_len + QB - 1) / QB, pairs = heads * max_rows;
     const int blocks = ((pairs + 7) / 8) * 8 * nqb;
     if (d != 64) return hipErrorInvalidValue;
-    // Three stages of K (64 x 64) and V^T (64 x 64) blocks, then a live mask
+    // STAGES stages of K (64 x 64) and V^T (64 x 64) blocks, then a live mask
     // per 64-key block a workgroup can reach (its keys start on a multiple of
     // 64 at most 63 before the row's, so ceil(max_len / 64) + 1 blocks).
-    const int bytes = 3 * 2 * 64 * 64 * 2 + ((max_len + 127) / 64) * 8;
+    const int bytes = STAGES * 2 * 64 * 64 * 2 + ((max_len + 127) / 64) * 8;
     if (bytes > 160 * 1024) return hipErrorInvalidValue;
     if (window < INT32_MAX)
-        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, true>), dim3(blocks), dim3(64 * (256 / (32 * ATT_QT))),
-                           bytes, s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
+        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, true, QB, STAGES>), dim3(blocks), dim3(THREADS), bytes,
+                           s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
     else
-        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, false>), dim3(blocks), dim3(64 * (256 / (32 * ATT_QT))),
-                           bytes, s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
+        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, false, QB, STAGES>), dim3(blocks), dim3(THREADS), bytes,
+                           s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
     return hipGetLastError();
 }
 

@@ -570,8 +570,17 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
         if constexpr (KIND != Epi::Residual) {
             if (fast) {
                 const bool f32 = KIND == Epi::Plain || e.out_f32;
+                // The rotary scatter stores its pass's chunks after the last
+                // one is made: each chunk reads its token's position and
+                // angles, and a load issued after a store waits for that
+                // store too (the vector memory counter retires in order).
+                // (Where the accumulators leave room: 128 registers a lane.)
+                constexpr bool DEFER = KIND == Epi::QkvRope && TM * TN * 16 <= 128;
+                constexpr int NK = PASS * CH / 64, NR = DEFER ? NK : 1;
+                u32x4_t rope_out[NR];
+                int rope_off[NR];
 #pragma unroll
-                for (int k = 0; k < PASS * CH / 64; ++k) {
+                for (int k = 0; k < NK; ++k) {
                     const int cc = ((lane + 64 * (k % PH)) % CH) * 8, n = nw + cc;
                     const float(&bias)[8] = cols.b[k % PH];
                     const float(&wsc)[8] = cols.w[k % PH];
@@ -649,9 +658,17 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                             }
                         }
                         const int off = ok ? (int)((((size_t)head * e.tcap + e.tok0 + m) * e.d + c) * sizeof(T)) : OOB;
-                        __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs, off, 0, 0);
+                        if constexpr (DEFER) {
+                            rope_out[k] = pack8<T>(v);
+                            rope_off[k] = off;
+                        } else {
+                            __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs, off, 0, 0);
+                        }
                     }
                 }
+                if constexpr (DEFER)
+#pragma unroll
+                    for (int k = 0; k < NK; ++k) __builtin_amdgcn_raw_buffer_store_b128(rope_out[k], rs, rope_off[k], 0, 0);
                 __builtin_amdgcn_wave_barrier();
                 continue;
             }
