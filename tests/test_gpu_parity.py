@@ -1007,14 +1007,14 @@ def test_fresh_ragged_batches_replay_their_bin_s_graph(context, family, monkeypa
     # bin replays that bin's graph with no capture, its kernels reading the
     # run's extent from the device, bit for bit the directly launched
     # kernels, with no host or device allocation. 16 rows of up to 320
-    # tokens reach four bins, the largest split into four parts.
+    # tokens reach four bins, the largest split into two parts.
     desc = small.bert(seed=43, hidden=128, heads=2, inter=256, positions=320, std=0.1) if family == "bert" else \
         small.modernbert(seed=43, hidden=128, heads=2, inter=192, positions=320, window=32, std=0.1)
     model = context.load(desc)
     batches = []
     g = np.random.Generator(np.random.PCG64(43))
     # (rows, columns, every column live): 5120, 4800 and 4100 live tokens
-    # take the split bin (four parts, then four of one and three rows).
+    # take the split bin (two parts).
     shapes = [(16, 320, True), (3, 40, False), (9, 300, False), (16, 300, True), (2, 256, False), (12, 320, False),
               (1, 5, False), (13, 316, True), (4, 320, True)]
     for k, (rows, seq, full) in enumerate(shapes):
