@@ -970,10 +970,10 @@ def test_a_bad_choices_string_is_refused(context, monkeypatch):
 
 # ---- Runs replayed from HIP graphs --------------------------------------------------------
 #
-# A run's launches are captured once per run shape and replayed: every
-# replay, with the host's own work (the rows' writes and the reads' syncs)
-# between them, gives the eager launches' vectors bit for bit, for two
-# shapes alternating in one session.
+# Each token bin's launches are captured once, at session_open, and
+# replayed for every run of the bin: every replay, with the host's own work
+# (the rows' writes and the reads' syncs) between them, gives the eager
+# launches' vectors bit for bit, for two shapes alternating in one session.
 
 @pytest.mark.parametrize("family", ["bert", "modernbert"])
 @pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
