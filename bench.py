@@ -198,6 +198,17 @@ def summarize_stats(stats_dir, workload, command):
             calls = sum(int(r["Calls"]) for r in sel)
             ns = sum(float(r["TotalDurationNs"]) for r in sel)
             lines.append(f"\nThe {tag}: {calls} launches, {ns / 1e6:.3f} ms, average {ns / calls / 1e3:.1f} µs a launch.")
+            if pat == "gemm_":
+                # The run's own products: the instantiations holding at least a
+                # tenth of the GEMM time (the rest are the tuner's candidates
+                # and the small bins' shapes), the figure the bench's
+                # avg_launch_us (HIP events, gaps between launches included)
+                # is to agree with.
+                main = [r for r in sel if float(r["TotalDurationNs"]) >= 0.1 * ns]
+                mc = sum(int(r["Calls"]) for r in main)
+                mns = sum(float(r["TotalDurationNs"]) for r in main)
+                lines.append(f"Its {len(main)} instantiations holding a tenth or more of that time (the run's own "
+                             f"products): {mc} launches, average {mns / mc / 1e3:.1f} µs a launch.")
     out = os.path.join(ROOT, "profiles", f"kernels_{workload}.md")
     with open(out, "w") as f:
         f.write("\n".join(lines) + "\n")
