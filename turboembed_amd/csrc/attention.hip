@@ -164,10 +164,14 @@ static hipError_t attention_t(hipStream_t s, const void *qkv, int tcap, int head
 // half h then holds key 16 (r / 8) + 8 h + r % 8, so registers 0..7 and
 // 8..15 are each 8 consecutive keys: exactly the 8 k-slots the lane feeds
 // the P^T V^T product per 16-key step, matching 16-byte reads of V^T rows.
-// Softmax runs in base 2 on v_exp_f32, one multiply-add and one exp2 a
-// score (the scale folded into the exponent); the row sums come from the
-// matrix cores (an all-ones tile times P^T, so they are the sums of the very
-// p values the context used), and the context is rescaled only when a
+// Softmax runs in base 2 on v_exp_f32 with the max already subtracted by
+// the matrix cores: Q enters pre-scaled by log2(e)/sqrt(d), and each
+// sub-block's score product starts with an all-ones tile times a tile
+// holding -m/16 for each query (m its running max, kept at a value that tile
+// represents exactly), so a score register holds s - m in log2 units and
+// the softmax takes exp2 of it as it is. The row sums accumulate on the
+// vector unit as v_dot2 of the 16-bit p values with 1s (F32): the sums of
+// the very p values the context used. The context is rescaled only when a
 // sub-block raises some query's max by more than 2^8. A query with no live
 // key in reach gets a zero context.
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -175,16 +179,32 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16_t __attribute__((ext_vector_type(16)));
 
 template <typename T> struct AttnMma;
+typedef _Float16 half2x_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2x_t __attribute__((ext_vector_type(2)));
 template <> struct AttnMma<_Float16> {
     typedef half8_t frag;
     static __device__ __forceinline__ floatx16_t run(frag a, frag b, floatx16_t c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    // c + the sum of the frag's 8 values (F32 accumulation, v_dot2 with 1s).
+    static __device__ __forceinline__ float sum8(frag a, float c) {
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+            c = __builtin_amdgcn_fdot2(half2x_t{a[e], a[e + 1]}, half2x_t{(_Float16)1.0f, (_Float16)1.0f}, c, false);
+        return c;
     }
 };
 template <> struct AttnMma<__bf16> {
     typedef bf16x8_t frag;
     static __device__ __forceinline__ floatx16_t run(frag a, frag b, floatx16_t c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float sum8(frag a, float c) {
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+            c = __builtin_amdgcn_fdot2_f32_bf16(bf16x2x_t{a[e], a[e + 1]}, bf16x2x_t{(__bf16)1.0f, (__bf16)1.0f}, c,
+                                                false);
+        return c;
     }
 };
 
@@ -277,28 +297,50 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
             qf[qt][s] = *(const frag *)&v;
         }
     }
+    // Q times log2(e)/sqrt(d), rounded to the operand type.
     const float scale = 1.4426950408889634f / sqrtf((float)D);
-    // o[qt][0 .. D/32 - 1]: the context of tile qt, transposed; o[qt][D/32]:
-    // its softmax sums, as the product of an all-ones V^T tile with P^T (every
-    // row of it is the sum of the p values the context used, summed in F32 by
-    // the matrix core).
-    floatx16_t o[QT][D / 32 + 1];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-        for (int t = 0; t <= D / 32; ++t) o[qt][t] = floatx16_t{};
+        for (int s = 0; s < D / 16; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[qt][s][e] = (T)((float)qf[qt][s][e] * scale);
+    // o[qt]: the context of tile qt, transposed; lsum[qt]: its softmax sums
+    // over this lane's 16 keys of each sub-block.
+    constexpr int NO = D / 32;
+    floatx16_t o[QT][NO];
+    float lsum[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        lsum[qt] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NO; ++t) o[qt][t] = floatx16_t{};
+    }
     frag ones;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = (T)1.0f;
-    // The running max of each tile's query, in scaled (log2) units. It moves
-    // only when a sub-block's max passes it by more than RESCALE (p <=
-    // 2^RESCALE stays exact enough in the operand type and finite in F32), so
-    // a wave rescales its context rarely; every p and the sums share the max
-    // in use, so the quotient is the softmax whatever that max is.
+    // The running max of each tile's query, in scaled (log2) units (0 before
+    // its first live key). It moves only when a sub-block's max passes it by
+    // more than RESCALE (p <= 2^RESCALE stays exact enough in the operand
+    // type and finite in F32), so a wave rescales its context rarely; every p
+    // and the sums share the max in use, so the quotient is the softmax
+    // whatever that max is. mb holds it as the bias tile (every element
+    // -m/16, so |m| reaches 16 times the operand type's largest value: far
+    // past any score); thr is the growth a sub-block's max must pass to move
+    // it (-inf until the first live key, whose sub-block's max it then
+    // takes).
     constexpr float RESCALE = 8.0f;
     float m_run[QT];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) m_run[qt] = -INFINITY;
+    for (int qt = 0; qt < QT; ++qt) m_run[qt] = 0.0f;
+    frag mb[QT];
+    float thr[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        thr[qt] = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mb[qt][e] = (T)0.0f;
+    }
 
     int k_lo = 0, k_hi = len;
     if (window < INT32_MAX) {
@@ -373,6 +415,11 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
         // (wave-uniform).
         bool work[2];
         floatx16_t scs[2][QT];
+        // The max both sub-blocks' scores were taken against (the first one's
+        // softmax may move it before the second's runs).
+        float m_used[QT];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) m_used[qt] = m_run[qt];
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             const int ks = kb + sub * 32;
@@ -381,6 +428,8 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) a[qt] = floatx16_t{};
             if (!WIN || work[sub]) {
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) a[qt] = AttnMma<T>::run(ones, mb[qt], a[qt]);
                 const int row = sub * 32 + swap23(ql);
 #pragma unroll
                 for (int s = 0; s < D / 16; ++s) {
@@ -398,6 +447,19 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
             const int ks = kb + sub * 32;   // the sub-block's first key
             if (!work[sub]) continue;
             floatx16_t (&sc)[QT] = scs[sub];
+            if (sub == 1) {
+                bool lagging = false;
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) lagging = lagging || m_run[qt] != m_used[qt];
+                if (__ballot(lagging) != 0) {
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) {
+                        const float lag = m_run[qt] - m_used[qt];
+#pragma unroll
+                        for (int rr = 0; rr < 16; ++rr) sc[qt][rr] -= lag;
+                    }
+                }
+            }
             // Mask (a sub-block wholly live and in every query's window skips
             // the per-key tests) and take each tile's max of the raw scores
             // for this lane's query (the scale is positive, so it keeps their
@@ -437,35 +499,46 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
             }
             // Every lane runs the same instructions below (the matrix cores
             // take the whole wave): a query with nothing live in reach yet adds
-            // zeros and keeps its state (-inf > -inf + RESCALE is false).
-            float mxs[QT];
+            // zeros and keeps its state (-inf > thr is false).
             bool grow[QT], any = false;
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
-                mxs[qt] = mx[qt] * scale;
-                grow[qt] = mxs[qt] > m_run[qt] + RESCALE;
+                grow[qt] = mx[qt] > thr[qt];
                 any = any || grow[qt];
             }
             if (__ballot(any) != 0) {
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt) {
-                    const float f = grow[qt] ? __builtin_amdgcn_exp2f(m_run[qt] - mxs[qt]) : 1.0f;   // 0 from -inf
+                    // The new max as the bias tile holds it, and the shift it
+                    // makes: this sub-block's scores move down by it, the
+                    // context so far by 2^-shift (nothing to scale before the
+                    // first live key).
+                    const T x = (T)((m_run[qt] + mx[qt]) * -0.0625f);
+                    const float m_new = (float)x * -16.0f, shift = grow[qt] ? m_new - m_run[qt] : 0.0f;
+                    const float f = grow[qt] && thr[qt] != -INFINITY ? __builtin_amdgcn_exp2f(-shift) : 1.0f;
 #pragma unroll
-                    for (int t = 0; t <= D / 32; ++t) o[qt][t] *= f;
-                    m_run[qt] = grow[qt] ? mxs[qt] : m_run[qt];
+                    for (int t = 0; t < NO; ++t) o[qt][t] *= f;
+                    lsum[qt] *= f;
+#pragma unroll
+                    for (int rr = 0; rr < 16; ++rr) sc[qt][rr] -= shift;
+                    if (grow[qt]) {
+                        m_run[qt] = m_new;
+                        thr[qt] = RESCALE;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) mb[qt][e] = x;
+                    }
                 }
             }
             frag pf[QT][2];
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
-                const float neg = m_run[qt] == -INFINITY ? 0.0f : -m_run[qt];
 #pragma unroll
                 for (int step = 0; step < 2; ++step) {
                     T pv[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        pv[e] = from_f32<T>(__builtin_amdgcn_exp2f(fmaf(sc[qt][step * 8 + e], scale, neg)));
+                    for (int e = 0; e < 8; ++e) pv[e] = from_f32<T>(__builtin_amdgcn_exp2f(sc[qt][step * 8 + e]));
                     pf[qt][step] = *(const frag *)pv;
+                    lsum[qt] = AttnMma<T>::sum8(pf[qt][step], lsum[qt]);
                 }
             }
 #pragma unroll
@@ -478,16 +551,17 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
 #pragma unroll
                     for (int qt = 0; qt < QT; ++qt) o[qt][t] = AttnMma<T>::run(vf, pf[qt][step], o[qt][t]);
                 }
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt) o[qt][D / 32] = AttnMma<T>::run(ones, pf[qt][step], o[qt][D / 32]);
             }
         }
     }
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
+        // A lane's sums cover its half's 16 keys of each sub-block (taken
+        // with every lane of the wave active).
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum[qt]), __float_as_uint(lsum[qt]), false, false);
+        const float l_tot = __uint_as_float(r[0]) + __uint_as_float(r[1]);
         const int query = qw + 32 * qt + ql;
         if (query >= len) continue;
-        const float l_tot = o[qt][D / 32][0];
         const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
         T *out = ctx + (size_t)(start + query) * heads * D + head * D;
 #pragma unroll
