@@ -242,7 +242,7 @@ template <int N> __device__ __forceinline__ void att_wait_vmcnt() {
 // of a live wave has work, and the score products run unconditionally (a
 // wave past its row's end computes scores it never uses): with no path that
 // skips them, their registers need no zeroing for one.
-template <typename T, int D, int QT, bool WIN, int QB, int STAGES>
+template <typename T, int D, int QT, bool WIN, int QB, int STAGES, int BPB>
 __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(const T *__restrict__ qkv, int tcap,
                                                                                int heads, Span sp, int nqb, Packing p,
                                                                                const int32_t *__restrict__ mask,
@@ -384,8 +384,13 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
         (void)kb;
 #endif
     };
+    // The workgroup syncs once every BPB blocks; at each sync the loads of
+    // the next BPB blocks AHEAD blocks on go out, into the slots of the BPB
+    // blocks every wave has just finished.
+    constexpr int AHEAD = STAGES - BPB;
+    static_assert(AHEAD >= BPB, "a sync's blocks were issued at an earlier sync");
 #pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st)
+    for (int st = 0; st < AHEAD; ++st)
         if (st < nb) issue(st, k_lo + st * KB);
     // Every block's live keys, once, before the loop (a mask read inside it
     // would make its wave wait on the prefetch loads too): block b's 64 keys
@@ -398,11 +403,17 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
 
     for (int bi = 0; bi < nb; ++bi) {
         const int kb = k_lo + bi * KB;
-        const int later = min(STAGES - 2, nb - 1 - bi);
-        if (later >= 1) att_wait_vmcnt<2 * LPW>();
-        else att_wait_vmcnt<0>();
-        __syncthreads();
-        if (bi + STAGES - 1 < nb) issue((bi + STAGES - 1) % STAGES, kb + (STAGES - 1) * KB);
+        if (bi % BPB == 0) {
+            // Blocks bi .. bi + BPB - 1 must have landed; blocks issued after
+            // them may still be in flight.
+            constexpr int LATER = AHEAD - BPB;
+            if (LATER > 0 && min(LATER, nb - bi - BPB) >= LATER) att_wait_vmcnt<2 * LPW * LATER>();
+            else att_wait_vmcnt<0>();
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < BPB; ++j)
+                if (bi + AHEAD + j < nb) issue((bi + AHEAD + j) % STAGES, kb + (AHEAD + j) * KB);
+        }
         const int stage = bi % STAGES;
         const char *kbase = ring + stage * SBYTES;
         const char *vbase = kbase + KBYTES;
@@ -588,7 +599,13 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
 #define ATT_QB 256
 #endif
 #ifndef ATT_STAGES
-#define ATT_STAGES 3
+#define ATT_STAGES 4
+#endif
+// 64-key blocks a workgroup sync covers (2: one sync per 128 keys, the
+// loads of the next two blocks issued at it, 64 KB of ring for two
+// workgroups a CU).
+#ifndef ATT_BPB
+#define ATT_BPB 2
 #endif
 
 template <typename T>
@@ -606,10 +623,10 @@ static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int
     const int bytes = STAGES * 2 * 64 * 64 * 2 + ((max_len + 127) / 64) * 8;
     if (bytes > 160 * 1024) return hipErrorInvalidValue;
     if (window < INT32_MAX)
-        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, true, QB, STAGES>), dim3(blocks), dim3(THREADS), bytes,
+        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, true, QB, STAGES, ATT_BPB>), dim3(blocks), dim3(THREADS), bytes,
                            s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
     else
-        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, false, QB, STAGES>), dim3(blocks), dim3(THREADS), bytes,
+        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, false, QB, STAGES, ATT_BPB>), dim3(blocks), dim3(THREADS), bytes,
                            s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
     return hipGetLastError();
 }
