@@ -66,7 +66,8 @@ inline Span span_tokens(int tokens) {
 
 // Packs the run's rows (batch and seq from the dimensions; batch at most
 // max_batch).
-hipError_t pack_rows(hipStream_t s, const int32_t *mask, const RunDims *dims, int max_batch, Packing p);
+hipError_t pack_rows(hipStream_t s, const int32_t *mask, const RunDims *dims, int max_batch, int max_seq,
+                     Packing p);
 
 // Int8 operand rows a LayerNorm can write beside its 16-bit output (the next
 // product's operand): the codes of each row's values as rounded to the 16-bit

@@ -14,11 +14,10 @@ namespace rocm {
 //
 // One workgroup. Each row's packed length is its last live column + 1
 // (reference core/src/cpu/encoder/mod.rs:395-405; core/cuda/kernels.cu:290-381):
-// integer maxima in LDS, then an exclusive scan in row order, then each
-// token's place. Integer work only, so the result is exact.
+// integer maxima, then an exclusive scan in row order. Integer work only,
+// so the result is exact.
 __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restrict__ mask,
-                                                         const RunDims *__restrict__ dims, Packing p,
-                                                         int starts_in_lds) {
+                                                         const RunDims *__restrict__ dims, Packing p) {
     extern __shared__ int32_t lens[];
     const int batch = uniform(dims->batch), seq = uniform(dims->seq);
     // Each wave takes whole rows: every lane's last live column among its
@@ -34,25 +33,26 @@ __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restri
         if (lane == 0) lens[r] = last;
     }
     __syncthreads();
-    const int n = batch * seq;
-    // Each row's start after its length (lens[batch + r]), both in LDS for
-    // the placement below.
     if (threadIdx.x == 0) {
         int t = 0;
         for (int r = 0; r < batch; ++r) {
             const int l = lens[r];
             p.start[r] = t;
             p.len[r] = l;
-            if (starts_in_lds) lens[batch + r] = t;
             t += l;
         }
         p.tokens[0] = t;
     }
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const int r = i / seq, c = i % seq;
-        if (c < lens[r]) {
-            const int at = (starts_in_lds ? lens[batch + r] : p.start[r]) + c;
+}
+
+// Each packed token's place, a thread per column of the rows (grid-strided):
+// a column under its row's length is token start + column.
+__global__ void __launch_bounds__(256) place_tokens_kernel(const RunDims *__restrict__ dims, Packing p) {
+    const int batch = uniform(dims->batch), seq = uniform(dims->seq), n = batch * seq;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        const int r = i / seq, c = i - r * seq;
+        if (c < p.len[r]) {
+            const int at = p.start[r] + c;
             p.at[at] = i;
             p.row[at] = r;
             p.pos[at] = c;
@@ -60,11 +60,12 @@ __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restri
     }
 }
 
-hipError_t pack_rows(hipStream_t s, const int32_t *mask, const RunDims *dims, int max_batch, Packing p) {
-    // The starts go to LDS beside the lengths when both fit.
-    const int in_lds = 2 * (size_t)max_batch * sizeof(int32_t) <= 64 * 1024 ? 1 : 0;
-    hipLaunchKernelGGL(pack_rows_kernel, dim3(1), dim3(1024), (1 + in_lds) * max_batch * sizeof(int32_t), s, mask,
-                       dims, p, in_lds);
+hipError_t pack_rows(hipStream_t s, const int32_t *mask, const RunDims *dims, int max_batch, int max_seq, Packing p) {
+    hipLaunchKernelGGL(pack_rows_kernel, dim3(1), dim3(1024), max_batch * sizeof(int32_t), s, mask, dims, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t blocks = std::min<size_t>(((size_t)max_batch * max_seq + 255) / 256, 1024);
+    hipLaunchKernelGGL(place_tokens_kernel, dim3(blocks), dim3(256), 0, s, dims, p);
     return hipGetLastError();
 }
 
@@ -383,84 +384,104 @@ __device__ __forceinline__ void ln_pair_apply(float (&v)[G][8], int hidden, int 
         for (int k = 0; k < 8; ++k) v[g][k] = (v[g][k] - mean) * inv * wv[g][k] + bv[g][k];
 }
 
-// add_layer_norm_kernel's work two rows a wave: each 32-lane half takes a
-// row, 8 consecutive columns a lane in each group of 256 (16-byte reads and
-// writes of 16-bit rows, where a wave a row moves 8 bytes a lane), and the
-// norm's weight and bias, read first, serve both rows. Hidden a multiple
-// of 8.
-template <int G, typename Y, typename H, bool RES_H>
+// add_layer_norm_kernel's work two rows a wave at a time: each 32-lane half
+// takes R rows in turn, 8 consecutive columns a lane in each group of 256
+// (16-byte reads and writes of 16-bit rows, where a wave a row moves 8 bytes
+// a lane), with the norm's weight and bias read once for them (both halves
+// read the same words). Every row's loads go out before the first row's
+// sums. Hidden a multiple of 8.
+template <int G, typename Y, typename H, bool RES_H, int R>
 __global__ void __launch_bounds__(256) add_ln_pair_kernel(Span sp, int hidden, float *__restrict__ x,
                                                           const Y *__restrict__ y, const float *__restrict__ ln_w,
                                                           const float *__restrict__ ln_b, float eps, int pre_norm,
                                                           int keep_f32, H *__restrict__ out_h, QuantOut qo) {
     const Live lv = live_of(sp);
-    const int local = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1);
-    // (A half's lanes all share its row; the sums stay within the half.)
-    if (local >= lv.tokens) return;
-    const int t = lv.tok0 + local;
+    // This half's first row (it takes R consecutive rows).
+    const int local0 = ((blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1)) * R;
+    // (A half's lanes all share its rows; the sums stay within the half.)
+    if (local0 >= lv.tokens) return;
     const int hl = threadIdx.x & 31;
-    float *row = x + (size_t)t * hidden;
-    const Y *yr = y + (size_t)t * hidden;
-    H *hr = out_h ? out_h + (size_t)t * hidden : nullptr;
     float wv[G][8], bv[G][8];
     load_wb8<G>(ln_w, ln_b, hidden, hl, wv, bv);
-    float v[G][8];
+    float v[R][G][8];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const int c = 8 * (hl + 32 * g);
-        if (c < hidden) {
-            float a[8];
-            if constexpr (RES_H) load8(hr + c, v[g]);
-            else load8(row + c, v[g]);
-            load8(yr + c, a);
+    for (int i = 0; i < R; ++i) {
+        const int t = lv.tok0 + min(local0 + i, lv.tokens - 1);
+        const float *row = x + (size_t)t * hidden;
+        const Y *yr = y + (size_t)t * hidden;
+        const H *hr = out_h + (size_t)t * hidden;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[g][k] = v[g][k] + a[k];
-        } else {
+        for (int g = 0; g < G; ++g) {
+            const int c = 8 * (hl + 32 * g);
+            if (c < hidden) {
+                float a[8];
+                if constexpr (RES_H) load8(hr + c, v[i][g]);
+                else load8(row + c, v[i][g]);
+                load8(yr + c, a);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[g][k] = 0.0f;
+                for (int k = 0; k < 8; ++k) v[i][g][k] = v[i][g][k] + a[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[i][g][k] = 0.0f;
+            }
         }
     }
-    if (pre_norm)
 #pragma unroll
-        for (int g = 0; g < G; ++g)
-            if (8 * (hl + 32 * g) < hidden) store8(row + 8 * (hl + 32 * g), v[g]);
-    ln_pair_apply<G>(v, hidden, hl, wv, bv, eps);
+    for (int i = 0; i < R; ++i) {
+        const int local = local0 + i;
+        if (local >= lv.tokens) break;
+        const int t = lv.tok0 + local;
+        float *row = x + (size_t)t * hidden;
+        H *hr = out_h ? out_h + (size_t)t * hidden : nullptr;
+        if (pre_norm)
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const int c = 8 * (hl + 32 * g);
-        if (c >= hidden) continue;
-        if (!pre_norm && keep_f32) store8(row + c, v[g]);
-        if (hr) store8(hr + c, v[g]);
-    }
-    if (qo.q) {
-        // The row's int8 codes from its values as rounded to H, as quant_row.
-        int8_t *qr = qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden;
-        float r[G][8], mx = 0.0f;
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                r[g][k] = 8 * (hl + 32 * g) < hidden ? to_f32(from_f32<H>(v[g][k])) : 0.0f;
-                mx = fmaxf(mx, fabsf(r[g][k]));
-            }
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        const float iv = mx > 0.0f ? 127.0f / mx : 0.0f;
+            for (int g = 0; g < G; ++g)
+                if (8 * (hl + 32 * g) < hidden) store8(row + 8 * (hl + 32 * g), v[i][g]);
+        ln_pair_apply<G>(v[i], hidden, hl, wv, bv, eps);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const int c = 8 * (hl + 32 * g);
             if (c >= hidden) continue;
-            uint32_t w[2] = {0, 0};
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int code = (int)fminf(fmaxf(rintf(r[g][k] * iv), -127.0f), 127.0f);
-                w[k >> 2] |= (uint32_t)(uint8_t)(int8_t)code << (8 * (k & 3));
-            }
-            *(uint2 *)(qr + c) = uint2{w[0], w[1]};
+            if (!pre_norm && keep_f32) store8(row + c, v[i][g]);
+            if (hr) store8(hr + c, v[i][g]);
         }
-        if (hl == 0) qo.scale[t] = mx / 127.0f;
+        if (qo.q) {
+            // The row's int8 codes from its values as rounded to H, as quant_row.
+            int8_t *qr = qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden;
+            float r[G][8], mx = 0.0f;
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    r[g][k] = 8 * (hl + 32 * g) < hidden ? to_f32(from_f32<H>(v[i][g][k])) : 0.0f;
+                    mx = fmaxf(mx, fabsf(r[g][k]));
+                }
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            const float iv = mx > 0.0f ? 127.0f / mx : 0.0f;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int c = 8 * (hl + 32 * g);
+                if (c >= hidden) continue;
+                uint32_t w[2] = {0, 0};
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int code = (int)fminf(fmaxf(rintf(r[g][k] * iv), -127.0f), 127.0f);
+                    w[k >> 2] |= (uint32_t)(uint8_t)(int8_t)code << (8 * (k & 3));
+                }
+                *(uint2 *)(qr + c) = uint2{w[0], w[1]};
+            }
+            if (hl == 0) qo.scale[t] = mx / 127.0f;
+        }
     }
 }
+
+// Rows a half-wave takes (2: BERT-base 0.9% faster a step than 1, with
+// the weight reads halved; 4 is 2.5% slower, its registers halving the
+// waves a SIMD).
+#ifndef LN_ROWS
+#define LN_ROWS 2
+#endif
 
 template <typename H, int G, typename Y>
 static hipError_t add_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y,
@@ -472,7 +493,8 @@ static hipError_t add_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden
     // must give the bits of the fused one.
     if constexpr (sizeof(Y) == 2 && sizeof(H) == 2) {
         if (res_h && hidden % 8 == 0) {
-            hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, true>), dim3((tokens + 7) / 8), dim3(256), 0, s, sp, hidden,
+            hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, true, LN_ROWS>), dim3((tokens + 8 * LN_ROWS - 1) / (8 * LN_ROWS)),
+                               dim3(256), 0, s, sp, hidden,
                                x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
             return hipGetLastError();
         }

@@ -1217,7 +1217,7 @@ static void encode(Session &s, const Bounds &bd, bool sequential) {
         run(NAME, CALL);   \
         tm.end();          \
     } while (0)
-    LAUNCH("pack_rows", pack_rows(st, s.mask, s.dims_dev, (int)s.max_batch, s.pk));
+    LAUNCH("pack_rows", pack_rows(st, s.mask, s.dims_dev, (int)s.max_batch, (int)s.max_seq, s.pk));
     // (A 16-bit residual starts in xh alone.)
     LAUNCH("embed_ln", embed_ln(st, whole, (int)bd.tokens, H, s.ids, s.types, s.pk, (int)m.position_offset, m.word,
                                 m.pos, m.type, m.emb_w, m.emb_b, m.eps, residual_in_operand(s) ? nullptr : s.x,
