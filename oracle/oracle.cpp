@@ -16,6 +16,7 @@
 //   - pooling, L2         core/src/cpu/encoder/mod.rs:426-482, job.rs:169-191
 // Built with -ffp-contract=off: every multiply-add the reference does not
 // fuse is rounded twice here too, and every one it fuses is an explicit fmaf.
+#include <immintrin.h>
 #include "oracle.h"
 
 #include <algorithm>
@@ -244,6 +245,9 @@ struct Linear {
     uint32_t n = 0, k = 0;
     std::vector<float> wt;   // [k][n]
     std::vector<float> bias; // [n], zeros where the model has none
+    // The same weights as panels of 16 outputs, [n / 16][k][16] (whole
+    // panels only): a panel's reduction reads consecutive memory.
+    std::vector<float> panels;
 };
 
 // The rows of W's parts one after another (each [n_i, k] row-major), in the
@@ -255,6 +259,9 @@ Linear pack_rows(const std::vector<const float *> &rows, uint32_t k) {
     l.wt.assign((size_t)l.n * k, 0.0f);
     for (uint32_t o = 0; o < l.n; ++o)
         for (uint32_t kk = 0; kk < k; ++kk) l.wt[(size_t)kk * l.n + o] = rows[o][kk];
+    l.panels.assign((size_t)(l.n / 16) * 16 * k, 0.0f);
+    for (uint32_t o = 0; o < l.n / 16 * 16; ++o)
+        for (uint32_t kk = 0; kk < k; ++kk) l.panels[((size_t)(o / 16) * k + kk) * 16 + o % 16] = rows[o][kk];
     l.bias.assign(l.n, 0.0f);
     return l;
 }
@@ -516,17 +523,46 @@ struct Run {
 
     // y[t][o] = epi(chain_k x[t][k] * w[o][k], o) for every packed token t: each
     // output one chain of fused multiply-adds over k in order (gemm.rs:66-142).
+    // (Blocks of 6 rows x 16 columns: the 96 chains stay in 12 AVX2 registers
+    // over the whole k loop; the order of each chain is unchanged.)
     template <class Epi>
     void linear(const float *xin, uint32_t ldx, const Linear &w, Epi epi) {
-        constexpr uint32_t RB = 4, CB = 64;
-        const size_t rblocks = (T() + RB - 1) / RB, cblocks = (w.n + CB - 1) / CB;
-        parallel(threads, rblocks * cblocks, [&](size_t task) {
-            const uint32_t r0 = (uint32_t)(task / cblocks) * RB, c0 = (uint32_t)(task % cblocks) * CB;
+        // A task: one 16-column panel of the weights (it stays in the core's
+        // cache) over RG blocks of rows.
+        constexpr uint32_t RB = 6, CB = 16, RG = 8;
+        const size_t rblocks = (T() + RB - 1) / RB, cblocks = (w.n + CB - 1) / CB, rgroups = (rblocks + RG - 1) / RG;
+        parallel(threads, rgroups * cblocks, [&](size_t task) {
+          const size_t cb = task % cblocks, rg = task / cblocks;
+          for (size_t rb = rg * RG; rb < std::min(rblocks, rg * RG + RG); ++rb) {
+            const uint32_t r0 = (uint32_t)rb * RB, c0 = (uint32_t)cb * CB;
             const uint32_t rows = std::min(RB, T() - r0), cols = std::min(CB, w.n - c0);
             alignas(64) float acc[RB][CB];
             for (uint32_t i = 0; i < RB; ++i)
                 for (uint32_t j = 0; j < CB; ++j) acc[i][j] = 0.0f;
-            if (cols == CB) {
+            if (cols == CB && rows == RB) {
+                // _mm256_fmadd_ps: eight fmaf, each rounded once.
+                const float *xr[RB];
+                for (uint32_t i = 0; i < RB; ++i) xr[i] = xin + (size_t)(r0 + i) * ldx;
+                __m256 c[RB][2];
+#pragma GCC unroll 6
+                for (uint32_t i = 0; i < RB; ++i) c[i][0] = c[i][1] = _mm256_setzero_ps();
+                const float *panel = &w.panels[(size_t)cb * w.k * CB];
+                for (uint32_t k = 0; k < w.k; ++k) {
+                    const float *wr = panel + (size_t)k * CB;
+                    const __m256 w0 = _mm256_loadu_ps(wr), w1 = _mm256_loadu_ps(wr + 8);
+#pragma GCC unroll 6
+                    for (uint32_t i = 0; i < RB; ++i) {
+                        const __m256 a = _mm256_broadcast_ss(xr[i] + k);
+                        c[i][0] = _mm256_fmadd_ps(a, w0, c[i][0]);
+                        c[i][1] = _mm256_fmadd_ps(a, w1, c[i][1]);
+                    }
+                }
+#pragma GCC unroll 6
+                for (uint32_t i = 0; i < RB; ++i) {
+                    _mm256_store_ps(acc[i], c[i][0]);
+                    _mm256_store_ps(acc[i] + 8, c[i][1]);
+                }
+            } else if (cols == CB) {
                 for (uint32_t k = 0; k < w.k; ++k) {
                     const float *wr = &w.wt[(size_t)k * w.n + c0];
                     for (uint32_t i = 0; i < rows; ++i) {
@@ -544,6 +580,7 @@ struct Run {
                 }
             }
             for (uint32_t i = 0; i < rows; ++i) epi(r0 + i, c0, cols, acc[i]);
+          }
         });
     }
 
@@ -692,17 +729,56 @@ struct Run {
             std::vector<float> masked(lp), sc(lp);
             for (uint32_t j = 0; j < lp; ++j) masked[j] = (j < len && mk[j]) ? 0.0f : kNegInf;
             const float *qv = &qkv[(size_t)start * ld];
+            // (With d a multiple of 8, eight keys' chains, or eight context
+            // columns' chains, run side by side in AVX2 registers, each in
+            // the order below: the same bits.)
+            const bool vec = d % 8 == 0;
+            std::vector<float> kt;
+            if (vec) {
+                // K^T of the head: d rows of lp keys, zeros past len.
+                kt.assign((size_t)d * lp, 0.0f);
+                for (uint32_t j = 0; j < len; ++j)
+                    for (uint32_t c = 0; c < d; ++c) kt[(size_t)c * lp + j] = qv[(size_t)j * ld + H + head * d + c];
+            }
             for (uint32_t i = 0; i < len; ++i) {
                 const float *q = qv + (size_t)i * ld + head * d;
-                for (uint32_t j = 0; j < lp; ++j) {
-                    float acc = 0.0f;
-                    if (j < len) {
-                        const float *k = qv + (size_t)j * ld + H + head * d;
-                        for (uint32_t c = 0; c < d; ++c) acc = __builtin_fmaf(q[c], k[c], acc);
+                if (vec) {
+                    // 32 keys (four chains of eight) at a time, then 16.
+                    uint32_t j0 = 0;
+                    for (; j0 + 32 <= lp; j0 += 32) {
+                        __m256 a[4] = {_mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps()};
+                        for (uint32_t c = 0; c < d; ++c) {
+                            const __m256 qc = _mm256_broadcast_ss(q + c);
+                            const float *kr = &kt[(size_t)c * lp + j0];
+                            for (int g = 0; g < 4; ++g) a[g] = _mm256_fmadd_ps(qc, _mm256_loadu_ps(kr + 8 * g), a[g]);
+                        }
+                        alignas(32) float acc[32];
+                        for (int g = 0; g < 4; ++g) _mm256_store_ps(acc + 8 * g, a[g]);
+                        for (uint32_t jj = 0; jj < 32; ++jj) sc[j0 + jj] = acc[jj] * scale + masked[j0 + jj];
                     }
-                    // The slots past len hold zeros in the reference's kt.
-                    const float s = acc * scale;
-                    sc[j] = s + masked[j];
+                    for (; j0 < lp; j0 += 16) {
+                        __m256 a0 = _mm256_setzero_ps(), a1 = _mm256_setzero_ps();
+                        for (uint32_t c = 0; c < d; ++c) {
+                            const __m256 qc = _mm256_broadcast_ss(q + c);
+                            a0 = _mm256_fmadd_ps(qc, _mm256_loadu_ps(&kt[(size_t)c * lp + j0]), a0);
+                            a1 = _mm256_fmadd_ps(qc, _mm256_loadu_ps(&kt[(size_t)c * lp + j0 + 8]), a1);
+                        }
+                        alignas(32) float acc[16];
+                        _mm256_store_ps(acc, a0);
+                        _mm256_store_ps(acc + 8, a1);
+                        for (uint32_t jj = 0; jj < 16; ++jj) sc[j0 + jj] = acc[jj] * scale + masked[j0 + jj];
+                    }
+                } else {
+                    for (uint32_t j = 0; j < lp; ++j) {
+                        float acc = 0.0f;
+                        if (j < len) {
+                            const float *k = qv + (size_t)j * ld + H + head * d;
+                            for (uint32_t c = 0; c < d; ++c) acc = __builtin_fmaf(q[c], k[c], acc);
+                        }
+                        // The slots past len hold zeros in the reference's kt.
+                        const float s = acc * scale;
+                        sc[j] = s + masked[j];
+                    }
                 }
                 if (m.ahead < len)
                     for (uint32_t j = std::min<uint64_t>((uint64_t)i + m.ahead + 1, len); j < len; ++j) sc[j] = kNegInf;
@@ -725,11 +801,26 @@ struct Run {
                     for (uint32_t l = 0; l < w; ++l) lanes[l] += lanes[l + w];
                 const float inv = 1.0f / lanes[0];
                 for (uint32_t j = 0; j < lp; ++j) sc[j] = sc[j] * inv;
-                for (uint32_t c = 0; c < d; ++c) {
-                    float acc = 0.0f;
-                    for (uint32_t j = 0; j < len; ++j)
-                        acc = __builtin_fmaf(sc[j], qv[(size_t)j * ld + 2 * H + head * d + c], acc);
-                    out[c] = acc;
+                if (vec) {
+                    // Up to eight groups of eight columns side by side.
+                    for (uint32_t c0 = 0; c0 < d; c0 += 64) {
+                        const uint32_t ng = std::min<uint32_t>(8, (d - c0) / 8);
+                        __m256 acc[8];
+                        for (uint32_t g = 0; g < 8; ++g) acc[g] = _mm256_setzero_ps();
+                        for (uint32_t j = 0; j < len; ++j) {
+                            const __m256 p = _mm256_broadcast_ss(&sc[j]);
+                            const float *vr = qv + (size_t)j * ld + 2 * H + head * d + c0;
+                            for (uint32_t g = 0; g < ng; ++g) acc[g] = _mm256_fmadd_ps(p, _mm256_loadu_ps(vr + 8 * g), acc[g]);
+                        }
+                        for (uint32_t g = 0; g < ng; ++g) _mm256_storeu_ps(out + c0 + 8 * g, acc[g]);
+                    }
+                } else {
+                    for (uint32_t c = 0; c < d; ++c) {
+                        float acc = 0.0f;
+                        for (uint32_t j = 0; j < len; ++j)
+                            acc = __builtin_fmaf(sc[j], qv[(size_t)j * ld + 2 * H + head * d + c], acc);
+                        out[c] = acc;
+                    }
                 }
             }
         });
