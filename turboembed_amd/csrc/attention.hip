@@ -590,8 +590,8 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
 
 // Query tiles of 32 a wave (1: 32 queries a wave, the registers for four
 // waves a SIMD; 2: 64, each K and V fragment read from LDS feeding two
-// tiles); queries a workgroup (ATT_QB: 256, eight waves, or 128, four); LDS
-// ring stages.
+// tiles, 16% slower at 64 x 512 with two waves a SIMD); queries a workgroup
+// (ATT_QB: 256, eight waves, or 128, four); LDS ring slots of 64 keys.
 #ifndef ATT_QT
 #define ATT_QT 1
 #endif
