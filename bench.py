@@ -173,10 +173,45 @@ def summarize_pmc(fetch_dir, write_dir, workload, command):
     print(json.dumps(out))
 
 
-def summarize_stats(stats_dir, workload, command):
+def unsplit_rooflines(rows, workload):
+    """Lines for a run of full-length rows whose launches each take the whole
+    batch (TURBO_ROCM_SPLIT=1, one length, no tuner): each matrix-core
+    kernel's achieved rate from its average launch, over the algorithmic
+    FLOPs one launch does."""
+    import re
+    shape = W.SHAPES[workload]
+    if (shape.lengths is not None or shape.family == S.TURBO_FAMILY_MODERNBERT or shape.task != S.TURBO_TASK_EMBED
+            or shape.compute_dtype or shape.precision != S.TURBO_PRECISION_FASTEST):
+        return []
+    T, H, I, L = shape.batch * shape.seq, shape.hidden, shape.intermediate, shape.layers
+    att = W.attention_flops(shape, [shape.seq] * shape.batch) / L
+    # The products by epilogue: 1 Q/K/V, 2 GELU, 6 bias (the out and FFN-out
+    # products, one launch each a layer).
+    groups = [("Q/K/V product", r"EpiE1E", 2.0 * T * H * 3 * H), ("FFN-in product (GELU)", r"EpiE2E", 2.0 * T * H * I),
+              ("out + FFN-out products (mean)", r"EpiE6E", (2.0 * T * H * H + 2.0 * T * I * H) / 2),
+              ("attention", r"attention_mfma_kernel", att)]
+    peak = PEAK["bf16" if shape.store == "bf16" else "f16"]
+    out = ["", "Each launch over the whole batch (full-length rows, one launch a layer per kernel): the main "
+           "instantiation of each kernel, its average launch against its algorithmic FLOPs.", "",
+           "| kernel | instantiation | calls | average µs | GFLOP a launch | TFLOP/s | of peak |", "|---|---|---|---|---|---|---|"]
+    for tag, pat, flops in groups:
+        sel = [r for r in rows if re.search(pat, r["Name"])]
+        if not sel:
+            continue
+        r = max(sel, key=lambda r: float(r["TotalDurationNs"]))
+        us = float(r["AverageNs"]) / 1e3
+        rate = flops / (us * 1e-6)
+        out.append(f"| {tag} | `{r['Name'][:60]}` | {r['Calls']} | {us:.1f} | {flops / 1e9:.1f} | {rate / 1e12:.0f} | "
+                   f"{100 * rate / peak:.1f}% |")
+    return out
+
+
+def summarize_stats(stats_dir, workload, command, summary_tag=""):
     """profiles/kernels_<workload>.md from a rocprofv3 --kernel-trace --stats
     run of this script: each kernel's calls, total and average duration, and
-    the GEMM kernel's launches over all its instantiations."""
+    the GEMM kernel's launches over all its instantiations. With summary_tag
+    "unsplit" (a run of whole-batch launches), kernels_<workload>_unsplit.md
+    with each matrix-core kernel's achieved rate."""
     import csv
     import glob
 
@@ -209,7 +244,9 @@ def summarize_stats(stats_dir, workload, command):
                 mns = sum(float(r["TotalDurationNs"]) for r in main)
                 lines.append(f"Its {len(main)} instantiations holding a tenth or more of that time (the run's own "
                              f"products): {mc} launches, average {mns / mc / 1e3:.1f} µs a launch.")
-    out = os.path.join(ROOT, "profiles", f"kernels_{workload}.md")
+    if summary_tag == "unsplit":
+        lines += unsplit_rooflines(rows, workload)
+    out = os.path.join(ROOT, "profiles", f"kernels_{workload}{'_' + summary_tag if summary_tag else ''}.md")
     with open(out, "w") as f:
         f.write("\n".join(lines) + "\n")
     print(out)
@@ -238,6 +275,9 @@ def main():
     ap.add_argument("--pmc-command", action="append", default=[], help="the profiling commands, for the summary")
     ap.add_argument("--summarize-stats", metavar="STATS_DIR",
                     help="write profiles/kernels_<workload>.md from a rocprofv3 --kernel-trace --stats run and exit")
+    ap.add_argument("--summary-tag", default="", choices=["", "unsplit"],
+                    help="with --summarize-stats: 'unsplit' for a run under TURBO_ROCM_SPLIT=1 of full-length rows "
+                         "(per-kernel rates added; written to kernels_<workload>_unsplit.md)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run (each row's encoder is "
@@ -248,7 +288,7 @@ def main():
         summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.workload, args.pmc_command)
         return
     if args.summarize_stats:
-        summarize_stats(args.summarize_stats, args.workload, args.pmc_command)
+        summarize_stats(args.summarize_stats, args.workload, args.pmc_command, args.summary_tag)
         return
     shape = W.SHAPES[args.workload]
     lengths = {"default": "default", "full": None}.get(args.lengths)
