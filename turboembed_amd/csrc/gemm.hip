@@ -825,7 +825,7 @@ template <typename T, typename OT, int BM, int BN, int WM, int WN, int STAGES, i
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int lda, const T *__restrict__ W, EpiArgs e,
                 int grid_n) {
-    constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
+    constexpr int WAVES = WM * WN;
     constexpr int EPC = 16 / (int)sizeof(T);                 // elements in a 16-byte chunk
     constexpr int ROWB = BK * (int)sizeof(T), CHUNKS = ROWB / 16;   // bytes and chunks of a tile row
     constexpr int RPI = 64 / CHUNKS;                      // rows one load instruction fills

@@ -203,7 +203,7 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(Span sp, int hidden, cons
     const Live lv = live_of(sp);
     const int local = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (local >= lv.tokens) return;
-    const int t = lv.tok0 + local, seq = lv.seq;
+    const int t = lv.tok0 + local;
     const int lane = threadIdx.x & 63;
     const int at = p.at[t];
     const int id = ids[at];
