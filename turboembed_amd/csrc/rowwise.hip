@@ -23,11 +23,22 @@ __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restri
     // Each wave takes whole rows: every lane's last live column among its
     // strided ones, then the wave's maximum (no atomics on a few shared words).
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    // (Rows of a multiple of 4 columns are read 16 bytes a lane, 256 columns
+    // a wave a step, the steps' reads issued together.)
+    typedef int int4_t __attribute__((ext_vector_type(4)));
     for (int r = wave; r < batch; r += waves) {
         const int32_t *row = mask + (size_t)r * seq;
         int last = 0;
-        for (int c = lane; c < seq; c += 64)
-            if (row[c] != 0) last = c + 1;
+        if ((seq & 3) == 0) {
+#pragma unroll 4
+            for (int c = 4 * lane; c < seq; c += 256) {
+                const int4_t v = *(const int4_t *)(row + c);
+                last = v[3] ? c + 4 : v[2] ? c + 3 : v[1] ? c + 2 : v[0] ? c + 1 : last;
+            }
+        } else {
+            for (int c = lane; c < seq; c += 64)
+                if (row[c] != 0) last = c + 1;
+        }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o, 64));
         if (lane == 0) lens[r] = last;
