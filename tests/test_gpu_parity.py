@@ -153,11 +153,15 @@ def test_a_gated_product_past_f16_saturates(context, family, precision):
     model.close()
 
 
-def test_packing_is_the_oracle_s_bit_for_bit(context):
-    desc = small.bert(seed=12)
-    ids, mask, types = small.ragged_rows(12, 9, 40, desc.vocab_size)
+@pytest.mark.parametrize("batch,width", [(9, 40), (9, 37), (9, 600), (480, 600)])
+def test_packing_is_the_oracle_s_bit_for_bit(context, batch, width):
+    # Row widths a multiple of 4 (the mask read 16 bytes a lane; 600 takes
+    # three steps of 256 columns) and one that is not (a column a lane); 480
+    # rows of 600 columns pass the placement grid's 1024 x 256 threads.
+    desc = small.bert(seed=12, positions=640)
+    ids, mask, types = small.ragged_rows(12, batch, width, desc.vocab_size)
     model = context.load(desc)
-    s = model.session(16, 64, S.TURBO_PRECISION_EXACT)
+    s = model.session(max(batch, 16), 640 if width > 64 else 64, S.TURBO_PRECISION_EXACT)
     s.embed(ids, mask, types)
     start, ln, at = s.packing()
     o_start, o_len, o_at = oracle.pack(mask)
