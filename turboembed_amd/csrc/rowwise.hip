@@ -24,24 +24,37 @@ __global__ void __launch_bounds__(1024) pack_rows_kernel(const int32_t *__restri
     // strided ones, then the wave's maximum (no atomics on a few shared words).
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     // (Rows of a multiple of 4 columns are read 16 bytes a lane, 256 columns
-    // a wave a step, the steps' reads issued together.)
+    // a wave a step; a wave's four rows at a time, their reads issued
+    // together.)
     typedef int int4_t __attribute__((ext_vector_type(4)));
-    for (int r = wave; r < batch; r += waves) {
-        const int32_t *row = mask + (size_t)r * seq;
-        int last = 0;
-        if ((seq & 3) == 0) {
+    constexpr int RW = 4;
+    for (int r0 = wave; r0 < batch; r0 += RW * waves) {
+        int last[RW];
+#pragma unroll
+        for (int j = 0; j < RW; ++j) {
+            const int r = r0 + j * waves;
+            last[j] = 0;
+            if (r >= batch) continue;
+            const int32_t *row = mask + (size_t)r * seq;
+            if ((seq & 3) == 0) {
 #pragma unroll 4
-            for (int c = 4 * lane; c < seq; c += 256) {
-                const int4_t v = *(const int4_t *)(row + c);
-                last = v[3] ? c + 4 : v[2] ? c + 3 : v[1] ? c + 2 : v[0] ? c + 1 : last;
+                for (int c = 4 * lane; c < seq; c += 256) {
+                    const int4_t v = *(const int4_t *)(row + c);
+                    last[j] = v[3] ? c + 4 : v[2] ? c + 3 : v[1] ? c + 2 : v[0] ? c + 1 : last[j];
+                }
+            } else {
+                for (int c = lane; c < seq; c += 64)
+                    if (row[c] != 0) last[j] = c + 1;
             }
-        } else {
-            for (int c = lane; c < seq; c += 64)
-                if (row[c] != 0) last = c + 1;
         }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o, 64));
-        if (lane == 0) lens[r] = last;
+        for (int j = 0; j < RW; ++j) {
+            int l = last[j];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) l = max(l, __shfl_xor(l, o, 64));
+            const int r = r0 + j * waves;
+            if (lane == 0 && r < batch) lens[r] = l;
+        }
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -537,11 +550,80 @@ static hipError_t add_ln_y(hipStream_t s, const Span &sp, int tokens, int hidden
     }
 }
 
+// embed_ln_kernel's work for a 16-bit residual (no F32 rows, no codes) two
+// tokens a wave: each 32-lane half takes a token, 8 consecutive columns a
+// lane in each group of 256 (twice the tokens' dependent id and row reads in
+// flight a wave), the norm's weight and bias read once for both.
+template <int G, typename H>
+__global__ void __launch_bounds__(256) embed_ln_pair_kernel(Span sp, int hidden, const int32_t *__restrict__ ids,
+                                                            const int32_t *__restrict__ types, Packing p, int offset,
+                                                            const float *__restrict__ word,
+                                                            const float *__restrict__ pos,
+                                                            const float *__restrict__ type,
+                                                            const float *__restrict__ ln_w,
+                                                            const float *__restrict__ ln_b, float eps,
+                                                            H *__restrict__ xh, const int32_t *__restrict__ zero_mask) {
+    const Live lv = live_of(sp);
+    const int local = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1);
+    // (A half's lanes all share its token; the sums stay within the half.)
+    if (local >= lv.tokens) return;
+    const int t = lv.tok0 + local, hl = threadIdx.x & 31;
+    const int at = p.at[t];
+    const int id = ids[at];
+    const int ty = types ? types[at] : 0;
+    const float *wr = word + (size_t)id * hidden;
+    const float *pr = pos ? pos + (size_t)(p.pos[t] + offset) * hidden : nullptr;
+    const float *tr = type ? type + (size_t)ty * hidden : nullptr;
+    float wv[G][8], bv[G][8];
+    load_wb8<G>(ln_w, ln_b, hidden, hl, wv, bv);
+    float v[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int c = 8 * (hl + 32 * g);
+        if (c < hidden) {
+            load8(wr + c, v[g]);
+            float a[8];
+            if (pr) {
+                load8(pr + c, a);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[g][k] = v[g][k] + a[k];
+            }
+            if (tr) {
+                load8(tr + c, a);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[g][k] = v[g][k] + a[k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[g][k] = 0.0f;
+        }
+    }
+    ln_pair_apply<G>(v, hidden, hl, wv, bv, eps);
+    // DeBERTa: a masked token is zero after the embedding.
+    if (zero_mask && zero_mask[at] == 0)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[g][k] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int c = 8 * (hl + 32 * g);
+        if (c < hidden) store8(xh + (size_t)t * hidden + c, v[g]);
+    }
+}
+
 template <typename H, int G>
 static hipError_t embed_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, const int32_t *ids,
                              const int32_t *types, const Packing &p, int offset, const float *word, const float *pos,
                              const float *type, const float *ln_w, const float *ln_b, float eps, float *x, void *xh,
                              const int32_t *zero_mask, const QuantOut &qo) {
+    if constexpr (sizeof(H) == 2) {
+        if (!x && xh && !qo.q && hidden % 8 == 0) {
+            hipLaunchKernelGGL((embed_ln_pair_kernel<G, H>), dim3((tokens + 7) / 8), dim3(256), 0, s, sp, hidden, ids,
+                               types, p, offset, word, pos, type, ln_w, ln_b, eps, (H *)xh, zero_mask);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((embed_ln_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp, hidden, ids, types, p,
                        offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh, zero_mask, qo);
     return hipGetLastError();
