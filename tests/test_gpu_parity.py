@@ -317,6 +317,34 @@ def test_matrix_core_attention_meets_the_oracle(context, family, heads, monkeypa
     model.close()
 
 
+@pytest.mark.parametrize("family", ["bert", "modernbert"])
+def test_matrix_core_attention_rescales_as_the_scalar_path_does(context, family, monkeypatch):
+    # Weights N(0, 0.3) spread a head's scores over tens of units, so in many
+    # rows a later 32-key sub-block's max passes the running max by more than
+    # 2^8 (log2 units) and the matrix-core kernel rescales the context so far
+    # and moves its bias tile. The scalar F32 path over the same 16-bit Q, K and
+    # V is the check, with the oracle at the dtype's floor beside it.
+    if family == "bert":
+        desc = small.bert(seed=31, hidden=128, heads=2, inter=256, positions=320, std=0.3)
+    else:
+        desc = small.modernbert(seed=31, hidden=128, heads=2, inter=192, positions=320, window=48, std=0.3)
+    ids, mask, types = small.ragged_rows(31, 6, 300, desc.vocab_size)
+    if family == "modernbert":
+        types = None
+    want = oracle.encode(desc, ids, mask, types)
+    model = context.load(desc)
+    got = {}
+    for path in ("mfma", "simple"):
+        monkeypatch.setenv("TURBO_ROCM_CHOICES", f"attention={path}")
+        s = model.session(8, 320, S.TURBO_PRECISION_FASTEST)
+        assert f"attn={path}" in s.choices()
+        got[path] = s.embed(ids, mask, types)
+        assert_close(got[path], want, s.compute_dtype)
+        s.close()
+    model.close()
+    assert small.cosine_rows(got["mfma"], got["simple"]).min() >= 0.9999
+
+
 # ---- The int8 tier ---------------------------------------------------------------------
 #
 # No reference kernel exists for it (the reference's one I8 encoder is a
