@@ -260,7 +260,7 @@ def main():
     ap.add_argument("--workload", default="bert-base", choices=sorted(W.SHAPES))
     ap.add_argument("--lengths", default="default", help="'default', 'full', or lo,hi")
     ap.add_argument("--cpu-rows", type=int, default=0,
-                    help="rows of the CPU baseline's sample (0: 4 rows, 1 on rows over 1024 tokens)")
+                    help="rows of the CPU baseline's sample (0: as many as about 10 s of CPU work takes)")
     ap.add_argument("--also-lengths", default="auto",
                     help="lo,hi: also time the same session on rows of lengths uniform in [lo, hi] under the mask "
                          "('auto': 64,512 for bert-base, none otherwise)")
@@ -449,29 +449,44 @@ def main():
     min_cos = None
     if not args.no_cpu:
         import oracle
-        # A bounded sample (about 10-30 s of CPU work): 4 rows, or on rows
-        # over 1024 tokens the batch's shortest row; its ranges with it.
-        n = args.cpu_rows or (1 if shape.seq > 1024 else 8)
-        n = min(n, shape.batch)
-        pick = np.argsort(lens, kind="stable")[:n] if shape.seq > 1024 else np.arange(n)
+        # A bounded sample, about 10 s of CPU work: the rows in order (on rows
+        # over 1024 tokens the shortest first), as many as the one-row pass
+        # before it says fit in 10 s (--cpu-rows fixes the count); its ranges
+        # with it.
+        order = np.argsort(lens, kind="stable") if shape.seq > 1024 else np.arange(shape.batch)
         # Every core this process may run on, one pinned thread each.
         threads = len(os.sched_getaffinity(0))
         oracle.set_pinning(True)
         model_name = oracle.cpu_model()
+        # A one-row pass first pages the code and the model's tables in; a
+        # second times a row (its pass alone: the oracle lays out the weights
+        # on every call, outside the time it reports).
+        for _ in range(2):
+            oracle.encode(desc, ids[order[:1]], mask[order[:1]], types[order[:1]], pooling=shape.pooling,
+                          normalize=shape.normalize, threads=threads)
+            row_s = oracle.last_encode_seconds()
+        # (A row's cost taken as growing with its length to the power 1.5:
+        # the products go with the tokens, attention with their square.)
+        if args.cpu_rows:
+            n = min(args.cpu_rows, shape.batch)
+        else:
+            l0, spent, n = max(int(lens[order[0]]), 1), 0.0, 0
+            while n < shape.batch:
+                spent += max(row_s, 1e-3) * (max(int(lens[order[n]]), 1) / l0) ** 1.5
+                if n > 0 and spent > 10.0:
+                    break
+                n += 1
+        pick = order[:n]
         print(f"# timed; CPU baseline on rows {pick.tolist()} ({int(lens[pick].sum())} tokens) on {threads} threads "
               f"({model_name})", file=sys.stderr, flush=True)
-        # A one-row pass first: pages the code and the model's tables in.
-        oracle.encode(desc, ids[pick[:1]], mask[pick[:1]], types[pick[:1]], pooling=shape.pooling,
-                      normalize=shape.normalize, threads=threads)
         sample_ranges, got_idx = None, pick
         if rngs:
             where = {int(r): i for i, r in enumerate(pick)}
             got_idx = [k for k, r in enumerate(rngs) if r[0] in where]
             sample_ranges = [(where[rngs[k][0]], rngs[k][1], rngs[k][2]) for k in got_idx]
-        c0 = time.perf_counter()
         want = oracle.encode(desc, ids[pick], mask[pick], types[pick], pooling=shape.pooling,
                              normalize=shape.normalize, ranges=sample_ranges, threads=threads)
-        cpu_s = time.perf_counter() - c0
+        cpu_s = oracle.last_encode_seconds()
         got = gpu_vecs[got_idx]
         cos = (got * want).sum(1) / np.linalg.norm(got, axis=1) / np.linalg.norm(want, axis=1)
         min_cos = float(cos.min())
@@ -480,7 +495,8 @@ def main():
         cpu = {"value": n / cpu_s, "unit": "sequences/s", "cores": threads, "kind": "port",
                "cpu_model": model_name,
                "sample": f"{n} of the {shape.batch} rows ({int(lens[pick].sum())} tokens{what}), all {shape.layers} "
-                         f"layers, one pass after a one-row warm-up, {cpu_s:.1f} s on {threads} pinned threads "
+                         f"layers, one pass after two one-row passes, {cpu_s:.1f} s on {threads} pinned threads (the rows' "
+                         f"pass, not the oracle's weight layout before it) "
                          f"({model_name})"}
 
     eff_lengths = shape.lengths if lengths == "default" else lengths

@@ -50,6 +50,8 @@ def lib():
         _lib.oracle_set_gated_limit.restype = None
         _lib.oracle_set_pinning.argtypes = [C.c_int32]
         _lib.oracle_set_pinning.restype = None
+        _lib.oracle_last_encode_seconds.argtypes = []
+        _lib.oracle_last_encode_seconds.restype = C.c_double
     return _lib
 
 
@@ -293,6 +295,12 @@ def rerank_fixture():
     ref = dict(first_ids=t["case.first_ids"], first_types=t["case.first_types"],
                first_lengths=t["case.first_lengths"], scores=t["case.scores"])
     return desc, pairs, head, info, ref
+
+
+def last_encode_seconds():
+    """Seconds the last encode spent on its rows (the weights' layout
+    before it excluded)."""
+    return float(lib().oracle_last_encode_seconds())
 
 
 def set_pinning(on):

@@ -21,6 +21,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -1015,6 +1016,10 @@ void say(char *why, uint32_t len, const char *msg) {
 
 }  // namespace
 
+// Seconds the last oracle_encode spent encoding (its rows' pass alone, not
+// the weights' layout before it): the benchmark's CPU figure.
+std::atomic<double> last_encode_s{0.0};
+
 extern "C" {
 
 int32_t oracle_encode(const turbo_backend_model *d, const turbo_backend_embed_rows *rows,
@@ -1025,7 +1030,9 @@ int32_t oracle_encode(const turbo_backend_model *d, const turbo_backend_embed_ro
         Model m;
         load(m, d);
         if (!rows->head) {
+            const auto t0 = std::chrono::steady_clock::now();
             encode(m, rows, ranges, count, threads, out, hidden);
+            last_encode_s.store(std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
             say(why, why_len, "");
             return TURBO_OK;
         }
@@ -1073,6 +1080,8 @@ uint32_t oracle_pack(const int32_t *mask, uint32_t batch, uint32_t seq, uint32_t
 }
 
 float oracle_exp(float x) { return cephes_exp(x); }
+
+double oracle_last_encode_seconds() { return last_encode_s.load(); }
 void oracle_set_gated_limit(float limit) { gated_limit.store(limit); }
 void oracle_set_pinning(int32_t on) { pin_threads.store(on ? 1 : 0); }
 uint32_t oracle_deberta_bucket(int64_t distance, uint32_t buckets, uint32_t maximum) {

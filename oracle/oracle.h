@@ -48,6 +48,8 @@ uint32_t oracle_pack(const int32_t *mask, uint32_t batch, uint32_t seq, uint32_t
 // ubinary. out holds rows * dim or rows * ((dim + 7) / 8) bytes.
 void  oracle_quantize(const float *x, uint32_t rows, uint32_t dim, uint32_t mode, const float *ranges, uint8_t *out);
 float oracle_exp(float x);
+// Seconds the last oracle_encode spent on its rows (the weights' layout excluded).
+double oracle_last_encode_seconds(void);
 /* A limit on the gated MLP's product act(gate) * up, 0 for none (the
  * default, the CPU path's F32): an F16 tier stores that product saturated at
  * 65504, and is checked against the oracle with this limit set. */
