@@ -317,8 +317,9 @@ def test_matrix_core_attention_meets_the_oracle(context, family, heads, monkeypa
     model.close()
 
 
+@pytest.mark.parametrize("tier", ["f16", "bf16"])
 @pytest.mark.parametrize("family", ["bert", "modernbert"])
-def test_matrix_core_attention_rescales_as_the_scalar_path_does(context, family, monkeypatch):
+def test_matrix_core_attention_rescales_as_the_scalar_path_does(context, family, tier, monkeypatch):
     # Weights N(0, 0.3) spread a head's scores over tens of units, so in many
     # rows a later 32-key sub-block's max passes the running max by more than
     # 2^8 (log2 units) and the matrix-core kernel rescales the context so far
@@ -328,6 +329,11 @@ def test_matrix_core_attention_rescales_as_the_scalar_path_does(context, family,
         desc = small.bert(seed=31, hidden=128, heads=2, inter=256, positions=320, std=0.3)
     else:
         desc = small.modernbert(seed=31, hidden=128, heads=2, inter=192, positions=320, window=48, std=0.3)
+    precision = S.TURBO_PRECISION_FASTEST
+    if tier == "bf16":
+        # (BF16 operands: the bias tile and the pre-scaled Q in BF16.)
+        from turboembed_amd.model import with_dtype
+        desc, precision = with_dtype(desc, "bf16"), S.TURBO_PRECISION_MODEL
     ids, mask, types = small.ragged_rows(31, 6, 300, desc.vocab_size)
     if family == "modernbert":
         types = None
@@ -336,13 +342,16 @@ def test_matrix_core_attention_rescales_as_the_scalar_path_does(context, family,
     got = {}
     for path in ("mfma", "simple"):
         monkeypatch.setenv("TURBO_ROCM_CHOICES", f"attention={path}")
-        s = model.session(8, 320, S.TURBO_PRECISION_FASTEST)
+        s = model.session(8, 320, precision)
         assert f"attn={path}" in s.choices()
         got[path] = s.embed(ids, mask, types)
         assert_close(got[path], want, s.compute_dtype)
+        dtype = s.compute_dtype
         s.close()
     model.close()
-    assert small.cosine_rows(got["mfma"], got["simple"]).min() >= 0.9999
+    # (BF16's 8-bit mantissa: its p values and Q carry 2^-9 rounding.)
+    bound = 0.9999 if dtype == S.TURBO_DTYPE_F16 else 0.999
+    assert small.cosine_rows(got["mfma"], got["simple"]).min() >= bound
 
 
 # ---- The int8 tier ---------------------------------------------------------------------
