@@ -128,6 +128,25 @@ def test_ragged_rows_meet_the_oracle(context, family, precision):
     model.close()
 
 
+def test_a_weight_past_f16_keeps_the_products_in_f32(context):
+    # One GEMM weight beyond F16's 65504 (layer 0's FFN-out, [0, 0]) keeps a
+    # FASTEST session's products in F32, as the reference's CUDA backend
+    # does (core/cuda/backend.cpp:1168-1225): the session reports F32 and its
+    # vectors meet the oracle at F32's bound.
+    desc = small.bert(seed=51)
+    w2 = 5 + 12   # [word, pos, type, ln w, ln b] + layer 0's [Wq, bq, Wk, bk, Wv, bv, Wo, bo, ln1, ln1b, W1, b1, W2]
+    desc.tensors[w2] = desc.tensors[w2].copy()
+    desc.tensors[w2][0, 0] = 70000.0
+    ids, mask, types = small.ragged_rows(51, 4, 40, desc.vocab_size)
+    model = context.load(desc)
+    s = model.session(4, 40, S.TURBO_PRECISION_FASTEST)
+    assert s.compute_dtype == S.TURBO_DTYPE_F32
+    got = s.embed(ids, mask, types)
+    assert_close(got, oracle.encode(desc, ids, mask, types), s.compute_dtype)
+    s.close()
+    model.close()
+
+
 @pytest.mark.parametrize("family", ["modernbert", "nomic"])
 @pytest.mark.parametrize("precision", [S.TURBO_PRECISION_FASTEST, "bf16", S.TURBO_PRECISION_EXACT])
 def test_a_gated_product_past_f16_saturates(context, family, precision):
