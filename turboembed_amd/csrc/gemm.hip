@@ -519,37 +519,22 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
         const int mt = mw + i * 32 + half * PASS;
         if constexpr (KIND == Epi::Qkv || KIND == Epi::QkvRope) {
             if (qkv_which == 2) {
-                // V^T: for each column, 8 consecutive tokens a lane.
-#pragma unroll
-                for (int k = 0; k < COLS * (PASS / 8) / 64; ++k) {
-                    const int u = lane + 64 * k, col = u / (PASS / 8), g = (u % (PASS / 8)) * 8;
-                    const int n = nw + col;
-                    if (n >= N) continue;
-                    int head, c;
-                    head_col(n - qkv_base, e.d, head, c);
-                    float v[8];
-                    const float bias = cols.bv[k];
-                    const int m = mt + g;
-                    if constexpr (SCALED) {
-                        const float ws = cols.wv[k];
-#pragma unroll
-                        for (int q = 0; q < 8; ++q) v[q] = dequant(scratch[(g + q) * SROW + col], ascale[m + q - mw], ws, bias);
-                    } else {
-#pragma unroll
-                        for (int q = 0; q < 8; ++q) v[q] = scratch[(g + q) * SROW + col];
-                    }
-                    T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + ((size_t)head * e.d + c) * e.tcap + e.tok0;
+                // V^T: 8 consecutive tokens of a column (of V^T's row vr =
+                // head * d + c) a lane.
+                auto put_vt = [&](int vr, int m, const float (&v)[8]) {
+                    T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + (size_t)vr * e.tcap + e.tok0;
 #if defined(__HIP_DEVICE_COMPILE__)
                     if (fast_v) {
                         // From the V block: rows past M, and a tail of fewer than 8, are dropped.
-                        const int off = m + 8 <= M ? (int)((((size_t)head * e.d + c) * e.tcap + e.tok0 + m) * sizeof(T)) : OOB;
+                        const int off = m + 8 <= M ? (int)((((size_t)vr) * e.tcap + e.tok0 + m) * sizeof(T)) : OOB;
                         __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs, off, 0, 0);
                         if (m + 8 > M && m < M) {
 #pragma unroll
                             for (int q = 0; q < 8; ++q)
                                 if (m + q < M) out[m + q] = from_f32<T>(v[q]);
                         }
-                    } else
+                        return;
+                    }
 #endif
                     if (m + 8 <= M && ((e.tcap | e.tok0) & 7) == 0) {
                         store8<T>(out + m, v);
@@ -557,6 +542,71 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
 #pragma unroll
                         for (int q = 0; q < 8; ++q)
                             if (m + q < M) out[m + q] = from_f32<T>(v[q]);
+                    }
+                };
+                if constexpr (KIND == Epi::Qkv && !SCALED && ((COLS / 2) * (PASS / 8)) % 64 == 0) {
+                    // Two adjacent columns a lane (8-byte reads of the staged
+                    // rows: half the LDS reads of one column a lane; the bias
+                    // is in the staged values). A column pair lies in one
+                    // head (d is even). (Not on the rotary shape: its
+                    // read-ahead angles leave no registers for it.)
+#pragma unroll
+                    for (int k = 0; k < (COLS / 2) * (PASS / 8) / 64; ++k) {
+                        const int u = lane + 64 * k, col = 2 * (u / (PASS / 8)), g = (u % (PASS / 8)) * 8;
+                        const int n = nw + col;
+                        if (n >= N) continue;
+                        int head, c;
+                        head_col(n - qkv_base, e.d, head, c);
+                        float v0[8], v1[8];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) {
+                            const float2 p2 = *(const float2 *)&scratch[(g + q) * SROW + col];
+                            v0[q] = p2.x;
+                            v1[q] = p2.y;
+                        }
+                        const int m = mt + g, vr = head * e.d + c;
+                        put_vt(vr, m, v0);
+                        put_vt(vr + 1, m, v1);
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < COLS * (PASS / 8) / 64; ++k) {
+                        const int u = lane + 64 * k, col = u / (PASS / 8), g = (u % (PASS / 8)) * 8;
+                        const int n = nw + col;
+                        if (n >= N) continue;
+                        int head, c;
+                        head_col(n - qkv_base, e.d, head, c);
+                        float v[8];
+                        const float bias = cols.bv[k];
+                        const int m = mt + g;
+                        if constexpr (SCALED) {
+                            const float ws = cols.wv[k];
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) v[q] = dequant(scratch[(g + q) * SROW + col], ascale[m + q - mw], ws, bias);
+                        } else {
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) v[q] = scratch[(g + q) * SROW + col];
+                        }
+                        T *out = (T *)e.out + (size_t)2 * e.heads * e.tcap * e.d + ((size_t)head * e.d + c) * e.tcap + e.tok0;
+#if defined(__HIP_DEVICE_COMPILE__)
+                        if (fast_v) {
+                            // From the V block: rows past M, and a tail of fewer than 8, are dropped.
+                            const int off = m + 8 <= M ? (int)((((size_t)head * e.d + c) * e.tcap + e.tok0 + m) * sizeof(T)) : OOB;
+                            __builtin_amdgcn_raw_buffer_store_b128(pack8<T>(v), rs, off, 0, 0);
+                            if (m + 8 > M && m < M) {
+#pragma unroll
+                                for (int q = 0; q < 8; ++q)
+                                    if (m + q < M) out[m + q] = from_f32<T>(v[q]);
+                            }
+                        } else
+#endif
+                        if (m + 8 <= M && ((e.tcap | e.tok0) & 7) == 0) {
+                            store8<T>(out + m, v);
+                        } else {
+#pragma unroll
+                            for (int q = 0; q < 8; ++q)
+                                if (m + q < M) out[m + q] = from_f32<T>(v[q]);
+                        }
                     }
                 }
                 __builtin_amdgcn_wave_barrier();
