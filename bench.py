@@ -252,6 +252,67 @@ def summarize_stats(stats_dir, workload, command, summary_tag=""):
     print(out)
 
 
+def library_compare(workload, reps=20):
+    """profiles/library_<workload>.md: the platform libraries on one layer's
+    products and attention of a full-length batch, through torch (its F16 or
+    BF16 linear, which calls hipBLASLt or rocBLAS, and its fused
+    scaled-dot-product attention), with HIP events on torch's stream. No
+    epilogue, no mask: the plain operations the session's kernels fuse more
+    into. Measurement only; the session never calls these."""
+    import torch
+    import torch.nn.functional as F
+    shape = W.SHAPES[workload]
+    dt = torch.bfloat16 if shape.store == "bf16" else torch.float16
+    B, L, H, I, nh = shape.batch, shape.seq, shape.hidden, shape.intermediate, shape.heads
+    M, d = B * L, shape.hidden // shape.heads
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    peak = PEAK["bf16" if dt == torch.bfloat16 else "f16"]
+    lines = [f"# Platform libraries on {workload}'s layer shapes", "", "Command (from the repository root, one MI355X):",
+             "", "```", f"python3 bench.py --workload {workload} --library-compare", "```", "",
+             f"torch {torch.__version__}, {torch.cuda.get_device_name(0)}; {str(dt).split('.')[-1]} operands, "
+             f"random normal, {reps} launches a figure after 3 untimed.", "",
+             "| operation | shape | average µs | TFLOP/s | of peak |", "|---|---|---|---|---|"]
+    for tag, n, k in (("Q/K/V product", 3 * H, H), ("out product", H, H), ("FFN-in product", I, H),
+                      ("FFN-out product", H, I)):
+        a = torch.randn(M, k, device=dev, dtype=dt, generator=g)
+        w = torch.randn(n, k, device=dev, dtype=dt, generator=g) * 0.05
+        us = timed(lambda: F.linear(a, w))
+        rate = 2.0 * M * n * k / (us * 1e-6)
+        lines.append(f"| {tag} (linear) | M {M}, N {n}, K {k} | {us:.1f} | {rate / 1e12:.0f} | {100 * rate / peak:.1f}% |")
+        del a, w
+    q, k_, v = (torch.randn(B, nh, L, d, device=dev, dtype=dt, generator=g) for _ in range(3))
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("memory-efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel(be):
+                us = timed(lambda: F.scaled_dot_product_attention(q, k_, v))
+        except RuntimeError as e:
+            lines.append(f"| attention ({name}) | {B}×{nh} heads, {L} tokens, d {d} | not available: "
+                         f"{str(e).splitlines()[0][:80]} | | |")
+            continue
+        rate = 4.0 * B * nh * L * L * d / (us * 1e-6)
+        lines.append(f"| attention ({name}) | {B}×{nh} heads, {L} tokens, d {d} | {us:.1f} | {rate / 1e12:.0f} | "
+                     f"{100 * rate / peak:.1f}% |")
+    out = os.path.join(ROOT, "profiles", f"library_{workload}.md")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -278,6 +339,9 @@ def main():
     ap.add_argument("--summary-tag", default="", choices=["", "unsplit"],
                     help="with --summarize-stats: 'unsplit' for a run under TURBO_ROCM_SPLIT=1 of full-length rows "
                          "(per-kernel rates added; written to kernels_<workload>_unsplit.md)")
+    ap.add_argument("--library-compare", action="store_true",
+                    help="time torch's linear and fused attention on the workload's full-length layer shapes, write "
+                         "profiles/library_<workload>.md and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run (each row's encoder is "
@@ -289,6 +353,9 @@ def main():
         return
     if args.summarize_stats:
         summarize_stats(args.summarize_stats, args.workload, args.pmc_command, args.summary_tag)
+        return
+    if args.library_compare:
+        library_compare(args.workload)
         return
     shape = W.SHAPES[args.workload]
     lengths = {"default": "default", "full": None}.get(args.lengths)
