@@ -562,6 +562,49 @@ def test_deberta_split_runs_meet_the_oracle(context, monkeypatch):
     model.close()
 
 
+def _deberta_rows(seed, batch, seq, vocab):
+    g = np.random.Generator(np.random.PCG64(seed))
+    lengths = np.concatenate([[seq, 131, 64, 33, 1], g.integers(1, seq + 1, batch - 5)])[:batch]
+    ids = g.integers(0, vocab, (batch, seq)).astype(np.int32)
+    mask = (np.arange(seq)[None, :] < lengths[:, None]).astype(np.int32)
+    mask[0, [5, 6, 100]] = 0          # holes
+    mask[1, 0] = 0                    # a masked first column
+    return ids, mask
+
+
+@pytest.mark.parametrize("tier", ["f16", "bf16"])
+def test_deberta_matrix_core_path_meets_the_oracle(context, monkeypatch, tier):
+    # Heads of 64 on F16 and BF16 take the matrix-core form: rows past one
+    # 128-query block, distances past the buckets' linear half (16 buckets,
+    # 256 positions), holes and a masked first column; the same rows through
+    # the scalar form, and a run long enough to split into two parts.
+    from test_deberta import small_deberta
+    from turboembed_amd.model import with_dtype
+    desc = small_deberta(seed=7, hidden=128, heads=2, inter=256, buckets=16, maximum=256, std=0.1)
+    if tier == "bf16":
+        desc = with_dtype(desc, "bf16")
+    ids, mask = _deberta_rows(8, 5, 200, desc.vocab_size)
+    want = oracle.encode(desc, ids, mask)
+    model = context.load(desc)
+    got = {}
+    for path in ("mfma", "simple"):
+        monkeypatch.setenv("TURBO_ROCM_CHOICES", f"attention={path}")
+        s = model.session(5, 200, S.TURBO_PRECISION_FASTEST)
+        assert f"attn={path}" in s.choices()
+        got[path] = s.embed(ids, mask)
+        assert_close(got[path], want, s.compute_dtype)
+        s.close()
+    assert small.cosine_rows(got["mfma"], got["simple"]).min() >= FLOOR[S.TURBO_DTYPE_F16]
+    monkeypatch.delenv("TURBO_ROCM_CHOICES")
+    ids, mask = _deberta_rows(9, 40, 200, desc.vocab_size)
+    assert mask.sum() >= 4096
+    monkeypatch.setenv("TURBO_ROCM_SPLIT", "2")
+    s = model.session(40, 200, S.TURBO_PRECISION_FASTEST)
+    assert_close(s.embed(ids, mask), oracle.encode(desc, ids, mask), s.compute_dtype)
+    s.close()
+    model.close()
+
+
 # ---- Split runs: two parts of the rows on two streams -------------------------------------
 #
 # A run of at least 4096 packed tokens and two rows or more runs its rows in

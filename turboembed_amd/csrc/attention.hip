@@ -732,12 +732,205 @@ __global__ void __launch_bounds__(256) deberta_attention_kernel(const T *__restr
     }
 }
 
+// The matrix-core form (F16 and BF16, 64-wide heads): one workgroup of 4
+// waves per (128-query block, head, row), each wave 32 queries and its own
+// pass over the row's keys, 32 at a time, with no workgroup sync. Scores are
+// transposed as in attention_mfma_kernel (S^T = K Q^T, a query per lane,
+// register r of half h holding key 16 (r / 8) + 8 h + r % 8), in log2 units:
+// Q enters times log2(e)/sqrt(3 d) and so do the query projections of the
+// relative rows. For a 32 x 32 tile the distances i - j take 63 values, so
+// their relative rows are a run of at most 64 (the bucket of a distance
+// never grows by more than one a step: the host checks its table). Two more
+// products over those rows give every score's relative terms at once:
+// C = PK Q^T (each query against each row's key projection) and
+// P = K PQ^T (each key against each row's query projection), both put in the
+// wave's LDS, from which each lane picks C[b(i - j)][i] and P[j][b(i - j)].
+// Then the online softmax per tile in F32 (exp2 of the score less the
+// running max) and the context transposed, O^T += V^T P^T, with P^T taken
+// from the score registers. A masked query (before the row's last live
+// token) scores 0 against every position of the row: the mean of their
+// values.
+template <typename T>
+__global__ void __launch_bounds__(256) deberta_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads, Span sp,
+                                                           int nqb, Packing p, const int32_t *__restrict__ mask,
+                                                           const float *__restrict__ pos,
+                                                           const int32_t *__restrict__ buckets, int positions,
+                                                           T *__restrict__ ctx) {
+    constexpr int D = 64, QB = 128;
+    typedef typename AttnMma<T>::frag frag;
+    typedef uint32_t vec4 __attribute__((ext_vector_type(4)));
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    // Per wave: C as [64 rows][32 queries], P as [32 keys][64 rows].
+    __shared__ float cbuf[4][64 * 32], pbuf[4][32 * 64];
+    const Live lv = live_of(sp);
+    const int pair = blockIdx.x / nqb, qb = blockIdx.x % nqb;
+    if (pair >= heads * lv.rows) return;
+    const int r = lv.row0 + pair / heads, head = pair % heads, seq = lv.seq;
+    const int len = p.len[r], start = p.start[r];
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, ql = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qw = qb * QB + wave * 32;
+    if (qw >= len) return;
+    const int H = heads * D;
+    const T *Q = qkv + ((size_t)head * tcap + start) * D;
+    const T *K = qkv + ((size_t)(heads + head) * tcap + start) * D;
+    const T *Vt = qkv + (size_t)2 * heads * tcap * D + (size_t)head * D * tcap;
+    const int32_t *mk = mask + (size_t)r * seq;
+    float *cw = cbuf[wave], *pw = pbuf[wave];
+    const float scale = 1.4426950408889634f / sqrtf(3.0f * D);
+
+    const int qi = min(qw + ql, len - 1);          // this lane's query (clamped past the row's end)
+    const bool q_masked = mk[qi] == 0;
+    frag qf[D / 16];
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+        const vec4 v = *(const vec4 *)(Q + (size_t)qi * D + s * 16 + h * 8);
+        qf[s] = *(const frag *)&v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[s][e] = (T)((float)qf[s][e] * scale);
+    }
+#if defined(__HIP_DEVICE_COMPILE__)
+    // V^T columns of this run start anywhere: 16-byte buffer loads at byte
+    // offsets, bounded by the head's V^T block.
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void *)Vt, (short)0, (int)min((size_t)D * tcap * 2, (size_t)0x7fffffff), 0x00020000);
+#endif
+    floatx16_t o[2] = {floatx16_t{}, floatx16_t{}};
+    float m_run = -INFINITY, lsum = 0.0f;
+    const int qlast = min(qw + 31, len - 1);
+    for (int ks = 0; ks < len; ks += 32) {
+        const int klast = min(ks + 31, len - 1);
+        // The tile's relative rows: b_lo .. b_hi, at most 64.
+        const int b_lo = buckets[qw - klast + positions - 1], b_hi = buckets[qlast - ks + positions - 1];
+        // Keys as the score product's rows: row m reads key swap23(m).
+        frag kf[D / 16];
+        {
+            const int key = min(ks + swap23(ql), len - 1);
+#pragma unroll
+            for (int s = 0; s < D / 16; ++s) {
+                const vec4 v = *(const vec4 *)(K + (size_t)key * D + s * 16 + h * 8);
+                kf[s] = *(const frag *)&v;
+            }
+        }
+        // C = PK Q^T, rows b_lo + 32 tb + m; then P = K PQ^T, columns b_lo + 32 tb + n.
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            const float *row = pos + (size_t)min(b_lo + 32 * tb + ql, b_hi) * 2 * H + head * D + h * 8;
+            floatx16_t c = floatx16_t{}, pp = floatx16_t{};
+#pragma unroll
+            for (int s = 0; s < D / 16; ++s) {
+                const f4 k0 = *(const f4 *)(row + H + s * 16), k1 = *(const f4 *)(row + H + s * 16 + 4);
+                const f4 q0 = *(const f4 *)(row + s * 16), q1 = *(const f4 *)(row + s * 16 + 4);
+                frag pk, pq;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    pk[e] = (T)k0[e];
+                    pk[e + 4] = (T)k1[e];
+                    pq[e] = (T)(q0[e] * scale);
+                    pq[e + 4] = (T)(q1[e] * scale);
+                }
+                c = AttnMma<T>::run(pk, qf[s], c);
+                pp = AttnMma<T>::run(kf[s], pq, pp);
+            }
+            // Output register rr of half h: row 8 (rr / 4) + 4 h + rr % 4, column ql.
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) {
+                const int m = 8 * (rr >> 2) + 4 * h + (rr & 3);
+                cw[(32 * tb + m) * 32 + ql] = c[rr];
+                pw[swap23(m) * 64 + 32 * tb + ql] = pp[rr];
+            }
+        }
+        floatx16_t sc = floatx16_t{};
+#pragma unroll
+        for (int s = 0; s < D / 16; ++s) sc = AttnMma<T>::run(kf[s], qf[s], sc);
+        const uint64_t live = __ballot(ks + ql <= klast && mk[ks + ql] != 0);
+        // This wave's LDS writes land before its lanes read each other's.
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        float mx = -INFINITY;
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) {
+            const int jl = 16 * (rr >> 3) + 8 * h + (rr & 7), key = ks + jl;
+            const int t = min(max(buckets[qi - min(key, len - 1) + positions - 1] - b_lo, 0), 63);
+            const float v = sc[rr] + cw[t * 32 + ql] + pw[jl * 64 + t];
+            const bool in_row = key < len;
+            sc[rr] = q_masked ? (in_row ? 0.0f : -INFINITY) : ((live >> jl) & 1u ? v : -INFINITY);
+            mx = fmaxf(mx, sc[rr]);
+        }
+        // Every lane has read C and P before the next tile writes them.
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        mx = max_across_halves(mx);
+        const float m_new = fmaxf(m_run, mx);
+        // Nothing live yet for this query: no weights, no rescale.
+        const float f = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        o[0] *= f;
+        o[1] *= f;
+        lsum *= f;
+        m_run = m_new;
+        frag pf[2];
+#pragma unroll
+        for (int step = 0; step < 2; ++step) {
+            T pv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                pv[e] = from_f32<T>(m_new == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[step * 8 + e] - m_new));
+            pf[step] = *(const frag *)pv;
+            lsum = AttnMma<T>::sum8(pf[step], lsum);
+        }
+#pragma unroll
+        for (int step = 0; step < 2; ++step) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                frag vf;
+#if defined(__HIP_DEVICE_COMPILE__)
+                // Keys ks + 16 step + 8 h .. + 7 of column 32 t + ql; those past
+                // the row's end weigh 0, whatever they read
+                // (the next column's first values, or zeros past the block).
+                const int c = 32 * t + ql, k0 = ks + 16 * step + 8 * h;
+                const vec4 v = __builtin_bit_cast(vec4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            rv, (c * tcap + start + k0) * 2, 0, 0));
+                vf = *(const frag *)&v;
+#else
+                vf = frag{};
+#endif
+                o[t] = AttnMma<T>::run(vf, pf[step], o[t]);
+            }
+        }
+    }
+    const auto rs = __builtin_amdgcn_permlane32_swap(__float_as_uint(lsum), __float_as_uint(lsum), false, false);
+    const float l_tot = __uint_as_float(rs[0]) + __uint_as_float(rs[1]);
+    const int query = qw + ql;
+    if (query >= len) return;
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    T *out = ctx + (size_t)(start + query) * H + head * D;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 16; rr += 4) {
+            const int c = 32 * t + 8 * (rr >> 2) + 4 * h;
+            T v4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v4[q] = from_f32<T>(o[t][rr + q] * inv);
+            *(uint2 *)(out + c) = *(const uint2 *)v4;
+        }
+}
+
 template <typename T>
 static hipError_t deberta_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
                             const int32_t *mask, const Span &sp, int max_rows, int max_len, const float *pos,
-                            const int32_t *buckets, int positions, void *ctx) {
+                            const int32_t *buckets, int positions, bool mfma, void *ctx) {
+    if (max_len > positions) return hipErrorInvalidValue;
+    if constexpr (sizeof(T) == 2) {
+        if (mfma && d == 64) {
+            const int nqb = (max_len + 127) / 128;
+            hipLaunchKernelGGL((deberta_mfma_kernel<T>), dim3(max_rows * heads * nqb), dim3(256), 0, s,
+                               (const T *)qkv, tcap, heads, sp, nqb, p, mask, pos, buckets, positions, (T *)ctx);
+            return hipGetLastError();
+        }
+    }
     const size_t lds = (size_t)4 * max_len * sizeof(float);
-    if (lds > 160 * 1024 || max_len > positions) return hipErrorInvalidValue;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
     hipLaunchKernelGGL((deberta_attention_kernel<T>), dim3(max_rows * heads), dim3(256), lds, s, (const T *)qkv, tcap,
                        heads, d, p, mask, sp, pos, buckets, positions, (T *)ctx, max_len);
     return hipGetLastError();
@@ -745,16 +938,18 @@ static hipError_t deberta_t(hipStream_t s, const void *qkv, int tcap, int heads,
 
 hipError_t deberta_attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
                              const int32_t *mask, const Span &sp, int max_rows, int max_len, const float *pos,
-                             const int32_t *buckets, int positions, void *ctx) {
+                             const int32_t *buckets, int positions, bool mfma, void *ctx) {
     if (max_len <= 0 || max_rows <= 0) return hipSuccess;
     switch (dt) {
     case Dt::F16:
         return deberta_t<_Float16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions,
-                                   ctx);
+                                   mfma, ctx);
     case Dt::BF16:
-        return deberta_t<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions, ctx);
+        return deberta_t<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions, mfma,
+                                 ctx);
     default:
-        return deberta_t<float>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions, ctx);
+        return deberta_t<float>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions, false,
+                                ctx);
     }
 }
 

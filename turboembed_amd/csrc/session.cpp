@@ -388,6 +388,9 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
         std::vector<int32_t> table((size_t)2 * m->positions - 1);
         for (int64_t dist = -(int64_t)m->positions + 1; dist < (int64_t)m->positions; ++dist)
             table[(size_t)(dist + m->positions - 1)] = (int32_t)deberta_bucket(dist, rel_buckets, rel_max);
+        m->rel_tiles = true;
+        for (size_t i = 0; i + 62 < table.size(); ++i)
+            m->rel_tiles = m->rel_tiles && table[i + 62] - table[i] <= 63 && table[i + 62] >= table[i];
         m->rel_table.reset(dev_alloc(table.size() * 4, "relative buckets"));
         check(hipMemcpy(m->rel_table.get(), table.data(), table.size() * 4, hipMemcpyHostToDevice), "relative buckets");
         check(hipDeviceSynchronize(), "relative projections");
@@ -1152,7 +1155,7 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
             LAUNCH("attention", deberta_attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, sp,
                                                   (int)bd.rows, (int)bd.max_len, L.pos_qk,
                                                   static_cast<const int32_t *>(m.rel_table.get()), (int)m.positions,
-                                                  s.ctxb));
+                                                  m.rel_tiles && !bc.simple_attention, s.ctxb));
         else
             LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, sp, (int)bd.rows,
                                           (int)bd.max_len, window, s.ctxb, bc.simple_attention));

@@ -131,6 +131,9 @@ struct Model {
     // of each distance d in [-(positions - 1), positions - 1] at d + positions - 1.
     bool deberta = false;
     DevPtr rel_pos, rel_table;
+    // No 63 consecutive distances span more than 64 relative rows (the
+    // matrix-core form's tiles hold that many).
+    bool rel_tiles = false;
     std::vector<Layer> ls;
     // Narrowed GEMM weights, per dtype (index Dt), made on first need.
     std::mutex lock;
