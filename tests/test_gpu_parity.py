@@ -575,12 +575,13 @@ def _deberta_rows(seed, batch, seq, vocab):
 @pytest.mark.parametrize("tier", ["f16", "bf16"])
 def test_deberta_matrix_core_path_meets_the_oracle(context, monkeypatch, tier):
     # Heads of 64 on F16 and BF16 take the matrix-core form: rows past one
-    # 128-query block, distances past the buckets' linear half (16 buckets,
-    # 256 positions), holes and a masked first column; the same rows through
-    # the scalar form, and a run long enough to split into two parts.
+    # 128-query block, tiles of distances wholly in the buckets' linear half
+    # (|i - j| <= 64 of 128 buckets, 256 positions) and tiles past it, holes
+    # and a masked first column; the same rows through the scalar form, and a
+    # run long enough to split into two parts.
     from test_deberta import small_deberta
     from turboembed_amd.model import with_dtype
-    desc = small_deberta(seed=7, hidden=128, heads=2, inter=256, buckets=16, maximum=256, std=0.1)
+    desc = small_deberta(seed=7, hidden=128, heads=2, inter=256, buckets=128, maximum=256, std=0.1)
     if tier == "bf16":
         desc = with_dtype(desc, "bf16")
     ids, mask = _deberta_rows(8, 5, 200, desc.vocab_size)

@@ -745,6 +745,10 @@ __global__ void __launch_bounds__(256) deberta_attention_kernel(const T *__restr
 // C = PK Q^T (each query against each row's key projection) and
 // P = K PQ^T (each key against each row's query projection), both put in the
 // wave's LDS, from which each lane picks C[b(i - j)][i] and P[j][b(i - j)].
+// The relative rows come narrowed to the operand type (the query half
+// unscaled: P takes the scale as it leaves the accumulators). A tile whose
+// 63 distances all fall in the buckets' linear half takes each score's row
+// by arithmetic instead of the table.
 // Then the online softmax per tile in F32 (exp2 of the score less the
 // running max) and the context transposed, O^T += V^T P^T, with P^T taken
 // from the score registers. A masked query (before the row's last live
@@ -753,17 +757,19 @@ __global__ void __launch_bounds__(256) deberta_attention_kernel(const T *__restr
 template <typename T>
 __global__ void __launch_bounds__(256) deberta_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads, Span sp,
                                                            int nqb, Packing p, const int32_t *__restrict__ mask,
-                                                           const float *__restrict__ pos,
+                                                           const T *__restrict__ pos,
                                                            const int32_t *__restrict__ buckets, int positions,
                                                            T *__restrict__ ctx) {
     constexpr int D = 64, QB = 128;
     typedef typename AttnMma<T>::frag frag;
     typedef uint32_t vec4 __attribute__((ext_vector_type(4)));
-    typedef float f4 __attribute__((ext_vector_type(4)));
     // Per wave: C as [64 rows][32 queries], P as [32 keys][64 rows].
     __shared__ float cbuf[4][64 * 32], pbuf[4][32 * 64];
     const Live lv = live_of(sp);
-    const int pair = blockIdx.x / nqb, qb = blockIdx.x % nqb;
+    // The query blocks of a (row, head) pair take numbers 8 apart: one XCD,
+    // whose L2 then holds the pair's keys, values and relative rows once.
+    const int L = blockIdx.x;
+    const int pair = (L / (8 * nqb)) * 8 + L % 8, qb = (L / 8) % nqb;
     if (pair >= heads * lv.rows) return;
     const int r = lv.row0 + pair / heads, head = pair % heads, seq = lv.seq;
     const int len = p.len[r], start = p.start[r];
@@ -802,6 +808,7 @@ __global__ void __launch_bounds__(256) deberta_mfma_kernel(const T *__restrict__
         const int klast = min(ks + 31, len - 1);
         // The tile's relative rows: b_lo .. b_hi, at most 64.
         const int b_lo = buckets[qw - klast + positions - 1], b_hi = buckets[qlast - ks + positions - 1];
+        const bool linear = b_hi - b_lo == (qlast - ks) - (qw - klast);
         // Keys as the score product's rows: row m reads key swap23(m).
         frag kf[D / 16];
         {
@@ -815,29 +822,20 @@ __global__ void __launch_bounds__(256) deberta_mfma_kernel(const T *__restrict__
         // C = PK Q^T, rows b_lo + 32 tb + m; then P = K PQ^T, columns b_lo + 32 tb + n.
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
-            const float *row = pos + (size_t)min(b_lo + 32 * tb + ql, b_hi) * 2 * H + head * D + h * 8;
+            const T *row = pos + (size_t)min(b_lo + 32 * tb + ql, b_hi) * 2 * H + head * D + h * 8;
             floatx16_t c = floatx16_t{}, pp = floatx16_t{};
 #pragma unroll
             for (int s = 0; s < D / 16; ++s) {
-                const f4 k0 = *(const f4 *)(row + H + s * 16), k1 = *(const f4 *)(row + H + s * 16 + 4);
-                const f4 q0 = *(const f4 *)(row + s * 16), q1 = *(const f4 *)(row + s * 16 + 4);
-                frag pk, pq;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    pk[e] = (T)k0[e];
-                    pk[e + 4] = (T)k1[e];
-                    pq[e] = (T)(q0[e] * scale);
-                    pq[e + 4] = (T)(q1[e] * scale);
-                }
-                c = AttnMma<T>::run(pk, qf[s], c);
-                pp = AttnMma<T>::run(kf[s], pq, pp);
+                const vec4 k4 = *(const vec4 *)(row + H + s * 16), q4 = *(const vec4 *)(row + s * 16);
+                c = AttnMma<T>::run(*(const frag *)&k4, qf[s], c);
+                pp = AttnMma<T>::run(kf[s], *(const frag *)&q4, pp);
             }
             // Output register rr of half h: row 8 (rr / 4) + 4 h + rr % 4, column ql.
 #pragma unroll
             for (int rr = 0; rr < 16; ++rr) {
                 const int m = 8 * (rr >> 2) + 4 * h + (rr & 3);
                 cw[(32 * tb + m) * 32 + ql] = c[rr];
-                pw[swap23(m) * 64 + 32 * tb + ql] = pp[rr];
+                pw[swap23(m) * 64 + 32 * tb + ql] = pp[rr] * scale;
             }
         }
         floatx16_t sc = floatx16_t{};
@@ -851,7 +849,8 @@ __global__ void __launch_bounds__(256) deberta_mfma_kernel(const T *__restrict__
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) {
             const int jl = 16 * (rr >> 3) + 8 * h + (rr & 7), key = ks + jl;
-            const int t = min(max(buckets[qi - min(key, len - 1) + positions - 1] - b_lo, 0), 63);
+            const int dist = qi - min(key, len - 1);
+            const int t = linear ? dist - (qw - klast) : min(max(buckets[dist + positions - 1] - b_lo, 0), 63);
             const float v = sc[rr] + cw[t * 32 + ql] + pw[jl * 64 + t];
             const bool in_row = key < len;
             sc[rr] = q_masked ? (in_row ? 0.0f : -INFINITY) : ((live >> jl) & 1u ? v : -INFINITY);
@@ -919,13 +918,14 @@ __global__ void __launch_bounds__(256) deberta_mfma_kernel(const T *__restrict__
 template <typename T>
 static hipError_t deberta_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
                             const int32_t *mask, const Span &sp, int max_rows, int max_len, const float *pos,
-                            const int32_t *buckets, int positions, bool mfma, void *ctx) {
+                            const int32_t *buckets, int positions, const void *pos_t, void *ctx) {
     if (max_len > positions) return hipErrorInvalidValue;
     if constexpr (sizeof(T) == 2) {
-        if (mfma && d == 64) {
-            const int nqb = (max_len + 127) / 128;
-            hipLaunchKernelGGL((deberta_mfma_kernel<T>), dim3(max_rows * heads * nqb), dim3(256), 0, s,
-                               (const T *)qkv, tcap, heads, sp, nqb, p, mask, pos, buckets, positions, (T *)ctx);
+        if (pos_t && d == 64) {
+            // A 1-D grid of groups of 8 (row, head) pairs times nqb query blocks.
+            const int nqb = (max_len + 127) / 128, blocks = ((max_rows * heads + 7) / 8) * 8 * nqb;
+            hipLaunchKernelGGL((deberta_mfma_kernel<T>), dim3(blocks), dim3(256), 0, s, (const T *)qkv, tcap, heads,
+                               sp, nqb, p, mask, (const T *)pos_t, buckets, positions, (T *)ctx);
             return hipGetLastError();
         }
     }
@@ -938,18 +938,18 @@ static hipError_t deberta_t(hipStream_t s, const void *qkv, int tcap, int heads,
 
 hipError_t deberta_attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
                              const int32_t *mask, const Span &sp, int max_rows, int max_len, const float *pos,
-                             const int32_t *buckets, int positions, bool mfma, void *ctx) {
+                             const int32_t *buckets, int positions, const void *pos_t, void *ctx) {
     if (max_len <= 0 || max_rows <= 0) return hipSuccess;
     switch (dt) {
     case Dt::F16:
         return deberta_t<_Float16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions,
-                                   mfma, ctx);
+                                   pos_t, ctx);
     case Dt::BF16:
-        return deberta_t<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions, mfma,
-                                 ctx);
+        return deberta_t<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions,
+                                 pos_t, ctx);
     default:
-        return deberta_t<float>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions, false,
-                                ctx);
+        return deberta_t<float>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, pos, buckets, positions,
+                                nullptr, ctx);
     }
 }
 

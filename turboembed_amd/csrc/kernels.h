@@ -97,11 +97,12 @@ hipError_t embed_ln(hipStream_t s, const Span &sp, int max_tokens, int hidden, c
 // query (mask 0 before the row's last live token) attends uniformly to every
 // position through it.
 // The span's rows; max_rows and max_len bound the grid and the LDS. With
-// mfma (F16 and BF16, d = 64) on the matrix cores; the caller sets it only
-// where no 63 consecutive distances span more than 64 relative rows.
+// pos_t (F16 and BF16, d = 64: the same table in the operand type) on the
+// matrix cores; the caller passes it only where no 63 consecutive distances
+// span more than 64 relative rows.
 hipError_t deberta_attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
                              const int32_t *mask, const Span &sp, int max_rows, int max_len, const float *pos,
-                             const int32_t *buckets, int positions, bool mfma, void *ctx);
+                             const int32_t *buckets, int positions, const void *pos_t, void *ctx);
 
 // out = LN(in) row by row over `tokens` rows of `hidden`; out_f32 and out_h
 // (in `dt`) may each be NULL, and out_f32 may be in (in place). ln_b NULL is

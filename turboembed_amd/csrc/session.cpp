@@ -388,9 +388,10 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
         std::vector<int32_t> table((size_t)2 * m->positions - 1);
         for (int64_t dist = -(int64_t)m->positions + 1; dist < (int64_t)m->positions; ++dist)
             table[(size_t)(dist + m->positions - 1)] = (int32_t)deberta_bucket(dist, rel_buckets, rel_max);
+        m->rel_rows = rows;
         m->rel_tiles = true;
-        for (size_t i = 0; i + 62 < table.size(); ++i)
-            m->rel_tiles = m->rel_tiles && table[i + 62] - table[i] <= 63 && table[i + 62] >= table[i];
+        for (size_t i = 0; i + 1 < table.size(); ++i)
+            m->rel_tiles = m->rel_tiles && (table[i + 1] - table[i] == 0 || table[i + 1] - table[i] == 1);
         m->rel_table.reset(dev_alloc(table.size() * 4, "relative buckets"));
         check(hipMemcpy(m->rel_table.get(), table.data(), table.size() * 4, hipMemcpyHostToDevice), "relative buckets");
         check(hipDeviceSynchronize(), "relative projections");
@@ -466,6 +467,27 @@ std::vector<LayerWeights> &Model::weights_in(Dt dt) {
     if (dt == Dt::F16 && over) f16_overflow = true;
     w = std::move(out);
     return w;
+}
+
+// DeBERTa-v2's relative projections narrowed to `dt` (F16 or BF16), made on
+// the first session that needs them and kept with the model; null where a
+// value passes F16's range (those sessions keep the F32 table's scalar path).
+const void *Model::rel_pos_in(Dt dt) {
+    std::lock_guard<std::mutex> g(lock);
+    DevPtr &p = rel_narrowed[(int)dt];
+    if (p) return rel_overflow[(int)dt] ? nullptr : p.get();
+    const size_t n = (size_t)layers * rel_rows * 2 * hidden;
+    OnDevice on(ctx->ordinal);
+    p.reset(dev_alloc(n * 2 + 256, "narrowed relative projections"));
+    int32_t *flag = reinterpret_cast<int32_t *>(static_cast<char *>(p.get()) + ((n * 2 + 255) & ~(size_t)255));
+    check(hipMemsetAsync(flag, 0, 4, ctx->stream), "narrowing relative projections");
+    check(narrow(ctx->stream, static_cast<const float *>(rel_pos.get()), p.get(), n, dt, flag),
+          "narrowing relative projections");
+    int32_t over = 0;
+    check(hipMemcpyAsync(&over, flag, 4, hipMemcpyDeviceToHost, ctx->stream), "narrowing relative projections");
+    check(hipStreamSynchronize(ctx->stream), "narrowing relative projections");
+    rel_overflow[(int)dt] = over != 0;
+    return rel_overflow[(int)dt] ? nullptr : p.get();
 }
 
 void model_release(Model *m) {
@@ -565,6 +587,8 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     if (dt == Dt::F32) s->w = &m->weights_in(Dt::F32);
     s->dt = dt;
     s->act = dt == Dt::I8 ? Dt::F16 : dt;
+    if (m->deberta && m->rel_tiles && s->act != Dt::F32 && m->hidden / m->heads == 64)
+        s->rel_pos_t = m->rel_pos_in(s->act);
     s->compute_dtype = dtype_of(dt);
     if (tuning && tuning->struct_size >= offsetof(turbo_backend_tuning, numerics_used) + 4) {
         if (tuning->numerics_allowed && !(tuning->numerics_allowed & numeric_of(dt)))
@@ -1155,7 +1179,11 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
             LAUNCH("attention", deberta_attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, sp,
                                                   (int)bd.rows, (int)bd.max_len, L.pos_qk,
                                                   static_cast<const int32_t *>(m.rel_table.get()), (int)m.positions,
-                                                  m.rel_tiles && !bc.simple_attention, s.ctxb));
+                                                  s.rel_pos_t && !bc.simple_attention
+                                                      ? static_cast<const char *>(s.rel_pos_t) +
+                                                            (size_t)l * m.rel_rows * 2 * H * dt_bytes(dt)
+                                                      : nullptr,
+                                                  s.ctxb));
         else
             LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, sp, (int)bd.rows,
                                           (int)bd.max_len, window, s.ctxb, bc.simple_attention));

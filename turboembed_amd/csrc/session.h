@@ -131,9 +131,13 @@ struct Model {
     // of each distance d in [-(positions - 1), positions - 1] at d + positions - 1.
     bool deberta = false;
     DevPtr rel_pos, rel_table;
-    // No 63 consecutive distances span more than 64 relative rows (the
-    // matrix-core form's tiles hold that many).
+    // The relative row of consecutive distances grows by 0 or 1 (so 63 of
+    // them span at most 64 rows: the matrix-core form's tiles hold that many).
     bool rel_tiles = false;
+    size_t rel_rows = 0;   // 2 position_buckets
+    DevPtr rel_narrowed[4];
+    bool rel_overflow[4] = {};
+    const void *rel_pos_in(Dt dt);
     std::vector<Layer> ls;
     // Narrowed GEMM weights, per dtype (index Dt), made on first need.
     std::mutex lock;
@@ -193,6 +197,9 @@ struct Session {
     RunDims *dims_host = nullptr, *dims_dev = nullptr;
     std::vector<uint32_t> row_lens;   // the write's row lengths (host, sized at open)
     std::vector<LayerWeights> *w = nullptr;
+    // DeBERTa-v2: the model's relative projections in the operand type, or
+    // null (the scalar attention on the F32 table).
+    const void *rel_pos_t = nullptr;
     Choices kc;            // kernel choices per bin of packed tokens
     std::string choices;   // kc as a choices string
     // One graph per bin of packed tokens, captured at session_open with the
