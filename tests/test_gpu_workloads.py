@@ -95,6 +95,29 @@ def test_bert_base_full_depth_meets_the_oracle(context, sharp):
     model.close()
 
 
+def test_deberta_v3_base_meets_the_oracle(context):
+    # The DeBERTa-v3-base-shaped workload at full width (hidden 768, 12 heads
+    # of 64, 256 relative buckets to distance 512) on 2 of its 12 layers in
+    # the F16 tier: two 512-token rows and two of U[64, 512] (tiles of
+    # distances inside the buckets' linear half and past it), through the
+    # matrix-core attention, within F16's floor of the oracle.
+    sh = W.SHAPES["deberta-v3-base"]
+    desc = W.model(sh, layers=2)
+    a = W.rows(sh, batch=2, lengths=None, seed=11)
+    b = W.rows(sh, batch=2, lengths=(64, sh.seq), seed=12)
+    ids, mask, types = (np.concatenate([x, y]) for x, y in zip(a, b))
+    print(f"deberta-v3-base rows of {mask.sum(1).tolist()} tokens, 2 layers", flush=True)
+    model = context.load(desc)
+    s = model.session(4, sh.seq, sh.precision)
+    assert s.compute_dtype == S.TURBO_DTYPE_F16 and "attn=mfma" in s.choices()
+    got = s.embed(ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
+    want = oracle.encode(desc, ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
+    print(f"  min cosine {small.cosine_rows(got, want).min():.7f}", flush=True)
+    assert_close(got, want, s.compute_dtype)
+    s.close()
+    model.close()
+
+
 @pytest.mark.parametrize("sharp", [False, True])
 def test_xlmr_large_bf16_ranges_meet_the_oracle(context, sharp):
     # C3 at full width (hidden 1024, 16 heads of 64, FFN 4096, vocab 250002,

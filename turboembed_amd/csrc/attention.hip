@@ -755,7 +755,7 @@ __global__ void __launch_bounds__(256) deberta_attention_kernel(const T *__restr
 // token) scores 0 against every position of the row: the mean of their
 // values.
 template <typename T>
-__global__ void __launch_bounds__(256) deberta_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads, Span sp,
+__global__ void __launch_bounds__(256) deberta_attention_mfma_kernel(const T *__restrict__ qkv, int tcap, int heads, Span sp,
                                                            int nqb, Packing p, const int32_t *__restrict__ mask,
                                                            const T *__restrict__ pos,
                                                            const int32_t *__restrict__ buckets, int positions,
@@ -924,7 +924,7 @@ static hipError_t deberta_t(hipStream_t s, const void *qkv, int tcap, int heads,
         if (pos_t && d == 64) {
             // A 1-D grid of groups of 8 (row, head) pairs times nqb query blocks.
             const int nqb = (max_len + 127) / 128, blocks = ((max_rows * heads + 7) / 8) * 8 * nqb;
-            hipLaunchKernelGGL((deberta_mfma_kernel<T>), dim3(blocks), dim3(256), 0, s, (const T *)qkv, tcap, heads,
+            hipLaunchKernelGGL((deberta_attention_mfma_kernel<T>), dim3(blocks), dim3(256), 0, s, (const T *)qkv, tcap, heads,
                                sp, nqb, p, mask, (const T *)pos_t, buckets, positions, (T *)ctx);
             return hipGetLastError();
         }

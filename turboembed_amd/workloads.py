@@ -1,6 +1,6 @@
 """The encoder workloads this backend is measured and checked on.
 
-Five encoder shapes with seeded random weights and seeded synthetic rows:
+Six encoder shapes with seeded random weights and seeded synthetic rows:
 
   minilm       MiniLM-L6-shaped BERT: 6 layers, hidden 384, 12 heads, FFN 1536 GELU,
                vocab 30522, 512 positions; 32 rows of lengths U[16, 128] padded to 128;
@@ -21,6 +21,11 @@ Five encoder shapes with seeded random weights and seeded synthetic rows:
                pairs, queries U[8, 32] tokens, passages U[64, 480] cut so each pair's
                one window [CLS] q [SEP] p [SEP] fits 512; types 0 then 1; CLS ->
                pooler (dense 768 + tanh) -> one logit.
+  deberta-v3-base
+               DeBERTa-v3-base-shaped DeBERTa-v2 encoder: 12 layers, hidden 768, 12
+               heads, FFN 3072 GELU, vocab 128100, relative attention over 256
+               log buckets to distance 512 (shared keys); 64 rows x 512 all live;
+               MEAN + L2; FASTEST (F16).
 
 Weights are N(0, 0.02) from numpy's PCG64 seeded by (workload seed, tensor
 index), so every tensor is reproducible on its own; LayerNorm weights are 1
@@ -84,6 +89,10 @@ SHAPES = {
                         rope=(160000.0, 10000.0), window=128, global_every=3, seed=4, cls_id=50281, sep_id=50282,
                         pad_id=50283, precision=S.TURBO_PRECISION_FASTEST, pooling=S.TURBO_POOLING_MEAN,
                         normalize=S.TURBO_NORMALIZE_NONE, batch=16, seq=8192, lengths=(2048, 8192)),
+    "deberta-v3-base": Shape("deberta-v3-base", S.TURBO_FAMILY_DEBERTA_V2, 12, 768, 12, 3072, 128100, 512, 1, 1e-7,
+                             seed=6, cls_id=1, sep_id=2, pad_id=0, precision=S.TURBO_PRECISION_FASTEST,
+                             pooling=S.TURBO_POOLING_MEAN, batch=64, seq=512, lengths=None,
+                             extra={"relative": (256, 512)}),
     "rerank": Shape("rerank", S.TURBO_FAMILY_BERT, 12, 768, 12, 3072, 30522, 512, 2, 1e-12, seed=5,
                     precision=S.TURBO_PRECISION_FASTEST, pooling=S.TURBO_POOLING_CLS,
                     normalize=S.TURBO_NORMALIZE_NONE, batch=256, seq=512, compute_dtype=S.TURBO_DTYPE_I8,
@@ -121,6 +130,14 @@ def model(shape: Shape, layers=None):
                          shape.eps, t, rope=shape.rope, attention_window=shape.window,
                          global_every=shape.global_every, mlp=S.TURBO_MLP_GATED,
                          activation=S.TURBO_ACTIVATION_GELU_ERF, norm=S.TURBO_NORM_LAYER_NO_BIAS)
+    elif shape.family == S.TURBO_FAMILY_DEBERTA_V2:
+        buckets, maximum = shape.extra["relative"]
+        t = [w(shape.vocab, H), ones(H), zeros(H), w(2 * buckets, H), ones(H), zeros(H)]
+        for _ in range(L):
+            t += [w(H, H), w(H), w(H, H), w(H), w(H, H), w(H), w(H, H), w(H), ones(H), zeros(H),
+                  w(I, H), w(I), w(H, I), w(H), ones(H), zeros(H)]
+        desc = ModelDesc(shape.family, L, H, shape.heads, I, shape.vocab, shape.positions, shape.token_types,
+                         shape.eps, t, relative=(buckets, maximum))
     else:
         raise ValueError(shape.family)
     desc.compute_dtype = shape.compute_dtype
@@ -199,7 +216,8 @@ def gemm_flops_per_token(shape: Shape):
 
 
 def attention_flops(shape: Shape, lengths):
-    """Algorithmic attention FLOPs (QK^T and PV) over rows of these lengths."""
+    """Algorithmic attention FLOPs (QK^T and PV, and DeBERTa-v2's two relative
+    terms) over rows of these lengths."""
     H, L = shape.hidden, shape.layers
     total = 0.0
     for n in lengths:
@@ -211,6 +229,10 @@ def attention_flops(shape: Shape, lengths):
             keys = sum(min(n, i + shape.window // 2 + 1) - max(0, i - shape.window // 2) for i in range(int(n)))
             total += 4 * g * H * n * n + 4 * loc * H * keys
             del w
+        elif shape.family == S.TURBO_FAMILY_DEBERTA_V2:
+            # Each score's three dot products (content, content to position,
+            # position to content) and its share of the context.
+            total += 8 * L * H * n * n
         else:
             total += 4 * L * H * n * n
     return total
