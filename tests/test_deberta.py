@@ -92,3 +92,26 @@ def test_visible_rows_ignore_masked_ids_and_masked_rows_share_one_state():
     got = oracle.encode(desc, ids, mask, pooling=S.TURBO_POOLING_CLS, normalize=S.TURBO_NORMALIZE_NONE)
     x, _ = plain.deberta_states(desc, ids[2], mask[2], uniform_masked=False)
     assert np.abs(got[2] - x[0]).max() > 1e-2
+
+
+def test_the_v3_base_workload_meets_the_textbook_at_full_width():
+    # The measured DeBERTa-v3-base shape (hidden 768, 12 heads, 256 buckets to
+    # distance 512) on one layer: a 300-token row reaches the log buckets
+    # (|i - j| > 128) and a row with a hole; the workload counts its
+    # attention at twice a plain encoder's FLOPs (three dot products a score
+    # and the context against two).
+    from turboembed_amd import workloads as W
+    sh = W.SHAPES["deberta-v3-base"]
+    desc = W.model(sh, layers=1)
+    assert desc.family == S.TURBO_FAMILY_DEBERTA_V2 and desc.relative == (256, 512)
+    assert len(desc.tensors) == S.DEBERTA_EMBEDDING_TENSORS + S.BERT_LAYER_TENSORS
+    g = np.random.Generator(np.random.PCG64(4))
+    ids = g.integers(0, sh.vocab, (2, 300)).astype(np.int32)
+    mask = np.ones((2, 300), np.int32)
+    mask[1, 200:] = 0
+    mask[1, 17] = 0
+    got = oracle.encode(desc, ids, mask, pooling=S.TURBO_POOLING_MEAN, normalize=S.TURBO_NORMALIZE_NONE)
+    want = plain.embed(desc, ids, mask, pooling=S.TURBO_POOLING_MEAN, normalize=S.TURBO_NORMALIZE_NONE)
+    assert np.abs(got - want).max() <= 1e-5 * (1 + np.abs(want).max()), np.abs(got - want).max()
+    bert = W.SHAPES["bert-base"]
+    assert W.attention_flops(sh, [300]) == 2 * W.attention_flops(bert, [300])
