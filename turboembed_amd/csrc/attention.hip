@@ -809,6 +809,10 @@ __global__ void __launch_bounds__(256) deberta_attention_mfma_kernel(const T *__
         // The tile's relative rows: b_lo .. b_hi, at most 64.
         const int b_lo = buckets[qw - klast + positions - 1], b_hi = buckets[qlast - ks + positions - 1];
         const bool linear = b_hi - b_lo == (qlast - ks) - (qw - klast);
+        // Otherwise lane l holds the row of distance qw - klast + l (to the
+        // tile's largest), and each score takes its row from that lane.
+        int brow = 0;
+        if (!linear) brow = buckets[min(qw - klast + lane, qlast - ks) + positions - 1];
         // Keys as the score product's rows: row m reads key swap23(m).
         frag kf[D / 16];
         {
@@ -850,7 +854,7 @@ __global__ void __launch_bounds__(256) deberta_attention_mfma_kernel(const T *__
         for (int rr = 0; rr < 16; ++rr) {
             const int jl = 16 * (rr >> 3) + 8 * h + (rr & 7), key = ks + jl;
             const int dist = qi - min(key, len - 1);
-            const int t = linear ? dist - (qw - klast) : min(max(buckets[dist + positions - 1] - b_lo, 0), 63);
+            const int t = linear ? dist - (qw - klast) : min(max(__shfl(brow, dist - (qw - klast), 64) - b_lo, 0), 63);
             const float v = sc[rr] + cw[t * 32 + ql] + pw[jl * 64 + t];
             const bool in_row = key < len;
             sc[rr] = q_masked ? (in_row ? 0.0f : -INFINITY) : ((live >> jl) & 1u ? v : -INFINITY);
