@@ -40,6 +40,11 @@ def kernel_flops(shape, tokens, lengths):
         "gemm_ffn_out": 2.0 * tokens * H * I,
         "attention": W.attention_flops(shape, lengths) / shape.layers,
     }
+    # The out and FFN-out products with the add + LayerNorm in their
+    # epilogue: the same products (the norm's few operations a value are not
+    # counted).
+    f["gemm_out_ln"] = f["gemm_out"]
+    f["gemm_ffn_out_ln"] = f["gemm_ffn_out"]
     return f
 
 
@@ -588,6 +593,11 @@ def main():
         "other_runs": extra_runs,
         "ranges": len(rngs) if rngs else 0,
         "tune_ms": sess.tuning.tune_ms,
+        # The tuner's timings of the bins this workload's run takes (ms a
+        # run through the first layer, parts overlapped as the run forks
+        # them), <bin>/<knob>/<variant>.
+        "tune_timings": {k: round(v, 4) for k, v in sess.timings.items()
+                         if k.split("/")[0] in ("le16k", "gt16k") or shape.batch * shape.seq <= 16384},
         "roofline": roofline,
         "hbm_tail": tail,
         "cpu_baseline": cpu,

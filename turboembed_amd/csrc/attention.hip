@@ -608,11 +608,11 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
 #define ATT_BPB 2
 #endif
 
-template <typename T>
+template <typename T, int QB>
 static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
                                    const int32_t *mask, const Span &sp, int max_rows, int max_len, int window,
                                    void *ctx) {
-    constexpr int QB = ATT_QB, STAGES = ATT_STAGES, THREADS = 64 * (QB / (32 * ATT_QT));
+    constexpr int STAGES = ATT_STAGES, THREADS = 64 * (QB / (32 * ATT_QT));
     // A 1-D grid of groups of 8 (row, head) pairs times nqb query blocks.
     const int nqb = (max_len + QB - 1) / QB, pairs = heads * max_rows;
     const int blocks = ((pairs + 7) / 8) * 8 * nqb;
@@ -631,17 +631,29 @@ static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int
     return hipGetLastError();
 }
 
+template <typename T>
+static hipError_t attention_mfma_path(hipStream_t s, const void *qkv, int tcap, int heads, int d, const Packing &p,
+                                      const int32_t *mask, const Span &sp, int max_rows, int max_len, int window,
+                                      void *ctx, int path) {
+    if (path == 2)
+        return attention_mfma_t<T, 128>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx);
+    return attention_mfma_t<T, ATT_QB>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx);
+}
+
 hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
                      const int32_t *mask, const Span &sp, int max_rows, int max_len, int window, void *ctx,
-                     bool simple) {
+                     int path) {
     if (max_len <= 0 || max_rows <= 0) return hipSuccess;
-    const bool mfma = d == 64 && !simple;
+    if (path < 0 || path > 2) return hipErrorInvalidValue;
+    const bool mfma = d == 64 && path != 1;
     switch (dt) {
     case Dt::F16:
-        return mfma ? attention_mfma_t<_Float16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx)
+        return mfma ? attention_mfma_path<_Float16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx,
+                                                    path)
                     : attention_t<_Float16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx);
     case Dt::BF16:
-        return mfma ? attention_mfma_t<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx)
+        return mfma ? attention_mfma_path<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx,
+                                                  path)
                     : attention_t<__bf16>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx);
     default: return attention_t<float>(s, qkv, tcap, heads, d, p, mask, sp, max_rows, max_len, window, ctx);
     }

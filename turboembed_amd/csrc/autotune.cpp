@@ -38,7 +38,9 @@ std::string format_choices(const Choices &c) {
             s += gemm_tile_name(x.tile[g]);
             s += ',';
         }
-        s += x.simple_attention ? "attn=simple;" : "attn=mfma;";
+        s += "attn=";
+        s += ATTN_NAME[x.attn >= 0 && x.attn < ATTN_PATHS ? x.attn : ATTN_MFMA];
+        s += ';';
     }
     const uint32_t k = forced_knobs(c);
     s += "forced=";
@@ -127,12 +129,15 @@ bool parse_choices(const char *s, Choices *c, bool force, std::string *why) {
                     if (force) next.bin[b].tile_forced[g] = KNOB_TILE;
                 }
         } else if (it.key == "attn" || it.key == "attention") {
-            if (it.value != "mfma" && it.value != "simple") {
+            int path = -1;
+            for (int a = 0; a < ATTN_PATHS; ++a)
+                if (it.value == ATTN_NAME[a]) path = a;
+            if (path < 0) {
                 *why = "unknown attention path '" + it.value + "'";
                 return false;
             }
             for (int b = b0; b < b1; ++b) {
-                next.bin[b].simple_attention = it.value == "simple";
+                next.bin[b].attn = path;
                 if (force) next.bin[b].attn_forced = KNOB_ATTN;
             }
         } else {

@@ -9,7 +9,7 @@
 // the bins its max_batch x max_seq reaches.
 //
 // A choices string, as format_choices writes it and parse_choices reads it:
-//   <bin>:qkv=<tile>,out=<tile>,ffn1=<tile>,ffn2=<tile>,attn=<mfma|simple>;...;forced=<knob>,...
+//   <bin>:qkv=<tile>,out=<tile>,ffn1=<tile>,ffn2=<tile>,attn=<mfma|mfma128|simple>;...;forced=<knob>,...
 // with a tile as the GEMM launcher names it ("auto" is its rule on the
 // run's own shape). "all:" names every bin; the older single items
 // "gemm=<tile>" and "attention=<path>" mean every product and every bin.
@@ -53,9 +53,15 @@ constexpr const char *GEMM_NAME[G_COUNT] = {"qkv", "out", "ffn1", "ffn2"};
 // What a choice was fixed by rather than left to the rule or the tuner.
 enum Knob : uint32_t { KNOB_TILE = 1, KNOB_ATTN = 2 };
 
+// The attention paths: the matrix-core kernel on 256-query workgroups of 8
+// waves, or on 128-query workgroups of 4 (twice the workgroups, each
+// streaming its keys for half the queries), and the scalar kernel.
+enum AttnPath : int { ATTN_MFMA = 0, ATTN_SIMPLE = 1, ATTN_MFMA128 = 2, ATTN_PATHS = 3 };
+constexpr const char *ATTN_NAME[ATTN_PATHS] = {"mfma", "simple", "mfma128"};
+
 struct BinChoice {
     int tile[G_COUNT] = {0, 0, 0, 0};   // 0: the launcher's rule on the run's shape
-    bool simple_attention = false;
+    int attn = ATTN_MFMA;
     uint32_t tile_forced[G_COUNT] = {0, 0, 0, 0};
     uint32_t attn_forced = 0;
 };

@@ -27,6 +27,7 @@
 
 #include "kernels.h"
 #include "devmath.h"
+#include "rowmath.h"
 
 namespace rocm {
 
@@ -337,15 +338,6 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 // and coalesced reads and writes of x for the residual. The values are the
 // accumulators exactly; only the order of the stores changes.
 constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
-
-template <typename T>
-__device__ __forceinline__ void store8(T *dst, const float (&v)[8]) {
-    typedef uint32_t vec4 __attribute__((ext_vector_type(4)));
-    T tmp[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) tmp[q] = from_f32<T>(v[q]);
-    *(vec4 *)dst = *(const vec4 *)tmp;
-}
 
 // Stores through a buffer resource: a lane whose row lies past the output
 // gets an offset past the resource's end and the hardware drops its store, so
@@ -871,41 +863,37 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
     }
 }
 
-template <typename T, typename OT, int BM, int BN, int WM, int WN, int STAGES, int BK, int OCC, Epi KIND>
-__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
-gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int lda, const T *__restrict__ W, EpiArgs e,
-                int grid_n) {
-    constexpr int WAVES = WM * WN;
-    constexpr int EPC = 16 / (int)sizeof(T);                 // elements in a 16-byte chunk
-    constexpr int ROWB = BK * (int)sizeof(T), CHUNKS = ROWB / 16;   // bytes and chunks of a tile row
-    constexpr int RPI = 64 / CHUNKS;                      // rows one load instruction fills
-    constexpr int TILE = (BM + BN) * ROWB;             // bytes of one stage
-    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA tiles per wave
-    constexpr int LA = BM / RPI / WAVES, LB = BN / RPI / WAVES;   // load instructions per wave per stage
-    constexpr int L = LA + LB;
+// The pipelined kernel's shape: a BM x BN output tile, WM x WN waves, a
+// STAGES-deep ring of BK-column stages.
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK>
+struct LdsTile {
+    static constexpr int WAVES = WM * WN;
+    static constexpr int EPC = 16 / (int)sizeof(T);                 // elements in a 16-byte chunk
+    static constexpr int ROWB = BK * (int)sizeof(T), CHUNKS = ROWB / 16;   // bytes and chunks of a tile row
+    static constexpr int RPI = 64 / CHUNKS;                         // rows one load instruction fills
+    static constexpr int TILE = (BM + BN) * ROWB;                   // bytes of one stage
+    static constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles per wave
+    static constexpr int LA = BM / RPI / WAVES, LB = BN / RPI / WAVES;   // load instructions per wave per stage
+    static constexpr int L = LA + LB;
     static_assert(ROWB == 128 || ROWB == 64, "tile rows of 64 or 128 bytes");
     static_assert(LA * RPI * WAVES == BM && LB * RPI * WAVES == BN, "whole row groups per wave");
     static_assert(STAGES >= 2 && STAGES * TILE <= 160 * 1024, "LDS");
     static_assert((STAGES - 2) * L < 64, "vmcnt");
-    typedef typename Mma<T>::frag frag;
-    typedef typename Mma<T>::acc acc_t;
-    extern __shared__ __attribute__((aligned(1024))) char smem[];
+};
 
-    const Live lv = live_of(sp);
-    const int M = lv.tokens;
-    // XCD-aware renumbering over the span's own tiles; blocks past them leave.
-    const int live = (M + BM - 1) / BM * grid_n;
-    if ((int)blockIdx.x >= live) return;
-    A += (size_t)lv.tok0 * a_tok;
-    place_epilogue<KIND, OT>(e, lv);
-    const int per = live / 8;
-    int b = blockIdx.x;
-    if (b < per * 8) b = (b % 8) * per + b / 8;
-    const int tile_n = b % grid_n, tile_m = b / grid_n;
-    const int m0 = tile_m * BM, n0 = tile_n * BN;
-    // The wave index is uniform: kept in scalar registers, the LDS bases of
-    // the direct loads (M0) need no per-load readfirstlane.
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+// The pipelined main loop: acc[i][j] (this wave's MFMA tiles, zeroed by the
+// caller) takes the sums over all of K of the BM x BN tile whose first row
+// and column are m0 and n0 (rows of A past M and of W past N read as the
+// last ones). Leaves every wave's last fragment reads done but the stages
+// still in use: the caller syncs before it reuses the LDS.
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK>
+__device__ __forceinline__ void lds_mainloop(char *smem, const T *__restrict__ A, int lda, const T *__restrict__ W,
+                                             int M, int N, int K, int m0, int n0, int wave, int lane,
+                                             typename Mma<T>::acc (&acc)[BM / WM / 32][BN / WN / 32]) {
+    using P = LdsTile<T, BM, BN, WM, WN, STAGES, BK>;
+    constexpr int EPC = P::EPC, ROWB = P::ROWB, CHUNKS = P::CHUNKS, RPI = P::RPI, TILE = P::TILE;
+    constexpr int TM = P::TM, TN = P::TN, LA = P::LA, LB = P::LB, L = P::L;
+    typedef typename Mma<T>::frag frag;
     const int wm = wave / WN, wn = wave % WN;
 
     // The operands are read through buffer resources based at the tile's
@@ -953,24 +941,6 @@ gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int l
         (void)k0;
 #endif
     };
-
-    // 16 rows a pass (half the staging LDS of 32, and the same row-wise
-    // stores); 32 for the QKV scatter when they fit, so each V^T column
-    // gets 64 contiguous bytes a store instead of 32.
-    constexpr bool QKV_KIND = KIND == Epi::Qkv || KIND == Epi::QkvRope;
-    constexpr int PASS = QKV_KIND && WAVES * 32 * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <=
-                                         STAGES * TILE
-                             ? 32
-                             : 16;
-    static_assert(WAVES * PASS * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <= STAGES * TILE,
-                  "epilogue staging fits the stages");
-    const int mw = m0 + wm * (BM / WM), nw = n0 + wn * (BN / WN);
-
-    acc_t acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{};
 
     const int nk = K / BK;
 #pragma unroll
@@ -1044,6 +1014,54 @@ gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int l
         }
     }
 
+}
+
+template <typename T, typename OT, int BM, int BN, int WM, int WN, int STAGES, int BK, int OCC, Epi KIND>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
+gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int lda, const T *__restrict__ W, EpiArgs e,
+                int grid_n) {
+    using P = LdsTile<T, BM, BN, WM, WN, STAGES, BK>;
+    constexpr int WAVES = P::WAVES, TILE = P::TILE, TM = P::TM, TN = P::TN;
+    typedef typename Mma<T>::acc acc_t;
+    extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+    const Live lv = live_of(sp);
+    const int M = lv.tokens;
+    // XCD-aware renumbering over the span's own tiles; blocks past them leave.
+    const int live = (M + BM - 1) / BM * grid_n;
+    if ((int)blockIdx.x >= live) return;
+    A += (size_t)lv.tok0 * a_tok;
+    place_epilogue<KIND, OT>(e, lv);
+    const int per = live / 8;
+    int b = blockIdx.x;
+    if (b < per * 8) b = (b % 8) * per + b / 8;
+    const int tile_n = b % grid_n, tile_m = b / grid_n;
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    // The wave index is uniform: kept in scalar registers, the LDS bases of
+    // the direct loads (M0) need no per-load readfirstlane.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+
+    // 16 rows a pass (half the staging LDS of 32, and the same row-wise
+    // stores); 32 for the QKV scatter when they fit, so each V^T column
+    // gets 64 contiguous bytes a store instead of 32.
+    constexpr bool QKV_KIND = KIND == Epi::Qkv || KIND == Epi::QkvRope;
+    constexpr int PASS = QKV_KIND && WAVES * 32 * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <=
+                                         STAGES * TILE
+                             ? 32
+                             : 16;
+    static_assert(WAVES * PASS * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <= STAGES * TILE,
+                  "epilogue staging fits the stages");
+    const int mw = m0 + wm * (BM / WM), nw = n0 + wn * (BN / WN);
+
+
+    acc_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{};
+    lds_mainloop<T, BM, BN, WM, WN, STAGES, BK>(smem, A, lda, W, M, N, K, m0, n0, wave, lane, acc);
+
     // The epilogue's per-column constants, read now (not held through the
     // main loop) and before the first store, so no store waits behind them.
     EpiCols<TN, PASS, sizeof(T) == 1> cols;
@@ -1097,8 +1115,163 @@ static hipError_t launch_lds(hipStream_t s, const GemmRows &gr, int M, int N, in
     return hipErrorInvalidValue;
 }
 
+// ---- Whole-row tiles: the residual add and the LayerNorm in the epilogue ------------
+//
+// A product whose N is the hidden size (attention-out, FFN-out) on BM x N
+// tiles, so each workgroup holds whole rows: y = A W^T + b, the residual add
+// and the row's LayerNorm happen in its epilogue, and y never goes to HBM
+// (the reference's LN-fused tile: core/cuda/autotune.h:40-41,
+// core/cuda/kernels.cu:2954-2955, chosen at core/cuda/backend.cpp:1807-1849).
+// The epilogue takes the tile's rows 32 WM at a time (one 32-row MFMA band
+// of every wave row): each wave stages its columns of them through LDS, y
+// rounded to the operand type as the separate product stores it; then each
+// 32-lane half norms whole rows with the row kernels' arithmetic
+// (rowmath.h: the same lane map, sums and rounding), so every row gets the
+// bits the product followed by add_layer_norm gives it. Post-norm rows
+// whose residual is carried in the 16-bit operand rows (out_h): read and
+// written there, and in F32 too with keep_f32.
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_ln_kernel(Span sp, int a_tok, int K, const T *__restrict__ A, int lda, const T *__restrict__ W, LnArgs e) {
+    using P = LdsTile<T, BM, BN, WM, WN, STAGES, BK>;
+    constexpr int WAVES = P::WAVES, TM = P::TM, TN = P::TN, G = BN / 256;
+    constexpr int PR = 32 * WM;         // rows a pass
+    constexpr int YS = BN + 8;          // staged row stride: 16 bytes of padding
+    constexpr int RH = PR / WAVES / 2;  // rows a half-wave norms a pass
+    static_assert(BN % 256 == 0 && RH >= 1 && RH * 2 * WAVES == PR, "whole rows a half-wave");
+    static_assert(PR * YS * (int)sizeof(T) + 2 * BN * 4 <= STAGES * P::TILE, "staging fits the stages");
+    typedef typename Mma<T>::acc acc_t;
+    extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+    const Live lv = live_of(sp);
+    const int M = lv.tokens;
+    // XCD-aware renumbering over the span's row tiles; blocks past them leave.
+    const int live = (M + BM - 1) / BM;
+    if ((int)blockIdx.x >= live) return;
+    A += (size_t)lv.tok0 * a_tok;
+    const int per = live / 8;
+    int b = blockIdx.x;
+    if (b < per * 8) b = (b % 8) * per + b / 8;
+    const int m0 = b * BM;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+
+    acc_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{};
+    lds_mainloop<T, BM, BN, WM, WN, STAGES, BK>(smem, A, lda, W, M, BN, K, m0, 0, wave, lane, acc);
+
+    const int h = lane >> 5, ql = lane & 31;
+    // The bias of this lane's columns 32 j + ql of the wave's, added as the
+    // sums go to LDS.
+    float bl[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bl[j] = e.bias ? e.bias[wn * (BN / WN) + 32 * j + ql] : 0.0f;
+    __syncthreads();   // every wave is done with the stages
+    T *ys = reinterpret_cast<T *>(smem);
+    float *lw = reinterpret_cast<float *>(smem + PR * YS * (int)sizeof(T));   // the norm's weight, then its bias
+    for (int c = tid; c < BN; c += 64 * WAVES) {
+        lw[c] = e.ln_w[c];
+        lw[BN + c] = e.ln_b ? e.ln_b[c] : 0.0f;
+    }
+    T *xh = reinterpret_cast<T *>(e.out_h) + (size_t)lv.tok0 * BN;
+    float *xf = e.x + (size_t)lv.tok0 * BN;
+    // The residual rows a half normalizes in pass i, 16 raw bytes of each
+    // group: read a pass ahead, so their latency hides behind the pass
+    // before (rows past M read row M - 1, and are not stored).
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    auto row_of = [&](int i, int q) {
+        const int pr = (wave * 2 + h) * RH + q;
+        return m0 + (pr / 32) * (BM / WM) + 32 * i + (pr % 32);
+    };
+    auto load_res = [&](int i, u32x4 (&r)[RH][G]) {
+#pragma unroll
+        for (int q = 0; q < RH; ++q) {
+            const int m = min(row_of(i, q), M - 1);
+#pragma unroll
+            for (int g = 0; g < G; ++g) r[q][g] = *(const u32x4 *)(xh + (size_t)m * BN + 8 * (ql + 32 * g));
+        }
+    };
+    u32x4 res[2][RH][G];
+    load_res(0, res[0]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        // Band i of this wave's rows is pass rows wm * 32 ..; register r of
+        // MFMA tile (i, j) is row 8 (r / 4) + 4 h + r % 4, column 32 j + ql.
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = wm * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                ys[row * YS + wn * (BN / WN) + 32 * j + ql] = from_f32<T>(acc[i][j][r] + bl[j]);
+            }
+        __syncthreads();
+        if (i + 1 < TM) load_res(i + 1, res[(i + 1) & 1]);
+#pragma unroll
+        for (int q = 0; q < RH; ++q) {
+            const int pr = (wave * 2 + h) * RH + q;   // the half's row of the pass
+            const int m = row_of(i, q);
+            if (m >= M) continue;   // (the same for the whole half)
+            float v[G][8];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int c = 8 * (ql + 32 * g);
+                float a[8];
+                load8(reinterpret_cast<const T *>(&res[i & 1][q][g]), v[g]);
+                load8(ys + pr * YS + c, a);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[g][k] = v[g][k] + a[k];
+            }
+            float mean, inv;
+            ln_pair_stats<G>(v, BN, ql, e.eps, mean, inv);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int c = 8 * (ql + 32 * g);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[g][k] = ln_out(v[g][k], mean, inv, lw[c + k], lw[BN + c + k]);
+                if (e.keep_f32) store8(xf + (size_t)m * BN + c, v[g]);
+                store8(xh + (size_t)m * BN + c, v[g]);
+            }
+        }
+        __syncthreads();   // the pass's rows are read before the next pass stages
+    }
+}
+
+// The whole-row block shape: 128 x 768, 8 waves as 1 x 8 (each 128 x 96),
+// 32 columns of k a stage in two stages (114 KB). (As 2 x 4 waves of 64 x
+// 192, both fragment sets double-buffered, it needs more than 256 registers.)
+template <typename T, int WM, int WN>
+static hipError_t launch_ln(hipStream_t s, const GemmRows &gr, int M, int K, const void *A, int lda, const void *W,
+                            const LnArgs &e) {
+    constexpr int BM = 128, BN = 768, STAGES = 2, BK = 32;
+    constexpr int bytes = LdsTile<T, BM, BN, WM, WN, STAGES, BK>::TILE * STAGES;
+    hipLaunchKernelGGL((gemm_ln_kernel<T, BM, BN, WM, WN, STAGES, BK>), dim3((M + BM - 1) / BM), dim3(64 * WM * WN),
+                       bytes, s, gr.sp, gr.a_tok, K, (const T *)A, lda, (const T *)W, e);
+    return hipGetLastError();
+}
+
+bool gemm_ln_takes(Dt dt, int hidden, int K, int lda, bool res_h) {
+    return dt == Dt::F16 && hidden == 768 && res_h && K % 32 == 0 && lda % 8 == 0;
+}
+
+bool gemm_ln_tile(int tile) { return tile == LN_TILE; }
+
+hipError_t gemm_ln(hipStream_t s, Dt dt, const Span &sp, int max_m, int hidden, int K, const void *A, int lda,
+                   int a_tok, const void *W, const LnArgs &e, int tile) {
+    if (max_m <= 0) return hipSuccess;
+    if (!gemm_ln_takes(dt, hidden, K, lda, e.res_h != 0) || !e.out_h || !e.ln_w || (e.keep_f32 && !e.x))
+        return hipErrorInvalidValue;
+    if (tile == 0) tile = LN_TILE;
+    if (!gemm_ln_tile(tile)) return hipErrorInvalidValue;
+    if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
+    const GemmRows gr{sp, a_tok ? a_tok : lda};
+    return launch_ln<_Float16, 1, 8>(s, gr, max_m, K, A, lda, W, e);
+}
+
 // The highest block-shape number.
-constexpr int TILES = 16;
+constexpr int TILES = 17;
 
 int gemm_tiles() { return TILES; }
 
@@ -1127,7 +1300,7 @@ bool gemm_made_to_fail(int tile) {
 static const char *const TILE_NAME[TILES + 1] = {
     "auto",      "r128x128",   "r256x128",     "r64x128",    "256x128", "128x128", "128x256",
     "256x256",   "128x128s2",  "256x128k32",   "128x256k32", "256x128k32s3", "256x256k32", "256x192",
-    "r64x64",    "256x384",    "256x384k32s4"};
+    "r64x64",    "256x384",    "256x384k32s4", "128x768ln"};
 
 const char *gemm_tile_name(int tile) { return tile >= 0 && tile <= TILES ? TILE_NAME[tile] : "?"; }
 
@@ -1293,6 +1466,8 @@ static hipError_t gemm_i8(hipStream_t s, const GemmRows &gr, int M, int N, int K
 hipError_t gemm(hipStream_t s, Dt dt, const Span &sp, int M, int N, int K, const void *A, int lda, int a_tok,
                 const void *W, const EpiArgs &e, int tile) {
     if (M <= 0) return hipSuccess;
+    // The whole-row shapes take a LayerNorm with them: gemm_ln.
+    if (gemm_ln_tile(tile)) return hipErrorInvalidValue;
     const GemmRows gr{sp, a_tok ? a_tok : lda};
     if (dt == Dt::I8) return gemm_i8(s, gr, M, N, K, A, lda, W, e, tile);
     if (K % (16 / (int)dt_bytes(dt)) != 0 || lda % (16 / (int)dt_bytes(dt)) != 0) return hipErrorInvalidValue;

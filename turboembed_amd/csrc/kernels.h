@@ -174,6 +174,29 @@ int gemm_tile_by_name(const char *s, size_t n);
 int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap);
 // The 256 x 384 block shape (8 waves of 128 x 96): a split run's products' shape.
 constexpr int WIDE_TILE = 15;
+// A post-norm product of N = hidden with the residual add and the LayerNorm
+// in its epilogue (whole-row tiles): y = A W^T + bias rounded to the operand
+// type, v = out_h + y, out_h = LN(v) (and x = LN(v) in F32 with keep_f32),
+// each row with the bits add_layer_norm gives it after the plain product.
+// Rows point at the run's token 0; the span's tokens are taken.
+struct LnArgs {
+    const float *bias = nullptr;   // [hidden] the product's bias, or NULL
+    float *x = nullptr;            // [tokens][hidden] F32 rows (written with keep_f32)
+    void *out_h = nullptr;         // [tokens][hidden] 16-bit rows: the residual, then LN(v)
+    const float *ln_w = nullptr, *ln_b = nullptr;   // ln_b NULL: no bias
+    float eps = 0;
+    int res_h = 1;                 // the residual is carried in out_h (the one form taken)
+    int keep_f32 = 0;
+};
+// The whole-row block shape (128 x 768, 8 waves of 128 x 96).
+constexpr int LN_TILE = 17;
+bool gemm_ln_tile(int tile);
+// Whether the fused kernel takes a product of this operand type, hidden size,
+// inner size and operand stride on a session whose residual is in the
+// 16-bit rows (res_h).
+bool gemm_ln_takes(Dt dt, int hidden, int K, int lda, bool res_h);
+hipError_t gemm_ln(hipStream_t s, Dt dt, const Span &sp, int max_m, int hidden, int K, const void *A, int lda,
+                   int a_tok, const void *W, const LnArgs &e, int tile = 0);
 // A test hook standing in for a device that cannot launch one block shape:
 // the shape a name spells (NULL or "" for none) fails to launch from now on.
 // False for a name that spells no shape. gemm_made_to_fail says whether a
@@ -184,12 +207,13 @@ bool gemm_made_to_fail(int tile);
 // Softmax attention within each row and head over Q and K ([heads][tcap][d]
 // each) and V transposed ([heads][d][tcap]), in `dt`, one after another in
 // qkv, into ctx [tokens, heads * d] in `dt`. window: keys within `window` of
-// the query (|i - j| <= window), or INT32_MAX. F16 and BF16 run on the matrix
-// cores unless `simple`; F32 runs the scalar path.
+// the query (|i - j| <= window), or INT32_MAX. F16 and BF16 heads of 64 run
+// on the matrix cores (path 0: 256-query workgroups; 2: 128-query ones)
+// unless path is 1; F32 runs the scalar path.
 // The span's rows; max_rows and max_len bound the grid.
 hipError_t attention(hipStream_t s, Dt dt, const void *qkv, int tcap, int heads, int d, const Packing &p,
                      const int32_t *mask, const Span &sp, int max_rows, int max_len, int window, void *ctx,
-                     bool simple = false);
+                     int path = 0);
 
 // A mean's tokens are summed in chunks of POOL_CHUNK, each chunk in token
 // order by its own workgroup, then the chunks' sums in chunk order: `part`

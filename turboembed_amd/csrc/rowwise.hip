@@ -7,6 +7,7 @@
 
 #include "kernels.h"
 #include "devmath.h"
+#include "rowmath.h"
 
 namespace rocm {
 
@@ -335,93 +336,30 @@ __global__ void __launch_bounds__(256) add_layer_norm_kernel(Span sp, int hidden
     if (qo.q) quant_row<G, H>(v, hidden, qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden, qo.scale + t);
 }
 
-// Eight consecutive columns at p, as F32.
-template <typename H> __device__ __forceinline__ void load8(const H *p, float (&v)[8]) {
-    typedef H h8 __attribute__((ext_vector_type(8)));
-    const h8 q = *(const h8 *)p;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = to_f32(q[k]);
-}
-__device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
-    const float4_t a = *(const float4_t *)p, b = *(const float4_t *)(p + 4);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = a[k], v[4 + k] = b[k];
-}
-template <typename H> __device__ __forceinline__ void store8(H *p, const float (&v)[8]) {
-    typedef H h8 __attribute__((ext_vector_type(8)));
-    h8 q;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) q[k] = from_f32<H>(v[k]);
-    *(h8 *)p = q;
-}
-__device__ __forceinline__ void store8(float *p, const float (&v)[8]) {
-    *(float4_t *)p = float4_t{v[0], v[1], v[2], v[3]};
-    *(float4_t *)(p + 4) = float4_t{v[4], v[5], v[6], v[7]};
-}
-
-// The sum over a 32-lane half of the wave.
-__device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-// A half-wave row's norm weight and bias (0 where absent), 8 columns a lane
-// in each group of 256.
-template <int G>
-__device__ __forceinline__ void load_wb8(const float *__restrict__ w, const float *__restrict__ b, int hidden, int hl,
-                                         float (&wv)[G][8], float (&bv)[G][8]) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const int c = 8 * (hl + 32 * g);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) wv[g][k] = bv[g][k] = 0.0f;
-        if (c >= hidden) continue;
-        load8(w + c, wv[g]);
-        if (b) load8(b + c, bv[g]);
-    }
-}
-
-// A half-wave row normalized, (v - mean) / sqrt(var + eps) * w + b.
-template <int G>
-__device__ __forceinline__ void ln_pair_apply(float (&v)[G][8], int hidden, int hl, const float (&wv)[G][8],
-                                              const float (&bv)[G][8], float eps) {
-    float s = 0.0f;
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int k = 0; k < 8; k += 2) s += v[g][k] + v[g][k + 1];
-    const float mean = half_sum(s) / (float)hidden;
-    float q = 0.0f;
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-        if (8 * (hl + 32 * g) < hidden)
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float c = v[g][k] - mean;
-                q = fmaf(c, c, q);
-            }
-    const float inv = 1.0f / sqrtf(half_sum(q) / (float)hidden + eps);
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[g][k] = (v[g][k] - mean) * inv * wv[g][k] + bv[g][k];
-}
-
 // add_layer_norm_kernel's work two rows a wave at a time: each 32-lane half
 // takes R rows in turn, 8 consecutive columns a lane in each group of 256
 // (16-byte reads and writes of 16-bit rows, where a wave a row moves 8 bytes
 // a lane), with the norm's weight and bias read once for them (both halves
 // read the same words). Every row's loads go out before the first row's
-// sums. Hidden a multiple of 8.
-template <int G, typename Y, typename H, bool RES_H, int R>
-__global__ void __launch_bounds__(256) add_ln_pair_kernel(Span sp, int hidden, float *__restrict__ x,
-                                                          const Y *__restrict__ y, const float *__restrict__ ln_w,
-                                                          const float *__restrict__ ln_b, float eps, int pre_norm,
-                                                          int keep_f32, H *__restrict__ out_h, QuantOut qo) {
+// sums. Hidden a multiple of 8. WAVES sets the block (64 WAVES threads),
+// its launch bound and the rows it takes (2 R a wave): a block launched
+// wider than its bound is refused by the runtime at launch, and rows
+// numbered for another width would be skipped or taken twice, so the
+// launcher derives both from this one parameter (pair_blocks).
+template <int WAVES, int R> static dim3 pair_blocks(int tokens) {
+    static_assert(WAVES >= 1 && WAVES <= 16 && R >= 1, "1 to 16 waves a block");
+    constexpr int ROWS = 2 * WAVES * R;   // rows a block
+    return dim3((tokens + ROWS - 1) / ROWS);
+}
+
+template <int G, typename Y, typename H, bool RES_H, int R, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES)
+add_ln_pair_kernel(Span sp, int hidden, float *__restrict__ x, const Y *__restrict__ y, const float *__restrict__ ln_w,
+                   const float *__restrict__ ln_b, float eps, int pre_norm, int keep_f32, H *__restrict__ out_h,
+                   QuantOut qo) {
     const Live lv = live_of(sp);
     // This half's first row (it takes R consecutive rows).
-    const int local0 = ((blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1)) * R;
+    const int local0 = ((blockIdx.x * WAVES + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1)) * R;
     // (A half's lanes all share its rows; the sums stay within the half.)
     if (local0 >= lv.tokens) return;
     const int hl = threadIdx.x & 31;
@@ -469,43 +407,17 @@ __global__ void __launch_bounds__(256) add_ln_pair_kernel(Span sp, int hidden, f
             if (!pre_norm && keep_f32) store8(row + c, v[i][g]);
             if (hr) store8(hr + c, v[i][g]);
         }
-        if (qo.q) {
-            // The row's int8 codes from its values as rounded to H, as quant_row.
-            int8_t *qr = qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden;
-            float r[G][8], mx = 0.0f;
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    r[g][k] = 8 * (hl + 32 * g) < hidden ? to_f32(from_f32<H>(v[i][g][k])) : 0.0f;
-                    mx = fmaxf(mx, fabsf(r[g][k]));
-                }
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-            const float iv = mx > 0.0f ? 127.0f / mx : 0.0f;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const int c = 8 * (hl + 32 * g);
-                if (c >= hidden) continue;
-                uint32_t w[2] = {0, 0};
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const int code = (int)fminf(fmaxf(rintf(r[g][k] * iv), -127.0f), 127.0f);
-                    w[k >> 2] |= (uint32_t)(uint8_t)(int8_t)code << (8 * (k & 3));
-                }
-                *(uint2 *)(qr + c) = uint2{w[0], w[1]};
-            }
-            if (hl == 0) qo.scale[t] = mx / 127.0f;
-        }
+        // The row's int8 codes from its values as rounded to H, as quant_row.
+        if (qo.q)
+            quant_pair_row<G, H>(v[i], hidden, hl, qo.q + (size_t)lv.tok0 * qo.tok_stride + (size_t)local * hidden,
+                                 qo.scale + t);
     }
 }
 
 // Rows a half-wave takes (2: BERT-base 0.9% faster a step than 1, with
 // the weight reads halved; 4 is 2.5% slower, its registers halving the
-// waves a SIMD).
-#ifndef LN_ROWS
-#define LN_ROWS 2
-#endif
+// waves a SIMD), and waves a block (4: two-wave blocks were 13% slower).
+constexpr int LN_ROWS = 2, LN_WAVES = 4;
 
 template <typename H, int G, typename Y>
 static hipError_t add_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, float *x, const void *y,
@@ -517,9 +429,9 @@ static hipError_t add_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden
     // must give the bits of the fused one.
     if constexpr (sizeof(Y) == 2 && sizeof(H) == 2) {
         if (res_h && hidden % 8 == 0) {
-            hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, true, LN_ROWS>), dim3((tokens + 8 * LN_ROWS - 1) / (8 * LN_ROWS)),
-                               dim3(256), 0, s, sp, hidden,
-                               x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
+            hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, true, LN_ROWS, LN_WAVES>),
+                               (pair_blocks<LN_WAVES, LN_ROWS>(tokens)), dim3(64 * LN_WAVES), 0, s,
+                               sp, hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
             return hipGetLastError();
         }
     }
@@ -554,8 +466,8 @@ static hipError_t add_ln_y(hipStream_t s, const Span &sp, int tokens, int hidden
 // tokens a wave: each 32-lane half takes a token, 8 consecutive columns a
 // lane in each group of 256 (twice the tokens' dependent id and row reads in
 // flight a wave), the norm's weight and bias read once for both.
-template <int G, typename H>
-__global__ void __launch_bounds__(256) embed_ln_pair_kernel(Span sp, int hidden, const int32_t *__restrict__ ids,
+template <int G, typename H, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) embed_ln_pair_kernel(Span sp, int hidden, const int32_t *__restrict__ ids,
                                                             const int32_t *__restrict__ types, Packing p, int offset,
                                                             const float *__restrict__ word,
                                                             const float *__restrict__ pos,
@@ -564,7 +476,7 @@ __global__ void __launch_bounds__(256) embed_ln_pair_kernel(Span sp, int hidden,
                                                             const float *__restrict__ ln_b, float eps,
                                                             H *__restrict__ xh, const int32_t *__restrict__ zero_mask) {
     const Live lv = live_of(sp);
-    const int local = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1);
+    const int local = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1);
     // (A half's lanes all share its token; the sums stay within the half.)
     if (local >= lv.tokens) return;
     const int t = lv.tok0 + local, hl = threadIdx.x & 31;
@@ -619,7 +531,8 @@ static hipError_t embed_ln_v(hipStream_t s, const Span &sp, int tokens, int hidd
                              const int32_t *zero_mask, const QuantOut &qo) {
     if constexpr (sizeof(H) == 2) {
         if (!x && xh && !qo.q && hidden % 8 == 0) {
-            hipLaunchKernelGGL((embed_ln_pair_kernel<G, H>), dim3((tokens + 7) / 8), dim3(256), 0, s, sp, hidden, ids,
+            hipLaunchKernelGGL((embed_ln_pair_kernel<G, H, LN_WAVES>), (pair_blocks<LN_WAVES, 1>(tokens)),
+                               dim3(64 * LN_WAVES), 0, s, sp, hidden, ids,
                                types, p, offset, word, pos, type, ln_w, ln_b, eps, (H *)xh, zero_mask);
             return hipGetLastError();
         }

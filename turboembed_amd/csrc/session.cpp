@@ -532,6 +532,7 @@ bool mfma_attention(Dt act, uint32_t head_width) { return act != Dt::F32 && head
 }  // namespace
 
 static void split_defaults(Session &s);
+static bool ln_fusable(const Session &s, int g);
 
 Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_backend_tuning *tuning) {
     if (desc->task != TURBO_TASK_EMBED && desc->task != TURBO_TASK_RERANK)
@@ -607,7 +608,7 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     Choices &kc = s->kc;
     kc.bins = bins_for((uint64_t)desc->max_batch * desc->max_seq);
     const bool mfma_attn = mfma_attention(s->act, m->hidden / m->heads);
-    for (int b = 0; b < kc.bins; ++b) kc.bin[b].simple_attention = !mfma_attn;
+    for (int b = 0; b < kc.bins; ++b) kc.bin[b].attn = mfma_attn ? ATTN_MFMA : ATTN_SIMPLE;
     split_defaults(*s);
     bool cached = false;
     if (tuned_mode && tuning->cached && *tuning->cached) {
@@ -615,14 +616,20 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         Choices c = kc;
         // A cached choice of a block shape that cannot launch here is not taken.
         bool launchable = true;
-        if (parse_choices(tuning->cached, &c, false, &why))
+        if (parse_choices(tuning->cached, &c, false, &why)) {
             for (int b = 0; b < c.bins; ++b)
-                for (int g = 0; g < G_COUNT; ++g)
+                for (int g = 0; g < G_COUNT; ++g) {
                     if (gemm_made_to_fail(c.bin[b].tile[g])) {
                         launchable = false;
                         why = std::string(BIN_NAME[b]) + ":" + GEMM_NAME[g] + "=" + gemm_tile_name(c.bin[b].tile[g]) +
                               " cannot launch on this device";
+                    } else if (gemm_ln_tile(c.bin[b].tile[g]) && !ln_fusable(*s, g)) {
+                        launchable = false;
+                        why = std::string(BIN_NAME[b]) + ":" + GEMM_NAME[g] + "=" + gemm_tile_name(c.bin[b].tile[g]) +
+                              " does not take this product";
                     }
+                }
+        }
         if (launchable && why.empty()) {
             kc = c;
             cached = true;
@@ -644,9 +651,19 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
                 fail(TURBO_E_UNSUPPORTED, std::string("rocm: ") + BIN_NAME[b] + ":" + GEMM_NAME[g] + "=" +
                                               gemm_tile_name(kc.bin[b].tile[g]) +
                                               ": the GEMM kernel cannot launch on this device");
+    // The whole-row shape carries the add + LayerNorm after an out or
+    // FFN-out product of a session whose residual is in 16-bit rows: forced
+    // on another product or session, it is refused.
+    for (int b = 0; b < kc.bins; ++b)
+        for (int g = 0; g < G_COUNT; ++g)
+            if (gemm_ln_tile(kc.bin[b].tile[g]) && !ln_fusable(*s, g))
+                fail(TURBO_E_UNSUPPORTED_OPTION, std::string("rocm: ") + BIN_NAME[b] + ":" + GEMM_NAME[g] + "=" +
+                                                     gemm_tile_name(kc.bin[b].tile[g]) +
+                                                     ": the LayerNorm-fused shape takes the out and FFN-out products "
+                                                     "of F16 post-norm sessions of hidden 768 alone");
     // The scalar path is the only one some sessions have.
     for (int b = 0; b < kc.bins; ++b)
-        if (!mfma_attn) kc.bin[b].simple_attention = true;
+        if (!mfma_attn) kc.bin[b].attn = ATTN_SIMPLE;
     const bool measure = ((mode == TURBO_AUTOTUNE_ON && !cached) || mode == TURBO_AUTOTUNE_RETUNE) && !all_forced(kc);
     if (const char *g = std::getenv("TURBO_ROCM_GRAPHS")) s->graphs = std::strcmp(g, "0") != 0;
 
@@ -1104,6 +1121,17 @@ static Bounds bounds_of(const Session &s, int b, uint32_t parts) {
 // coarsely), as do pre-norm models, whose residual no norm bounds.
 static bool residual_in_operand(const Session &s) { return s.act == Dt::F16 && !s.model->modern; }
 
+// Whether product g (out or FFN-out) can take its residual add and
+// LayerNorm in its epilogue (the whole-row shape, LN_TILE): post-norm F16
+// sessions carrying the residual in the 16-bit rows, at a hidden size the
+// kernel is built for.
+static bool ln_fusable(const Session &s, int g) {
+    const Model &m = *s.model;
+    if (g != G_OUT && g != G_FFN2) return false;
+    const int K = g == G_OUT ? (int)m.hidden : (int)m.inter;
+    return s.dt == Dt::F16 && residual_in_operand(s) && gemm_ln_takes(s.dt, (int)m.hidden, K, K, true);
+}
+
 // The layers over part `part` of the run's rows, on stream st: every
 // product, norm and attention launch reads that part's rows and tokens from
 // the run's dimensions. Layer reads pool their ranges as they pass.
@@ -1152,6 +1180,26 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
         }
         LAUNCH(NAMES[g], gemm(st, s.dt, sp, T, lg.N, lg.K, A, lg.K, a_tok, lg.W, lg.e, bc.tile[g]));
     };
+    // The out or FFN-out product of layer l with its residual add and the
+    // norm (w, b) in its epilogue, when the bin's choice for it is the
+    // whole-row shape: whether it ran so. (F16 post-norm sessions alone,
+    // whose residual is carried in xh; no int8 rows follow.)
+    auto mm_ln = [&](uint32_t l, GemmSlot g, const float *w, const float *b, bool keep_f32) {
+        if (bc.tile[g] != LN_TILE || !ln_fusable(s, g)) return false;
+        const LayerGemm lg = layer_gemm(s, l, g);
+        LnArgs ln;
+        ln.bias = lg.e.bias;
+        ln.x = s.x;
+        ln.out_h = s.xh;
+        ln.ln_w = w;
+        ln.ln_b = b;
+        ln.eps = m.eps;
+        ln.res_h = 1;
+        ln.keep_f32 = keep_f32 ? 1 : 0;
+        LAUNCH(g == G_OUT ? "gemm_out_ln" : "gemm_ffn_out_ln",
+               gemm_ln(st, s.dt, sp, T, H, lg.K, lg.A, lg.K, 0, lg.W, ln, LN_TILE));
+        return true;
+    };
     // The GEMM operand copy of x after an add + LayerNorm: xh, or on the F32
     // tier x itself (post-norm) or xh as F32 (pre-norm).
     void *norm_out = f32 && !m.modern ? nullptr : s.xh;
@@ -1164,7 +1212,8 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
     // final_norm(x), the scale the final states are on
     // (core/src/cpu/encoder/rotary/mod.rs:84-86, 161-168), normed into y,
     // which is free between a layer's last add and the next layer's out product.
-    const uint32_t nl = s.tap_alone ? m.layers + 1 - s.taps : m.layers;
+    uint32_t nl = s.tap_alone ? m.layers + 1 - s.taps : m.layers;
+    if (s.layers_limit) nl = std::min(nl, s.layers_limit);   // the tuner's runs
     const uint32_t reads = s.tap_alone ? 1 : s.taps;
     const int od = (int)s.output_dim;
     for (uint32_t l = 0; l < nl; ++l) {
@@ -1179,40 +1228,45 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
             LAUNCH("attention", deberta_attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, sp,
                                                   (int)bd.rows, (int)bd.max_len, L.pos_qk,
                                                   static_cast<const int32_t *>(m.rel_table.get()), (int)m.positions,
-                                                  s.rel_pos_t && !bc.simple_attention
+                                                  s.rel_pos_t && bc.attn != ATTN_SIMPLE
                                                       ? static_cast<const char *>(s.rel_pos_t) +
                                                             (size_t)l * m.rel_rows * 2 * H * dt_bytes(dt)
                                                       : nullptr,
                                                   s.ctxb));
         else
             LAUNCH("attention", attention(st, dt, s.qkv, (int)s.tcap, heads, dh, s.pk, s.mask, sp, (int)bd.rows,
-                                          (int)bd.max_len, window, s.ctxb, bc.simple_attention));
-        mm(l, G_OUT);
-        // Post-norm: x = LN1(x + y). Pre-norm: x += y, xh = LN_mlp(x).
-        if (m.modern)
-            LAUNCH("add_layer_norm",
-                   add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt, qo));
-        else
-            LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0, norm_out,
-                                                    dt, qo, res_h, !res_h));
+                                          (int)bd.max_len, window, s.ctxb, bc.attn));
+        // Post-norm: x = LN1(x + y), in the product's epilogue on the
+        // whole-row shape. Pre-norm: x += y, xh = LN_mlp(x).
+        if (!mm_ln(l, G_OUT, L.ln1_w, L.ln1_b, !res_h)) {
+            mm(l, G_OUT);
+            if (m.modern)
+                LAUNCH("add_layer_norm",
+                       add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln2_w, nullptr, m.eps, 1, norm_out, dt, qo));
+            else
+                LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln1_w, L.ln1_b, m.eps, 0,
+                                                        norm_out, dt, qo, res_h, !res_h));
+        }
         aq_ready = i8;
         mm(l, G_FFN1);
-        mm(l, G_FFN2);
         // Post-norm: x = LN2(x + y). Pre-norm: x += y and the next layer's
         // attention norm into xh, or after the last layer x = LN_final(x + y).
         const QuantOut next = l + 1 < nl ? qo : QuantOut();
         // A 16-bit residual writes the F32 rows where they are read: after
         // the last layer, and after a layer whose ranges are read.
         const bool keep_f32 = !res_h || l + 1 == nl || (reads > 1 && l + reads >= nl);
-        if (!m.modern)
-            LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0, norm_out,
-                                                    dt, next, res_h, keep_f32));
-        else if (l + 1 < nl)
-            LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, m.ls[l + 1].ln1_w, nullptr, m.eps,
-                                                    1, norm_out, dt, next));
-        else
-            LAUNCH("add_layer_norm",
-                   add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
+        if (!mm_ln(l, G_FFN2, L.ln2_w, L.ln2_b, keep_f32)) {
+            mm(l, G_FFN2);
+            if (!m.modern)
+                LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, L.ln2_w, L.ln2_b, m.eps, 0,
+                                                        norm_out, dt, next, res_h, keep_f32));
+            else if (l + 1 < nl)
+                LAUNCH("add_layer_norm", add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, m.ls[l + 1].ln1_w, nullptr,
+                                                        m.eps, 1, norm_out, dt, next));
+            else
+                LAUNCH("add_layer_norm",
+                       add_layer_norm(st, sp, T, H, s.x, s.y, s.ydt, m.final_w, nullptr, m.eps, 0, nullptr, dt));
+        }
         aq_ready = i8 && l + 1 < nl;
         if (reads > 1 && l + 1 < nl && l + reads >= nl) {
             const float *src = s.x;
@@ -1344,101 +1398,175 @@ void launch_run(Session &s) {
     encode(s, bounds_of(s, b, s.parts), s.timing);
 }
 
-// The tuner: each bin's four products timed at the bin's token count with
-// each candidate block shape, on operands of uniform values in the
-// session's own buffers; a candidate replaces the bin's choice (the rule's,
-// or the cached one: the incumbent, timed first) when it is faster by the
-// margin. In a bin whose runs split into parts, a product on the 256 x 384
-// shape (split_defaults) keeps it. Largest bins first, as they cost the
-// most; stops at the budget. Returns whether anything was timed.
+// Rows for the tuner's runs of bin b: the bin's token count (its upper edge,
+// or the session's capacity) as rows of max_seq tokens, the last one
+// shorter, ids spread over the vocabulary, types 0, one vector a row.
+static void write_tuner_rows(Session &s, int b) {
+    const Model &m = *s.model;
+    const uint32_t T = bin_tokens(b, s.tcap), S = s.max_seq;
+    const uint32_t rows = std::min<uint32_t>(s.max_batch, (T + S - 1) / S);
+    std::vector<int32_t> ids((size_t)rows * S), mask((size_t)rows * S, 0);
+    for (size_t i = 0; i < ids.size(); ++i) ids[i] = (int32_t)((i * 7919 + 1000) % m.vocab);
+    for (uint32_t r = 0; r < rows; ++r) {
+        const uint32_t len = std::min(S, T - std::min(T, r * S));
+        for (uint32_t p = 0; p < std::max(len, 1u); ++p) mask[(size_t)r * S + p] = 1;
+    }
+    turbo_backend_embed_rows d{};
+    d.struct_size = sizeof d;
+    d.batch = rows;
+    d.seq = S;
+    d.ids = ids.data();
+    d.mask = mask.data();
+    d.pooling = TURBO_POOLING_CLS;
+    d.normalize = TURBO_NORMALIZE_NONE;
+    d.output_dim = m.hidden;
+    session_write(&s, &d, nullptr, 0);
+}
+
+// Bin b's run through its first `layers` layers with the bin's current
+// choices, captured as a graph (its parts forked as a run's are) and
+// replayed back to back for about target_ms: milliseconds a replay.
+static float time_layers(Session &s, int b, uint32_t layers, float target_ms, hipEvent_t e0, hipEvent_t e1) {
+    hipStream_t st = s.ctx->stream;
+    s.layers_limit = layers;
+    struct Reset {
+        Session &s;
+        ~Reset() { s.layers_limit = 0; }
+    } reset{s};
+    check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "the tuner's graph");
+    hipGraph_t g = nullptr;
+    try {
+        encode(s, bounds_of(s, b, parts_of_bin(s, b)), false);
+    } catch (...) {
+        (void)hipStreamEndCapture(st, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    check(hipStreamEndCapture(st, &g), "the tuner's graph");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    check(ie, "the tuner's graph");
+    struct Drop {
+        hipGraphExec_t e;
+        ~Drop() { (void)hipGraphExecDestroy(e); }
+    } drop{exec};
+    // Two replays to warm up, timed for the count that fills target_ms.
+    check(hipEventRecord(e0, st), "the tuner's events");
+    for (int i = 0; i < 2; ++i) check(hipGraphLaunch(exec, st), "the tuner's run");
+    check(hipEventRecord(e1, st), "the tuner's events");
+    check(hipEventSynchronize(e1), "the tuner's run");
+    float ms = 0;
+    check(hipEventElapsedTime(&ms, e0, e1), "the tuner's events");
+    const int n = std::min(64, std::max(4, (int)(target_ms / std::max(ms / 2, 1e-3f))));
+    check(hipEventRecord(e0, st), "the tuner's events");
+    for (int i = 0; i < n; ++i) check(hipGraphLaunch(exec, st), "the tuner's run");
+    check(hipEventRecord(e1, st), "the tuner's events");
+    check(hipEventSynchronize(e1), "the tuner's run");
+    check(hipEventElapsedTime(&ms, e0, e1), "the tuner's events");
+    return ms / n;
+}
+
+// The tuner (the counterpart of the reference's, core/cuda/backend.cpp:
+// 2419-2880, core/cuda/autotune.h:21-41): for each bin, largest first, the
+// knobs in turn -- each product's block shape (with, for the out and FFN-out
+// products of a session that can fuse it, the whole-row shape carrying the
+// add + LayerNorm) and the attention path -- each candidate timed as the
+// bin's run through its first layer (the first global and local layers of a
+// windowed model) on rows of the bin's token count, as the run launches it:
+// split into its parts on the context's streams, captured and replayed back
+// to back for a few milliseconds (sustained: short bursts run at clocks a
+// sustained run does not). The incumbent (the rule's choice, or the cached
+// one) is timed again at each knob; a candidate replaces it when it is 2%
+// faster. Forced knobs and shapes that cannot launch are not timed. Lines
+// <bin>/<knob>/<variant>=<ms a layer's run>. Stops at the budget. Returns
+// whether anything was timed.
 bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
     using Clock = std::chrono::steady_clock;
     const Clock::time_point deadline = Clock::now() + std::chrono::milliseconds(budget_ms);
-    constexpr float MARGIN = 0.97f;   // a candidate must be 3% faster
-    constexpr int REPS = 3;
+    constexpr float MARGIN = 0.98f;
     Model &m = *s.model;
-    hipStream_t st = s.ctx->stream;
-    const size_t H = m.hidden, I = m.inter, tcap = s.tcap;
-    // Operands: x uniform in [-1, 1), and the activations from it.
-    check(fill_uniform(st, s.x, tcap * H, 1.0f, 17), "the tuner's operands");
-    if (s.act == Dt::F32) {
-        check(fill_uniform(st, (float *)s.xh, tcap * H, 1.0f, 18), "the tuner's operands");
-        check(fill_uniform(st, (float *)s.ctxb, tcap * H, 1.0f, 19), "the tuner's operands");
-        check(fill_uniform(st, (float *)s.ffn, tcap * I, 1.0f, 20), "the tuner's operands");
-    } else {
-        check(narrow(st, s.x, s.xh, tcap * H, s.act, nullptr), "the tuner's operands");
-        check(narrow(st, s.x, s.ctxb, tcap * H, s.act, nullptr), "the tuner's operands");
-        const size_t el = dt_bytes(s.act);
-        for (size_t o = 0; o < tcap * I; o += tcap * H)
-            check(narrow(st, s.x, static_cast<char *>(s.ffn) + o * el, std::min(tcap * H, tcap * I - o), s.act, nullptr),
-                  "the tuner's operands");
-    }
-    // No rows are written yet: every token sits at position 0 for the
-    // rotary epilogue of the tuner's products.
-    check(hipMemsetAsync(s.pk.pos, 0, tcap * 4, st), "the tuner's operands");
-    hipEvent_t ev[2 * REPS];
-    for (hipEvent_t &e : ev) check(hipEventCreate(&e), "the tuner's events");
+    const uint32_t layers = m.window && m.global_every > 1 ? std::min(m.layers, m.global_every) : 1;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    check(hipEventCreate(&e0), "the tuner's events");
     struct Events {
-        hipEvent_t *ev;
+        hipEvent_t a, b;
         ~Events() {
-            for (int i = 0; i < 2 * REPS; ++i) (void)hipEventDestroy(ev[i]);
+            if (a) (void)hipEventDestroy(a);
+            if (b) (void)hipEventDestroy(b);
         }
-    } guard{ev};
+    } guard{e0, nullptr};
+    check(hipEventCreate(&e1), "the tuner's events");
+    guard.b = e1;
+    const bool mfma_attn = mfma_attention(s.act, m.hidden / m.heads);
     bool any = false;
     char line[160];
-    for (int b = s.kc.bins - 1; b >= 0; --b) {
-        // The rows a launch of the bin takes at most: the bin's, or a part's.
+    for (int b = s.kc.bins - 1; b >= 0 && Clock::now() < deadline; --b) {
         const uint32_t P = parts_of_bin(s, b);
-        const int M = (int)bounds_of(s, b, P).part_tokens;
+        write_tuner_rows(s, b);
+        const float target = P > 1 ? 6.0f : 2.0f;
         BinChoice &bc = s.kc.bin[b];
-        for (int g = 0; g < G_COUNT; ++g) {
-            if (bc.tile_forced[g] || (P > 1 && bc.tile[g] == WIDE_TILE)) continue;
-            LayerGemm lg = layer_gemm(s, 0, (GemmSlot)g);
-            const void *A = lg.A;
-            if (s.dt == Dt::I8) {
-                check(quantize_rows(st, A, Dt::F16, M, lg.K, lg.K, s.aq, s.ascale), "the tuner's operands");
-                lg.e.a_scale = s.ascale;
-                lg.e.w_scale = lg.wscale;
-                A = s.aq;
+        auto timed = [&](const char *knob, const char *variant) {
+            const float ms = time_layers(s, b, layers, target, e0, e1);
+            std::snprintf(line, sizeof line, "%s/%s/%s=%.4f\n", BIN_NAME[b], knob, variant, ms);
+            *timings += line;
+            any = true;
+            return ms;
+        };
+        // The clock settles under the bin's load before the first timing.
+        (void)time_layers(s, b, layers, 10.0f, e0, e1);
+        for (int g = 0; g < G_COUNT && Clock::now() < deadline; ++g) {
+            if (bc.tile_forced[g]) continue;
+            const LayerGemm lg = layer_gemm(s, 0, (GemmSlot)g);
+            int cand[20];
+            int n = gemm_candidates(s.dt, lg.K, lg.K, lg.e, cand, 18);
+            // Split bins: the large shapes alone (each part's product fills
+            // about half the chip beside the other part's).
+            if (P > 1) {
+                int k = 0;
+                for (int i = 0; i < n; ++i)
+                    if (cand[i] == WIDE_TILE || cand[i] == 7 || cand[i] == 13 || cand[i] == 16) cand[k++] = cand[i];
+                n = k;
             }
-            int cand[16];
-            cand[0] = bc.tile[g];
-            const int n = 1 + gemm_candidates(s.dt, lg.K, lg.K, lg.e, cand + 1, 15);
-            float incumbent = 0, fastest = 0;
-            int best = -1;
-            for (int i = 0; i < n; ++i) {
-                if (i > 0 && cand[i] == cand[0]) continue;
-                // A block shape that cannot launch here is not timed.
-                if (gemm_made_to_fail(cand[i])) continue;
-                if (Clock::now() >= deadline) break;
-                auto launch = [&]() { return gemm(st, s.dt, M, lg.N, lg.K, A, lg.K, lg.W, lg.e, cand[i]); };
-                check(launch(), "the tuner's GEMM");
-                for (int r = 0; r < REPS; ++r) {
-                    check(hipEventRecord(ev[2 * r], st), "the tuner's events");
-                    check(launch(), "the tuner's GEMM");
-                    check(hipEventRecord(ev[2 * r + 1], st), "the tuner's events");
+            if (ln_fusable(s, g)) cand[n++] = LN_TILE;
+            const int incumbent = bc.tile[g];
+            float best = timed(GEMM_NAME[g], gemm_tile_name(incumbent));
+            int pick = incumbent;
+            const float bar = best;
+            for (int i = 0; i < n && Clock::now() < deadline; ++i) {
+                if (cand[i] == incumbent || gemm_made_to_fail(cand[i])) continue;
+                bc.tile[g] = cand[i];
+                float ms = 0;
+                try {
+                    ms = timed(GEMM_NAME[g], gemm_tile_name(cand[i]));
+                } catch (...) {
+                    bc.tile[g] = incumbent;
+                    throw;
                 }
-                check(hipStreamSynchronize(st), "the tuner's GEMM");
-                float least = 0;
-                for (int r = 0; r < REPS; ++r) {
-                    float ms = 0;
-                    check(hipEventElapsedTime(&ms, ev[2 * r], ev[2 * r + 1]), "the tuner's events");
-                    least = r == 0 ? ms : std::min(least, ms);
-                }
-                std::snprintf(line, sizeof line, "%s/%s/%s=%.4f\n", BIN_NAME[b], GEMM_NAME[g], gemm_tile_name(cand[i]),
-                              least);
-                *timings += line;
-                any = true;
-                if (i == 0) {
-                    incumbent = least;
-                } else if (best < 0 || least < fastest) {
-                    best = i;
-                    fastest = least;
+                bc.tile[g] = incumbent;
+                if (ms < best) {
+                    best = ms;
+                    pick = cand[i];
                 }
             }
-            if (incumbent > 0 && best > 0 && fastest <= MARGIN * incumbent) bc.tile[g] = cand[best];
+            if (pick != incumbent && best <= MARGIN * bar) bc.tile[g] = pick;
+        }
+        if (mfma_attn && !bc.attn_forced && !m.deberta && Clock::now() < deadline) {
+            const int incumbent = bc.attn;
+            const float bar = timed("attn", ATTN_NAME[incumbent]);
+            const int other = incumbent == ATTN_MFMA ? ATTN_MFMA128 : ATTN_MFMA;
+            bc.attn = other;
+            float ms = 0;
+            try {
+                ms = timed("attn", ATTN_NAME[other]);
+            } catch (...) {
+                bc.attn = incumbent;
+                throw;
+            }
+            bc.attn = ms <= MARGIN * bar ? other : incumbent;
         }
     }
+    s.written = false;
     s.ctx->say(LOG_DEBUG, "rocm: tuned kernels: " + format_choices(s.kc));
     return any;
 }

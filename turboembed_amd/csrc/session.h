@@ -209,6 +209,7 @@ struct Session {
     // timed launch by launch, launch their kernels directly. Off with
     // TURBO_ROCM_GRAPHS=0.
     bool graphs = true;
+    uint32_t layers_limit = 0;   // the tuner's runs: the first layers alone (0: every layer)
     hipGraphExec_t graph[BINS] = {};
     uint32_t bin_parts[BINS] = {};   // parts a bin's graph runs (its runs use as many or fewer)
     uint64_t captures = 0, graph_launches = 0;   // counted for the graphs hook
