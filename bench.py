@@ -438,25 +438,44 @@ def main():
 
     wrr_ms = write_run_read([(ids, mask, types)], args.steps)
 
-    # Per-kernel times from HIP events on the session's stream, one run.
+    # Per-kernel times from HIP events, one run launched directly as the
+    # replayed run executes (a split run's two parts side by side), each
+    # launch's pair of events on its own stream.
     sess.set_timing(True)
     sess.replay(1)
     times = sess.times()
     counts = sess.launches()
+    intervals = sess.intervals()
     sess.set_timing(False)
     per = kernel_flops(shape, tokens, lens)
     gemm_names = [k for k in times if k.startswith("gemm_")]
     gemm_ms = sum(times[k] for k in gemm_names)
     gemm_flops = sum(per[k] for k in gemm_names) * shape.layers
     total_flops = W.gemm_flops_per_token(shape) * tokens + W.attention_flops(shape, lens)
+
+    def busy_ms(names):
+        """The run's time with at least one launch of these kernels running:
+        the union of their launches' intervals over every stream."""
+        total, end = 0.0, float("-inf")
+        for a, b in sorted((a, b) for n, a, b in intervals if n in names):
+            if b > end:
+                total += b - max(a, end)
+                end = b
+        return total
+
     # The dominant kernel: the GEMM kernel (every linear layer's launches),
-    # or attention when it takes longer.
-    if times.get("attention", 0.0) > gemm_ms:
+    # or attention when it is busy longer. Its rate is its FLOPs over the
+    # time it was running (the parts' launches overlap, so their own
+    # durations sum past that time).
+    gemm_busy = busy_ms(set(gemm_names))
+    if busy_ms({"attention"}) > gemm_busy:
         dom, dom_ms, dom_flops, dom_launches = "attention", times["attention"], per["attention"] * shape.layers, \
             counts["attention"]
+        dom_busy = busy_ms({"attention"})
     else:
         dom, dom_ms, dom_flops, dom_launches = "gemm", gemm_ms, gemm_flops, sum(counts[k] for k in gemm_names)
-    achieved = dom_flops / (dom_ms / 1e3)
+        dom_busy = gemm_busy
+    achieved = dom_flops / (dom_busy / 1e3)
     traffic = None
     if dom == "gemm" and os.path.exists(traffic_file(args.workload)):
         with open(traffic_file(args.workload)) as f:
@@ -476,7 +495,11 @@ def main():
     roofline = {"kernel": dom, "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[dtype] / 1e12,
                 "unit": "TOP/s" if dtype == "i8" else "TFLOP/s", "frac": achieved / PEAK[dtype], "traffic": traffic,
                 "launches_per_step": dom_launches, "avg_launch_us": dom_ms / dom_launches * 1e3,
-                "flops_per_launch": dom_flops / dom_launches}
+                "flops_per_launch": dom_flops / dom_launches,
+                # The kernel's busy time in the timed run (at most the step),
+                # and how many of its launches ran at once on average.
+                "busy_us_per_step": dom_busy * 1e3, "overlap": dom_ms / dom_busy,
+                "timed_run_ms": max(b for _, _, b in intervals)}
 
     # The memory-bound kernels against HBM's published rate.
     n_out = len(rngs) if rngs else shape.batch

@@ -94,19 +94,19 @@ int32_t turbo_rocm_rerank_run(void *session, const int32_t *ids, const int32_t *
                               const float *pooler_weight, const float *pooler_bias, const float *classifier_weight,
                               float classifier_bias, float *scores, turbo_error *err);
 
-/* turbo_rocm_buffer_quantize_static: buffer_quantize (the table's entry,
- * turbo_backend.h:610-626) without an allocation. It has no counterpart in
- * the reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). The same codes, byte for byte, staged in a fixed device area of
- * 16 MiB a GPU (allocated once with the library, held until the process
- * ends) instead of memory allocated per call: the codes, then on a 256-byte
- * boundary the int8 ranges ([2, dim] F32), must fit it, or the call fails
- * with TURBO_E_INVALID_ARGUMENT before any device work. It calls no
- * allocating routine. Calls that overlap on one GPU through different
- * contexts share the area and race; calls through one context are serialized.
- * run, when not NULL, gets the int8 ranges' bytes in h2d_bytes and no
- * device allocation. */
+/* turbo_rocm_buffer_quantize_static: this backend's buffer_quantize entry
+ * without an allocation. It has no counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The same codes, byte
+ * for byte, as buffer_quantize, staged in a fixed device area of 16 MiB a GPU
+ * (allocated once with the library, held until the process ends) instead of
+ * memory allocated per call: the codes, then on a 256-byte boundary the int8
+ * ranges ([2, dim] F32), must fit it, or the call fails with
+ * TURBO_E_INVALID_ARGUMENT before any device work. It calls no allocating
+ * routine. Every context on a GPU shares that GPU's area; a lock per GPU,
+ * held through the call, serializes calls from any thread and context. run,
+ * when not NULL, gets the int8 ranges' bytes in h2d_bytes and the device
+ * allocations the call made (none) in device_allocs. */
 int32_t turbo_rocm_buffer_quantize_static(void *buffer, uint32_t quantization, const float *int8_ranges, uint32_t rows,
                                           uint32_t dim, turbo_backend_run *run, turbo_error *err);
 
@@ -131,12 +131,17 @@ int32_t turbo_rocm_session_packing(void *session, int32_t *start, int32_t *len, 
 /* The last run's final hidden states, [tokens, hidden] F32. */
 int32_t turbo_rocm_session_hidden(void *session, float *out, uint64_t floats, turbo_error *err);
 
-/* Times every kernel of the session's later runs with HIP events on the
- * context's stream; turbo_rocm_session_times then writes
+/* Times every kernel of the session's later runs with HIP events, each
+ * launch's pair on the stream it runs on (a split run's parts side by side,
+ * as the run executes them; its runs launch their kernels directly rather
+ * than replay a graph); turbo_rocm_session_times then writes
  * "<kernel> <ms> <launches>" lines: the milliseconds summed over the last
- * run's launches of that kernel, and how many there were. */
+ * run's launches of that kernel, and how many there were;
+ * turbo_rocm_session_intervals writes "<kernel> <start> <end>" a launch, in
+ * ms from the run's start, in launch order. */
 int32_t turbo_rocm_session_timing(void *session, uint32_t on, turbo_error *err);
 int32_t turbo_rocm_session_times(void *session, char *out, uint32_t len, turbo_error *err);
+int32_t turbo_rocm_session_intervals(void *session, char *out, uint32_t len, turbo_error *err);
 
 /* Runs the last written rows `runs` more times, back to back on the
  * context's stream, then waits: the rows stay resident on the device, so

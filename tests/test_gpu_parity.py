@@ -191,6 +191,24 @@ def test_packing_is_the_oracle_s_bit_for_bit(context, batch, width):
     model.close()
 
 
+def test_packing_on_planes_of_an_odd_capacity(context):
+    # A session of 3 x 5 token slots keeps its mask plane 16-byte aligned,
+    # so rows of 4 columns (read 16 bytes a lane) pack as the oracle does.
+    desc = small.bert(seed=13, positions=64)
+    ids, mask, types = small.ragged_rows(13, 3, 4, desc.vocab_size)
+    model = context.load(desc)
+    s = model.session(3, 5, S.TURBO_PRECISION_EXACT)
+    got = s.embed(ids, mask, types)
+    start, ln, at = s.packing()
+    o_start, o_len, o_at = oracle.pack(mask)
+    assert np.array_equal(start, o_start.astype(np.int32))
+    assert np.array_equal(ln, o_len.astype(np.int32))
+    assert np.array_equal(at, o_at.astype(np.int32))
+    assert_close(got, oracle.encode(desc, ids, mask, types), s.compute_dtype)
+    s.close()
+    model.close()
+
+
 @pytest.mark.parametrize("precision", [S.TURBO_PRECISION_EXACT, S.TURBO_PRECISION_FASTEST])
 def test_ranges(context, precision):
     desc = small.bert(seed=13)
@@ -602,6 +620,37 @@ def test_deberta_matrix_core_path_meets_the_oracle(context, monkeypatch, tier):
     monkeypatch.setenv("TURBO_ROCM_SPLIT", "2")
     s = model.session(40, 200, S.TURBO_PRECISION_FASTEST)
     assert_close(s.embed(ids, mask), oracle.encode(desc, ids, mask), s.compute_dtype)
+    s.close()
+    model.close()
+
+
+def test_deberta_projections_past_f16_run_the_scalar_form(context):
+    # Layer 0's query projections of the relative rows pass F16's range: a
+    # weight of 3e4 (within F16) on a hidden column that every LayerNorm
+    # zeroes in the states but the relative rows' norm carries at 10, in head
+    # dimensions whose keys are zero, so every score stays moderate. The F16
+    # session keeps those projections in F32 on the scalar form, its choices
+    # say so, and its vectors meet the oracle.
+    from test_deberta import small_deberta
+    from turboembed_amd.model import with_dtype
+    desc = with_dtype(small_deberta(seed=7, hidden=128, heads=2, inter=256, buckets=128, maximum=256, std=0.1),
+                      "f32")
+    t, col, dims = desc.tensors, 5, [0, 1, 2, 3]
+    t[1][col] = t[2][col] = 0.0                   # the embedding norm zeroes the column
+    t[4][col] = 10.0                              # the relative rows' norm carries it
+    for layer in range(desc.layers):
+        for i in (8, 9, 14, 15):                  # the layers' norms zero it too
+            t[6 + 16 * layer + i][col] = 0.0
+    t[6 + 2][dims, :] = 0.0                       # layer 0's keys are zero in these dimensions
+    t[6 + 3][dims] = 0.0
+    t[6 + 0][dims, col] = 3.0e4                   # its queries weigh the column
+    ids, mask = _deberta_rows(10, 5, 200, desc.vocab_size)
+    want = oracle.encode(desc, ids, mask)
+    model = context.load(desc)
+    s = model.session(5, 200, S.TURBO_PRECISION_FASTEST)
+    assert s.compute_dtype == S.TURBO_DTYPE_F16
+    assert "attn=simple" in s.choices() and "attn=mfma" not in s.choices(), s.choices()
+    assert_close(s.embed(ids, mask), want, s.compute_dtype)
     s.close()
     model.close()
 

@@ -187,6 +187,69 @@ def test_modernbert_long_rows_meet_the_oracle(context, sharp):
     model.close()
 
 
+def test_xlmr_large_full_depth_ranges_meet_the_oracle(context):
+    # C3 at all 24 layers in the BF16 tier on one 4096-token row cut into its
+    # 64 ranges (the reference holds one row's ranges to its CPU path,
+    # core/tests/cuda_ranges.rs:223-262): every range within BF16's floor of
+    # the oracle, and the whole-row range the row's mean bit for bit.
+    sh = W.SHAPES["xlmr-large"]
+    print("xlmr-large: building the 24-layer model", flush=True)
+    desc = with_dtype(W.model(dataclasses.replace(sh, store="f32")), "bf16")
+    ids, mask, types = W.rows(sh, batch=1, lengths=None, seed=21)
+    ranges = W.ranges(sh, mask)
+    whole = _whole_rows(mask)
+    assert len(ranges) == sh.ranges_per_row and mask.sum() == sh.seq and desc.layers == 24
+    model = context.load(desc)
+    s = model.session(1, sh.seq, sh.precision, max_ranges=len(ranges))
+    assert s.compute_dtype == S.TURBO_DTYPE_BF16
+    s.write_ranges(ids, mask, ranges, types, normalize=NONE)
+    s.run()
+    got = s.read()
+    print("xlmr-large: the oracle's pass", flush=True)
+    want = oracle.encode(desc, ids, mask, types, ranges=ranges + whole, normalize=NONE)
+    print(f"  min range cosine {small.cosine_rows(got, want[:len(ranges)]).min():.6f}", flush=True)
+    assert_close(got, want[:len(ranges)], s.compute_dtype)
+    row = s.embed(ids, mask, types, pooling=MEAN, normalize=NONE)
+    assert_close(row, want[len(ranges):], s.compute_dtype)
+    s.write_ranges(ids, mask, whole, types, normalize=NONE)
+    s.run()
+    assert np.array_equal(s.read(), row)
+    s.close()
+    model.close()
+
+
+def test_modernbert_full_depth_meets_the_oracle(context):
+    # C4 at all 22 layers (8 global, 14 local within 64 keys) in the F16 tier
+    # on one 8192-token row (RoPE to position 8191): the row's mean and its
+    # 256-token ranges within F16's floor of the oracle, and the whole-row
+    # range the row's mean bit for bit.
+    sh = W.SHAPES["modernbert"]
+    print("modernbert: building the 22-layer model", flush=True)
+    desc = W.model(sh)
+    ids, mask, _ = W.rows(sh, batch=1, lengths=None, seed=23)
+    whole = _whole_rows(mask)
+    chunks = [(0, a, a + 256) for a in range(0, sh.seq, 256)]
+    assert mask.sum() == 8192 and desc.layers == 22 and desc.global_every == 3
+    model = context.load(desc)
+    s = model.session(1, sh.seq, sh.precision, max_ranges=len(chunks))
+    assert s.compute_dtype == S.TURBO_DTYPE_F16
+    row = s.embed(ids, mask, None, pooling=MEAN, normalize=NONE)
+    print("modernbert: the oracle's pass", flush=True)
+    want = oracle.encode(desc, ids, mask, None, ranges=whole + chunks, normalize=NONE)
+    print(f"  row cosine {small.cosine_rows(row, want[:1]).min():.7f}", flush=True)
+    assert_close(row, want[:1], s.compute_dtype)
+    s.write_ranges(ids, mask, chunks, None, normalize=NONE)
+    s.run()
+    got = s.read()
+    print(f"  {len(chunks)} ranges, min cosine {small.cosine_rows(got, want[1:]).min():.7f}", flush=True)
+    assert_close(got, want[1:], s.compute_dtype)
+    s.write_ranges(ids, mask, whole, None, normalize=NONE)
+    s.run()
+    assert np.array_equal(s.read(), row)
+    s.close()
+    model.close()
+
+
 # The rank agreement C5 is held to. The reference has no int8 encoder and
 # no rank bound of its own. On this random-init cross-encoder the pairs'
 # CLS states differ by little (their scores spread over a few hundredths),

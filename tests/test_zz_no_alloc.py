@@ -79,3 +79,33 @@ def test_static_codes_past_the_area_are_refused(context):
     # The table's own call takes it (it allocates).
     buf.quantize(INT8, 1, dim, ranges)
     buf.close()
+
+
+def test_static_calls_through_two_contexts_on_two_threads_keep_their_codes(runtime):
+    # Both contexts' calls stage in the GPU's one area; the lock per GPU
+    # holds each call's codes until it has copied them out, so every call
+    # gets its own codes whichever thread's call runs beside it.
+    import threading
+    ctxs = [runtime.context(0), runtime.context(0)]
+    cases = [_inputs(80, 300, 512), _inputs(81, 450, 384)]
+    want = [_codes(ctxs[i], x, INT8, r, static=False)[0] for i, (x, r) in enumerate(cases)]
+    bad = []
+
+    def calls(i):
+        try:
+            for _ in range(40):
+                got, run = _codes(ctxs[i], cases[i][0], INT8, cases[i][1], static=True)
+                if not np.array_equal(got, want[i]) or run.device_allocs != 0:
+                    bad.append(i)
+                    return
+        except Exception as e:   # noqa: BLE001 (reported below)
+            bad.append(repr(e))
+
+    threads = [threading.Thread(target=calls, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for c in ctxs:
+        c.close()
+    assert not bad, bad

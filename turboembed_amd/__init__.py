@@ -53,6 +53,7 @@ def library():
         "turbo_rocm_session_hidden": [P, P, C.c_uint64, E],
         "turbo_rocm_session_timing": [P, u32, E],
         "turbo_rocm_session_times": [P, C.c_char_p, u32, E],
+        "turbo_rocm_session_intervals": [P, C.c_char_p, u32, E],
         "turbo_rocm_session_choices": [P, C.c_char_p, u32, E],
         "turbo_rocm_session_replay": [P, u32, E],
         "turbo_rocm_session_graphs": [P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), E],
@@ -493,6 +494,18 @@ class Session:
         err = S.new_error()
         _ok(self.lib.turbo_rocm_session_times(self.h, buf, 8192, C.byref(err)), err)
         return {name: int(n) for name, _, n in (line.split() for line in buf.value.decode().splitlines())}
+
+    def intervals(self):
+        """The last timed run's launches: (kernel, start ms, end ms) from the
+        run's start, in launch order."""
+        buf = C.create_string_buffer(1 << 16)
+        err = S.new_error()
+        _ok(self.lib.turbo_rocm_session_intervals(self.h, buf, 1 << 16, C.byref(err)), err)
+        out = []
+        for line in buf.value.decode().splitlines():
+            name, a, b = line.split()
+            out.append((name, float(a), float(b)))
+        return out
 
     def replay(self, runs):
         """Run the written rows `runs` more times on the device, then wait."""

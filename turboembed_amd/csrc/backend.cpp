@@ -548,9 +548,16 @@ const turbo_backend turbo_rocm_backend = {
 // Every call on one GPU shares the area, so calls that overlap on one GPU
 // (through two contexts) race; calls through one context are serialized by
 // its lock. Nothing in the area needs clearing: every code byte is written.
+// One lock per device for its fixed staging area: every context on a GPU
+// shares the area, so a call holds its device's lock from the ranges' copy
+// in to the codes' copy out (the seam's threading rule: a backend takes its
+// own locks, reference include/turbo/turbo_backend.h:19-20).
+static std::mutex scratch_locks[MAX_DEVICES];
+
 int32_t turbo_rocm_buffer_quantize_static(void *buf, uint32_t quantization, const float *int8_ranges, uint32_t rows,
                                           uint32_t dim, turbo_backend_run *run, turbo_error *err) {
     return guarded(err, [&] {
+        const uint64_t dev0 = device_allocs.load();
         Buffer *b = static_cast<Buffer *>(buf);
         const uint64_t code_bytes = quantize_codes_bytes(b, quantization, int8_ranges, rows, dim);
         if (code_bytes == 0) return TURBO_OK;
@@ -563,6 +570,9 @@ int32_t turbo_rocm_buffer_quantize_static(void *buf, uint32_t quantization, cons
                                                "int8 ranges); " + std::to_string(rows) + " by " + std::to_string(dim) +
                                                " values need " + std::to_string(need));
         std::lock_guard<std::recursive_mutex> g(b->ctx->lock);
+        if (b->ctx->ordinal < 0 || b->ctx->ordinal >= MAX_DEVICES)
+            fail(TURBO_E_RUNTIME, "rocm: device " + std::to_string(b->ctx->ordinal) + " has no staging area");
+        std::lock_guard<std::mutex> area_lock(scratch_locks[b->ctx->ordinal]);
         OnDevice on(b->ctx->ordinal);
         void *area = b->ctx->scratch;
         if (!area) fail(TURBO_E_RUNTIME, "rocm: the device's staging area was not found at context creation");
@@ -577,7 +587,10 @@ int32_t turbo_rocm_buffer_quantize_static(void *buf, uint32_t quantization, cons
               "buffer_quantize_static");
         check(hipMemcpyAsync(b->dev, codes, code_bytes, hipMemcpyDeviceToDevice, st), "buffer_quantize_static");
         check(hipStreamSynchronize(st), "buffer_quantize_static");
-        if (run && i8) run->h2d_bytes += (uint64_t)2 * dim * 4;
+        if (run) {
+            if (i8) run->h2d_bytes += (uint64_t)2 * dim * 4;
+            run->device_allocs += device_allocs.load() - dev0;
+        }
         return TURBO_OK;
     });
 }

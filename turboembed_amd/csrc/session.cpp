@@ -534,6 +534,10 @@ bool mfma_attention(Dt act, uint32_t head_width) { return act != Dt::F32 && head
 static void split_defaults(Session &s);
 static bool ln_fusable(const Session &s, int g);
 
+// The ints between the rows' ids, mask and types planes: max_batch x
+// max_seq, rounded up to a multiple of 4.
+static size_t plane_ints(const Session &s) { return ((size_t)s.max_batch * s.max_seq + 3) / 4 * 4; }
+
 Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_backend_tuning *tuning) {
     if (desc->task != TURBO_TASK_EMBED && desc->task != TURBO_TASK_RERANK)
         fail(TURBO_E_UNSUPPORTED_TASK, "rocm: task " + std::to_string(desc->task));
@@ -607,7 +611,11 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
         s->split_parts = (uint32_t)std::min<long>(std::max<long>(std::strtol(g, nullptr, 10), 1), Session::MAX_PARTS);
     Choices &kc = s->kc;
     kc.bins = bins_for((uint64_t)desc->max_batch * desc->max_seq);
-    const bool mfma_attn = mfma_attention(s->act, m->hidden / m->heads);
+    // DeBERTa-v2's matrix-core form needs its relative projections in the
+    // operand type: a model whose projections pass F16's range (or whose
+    // buckets the form's tiles cannot hold) runs the scalar form, and its
+    // choices say so.
+    const bool mfma_attn = mfma_attention(s->act, m->hidden / m->heads) && !(m->deberta && !s->rel_pos_t);
     for (int b = 0; b < kc.bins; ++b) kc.bin[b].attn = mfma_attn ? ATTN_MFMA : ATTN_SIMPLE;
     split_defaults(*s);
     bool cached = false;
@@ -678,12 +686,15 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     // Rows, the run's dimensions and the ranges in one allocation, in the
     // staging buffer's order: the ids, mask and types planes, then (on a
     // 64-byte boundary) the dimensions, the ranges right after them.
-    const size_t dims_at = (3 * B * S + 15) / 16 * 16;
+    // (Each plane starts on 16 bytes: the packing kernel reads a row's mask
+    // 16 bytes a lane when the run's seq is a multiple of 4.)
+    const size_t plane = plane_ints(*s);
+    const size_t dims_at = (3 * plane + 15) / 16 * 16;
     s->staging_ints = dims_at + sizeof(RunDims) / 4 + 3 * (size_t)s->max_ranges;
     int32_t *rows = static_cast<int32_t *>(alloc(s->staging_ints * 4, "session rows"));
     s->ids = rows;
-    s->mask = rows + B * S;
-    s->types = rows + 2 * B * S;
+    s->mask = rows + plane;
+    s->types = rows + 2 * plane;
     s->dims_dev = reinterpret_cast<RunDims *>(rows + dims_at);
     s->ranges = reinterpret_cast<uint32_t *>(s->dims_dev + 1);
     check(hipMemset(s->dims_dev, 0, sizeof(RunDims)), "session rows");
@@ -783,6 +794,7 @@ void session_release(Session *s) {
         for (hipGraphExec_t g : s->graph)
             if (g) (void)hipGraphExecDestroy(g);
         for (hipEvent_t e : s->ev) (void)hipEventDestroy(e);
+        if (s->ev0) (void)hipEventDestroy(s->ev0);
         s->owned.clear();
     }
     delete s;
@@ -874,7 +886,7 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     OnDevice on(s->ctx->ordinal);
     // The staging buffer may still feed the last write's copy.
     check(hipStreamSynchronize(s->ctx->stream), "embed_write");
-    const size_t plane = (size_t)s->max_batch * s->max_seq;
+    const size_t plane = plane_ints(*s);
     int32_t *ids = s->staging, *mask = ids + plane, *types = mask + plane;
     uint32_t *rg = reinterpret_cast<uint32_t *>(s->dims_host + 1);
     uint32_t tokens = 0, max_len = 0;
@@ -993,18 +1005,24 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
     s->written = true;
 }
 
-// Records an event pair around each launch when the session times its runs.
+// Records, when the session times its runs, an event on the first stream as
+// the run starts and an event pair around each launch on the launch's own
+// stream, so a launch's interval is measured as the run executes it (a split
+// run's parts side by side).
 struct Timer {
     Session &s;
-    explicit Timer(Session &ss) : s(ss) { s.ev_used = 0; }
-    void begin(const char *name) {
+    explicit Timer(Session &ss) : s(ss) {
+        s.ev_used = 0;
+        if (s.timing && s.ev0) (void)hipEventRecord(s.ev0, s.ctx->stream);
+    }
+    void begin(const char *name, hipStream_t st) {
         if (!s.timing || s.ev_used + 2 > s.ev.size()) return;
         s.ev_name[s.ev_used / 2] = name;
-        (void)hipEventRecord(s.ev[s.ev_used], s.ctx->stream);
+        (void)hipEventRecord(s.ev[s.ev_used], st);
     }
-    void end() {
+    void end(hipStream_t st) {
         if (!s.timing || s.ev_used + 2 > s.ev.size()) return;
-        (void)hipEventRecord(s.ev[s.ev_used + 1], s.ctx->stream);
+        (void)hipEventRecord(s.ev[s.ev_used + 1], st);
         s.ev_used += 2;
     }
 };
@@ -1135,7 +1153,16 @@ static bool ln_fusable(const Session &s, int g) {
 // The layers over part `part` of the run's rows, on stream st: every
 // product, norm and attention launch reads that part's rows and tokens from
 // the run's dimensions. Layer reads pool their ranges as they pass.
-static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, Timer &tm) {
+// The layers a run takes: every one, or through the one read alone (a
+// model cut after it); the tuner's runs the first few alone.
+static uint32_t layers_of_run(const Session &s) {
+    const Model &m = *s.model;
+    uint32_t nl = s.tap_alone ? m.layers + 1 - s.taps : m.layers;
+    if (s.layers_limit) nl = std::min(nl, s.layers_limit);
+    return nl;
+}
+
+static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, Timer &tm, uint32_t l0, uint32_t l1) {
     Model &m = *s.model;
     const int H = (int)m.hidden, I = (int)m.inter, heads = (int)m.heads, dh = H / heads;
     const Dt dt = s.act;   // activations; the GEMMs take s.dt
@@ -1144,11 +1171,11 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
     const Span sp = span_of(s.dims_dev, part), whole = span_of(s.dims_dev, -1);
     const int T = (int)bd.part_tokens;   // the grids' rows
     auto run = [&](const char *name, hipError_t e) { check(e, name); };
-#define LAUNCH(NAME, CALL) \
-    do {                   \
-        tm.begin(NAME);    \
-        run(NAME, CALL);   \
-        tm.end();          \
+#define LAUNCH(NAME, CALL)  \
+    do {                    \
+        tm.begin(NAME, st); \
+        run(NAME, CALL);    \
+        tm.end(st);         \
     } while (0)
     // One GEMM of the layer. On the I8 tier its operand rows are quantized
     // first (per token; each part's rows at its own tokens of the operand
@@ -1164,7 +1191,9 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
         qo.scale = s.ascale;
         qo.tok_stride = qrow;
     }
-    bool aq_ready = false;
+    // (The int8 rows of a layer's first operand are the previous layer's
+    // last norm's.)
+    bool aq_ready = i8 && l0 > 0;
     auto mm = [&](uint32_t l, GemmSlot g) {
         LayerGemm lg = layer_gemm(s, l, g);
         const void *A = lg.A;
@@ -1212,11 +1241,10 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
     // final_norm(x), the scale the final states are on
     // (core/src/cpu/encoder/rotary/mod.rs:84-86, 161-168), normed into y,
     // which is free between a layer's last add and the next layer's out product.
-    uint32_t nl = s.tap_alone ? m.layers + 1 - s.taps : m.layers;
-    if (s.layers_limit) nl = std::min(nl, s.layers_limit);   // the tuner's runs
+    const uint32_t nl = layers_of_run(s);
     const uint32_t reads = s.tap_alone ? 1 : s.taps;
     const int od = (int)s.output_dim;
-    for (uint32_t l = 0; l < nl; ++l) {
+    for (uint32_t l = l0; l < std::min(l1, nl); ++l) {
         const Model::Layer &L = m.ls[l];
         int window = INT32_MAX;
         if (m.rotary) {
@@ -1284,9 +1312,8 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
 
 // A run's launches on the context's streams: the whole run's embedding,
 // each part's layers (forked onto the side streams and joined back), the
-// pooling. With `sequential`, every part on the first stream in turn (a
-// timed run: its events are on the first stream).
-static void encode(Session &s, const Bounds &bd, bool sequential) {
+// pooling.
+static void encode(Session &s, const Bounds &bd) {
     Model &m = *s.model;
     Context &c = *s.ctx;
     hipStream_t st = c.stream;
@@ -1296,11 +1323,11 @@ static void encode(Session &s, const Bounds &bd, bool sequential) {
     const Span whole = span_of(s.dims_dev, -1);
     Timer tm(s);
     auto run = [&](const char *name, hipError_t e) { check(e, name); };
-#define LAUNCH(NAME, CALL) \
-    do {                   \
-        tm.begin(NAME);    \
-        run(NAME, CALL);   \
-        tm.end();          \
+#define LAUNCH(NAME, CALL)  \
+    do {                    \
+        tm.begin(NAME, st); \
+        run(NAME, CALL);    \
+        tm.end(st);         \
     } while (0)
     LAUNCH("pack_rows", pack_rows(st, s.mask, s.dims_dev, (int)s.max_batch, (int)s.max_seq, s.pk));
     // (A 16-bit residual starts in xh alone.)
@@ -1314,16 +1341,20 @@ static void encode(Session &s, const Bounds &bd, bool sequential) {
     // A split run: the rows' parts run their layers on the context's
     // streams, forked here and joined before the pooling, so one part's
     // memory-bound and latency-bound launches overlap another's products.
-    if (bd.parts > 1 && !sequential) {
+    // (Launched directly, the parts' layers go out in turn, a layer of each
+    // part at a time, so every stream has work from the start.)
+    const uint32_t nl = layers_of_run(s);
+    if (bd.parts > 1) {
         check(hipEventRecord(c.fork, st), "forking the run");
         for (uint32_t i = 1; i < bd.parts; ++i) check(hipStreamWaitEvent(c.side[i - 1], c.fork, 0), "forking the run");
-        for (uint32_t i = 0; i < bd.parts; ++i) run_layers(s, i == 0 ? st : c.side[i - 1], (int)i, bd, tm);
+        for (uint32_t l = 0; l < nl; ++l)
+            for (uint32_t i = 0; i < bd.parts; ++i) run_layers(s, i == 0 ? st : c.side[i - 1], (int)i, bd, tm, l, l + 1);
         for (uint32_t i = 1; i < bd.parts; ++i) {
             check(hipEventRecord(c.join[i - 1], c.side[i - 1]), "joining the run");
             check(hipStreamWaitEvent(st, c.join[i - 1], 0), "joining the run");
         }
     } else {
-        for (uint32_t i = 0; i < bd.parts; ++i) run_layers(s, st, (int)i, bd, tm);
+        run_layers(s, st, 0, bd, tm, 0, nl);
     }
     const uint32_t reads = s.tap_alone ? 1 : s.taps;
     LAUNCH("pool", pool(st, s.dims_dev, (int)bd.items, s.x, H, s.pk, s.mask, s.ranges, s.pool_scratch,
@@ -1358,7 +1389,7 @@ static void capture_bin(Session &s, int b) {
     check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capturing a bin's graph");
     hipGraph_t g = nullptr;
     try {
-        encode(s, bounds_of(s, b, s.bin_parts[b]), false);
+        encode(s, bounds_of(s, b, s.bin_parts[b]));
     } catch (...) {
         (void)hipStreamEndCapture(st, &g);
         if (g) (void)hipGraphDestroy(g);
@@ -1395,7 +1426,7 @@ void launch_run(Session &s) {
             return;
         }
     }
-    encode(s, bounds_of(s, b, s.parts), s.timing);
+    encode(s, bounds_of(s, b, s.parts));
 }
 
 // Rows for the tuner's runs of bin b: the bin's token count (its upper edge,
@@ -1436,7 +1467,7 @@ static float time_layers(Session &s, int b, uint32_t layers, float target_ms, hi
     check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "the tuner's graph");
     hipGraph_t g = nullptr;
     try {
-        encode(s, bounds_of(s, b, parts_of_bin(s, b)), false);
+        encode(s, bounds_of(s, b, parts_of_bin(s, b)));
     } catch (...) {
         (void)hipStreamEndCapture(st, &g);
         if (g) (void)hipGraphDestroy(g);
@@ -1657,6 +1688,7 @@ int32_t turbo_rocm_session_timing(void *session, uint32_t on_, turbo_error *err)
             s->ev.resize(2 * (16 + 16 * s->model->layers * Session::MAX_PARTS));
             for (auto &e : s->ev) check(hipEventCreate(&e), "hipEventCreate");
             s->ev_name.assign(s->ev.size() / 2, nullptr);
+            check(hipEventCreate(&s->ev0), "hipEventCreate");
         }
         s->timing = on_ != 0;
         return TURBO_OK;
@@ -1683,6 +1715,26 @@ int32_t turbo_rocm_session_times(void *session, char *out, uint32_t len, turbo_e
         for (auto &n : order) {
             char line[128];
             std::snprintf(line, sizeof line, "%s %.6f %u\n", n.c_str(), by[n].first, by[n].second);
+            t += line;
+        }
+        if (len) std::snprintf(out, len, "%s", t.c_str());
+        return TURBO_OK;
+    });
+}
+
+int32_t turbo_rocm_session_intervals(void *session, char *out, uint32_t len, turbo_error *err) {
+    return guarded(err, [&] {
+        Session *s = static_cast<Session *>(session);
+        // The last timed run's launches in the order they were made: name,
+        // then start and end in ms from the run's start.
+        std::string t;
+        OnDevice on(s->ctx->ordinal);
+        for (size_t i = 0; s->timing && s->ev0 && i + 1 < s->ev_used; i += 2) {
+            float a = 0, b = 0;
+            check(hipEventElapsedTime(&a, s->ev0, s->ev[i]), "the run's events");
+            check(hipEventElapsedTime(&b, s->ev0, s->ev[i + 1]), "the run's events");
+            char line[128];
+            std::snprintf(line, sizeof line, "%s %.6f %.6f\n", s->ev_name[i / 2], a, b);
             t += line;
         }
         if (len) std::snprintf(out, len, "%s", t.c_str());

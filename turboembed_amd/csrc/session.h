@@ -214,8 +214,9 @@ struct Session {
     uint32_t bin_parts[BINS] = {};   // parts a bin's graph runs (its runs use as many or fewer)
     uint64_t captures = 0, graph_launches = 0;   // counted for the graphs hook
     // Per-launch timing (a test and benchmark hook): events around each
-    // kernel of a run, by name.
+    // kernel of a run on its own stream, by name, and the run's start.
     bool timing = false;
+    hipEvent_t ev0 = nullptr;   // the timed run's start
     std::vector<hipEvent_t> ev;
     std::vector<const char *> ev_name;
     size_t ev_used = 0;
