@@ -257,6 +257,107 @@ def summarize_stats(stats_dir, workload, command, summary_tag=""):
     print(out)
 
 
+PMC_PASSES = (
+    # Matrix cores, vector unit, waves (one counter set a pass: 8 SQ and 1 GRBM counter).
+    "GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_INSTS_VALU "
+    "SQ_WAVE_CYCLES SQ_WAVES SQ_VALU_MFMA_COEXEC_CYCLES",
+    # LDS and waits.
+    "GRBM_GUI_ACTIVE SQ_LDS_IDX_ACTIVE SQ_LDS_BANK_CONFLICT SQ_INSTS_LDS SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS "
+    "SQ_LDS_ADDR_CONFLICT SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY",
+)
+
+
+def summarize_counters(dirs, workload, command):
+    """profiles/counters_<workload>.md and .json from rocprofv3 --pmc runs of
+    this script, one a counter set of PMC_PASSES (each dispatch counted on its
+    own): per kernel instantiation, the matrix cores' busy share of the
+    SIMD-cycles of its dispatches, the vector unit's active share, and the
+    LDS's. The share's normalization (how the profiler sums GRBM_GUI_ACTIVE
+    and the SQ counters over the chip's 8 XCDs) is read off the MFMA probe's
+    dispatches, whose every wave keeps eight independent product chains in
+    flight on every SIMD: their busy share is taken as full, and the factor
+    that makes it so is applied to every kernel and printed. The algorithmic
+    check beside it: SQ_INSTS_MFMA x the cycles one 32x32x16 product holds a
+    SIMD's matrix core (32 on gfx950: 32768 FLOP at 1024 a cycle), over the
+    same SIMD-cycles."""
+    import csv
+    import glob
+    import re
+
+    SIMDS = 256 * 4
+    per = {}      # kernel -> counter -> summed value
+    calls = {}    # kernel -> dispatches (of the first pass)
+    for n, d in enumerate(dirs):
+        seen = set()
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                k = r["Kernel_Name"]
+                per.setdefault(k, {})
+                c = r["Counter_Name"]
+                per[k][c] = per[k].get(c, 0.0) + float(r["Counter_Value"])
+                if n == 0 and c == "GRBM_GUI_ACTIVE" and (k, r["Dispatch_Id"]) not in seen:
+                    seen.add((k, r["Dispatch_Id"]))
+                    calls[k] = calls.get(k, 0) + 1
+    # GRBM_GUI_ACTIVE appears in every pass: its per-pass sums add up, so
+    # each kernel's cycles are their mean over the passes.
+    for k, v in per.items():
+        if "GRBM_GUI_ACTIVE" in v:
+            v["GRBM_GUI_ACTIVE"] /= len(dirs)
+
+    def short(k):
+        m = re.match(r"_ZN4rocm\d+(\w+?)I", k)
+        base = m.group(1) if m else k.split("(")[0]
+        shape = re.findall(r"Li(\d+)E", k)
+        return base + ("<" + ",".join(shape) + ">" if shape else "")
+
+    def simd_cycles(v):
+        return v.get("GRBM_GUI_ACTIVE", 0.0) * SIMDS
+
+    probe = [k for k in per if "mfma_probe" in k]
+    raw_probe = sum(per[k].get("SQ_VALU_MFMA_BUSY_CYCLES", 0) for k in probe) / max(
+        1.0, sum(simd_cycles(per[k]) for k in probe))
+    factor = 1.0 / raw_probe if raw_probe > 0 else 1.0
+    rows = sorted(per.items(), key=lambda kv: -kv[1].get("GRBM_GUI_ACTIVE", 0.0))
+    total = sum(v.get("GRBM_GUI_ACTIVE", 0.0) for _, v in rows)
+    lines = [f"# Hardware counters per kernel: {workload}", "",
+             "Commands (from the repository root, one MI355X; each pass counts every dispatch on its own):", "",
+             "```", *command, "```", "",
+             f"Matrix-core busy share = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x {SIMDS} SIMDs) x {factor:.4g}: "
+             f"the factor makes the MFMA probe's dispatches (8 independent 32x32x16 chains a wave on every SIMD) read "
+             f"as fully busy (raw {raw_probe:.4g}). \"by count\" = SQ_INSTS_MFMA x 32 cycles over the same SIMD-cycles "
+             f"x the factor. VALU active = SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES (a wave's cycles issuing vector "
+             f"instructions); LDS active = SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE x 256 CUs) x the factor; bank "
+             f"conflicts = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE; waiting = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES.", "",
+             "| kernel | dispatches | share of GPU cycles | matrix cores busy | by count | VALU active | LDS active "
+             "| LDS bank conflicts | waiting on a dependency |", "|---|---|---|---|---|---|---|---|---|"]
+    out = {"workload": workload, "command": command, "factor": factor, "probe_raw": raw_probe, "kernels": {}}
+    for k, v in rows:
+        sc = simd_cycles(v)
+        if sc <= 0:
+            continue
+        g = v.get("GRBM_GUI_ACTIVE", 0.0)
+        mf = v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / sc * factor
+        cnt = v.get("SQ_INSTS_MFMA", 0.0) * 32 / sc * factor
+        wc = v.get("SQ_WAVE_CYCLES", 0.0)
+        valu = v.get("SQ_ACTIVE_INST_VALU", 0.0) / wc if wc else 0.0
+        lds = v.get("SQ_LDS_IDX_ACTIVE", 0.0) / (g * 256) * factor if g else 0.0
+        conf = v.get("SQ_LDS_BANK_CONFLICT", 0.0) / v["SQ_LDS_IDX_ACTIVE"] if v.get("SQ_LDS_IDX_ACTIVE") else 0.0
+        wait = v.get("SQ_WAIT_INST_ANY", 0.0) / wc if wc else 0.0
+        out["kernels"][k] = {"short": short(k), "dispatches": calls.get(k, 0), "gpu_cycles": g, "mfma_busy": mf,
+                             "mfma_busy_by_count": cnt, "valu_active": valu, "lds_active": lds,
+                             "lds_bank_conflicts": conf, "waiting": wait, "counters": v}
+        if g / total < 0.005:
+            continue
+        lines.append(f"| `{short(k)}` | {calls.get(k, 0)} | {100 * g / total:.1f}% | {100 * mf:.1f}% | {100 * cnt:.1f}% "
+                     f"| {100 * valu:.1f}% | {100 * lds:.1f}% | {100 * conf:.1f}% | {100 * wait:.1f}% |")
+    base = os.path.join(ROOT, "profiles", f"counters_{workload}")
+    with open(base + ".md", "w") as f:
+        f.write("\n".join(lines) + "\n")
+    with open(base + ".json", "w") as f:
+        json.dump(out, f, indent=1)
+    print("\n".join(lines))
+
+
 def library_compare(workload, reps=20):
     """profiles/library_<workload>.md: the platform libraries on one layer's
     products and attention of a full-length batch, through torch (its F16 or
@@ -344,6 +445,8 @@ def main():
     ap.add_argument("--summary-tag", default="", choices=["", "unsplit"],
                     help="with --summarize-stats: 'unsplit' for a run under TURBO_ROCM_SPLIT=1 of full-length rows "
                          "(per-kernel rates added; written to kernels_<workload>_unsplit.md)")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="PASS_DIR",
+                    help="write profiles/counters_<workload>.md from rocprofv3 --pmc runs of PMC_PASSES and exit")
     ap.add_argument("--library-compare", action="store_true",
                     help="time torch's linear and fused attention on the workload's full-length layer shapes, write "
                          "profiles/library_<workload>.md and exit")
@@ -355,6 +458,9 @@ def main():
 
     if args.summarize_pmc:
         summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.workload, args.pmc_command)
+        return
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters, args.workload, args.pmc_command)
         return
     if args.summarize_stats:
         summarize_stats(args.summarize_stats, args.workload, args.pmc_command, args.summary_tag)

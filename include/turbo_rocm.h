@@ -131,6 +131,12 @@ int32_t turbo_rocm_session_packing(void *session, int32_t *start, int32_t *len, 
 /* The last run's final hidden states, [tokens, hidden] F32. */
 int32_t turbo_rocm_session_hidden(void *session, float *out, uint64_t floats, turbo_error *err);
 
+/* The backend's heap allocations so far: every malloc-family and operator
+ * new call its own code has made (counted as they happen), in the process
+ * and on the calling thread. A run's turbo_backend_run.host_allocs is the
+ * change of the thread's count across it. Either pointer may be NULL. */
+int32_t turbo_rocm_host_allocs(uint64_t *process, uint64_t *thread, turbo_error *err);
+
 /* Times every kernel of the session's later runs with HIP events, each
  * launch's pair on the stream it runs on (a split run's parts side by side,
  * as the run executes them; its runs launch their kernels directly rather

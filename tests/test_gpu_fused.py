@@ -20,8 +20,12 @@ import small
 
 pytestmark = pytest.mark.gpu
 
-FUSED = "all:out=128x768ln,ffn2=128x768ln"
+SHAPES = ["128x768ln"]
 UNFUSED = "all:out=256x384,ffn2=256x384"
+
+
+def fused(shape):
+    return f"all:out={shape},ffn2={shape}"
 
 
 def _session(model, monkeypatch, choices, *a, split=None, **kw):
@@ -46,9 +50,10 @@ def _rows(seed, batch, seq, vocab, lo):
     return ids, mask, types
 
 
+@pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("split", ["0", "2"])
 @pytest.mark.parametrize("lo", [1, 200])
-def test_fused_norms_are_the_separate_norms_bits(context, monkeypatch, split, lo):
+def test_fused_norms_are_the_separate_norms_bits(context, monkeypatch, shape, split, lo):
     # BERT-base width (hidden 768, FFN 3072) at 2 layers; ragged rows whose
     # packed tokens are no multiple of the 128-row tile, one row of a
     # single token when lo is 1.
@@ -59,9 +64,9 @@ def test_fused_norms_are_the_separate_norms_bits(context, monkeypatch, split, lo
         mask[4] = 0
         mask[4, 0] = 1
     model = context.load(desc)
-    f = _session(model, monkeypatch, FUSED, 12, 512, sh.precision, max_ranges=64, split=split)
+    f = _session(model, monkeypatch, fused(shape), 12, 512, sh.precision, max_ranges=64, split=split)
     u = _session(model, monkeypatch, UNFUSED, 12, 512, sh.precision, max_ranges=64, split=split)
-    assert "out=128x768ln" in f.choices() and "ffn2=128x768ln" in f.choices()
+    assert f"out={shape}," in f.choices() and f"ffn2={shape}," in f.choices()
     assert f.compute_dtype == S.TURBO_DTYPE_F16
     got = f.embed(ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
     want = u.embed(ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
@@ -90,13 +95,14 @@ def test_fused_norms_are_the_separate_norms_bits(context, monkeypatch, split, lo
     model.close()
 
 
-def test_fused_bert_base_meets_the_oracle_at_full_depth(context, monkeypatch):
+@pytest.mark.parametrize("shape", SHAPES)
+def test_fused_bert_base_meets_the_oracle_at_full_depth(context, monkeypatch, shape):
     # All 12 layers of BERT-base F16 on two rows of 512 and 300 tokens.
     sh = W.SHAPES["bert-base"]
     desc = W.model(sh)
     ids, mask, types = W.rows(sh, batch=2, lengths=(300, 512), seed=3)
     model = context.load(desc)
-    f = _session(model, monkeypatch, FUSED, 64, 512, sh.precision)
+    f = _session(model, monkeypatch, fused(shape), 64, 512, sh.precision)
     got = f.embed(ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
     want = oracle.encode(desc, ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
     cos = small.cosine_rows(got, want)
@@ -107,7 +113,8 @@ def test_fused_bert_base_meets_the_oracle_at_full_depth(context, monkeypatch):
 
 @pytest.mark.parametrize("choice, precision", [("qkv=128x768ln", S.TURBO_PRECISION_FASTEST),
                                                ("ffn1=128x768ln", S.TURBO_PRECISION_FASTEST),
-                                               ("out=128x768ln", S.TURBO_PRECISION_EXACT)])
+                                               ("out=128x768ln", S.TURBO_PRECISION_EXACT),
+                                               ("ffn2=128x768ln", S.TURBO_PRECISION_EXACT)])
 def test_the_fused_shape_is_refused_where_it_cannot_run(context, monkeypatch, choice, precision):
     sh = W.SHAPES["bert-base"]
     model = context.load(W.model(sh, layers=1))

@@ -1121,6 +1121,35 @@ def test_a_bad_choices_string_is_refused(context, monkeypatch):
     model.close()
 
 
+# ---- Allocations ----------------------------------------------------------------------------
+#
+# The backend's heap allocations are counted as they happen (the library is
+# linked with malloc and operator new wrapped, so every such call its code
+# makes is seen): opening a session moves the count; writing rows, running
+# and reading allocate nothing, on this thread or any other, and each run
+# reports it (turbo_backend.h:519-530; the reference's counting allocator,
+# core/tests/allocations.rs).
+def test_an_open_allocates_and_writes_runs_and_reads_do_not(context):
+    desc = small.bert(seed=51)
+    a = small.ragged_rows(51, 5, 48, desc.vocab_size)
+    b = small.ragged_rows(52, 7, 30, desc.vocab_size)
+    model = context.load(desc)
+    p0, t0 = T.host_allocs()
+    s = model.session(8, 64, S.TURBO_PRECISION_FASTEST)
+    p1, t1 = T.host_allocs()
+    assert t1 > t0 and p1 - p0 >= t1 - t0, (p0, t0, p1, t1)
+    s.embed(*a)
+    p2, t2 = T.host_allocs()
+    for rows in (a, b, a):
+        s.write_tokens(*rows)
+        s.run()
+        assert s.run_info.host_allocs == 0 and s.run_info.device_allocs == 0
+        s.read()
+    assert T.host_allocs() == (p2, t2)
+    s.close()
+    model.close()
+
+
 # ---- Runs replayed from HIP graphs --------------------------------------------------------
 #
 # Each token bin's launches are captured once, at session_open, and

@@ -54,6 +54,7 @@ def library():
         "turbo_rocm_session_timing": [P, u32, E],
         "turbo_rocm_session_times": [P, C.c_char_p, u32, E],
         "turbo_rocm_session_intervals": [P, C.c_char_p, u32, E],
+        "turbo_rocm_host_allocs": [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), E],
         "turbo_rocm_session_choices": [P, C.c_char_p, u32, E],
         "turbo_rocm_session_replay": [P, u32, E],
         "turbo_rocm_session_graphs": [P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), E],
@@ -577,6 +578,15 @@ def copy_probe(nbytes, iters=5, ordinal=0):
     err = S.new_error()
     _ok(library().turbo_rocm_copy_probe(ordinal, nbytes, iters, C.byref(ms), C.byref(err)), err)
     return ms.value
+
+
+def host_allocs():
+    """(process, calling thread): the backend's heap allocations so far, every
+    malloc-family and operator new call its own code has made."""
+    p, t = C.c_uint64(), C.c_uint64()
+    err = S.new_error()
+    _ok(library().turbo_rocm_host_allocs(C.byref(p), C.byref(t), C.byref(err)), err)
+    return p.value, t.value
 
 
 def fail_variant(name=None):

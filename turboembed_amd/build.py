@@ -17,7 +17,12 @@ LIB = os.path.join(HERE, "libturbo_rocm.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["rowwise.hip", "gemm.hip", "attention.hip", "session.cpp", "backend.cpp", "checks.cpp", "rerank.cpp",
-           "autotune.cpp"]
+           "autotune.cpp", "allocs.cpp"]
+
+# The backend's own heap allocations are counted (allocs.cpp): its objects'
+# calls of these go to the __wrap_ functions there first.
+WRAPPED = ["malloc", "calloc", "realloc", "aligned_alloc", "posix_memalign", "_Znwm", "_Znam",
+           "_ZnwmRKSt9nothrow_t", "_ZnamRKSt9nothrow_t", "_ZnwmSt11align_val_t", "_ZnamSt11align_val_t"]
 
 # Per-source device flags. Attention: matrix-core results in ordinary VGPRs,
 # so the softmax's vector ops on its accumulators need no copies through the
@@ -63,7 +68,7 @@ def build(verbose=False):
                 print(err)
     objs = [o for o, _ in results]
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp] + objs
+    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp] + objs + [f"-Wl,--wrap={w}" for w in WRAPPED]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

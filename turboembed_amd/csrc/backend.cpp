@@ -51,15 +51,14 @@ void fill(turbo_error *err, int32_t code, uint32_t field, const std::string &m) 
 }
 
 std::atomic<uint64_t> device_allocs{0};
-std::atomic<uint64_t> host_allocs{0};
-static thread_local uint64_t host_allocs_here = 0;
+static thread_local uint64_t device_allocs_here = 0;
 
-void counted_host_alloc() {
-    host_allocs.fetch_add(1, std::memory_order_relaxed);
-    ++host_allocs_here;
+void counted_device_alloc() {
+    device_allocs.fetch_add(1, std::memory_order_relaxed);
+    ++device_allocs_here;
 }
 
-uint64_t host_allocs_on_thread() { return host_allocs_here; }
+uint64_t device_allocs_on_thread() { return device_allocs_here; }
 
 void *dev_alloc(size_t bytes, const char *what) {
     void *p = nullptr;
@@ -71,7 +70,7 @@ void *dev_alloc(size_t bytes, const char *what) {
              std::string("rocm: ") + what + ": " + std::to_string(bytes) + " bytes of device memory");
     }
     check(e, what);
-    ++device_allocs;
+    counted_device_alloc();
     return p;
 }
 
@@ -201,7 +200,6 @@ int32_t context_create(uint32_t ordinal, turbo_log_fn log, void *ud, void **out,
     return guarded(err, [&] {
         if (ordinal >= devices().size()) fail(TURBO_E_DEVICE_NOT_FOUND, "rocm: no device " + std::to_string(ordinal));
         auto c = std::make_unique<Context>();
-        counted_host_alloc();
         c->ordinal = devices()[ordinal];
         c->log = log;
         c->log_user_data = ud;
@@ -274,11 +272,11 @@ int32_t buffer_alloc(void *ctx, const turbo_buffer_desc *desc, void **out, void 
         b->placement = desc->placement;
         b->bytes = desc_bytes(desc);
         b->owned = true;
-        counted_host_alloc();
         switch (desc->placement) {
         case TURBO_PLACE_DEVICE: b->dev = dev_alloc(b->bytes, "buffer_alloc"); break;
         case TURBO_PLACE_PINNED:
             check(hipHostMalloc(&b->host, b->bytes, hipHostMallocDefault), "hipHostMalloc");
+            counted_device_alloc();   // page-locked memory is the driver's
             b->dev = b->host;
             break;
         case TURBO_PLACE_SHARED:
@@ -286,10 +284,10 @@ int32_t buffer_alloc(void *ctx, const turbo_buffer_desc *desc, void **out, void 
             // device reads and writes it over the bus). Managed memory is
             // not host-addressable on a device without XNACK.
             check(hipHostMalloc(&b->host, b->bytes ? b->bytes : 1, hipHostMallocDefault), "hipHostMalloc");
+            counted_device_alloc();   // page-locked memory is the driver's
             b->dev = b->host;
             break;
         case TURBO_PLACE_HOST:
-            counted_host_alloc();
             b->host = std::malloc(b->bytes ? b->bytes : 1);
             if (!b->host) fail(TURBO_E_OUT_OF_MEMORY, "rocm: host buffer");
             break;
@@ -310,7 +308,6 @@ int32_t buffer_import(void *ctx, const turbo_buffer_desc *desc, const turbo_nati
         b->placement = desc->placement;
         b->bytes = desc_bytes(desc);
         b->owned = false;
-        counted_host_alloc();
         char *p = reinterpret_cast<char *>(handle->handle) + handle->offset;
         if (handle->kind == TURBO_HANDLE_CUDA_PTR && desc->placement == TURBO_PLACE_DEVICE) {
             b->dev = p;
@@ -419,7 +416,7 @@ int32_t buffer_quantize(void *buf, uint32_t quantization, const float *int8_rang
         const bool i8 = quantization == TURBO_QUANTIZE_INT8;
         std::lock_guard<std::recursive_mutex> g(b->ctx->lock);
         OnDevice on(b->ctx->ordinal);
-        const uint64_t dev0 = device_allocs.load();
+        const uint64_t dev0 = device_allocs_on_thread();
         DevPtr codes(dev_alloc(code_bytes, "quantized codes"));
         DevPtr ranges;
         hipStream_t st = b->ctx->stream;
@@ -434,7 +431,7 @@ int32_t buffer_quantize(void *buf, uint32_t quantization, const float *int8_rang
         check(hipMemcpyAsync(b->dev, codes.get(), code_bytes, hipMemcpyDeviceToDevice, st), "buffer_quantize");
         check(hipStreamSynchronize(st), "buffer_quantize");
         if (run) {
-            run->device_allocs += device_allocs.load() - dev0;
+            run->device_allocs += device_allocs_on_thread() - dev0;
             if (i8) run->h2d_bytes += (uint64_t)2 * dim * 4;
         }
         return TURBO_OK;
@@ -557,7 +554,7 @@ static std::mutex scratch_locks[MAX_DEVICES];
 int32_t turbo_rocm_buffer_quantize_static(void *buf, uint32_t quantization, const float *int8_ranges, uint32_t rows,
                                           uint32_t dim, turbo_backend_run *run, turbo_error *err) {
     return guarded(err, [&] {
-        const uint64_t dev0 = device_allocs.load();
+        const uint64_t dev0 = device_allocs_on_thread();
         Buffer *b = static_cast<Buffer *>(buf);
         const uint64_t code_bytes = quantize_codes_bytes(b, quantization, int8_ranges, rows, dim);
         if (code_bytes == 0) return TURBO_OK;
@@ -589,7 +586,7 @@ int32_t turbo_rocm_buffer_quantize_static(void *buf, uint32_t quantization, cons
         check(hipStreamSynchronize(st), "buffer_quantize_static");
         if (run) {
             if (i8) run->h2d_bytes += (uint64_t)2 * dim * 4;
-            run->device_allocs += device_allocs.load() - dev0;
+            run->device_allocs += device_allocs_on_thread() - dev0;
         }
         return TURBO_OK;
     });

@@ -1133,13 +1133,13 @@ static hipError_t launch_lds(hipStream_t s, const GemmRows &gr, int M, int N, in
 template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_ln_kernel(Span sp, int a_tok, int K, const T *__restrict__ A, int lda, const T *__restrict__ W, LnArgs e) {
-    using P = LdsTile<T, BM, BN, WM, WN, STAGES, BK>;
-    constexpr int WAVES = P::WAVES, TM = P::TM, TN = P::TN, G = BN / 256;
+    constexpr int WAVES = WM * WN, TM = BM / WM / 32, TN = BN / WN / 32, G = BN / 256;
+    constexpr int STAGE_BYTES = (BM + BN) * BK * (int)sizeof(T);
     constexpr int PR = 32 * WM;         // rows a pass
     constexpr int YS = BN + 8;          // staged row stride: 16 bytes of padding
     constexpr int RH = PR / WAVES / 2;  // rows a half-wave norms a pass
     static_assert(BN % 256 == 0 && RH >= 1 && RH * 2 * WAVES == PR, "whole rows a half-wave");
-    static_assert(PR * YS * (int)sizeof(T) + 2 * BN * 4 <= STAGES * P::TILE, "staging fits the stages");
+    static_assert(PR * YS * (int)sizeof(T) + 2 * BN * 4 <= STAGES * STAGE_BYTES, "staging fits the stages");
     typedef typename Mma<T>::acc acc_t;
     extern __shared__ __attribute__((aligned(1024))) char smem[];
 
@@ -1241,12 +1241,14 @@ gemm_ln_kernel(Span sp, int a_tok, int K, const T *__restrict__ A, int lda, cons
 
 // The whole-row block shape: 128 x 768, 8 waves as 1 x 8 (each 128 x 96),
 // 32 columns of k a stage in two stages (114 KB). (As 2 x 4 waves of 64 x
-// 192, both fragment sets double-buffered, it needs more than 256 registers.)
-template <typename T, int WM, int WN>
+// 192, both fragment sets double-buffered, it needs more than 256
+// registers; 16 columns of k in five stages, loads four steps ahead, made
+// the FFN-out product slower: 278 against 207 us at 32768 rows.)
+template <typename T, int WM, int WN, int STAGES, int BK>
 static hipError_t launch_ln(hipStream_t s, const GemmRows &gr, int M, int K, const void *A, int lda, const void *W,
                             const LnArgs &e) {
-    constexpr int BM = 128, BN = 768, STAGES = 2, BK = 32;
-    constexpr int bytes = LdsTile<T, BM, BN, WM, WN, STAGES, BK>::TILE * STAGES;
+    constexpr int BM = 128, BN = 768;
+    constexpr int bytes = (BM + BN) * BK * (int)sizeof(T) * STAGES;
     hipLaunchKernelGGL((gemm_ln_kernel<T, BM, BN, WM, WN, STAGES, BK>), dim3((M + BM - 1) / BM), dim3(64 * WM * WN),
                        bytes, s, gr.sp, gr.a_tok, K, (const T *)A, lda, (const T *)W, e);
     return hipGetLastError();
@@ -1267,7 +1269,7 @@ hipError_t gemm_ln(hipStream_t s, Dt dt, const Span &sp, int max_m, int hidden, 
     if (!gemm_ln_tile(tile)) return hipErrorInvalidValue;
     if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
     const GemmRows gr{sp, a_tok ? a_tok : lda};
-    return launch_ln<_Float16, 1, 8>(s, gr, max_m, K, A, lda, W, e);
+    return launch_ln<_Float16, 1, 8, 2, 32>(s, gr, max_m, K, A, lda, W, e);
 }
 
 // The highest block-shape number.
@@ -1446,7 +1448,9 @@ static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K,
 }
 
 // The int8 tier: the pipelined kernel alone, on 128-byte rows (K a multiple
-// of 128) or 64-byte rows (K a multiple of 64).
+// of 128) or 64-byte rows (K a multiple of 64). (256 x 384 tiles of 128 x 96
+// waves spill their dequantizing epilogue's per-column scales and biases:
+// the rerank workload took 18.05 ms a step on them against 17.43 on 256 x 256.)
 static hipError_t gemm_i8(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda, const void *W,
                           const EpiArgs &e,
                           int tile) {

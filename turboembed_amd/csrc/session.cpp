@@ -149,7 +149,6 @@ Model *model_load(Context *c, const turbo_backend_model *d) {
         fail(TURBO_E_UNSUPPORTED, "rocm: compute_dtype " + std::to_string(fixed));
 
     auto m = std::make_unique<Model>();
-    counted_host_alloc();
     m->ctx = c;
     m->int8 = fixed == TURBO_DTYPE_I8;
     m->family = d->family;
@@ -573,7 +572,6 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     // capture.
     std::lock_guard<std::recursive_mutex> on_ctx(m->ctx->lock);
     auto s = std::make_unique<Session>();
-    counted_host_alloc();
     s->model = m;
     s->ctx = m->ctx;
     s->task = desc->task;
@@ -699,7 +697,6 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     s->ranges = reinterpret_cast<uint32_t *>(s->dims_dev + 1);
     check(hipMemset(s->dims_dev, 0, sizeof(RunDims)), "session rows");
     s->row_lens.assign(B, 0);
-    counted_host_alloc();
     int32_t *pk = static_cast<int32_t *>(alloc((2 * B + 3 * s->tcap + 64) * 4, "session packing"));
     s->pk.start = pk;
     s->pk.len = pk + B;
@@ -743,6 +740,7 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     s->output.bytes = outs * H * 4;
     s->output.owned = false;
     check(hipHostMalloc((void **)&s->staging, s->staging_ints * 4, hipHostMallocDefault), "session staging");
+    counted_device_alloc();   // page-locked memory is the driver's
     s->dims_host = reinterpret_cast<RunDims *>(s->staging + dims_at);
 
     const auto t0 = std::chrono::steady_clock::now();
@@ -1140,7 +1138,7 @@ static Bounds bounds_of(const Session &s, int b, uint32_t parts) {
 static bool residual_in_operand(const Session &s) { return s.act == Dt::F16 && !s.model->modern; }
 
 // Whether product g (out or FFN-out) can take its residual add and
-// LayerNorm in its epilogue (the whole-row shape, LN_TILE): post-norm F16
+// LayerNorm in its epilogue (the whole-row shapes): post-norm F16
 // sessions carrying the residual in the 16-bit rows, at a hidden size the
 // kernel is built for.
 static bool ln_fusable(const Session &s, int g) {
@@ -1214,7 +1212,7 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
     // whole-row shape: whether it ran so. (F16 post-norm sessions alone,
     // whose residual is carried in xh; no int8 rows follow.)
     auto mm_ln = [&](uint32_t l, GemmSlot g, const float *w, const float *b, bool keep_f32) {
-        if (bc.tile[g] != LN_TILE || !ln_fusable(s, g)) return false;
+        if (!gemm_ln_tile(bc.tile[g]) || !ln_fusable(s, g)) return false;
         const LayerGemm lg = layer_gemm(s, l, g);
         LnArgs ln;
         ln.bias = lg.e.bias;
@@ -1226,7 +1224,7 @@ static void run_layers(Session &s, hipStream_t st, int part, const Bounds &bd, T
         ln.res_h = 1;
         ln.keep_f32 = keep_f32 ? 1 : 0;
         LAUNCH(g == G_OUT ? "gemm_out_ln" : "gemm_ffn_out_ln",
-               gemm_ln(st, s.dt, sp, T, H, lg.K, lg.A, lg.K, 0, lg.W, ln, LN_TILE));
+               gemm_ln(st, s.dt, sp, T, H, lg.K, lg.A, lg.K, 0, lg.W, ln, bc.tile[g]));
         return true;
     };
     // The GEMM operand copy of x after an add + LayerNorm: xh, or on the F32
@@ -1605,7 +1603,7 @@ bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
 void session_run(Session *s, turbo_backend_run *out) {
     if (!s->written) fail(TURBO_E_INVALID_STATE, "rocm: the session has no rows written since its last run");
     s->written = false;
-    const uint64_t dev0 = device_allocs.load(), host0 = host_allocs_on_thread();
+    const uint64_t dev0 = device_allocs_on_thread(), host0 = host_allocs_on_thread();
     {
         std::lock_guard<std::recursive_mutex> g(s->ctx->lock);
         OnDevice on(s->ctx->ordinal);
@@ -1625,7 +1623,7 @@ void session_run(Session *s, turbo_backend_run *out) {
     out->h2d_bytes = s->h2d;
     out->d2h_bytes = 0;
     out->host_allocs = host_allocs_on_thread() - host0;
-    out->device_allocs = device_allocs.load() - dev0;
+    out->device_allocs = device_allocs_on_thread() - dev0;
     uint32_t *st = out->stage;
     st[TURBO_EMBED_STAGE_UPLOAD] = TURBO_STAGE_DEVICE;
     st[TURBO_EMBED_STAGE_LOOKUP] = TURBO_STAGE_DEVICE;
@@ -1642,6 +1640,14 @@ void session_run(Session *s, turbo_backend_run *out) {
 using namespace rocm;
 
 extern "C" {
+
+int32_t turbo_rocm_host_allocs(uint64_t *process, uint64_t *thread, turbo_error *err) {
+    return guarded(err, [&] {
+        if (process) *process = host_allocs.load();
+        if (thread) *thread = host_allocs_on_thread();
+        return TURBO_OK;
+    });
+}
 
 int32_t turbo_rocm_fail_variant(const char *name, turbo_error *err) {
     return guarded(err, [&] {
@@ -1684,7 +1690,6 @@ int32_t turbo_rocm_session_timing(void *session, uint32_t on_, turbo_error *err)
         Session *s = static_cast<Session *>(session);
         OnDevice on(s->ctx->ordinal);
         if (on_ && s->ev.empty()) {
-            counted_host_alloc();
             s->ev.resize(2 * (16 + 16 * s->model->layers * Session::MAX_PARTS));
             for (auto &e : s->ev) check(hipEventCreate(&e), "hipEventCreate");
             s->ev_name.assign(s->ev.size() / 2, nullptr);

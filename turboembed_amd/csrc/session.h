@@ -33,12 +33,17 @@ void fill(turbo_error *err, int32_t code, uint32_t field, const std::string &m);
 void *dev_alloc(size_t bytes, const char *what);
 const std::vector<int> &devices();
 
+// Device allocations (device memory, and page-locked host memory, which is
+// the driver's) made by the backend, in the process and on the calling
+// thread: a call reports the change of the thread's count across it.
 extern std::atomic<uint64_t> device_allocs;
-// The backend's own heap allocations (its handles and host buffers), on
-// every thread and on the calling thread: a run reports the change of the
-// calling thread's count across it (reference core/cuda/backend.cpp:150-175).
+void counted_device_alloc();
+uint64_t device_allocs_on_thread();
+// The backend's own heap allocations, every one its code makes (allocs.cpp:
+// the library is linked with malloc and operator new wrapped), on every
+// thread and on the calling thread: a run reports the change of the calling
+// thread's count across it (reference core/cuda/backend.cpp:146-175).
 extern std::atomic<uint64_t> host_allocs;
-void counted_host_alloc();
 uint64_t host_allocs_on_thread();
 
 // Every entry point: a status, the caller's turbo_error filled, nothing
