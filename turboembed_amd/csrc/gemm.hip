@@ -179,9 +179,13 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs &e, int M, int N, in
     }
 }
 
+// ks > 0: split K, the grid's y-th slice of ks columns of k (W's rows stay
+// K long), its F32 sums (Plain epilogue, no bias) into slice y of the
+// output, split_stride floats apart; splitk_reduce adds the slices.
 template <typename T, int BM, int BN, int BK, Epi KIND>
 __global__ void __launch_bounds__(256) gemm_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int lda,
-                                                   const T *__restrict__ W, EpiArgs e, int grid_n) {
+                                                   const T *__restrict__ W, EpiArgs e, int grid_n, int ks = 0,
+                                                   size_t split_stride = 0) {
     constexpr int VEC = 16 / sizeof(T);          // elements in 16 bytes
     constexpr int STRIDE = BK + VEC;             // LDS row, padded by 16 bytes
     constexpr int TM = BM / 64, TN = BN / 64;    // MFMA tiles per wave (2 x 2 waves)
@@ -202,12 +206,18 @@ __global__ void __launch_bounds__(256) gemm_kernel(Span sp, int a_tok, int N, in
     const int live = (M + BM - 1) / BM * grid_n;
     if ((int)blockIdx.x >= live) return;
     A += (size_t)lv.tok0 * a_tok;
+    // (A span whose rows pass a slice's would write into the next: such a
+    // launch leaves, and the session never makes one.)
+    if (ks && (size_t)(lv.tok0 + M) * N > split_stride) return;
+    if (ks) e.out = (float *)e.out + blockIdx.y * split_stride;
     place_epilogue<KIND, T>(e, lv);
     const int per = live / 8;
     int b = blockIdx.x;
     if (b < per * 8) b = (b % 8) * per + b / 8;
     const int tile_n = b % grid_n, tile_m = b / grid_n;
     const int m0 = tile_m * BM, n0 = tile_n * BN;
+    // This block's columns of k: all of them, or its split's.
+    const int kb = ks ? (int)blockIdx.y * ks : 0, ke = ks ? min(K, kb + ks) : K;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -218,13 +228,13 @@ __global__ void __launch_bounds__(256) gemm_kernel(Span sp, int a_tok, int N, in
         for (int i = 0; i < LA; ++i) {
             const int v = tid + 256 * i, r = v / VROW, c = (v % VROW) * VEC;
             const int gm = min(m0 + r, M - 1), gk = k0 + c;
-            ra[i] = gk + VEC <= K ? *(const vec4 *)(A + (size_t)gm * lda + gk) : vec4{0, 0, 0, 0};
+            ra[i] = gk + VEC <= ke ? *(const vec4 *)(A + (size_t)gm * lda + gk) : vec4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int i = 0; i < LB; ++i) {
             const int v = tid + 256 * i, r = v / VROW, c = (v % VROW) * VEC;
             const int gn = min(n0 + r, N - 1), gk = k0 + c;
-            rb[i] = gk + VEC <= K ? *(const vec4 *)(W + (size_t)gn * K + gk) : vec4{0, 0, 0, 0};
+            rb[i] = gk + VEC <= ke ? *(const vec4 *)(W + (size_t)gn * K + gk) : vec4{0, 0, 0, 0};
         }
     };
     auto store = [&](int buf) {
@@ -246,15 +256,15 @@ __global__ void __launch_bounds__(256) gemm_kernel(Span sp, int a_tok, int N, in
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = floatx16{};
 
-    const int nk = (K + BK - 1) / BK;
-    load(0);
+    const int nk = (ke - kb + BK - 1) / BK;
+    load(kb);
     store(0);
     __syncthreads();
     const int row_a = wm * (BM / 2) + (lane & 31), row_b = BM + wn * (BN / 2) + (lane & 31);
     const int col = (lane >> 5) * HALF;
     for (int kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) load((kt + 1) * BK);
+        if (kt + 1 < nk) load(kb + (kt + 1) * BK);
         const T *base = lds[buf];
 #pragma unroll
         for (int s = 0; s < HALF / EPM; ++s) {
@@ -305,6 +315,62 @@ static hipError_t launch(hipStream_t s, const GemmRows &gr, int M, int N, int K,
     return hipErrorInvalidValue;
 }
 
+
+// ---- Split K for products too small to fill the chip --------------------------------
+//
+// A Bias product (out or FFN-out: N the hidden size) of few row tiles runs
+// its K in `splits` slices, each slice's tiles a block of the grid's y-th
+// row, their F32 sums into a workspace slice; then one pass adds the slices
+// in slice order (no float atomics: the same bits every run), adds the bias
+// and stores the product as the Bias epilogue does (F32, the operand type,
+// or BF16). The reference's tuner offers split-K as its SkMode knob
+// (core/cuda/kernels.h:166-175, core/cuda/kernels.cu:4449-4469).
+template <typename T>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(Span sp, const float *__restrict__ ws, int splits,
+                                                            size_t stride, int N, EpiArgs e) {
+    const Live lv = live_of(sp);
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;   // 4 consecutive outputs a thread
+    const int n = (int)(i * 4 % N), m = (int)(i * 4 / N);
+    if (m >= lv.tokens || (size_t)(lv.tok0 + lv.tokens) * N > stride) return;
+    const size_t at = (size_t)(lv.tok0 + m) * N + n;
+    typedef float float4_v __attribute__((ext_vector_type(4)));
+    float4_v v = *(const float4_v *)(ws + at);
+    for (int s = 1; s < splits; ++s) v += *(const float4_v *)(ws + s * stride + at);
+    float o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = v[q] + (e.bias ? e.bias[n + q] : 0.0f);
+    const size_t out = (size_t)(lv.tok0 + m) * e.ldo + n;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (e.out_f32) ((float *)e.out)[out + q] = o[q];
+        else if (sizeof(T) == 2 && e.out_bf16) ((__bf16 *)e.out)[out + q] = from_f32<__bf16>(o[q]);
+        else ((T *)e.out)[out + q] = from_f32<T>(o[q]);
+    }
+}
+
+template <typename T, int BM, int BN, int BK>
+static hipError_t launch_split(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda,
+                               const void *W, const EpiArgs &e, int splits) {
+    // Slices of whole BK steps; the workspace holds every slice's rows.
+    const int ks = ((K + splits - 1) / splits + BK - 1) / BK * BK;
+    splits = (K + ks - 1) / ks;
+    const size_t stride = (size_t)M * N;
+    if (e.kind != Epi::Bias || !e.ws || N % 4 != 0 || (size_t)splits * stride > e.ws_floats || e.ldo < N)
+        return hipErrorInvalidValue;
+    EpiArgs p;
+    p.kind = Epi::Plain;
+    p.out = e.ws;
+    p.ldo = N;
+    const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM;
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, BK, Epi::Plain>), dim3(gn * gm, splits), dim3(256), 0, s, gr.sp,
+                       gr.a_tok, N, K, (const T *)A, lda, (const T *)W, p, gn, ks, stride);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const size_t quads = stride / 4;
+    hipLaunchKernelGGL((splitk_reduce_kernel<T>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, gr.sp, e.ws,
+                       splits, stride, N, e);
+    return hipGetLastError();
+}
 
 // ---- The pipelined kernel (16-bit operands, K a multiple of 64) -------------------
 //
@@ -1260,6 +1326,8 @@ bool gemm_ln_takes(Dt dt, int hidden, int K, int lda, bool res_h) {
 
 bool gemm_ln_tile(int tile) { return tile == LN_TILE; }
 
+bool gemm_splitk_tile(int tile) { return tile == SPLITK_TILE_4 || tile == SPLITK_TILE_2; }
+
 hipError_t gemm_ln(hipStream_t s, Dt dt, const Span &sp, int max_m, int hidden, int K, const void *A, int lda,
                    int a_tok, const void *W, const LnArgs &e, int tile) {
     if (max_m <= 0) return hipSuccess;
@@ -1273,7 +1341,7 @@ hipError_t gemm_ln(hipStream_t s, Dt dt, const Span &sp, int max_m, int hidden, 
 }
 
 // The highest block-shape number.
-constexpr int TILES = 17;
+constexpr int TILES = 19;
 
 int gemm_tiles() { return TILES; }
 
@@ -1302,7 +1370,7 @@ bool gemm_made_to_fail(int tile) {
 static const char *const TILE_NAME[TILES + 1] = {
     "auto",      "r128x128",   "r256x128",     "r64x128",    "256x128", "128x128", "128x256",
     "256x256",   "128x128s2",  "256x128k32",   "128x256k32", "256x128k32s3", "256x256k32", "256x192",
-    "r64x64",    "256x384",    "256x384k32s4", "128x768ln"};
+    "r64x64",    "256x384",    "256x384k32s4", "128x768ln", "r128x128sk4", "r64x64sk2"};
 
 const char *gemm_tile_name(int tile) { return tile >= 0 && tile <= TILES ? TILE_NAME[tile] : "?"; }
 
@@ -1410,12 +1478,15 @@ static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K,
     }
     if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
     // A pipelined shape asked of an operand it cannot take runs the staged kernel.
-    if (((tile >= 4 && tile <= 13) || tile >= 15) && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
+    if (((tile >= 4 && tile <= 13) || tile == 15 || tile == 16) && !pipelined) tile = (N % 128 == 0 && M >= 8192) ? 2 : 1;
     // Q, K and V must each start on a wave's column boundary: a shape whose
     // waves are wider than 64 columns runs 64-column waves (K = hidden is a
     // multiple of 64 on the pipelined kernel) when they do not.
     if ((e.kind == Epi::Qkv || e.kind == Epi::QkvRope) && e.hidden % wave_cols(tile) != 0) tile = 7;
     switch (tile) {
+    // Split K: the staged kernel's tiles over K in 4 (128 x 128) or 2 (64 x 64) slices.
+    case SPLITK_TILE_4: return launch_split<T, 128, 128, BK>(s, gr, M, N, K, A, lda, W, e, 4);
+    case SPLITK_TILE_2: return launch_split<T, 64, 64, BK>(s, gr, M, N, K, A, lda, W, e, 2);
     case 1: return launch<T, 128, 128, BK>(s, gr, M, N, K, A, lda, W, e);
     case 2: return launch<T, 256, 128, BK>(s, gr, M, N, K, A, lda, W, e);
     case 3: return launch<T, 64, 128, BK>(s, gr, M, N, K, A, lda, W, e);
@@ -1470,8 +1541,10 @@ static hipError_t gemm_i8(hipStream_t s, const GemmRows &gr, int M, int N, int K
 hipError_t gemm(hipStream_t s, Dt dt, const Span &sp, int M, int N, int K, const void *A, int lda, int a_tok,
                 const void *W, const EpiArgs &e, int tile) {
     if (M <= 0) return hipSuccess;
-    // The whole-row shapes take a LayerNorm with them: gemm_ln.
+    // The whole-row shapes take a LayerNorm with them: gemm_ln. Split K is
+    // for Bias products with a workspace, off the int8 tier.
     if (gemm_ln_tile(tile)) return hipErrorInvalidValue;
+    if (gemm_splitk_tile(tile) && (e.kind != Epi::Bias || !e.ws || dt == Dt::I8)) return hipErrorInvalidValue;
     const GemmRows gr{sp, a_tok ? a_tok : lda};
     if (dt == Dt::I8) return gemm_i8(s, gr, M, N, K, A, lda, W, e, tile);
     if (K % (16 / (int)dt_bytes(dt)) != 0 || lda % (16 / (int)dt_bytes(dt)) != 0) return hipErrorInvalidValue;

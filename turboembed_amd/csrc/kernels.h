@@ -148,6 +148,9 @@ struct EpiArgs {
     int out_bf16 = 0;              // Bias on F16 operands: BF16 outputs (F32's range at half its bytes)
     // I8 operands: output (m, n) is the int32 sum times a_scale[m] * w_scale[n].
     const float *a_scale = nullptr, *w_scale = nullptr;
+    // Split K (Bias products): the F32 slices' workspace and its capacity.
+    float *ws = nullptr;
+    size_t ws_floats = 0;
 };
 
 // C[m, n] = sum_k A[m, k] W[n, k] over the span's tokens m (rows of A, ld
@@ -190,6 +193,11 @@ struct LnArgs {
 };
 // The whole-row block shape (128 x 768, 8 waves of 128 x 96).
 constexpr int LN_TILE = 17;
+// Split K on the staged kernel (Bias products with EpiArgs.ws): 128 x 128
+// tiles over 4 slices of K, 64 x 64 over 2. The workspace takes slices x
+// M x N floats.
+constexpr int SPLITK_TILE_4 = 18, SPLITK_TILE_2 = 19, SPLITK_MAX = 4;
+bool gemm_splitk_tile(int tile);
 bool gemm_ln_tile(int tile);
 // Whether the fused kernel takes a product of this operand type, hidden size,
 // inner size and operand stride on a session whose residual is in the

@@ -961,20 +961,19 @@ __global__ void __launch_bounds__(256) quantize_span_kernel(Span sp, const S *__
     const S *row = src + (size_t)t * ld;
     float v[QMAXK][8];
     float mx = 0.0f;
+    // (Eight values a lane a step: one 16-byte load of F16, two of F32;
+    // every step's loads go out before the first maximum.)
 #pragma unroll
     for (int k = 0; k < QMAXK; ++k) {
         const int c = 8 * (lane + 64 * k);
-        if (c < cols) {
-            float a[4], b[4];
-            load4(row + c, a);
-            load4(row + c + 4, b);
+        if (c < cols) load8(row + c, v[k]);
+    }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                v[k][q] = a[q];
-                v[k][4 + q] = b[q];
-                mx = fmaxf(mx, fmaxf(fabsf(a[q]), fabsf(b[q])));
-            }
-        }
+    for (int k = 0; k < QMAXK; ++k) {
+        const int c = 8 * (lane + 64 * k);
+        if (c < cols)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(v[k][q]));
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));

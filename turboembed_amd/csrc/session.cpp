@@ -533,6 +533,16 @@ bool mfma_attention(Dt act, uint32_t head_width) { return act != Dt::F32 && head
 static void split_defaults(Session &s);
 static bool ln_fusable(const Session &s, int g);
 
+// Split K takes the out and FFN-out products (N the hidden size) of the
+// bins whose runs do not split into parts and hold at most SPLITK_ROWS
+// packed tokens, off the int8 tier: launches of a few row tiles.
+constexpr uint32_t SPLITK_ROWS = 4096;
+static uint32_t parts_of_bin(const Session &s, int b);
+static bool splitk_fits(const Session &s, int b, int g) {
+    return (g == G_OUT || g == G_FFN2) && s.dt != Dt::I8 && parts_of_bin(s, b) == 1 &&
+           bin_tokens(b, (uint64_t)s.max_batch * s.max_seq) <= SPLITK_ROWS;
+}
+
 // The ints between the rows' ids, mask and types planes: max_batch x
 // max_seq, rounded up to a multiple of 4.
 static size_t plane_ints(const Session &s) { return ((size_t)s.max_batch * s.max_seq + 3) / 4 * 4; }
@@ -629,7 +639,8 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
                         launchable = false;
                         why = std::string(BIN_NAME[b]) + ":" + GEMM_NAME[g] + "=" + gemm_tile_name(c.bin[b].tile[g]) +
                               " cannot launch on this device";
-                    } else if (gemm_ln_tile(c.bin[b].tile[g]) && !ln_fusable(*s, g)) {
+                    } else if ((gemm_ln_tile(c.bin[b].tile[g]) && !ln_fusable(*s, g)) ||
+                               (gemm_splitk_tile(c.bin[b].tile[g]) && !splitk_fits(*s, b, g))) {
                         launchable = false;
                         why = std::string(BIN_NAME[b]) + ":" + GEMM_NAME[g] + "=" + gemm_tile_name(c.bin[b].tile[g]) +
                               " does not take this product";
@@ -667,6 +678,13 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
                                                      gemm_tile_name(kc.bin[b].tile[g]) +
                                                      ": the LayerNorm-fused shape takes the out and FFN-out products "
                                                      "of F16 post-norm sessions of hidden 768 alone");
+    for (int b = 0; b < kc.bins; ++b)
+        for (int g = 0; g < G_COUNT; ++g)
+            if (gemm_splitk_tile(kc.bin[b].tile[g]) && !splitk_fits(*s, b, g))
+                fail(TURBO_E_UNSUPPORTED_OPTION, std::string("rocm: ") + BIN_NAME[b] + ":" + GEMM_NAME[g] + "=" +
+                                                     gemm_tile_name(kc.bin[b].tile[g]) +
+                                                     ": split K takes the out and FFN-out products of bins of at "
+                                                     "most 4096 tokens whose runs do not split, off the int8 tier");
     // The scalar path is the only one some sessions have.
     for (int b = 0; b < kc.bins; ++b)
         if (!mfma_attn) kc.bin[b].attn = ATTN_SIMPLE;
@@ -725,6 +743,12 @@ Session *session_open(Model *m, const turbo_backend_session_desc *desc, turbo_ba
     // bytes an element.
     s->ydt = s->act == Dt::F32 ? Dt::F32 : m->rotary ? Dt::BF16 : s->act;
     s->y = alloc(s->tcap * H * (m->rotary ? 4 : dt_bytes(s->ydt)), "session products");
+    // Split K's slices: SPLITK_MAX of the small bins' largest out or FFN-out
+    // product (rows x hidden F32).
+    if (dt != Dt::I8) {
+        s->splitk_floats = (size_t)SPLITK_MAX * std::min<size_t>(s->tcap, SPLITK_ROWS) * H;
+        s->splitk_ws = static_cast<float *>(alloc(s->splitk_floats * 4, "session split-K slices"));
+    }
     if (dt == Dt::I8) {
         s->aq = static_cast<int8_t *>(alloc(s->tcap * std::max(H, I), "session int8 operand"));
         s->ascale = static_cast<float *>(alloc(s->tcap * 4, "session int8 scales"));
@@ -1087,6 +1111,8 @@ static LayerGemm layer_gemm(Session &s, uint32_t l, GemmSlot g) {
         r.e.ldo = H;
         r.e.out_f32 = s.ydt == Dt::F32 ? 1 : 0;
         r.e.out_bf16 = s.ydt == Dt::BF16 && s.act == Dt::F16 ? 1 : 0;
+        r.e.ws = s.splitk_ws;
+        r.e.ws_floats = s.splitk_floats;
         break;
     default:
         r.N = (int)L.n_in;
@@ -1548,7 +1574,7 @@ bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
             if (bc.tile_forced[g]) continue;
             const LayerGemm lg = layer_gemm(s, 0, (GemmSlot)g);
             int cand[20];
-            int n = gemm_candidates(s.dt, lg.K, lg.K, lg.e, cand, 18);
+            int n = gemm_candidates(s.dt, lg.K, lg.K, lg.e, cand, 16);   // (room for 3 more below)
             // Split bins: the large shapes alone (each part's product fills
             // about half the chip beside the other part's).
             if (P > 1) {
@@ -1558,6 +1584,10 @@ bool tune(Session &s, uint32_t budget_ms, std::string *timings) {
                 n = k;
             }
             if (ln_fusable(s, g)) cand[n++] = LN_TILE;
+            if (splitk_fits(s, b, g)) {
+                cand[n++] = SPLITK_TILE_4;
+                cand[n++] = SPLITK_TILE_2;
+            }
             const int incumbent = bc.tile[g];
             float best = timed(GEMM_NAME[g], gemm_tile_name(incumbent));
             int pick = incumbent;

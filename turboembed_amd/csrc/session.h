@@ -173,6 +173,8 @@ struct Session {
     int8_t *aq = nullptr;    // I8: a GEMM's quantized operand [tcap, max(H, I)]
     float *ascale = nullptr; // I8: its per-token scales [tcap]
     float *out = nullptr;    // [max(max_batch, max_ranges), H] F32
+    float *splitk_ws = nullptr;   // split K's F32 slices (not on the int8 tier)
+    size_t splitk_floats = 0;
     PoolScratch pool_scratch;   // the means' chunk sums
     Buffer output;
     int32_t *staging = nullptr;   // pinned: ids, mask, types planes then ranges
