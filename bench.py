@@ -193,30 +193,86 @@ def unsplit_rooflines(rows, workload):
     # The products by epilogue: 1 Q/K/V, 2 GELU, 6 bias (the out and FFN-out
     # products, one launch each a layer).
     groups = [("Q/K/V product", r"EpiE1E", 2.0 * T * H * 3 * H), ("FFN-in product (GELU)", r"EpiE2E", 2.0 * T * H * I),
-              ("out + FFN-out products (mean)", r"EpiE6E", (2.0 * T * H * H + 2.0 * T * I * H) / 2),
               ("attention", r"attention_mfma_kernel", att)]
     peak = PEAK["bf16" if shape.store == "bf16" else "f16"]
     out = ["", "Each launch over the whole batch (full-length rows, one launch a layer per kernel): the main "
            "instantiation of each kernel, its average launch against its algorithmic FLOPs.", "",
            "| kernel | instantiation | calls | average µs | GFLOP a launch | TFLOP/s | of peak |", "|---|---|---|---|---|---|---|"]
+
+    def line(tag, name, calls, us, flops):
+        rate = flops / (us * 1e-6)
+        out.append(f"| {tag} | {name} | {calls} | {us:.1f} | {flops / 1e9:.1f} | {rate / 1e12:.0f} | "
+                   f"{100 * rate / peak:.1f}% |")
+
     for tag, pat, flops in groups:
         sel = [r for r in rows if re.search(pat, r["Name"])]
-        if not sel:
-            continue
-        r = max(sel, key=lambda r: float(r["TotalDurationNs"]))
-        us = float(r["AverageNs"]) / 1e3
-        rate = flops / (us * 1e-6)
-        out.append(f"| {tag} | `{r['Name'][:60]}` | {r['Calls']} | {us:.1f} | {flops / 1e9:.1f} | {rate / 1e12:.0f} | "
-                   f"{100 * rate / peak:.1f}% |")
+        if sel:
+            r = max(sel, key=lambda r: float(r["TotalDurationNs"]))
+            line(tag, f"`{r['Name'][:60]}`", r["Calls"], float(r["AverageNs"]) / 1e3, flops)
+    # A layer's out and FFN-out products together, whichever epilogue each
+    # takes (the bias epilogue before a separate add + LayerNorm, or the
+    # whole-row tile with the add + LayerNorm fused): their summed time a
+    # layer against both products' FLOPs.
+    sel = [r for r in rows if re.search(r"EpiE6E|gemm_ln_kernel", r["Name"])]
+    calls = sum(int(r["Calls"]) for r in sel)
+    if sel and calls % 2 == 0:
+        ns = sum(float(r["TotalDurationNs"]) for r in sel)
+        line("out + FFN-out products (a layer's pair)", "bias epilogue or fused add + LayerNorm", calls // 2,
+             ns / (calls // 2) / 1e3, 2.0 * T * H * H + 2.0 * T * I * H)
     return out
 
 
-def summarize_stats(stats_dir, workload, command, summary_tag=""):
+def timed_run_from_trace(stats_dir, bench_log):
+    """The bench's timed run in the kernel trace of the profiled command: the
+    run at the JSON line's roofline.timed_run_index (each run's first kernel
+    is pack_rows_kernel), its GEMM launches' average duration and busy time
+    beside what the bench's HIP events gave for the same run."""
+    import csv
+    import glob
+    line = None
+    for text in open(bench_log, errors="replace"):
+        if text.startswith('{"metric"'):
+            line = json.loads(text)
+    traces = glob.glob(os.path.join(stats_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not line or "timed_run_index" not in line.get("roofline", {}) or not traces:
+        return []
+    rf = line["roofline"]
+    rows = []
+    for f in traces:
+        rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if "pack_rows_kernel" in r["Kernel_Name"]]
+    k = rf["timed_run_index"]
+    if k >= len(starts):
+        return []
+    run = rows[starts[k]:starts[k + 1] if k + 1 < len(starts) else len(rows)]
+    spans = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in run if "gemm_" in r["Kernel_Name"])
+    if not spans:
+        return []
+    busy, end = 0, -1
+    for a, b in spans:
+        if b > end:
+            busy += b - max(a, end)
+            end = b
+    mean = sum(b - a for a, b in spans) / len(spans) / 1e3
+    streams = sorted({r["Stream_Id"] for r in run})
+    return ["", f"The bench's timed run (run {k} of the command, its kernels on stream(s) {', '.join(streams)}) in the "
+            f"kernel trace: {len(spans)} GEMM launches, average {mean:.1f} µs a launch, busy {busy / 1e3:.0f} µs "
+            f"(the union of their intervals). The bench's HIP events for the same run: "
+            f"{rf['launches_per_step']} launches, average {rf['avg_launch_us']:.1f} µs, busy "
+            f"{rf['busy_us_per_step']:.0f} µs; roofline {rf['achieved']:.0f} {rf['unit']}, "
+            f"{100 * rf['frac']:.1f}% of peak."]
+
+
+def summarize_stats(stats_dir, workload, command, summary_tag="", bench_log=None):
     """profiles/kernels_<workload>.md from a rocprofv3 --kernel-trace --stats
     run of this script: each kernel's calls, total and average duration, and
-    the GEMM kernel's launches over all its instantiations. With summary_tag
-    "unsplit" (a run of whole-batch launches), kernels_<workload>_unsplit.md
-    with each matrix-core kernel's achieved rate."""
+    the GEMM kernel's launches over all its instantiations; with the
+    profiled command's output (bench_log), the timed run's GEMM launches
+    from the kernel trace beside the bench's HIP events for that run. With
+    summary_tag "unsplit" (a run of whole-batch launches),
+    kernels_<workload>_unsplit.md with each matrix-core kernel's achieved
+    rate."""
     import csv
     import glob
 
@@ -240,15 +296,14 @@ def summarize_stats(stats_dir, workload, command, summary_tag=""):
             lines.append(f"\nThe {tag}: {calls} launches, {ns / 1e6:.3f} ms, average {ns / calls / 1e3:.1f} µs a launch.")
             if pat == "gemm_":
                 # The run's own products: the instantiations holding at least a
-                # tenth of the GEMM time (the rest are the tuner's candidates
-                # and the small bins' shapes), the figure the bench's
-                # avg_launch_us (HIP events, gaps between launches included)
-                # is to agree with.
+                # tenth of the GEMM time (the rest are the small bins' shapes).
                 main = [r for r in sel if float(r["TotalDurationNs"]) >= 0.1 * ns]
                 mc = sum(int(r["Calls"]) for r in main)
                 mns = sum(float(r["TotalDurationNs"]) for r in main)
                 lines.append(f"Its {len(main)} instantiations holding a tenth or more of that time (the run's own "
                              f"products): {mc} launches, average {mns / mc / 1e3:.1f} µs a launch.")
+    if bench_log:
+        lines += timed_run_from_trace(stats_dir, bench_log)
     if summary_tag == "unsplit":
         lines += unsplit_rooflines(rows, workload)
     out = os.path.join(ROOT, "profiles", f"kernels_{workload}{'_' + summary_tag if summary_tag else ''}.md")
@@ -442,6 +497,8 @@ def main():
     ap.add_argument("--pmc-command", action="append", default=[], help="the profiling commands, for the summary")
     ap.add_argument("--summarize-stats", metavar="STATS_DIR",
                     help="write profiles/kernels_<workload>.md from a rocprofv3 --kernel-trace --stats run and exit")
+    ap.add_argument("--bench-log", metavar="FILE",
+                    help="with --summarize-stats: the profiled command's output, whose JSON line names the timed run")
     ap.add_argument("--summary-tag", default="", choices=["", "unsplit"],
                     help="with --summarize-stats: 'unsplit' for a run under TURBO_ROCM_SPLIT=1 of full-length rows "
                          "(per-kernel rates added; written to kernels_<workload>_unsplit.md)")
@@ -463,7 +520,7 @@ def main():
         summarize_counters(args.summarize_counters, args.workload, args.pmc_command)
         return
     if args.summarize_stats:
-        summarize_stats(args.summarize_stats, args.workload, args.pmc_command, args.summary_tag)
+        summarize_stats(args.summarize_stats, args.workload, args.pmc_command, args.summary_tag, args.bench_log)
         return
     if args.library_compare:
         library_compare(args.workload)
@@ -545,8 +602,10 @@ def main():
     wrr_ms = write_run_read([(ids, mask, types)], args.steps)
 
     # Per-kernel times from HIP events, one run launched directly as the
-    # replayed run executes (a split run's two parts side by side), each
-    # launch's pair of events on its own stream.
+    # replayed run executes (a split run's two parts side by side, no marker
+    # between launches): each launch's pair of events is bound to its
+    # kernels' own dispatch packets (the start of the first, the end of the
+    # last), the timestamps a kernel trace reads.
     sess.set_timing(True)
     sess.replay(1)
     times = sess.times()
@@ -605,7 +664,11 @@ def main():
                 # The kernel's busy time in the timed run (at most the step),
                 # and how many of its launches ran at once on average.
                 "busy_us_per_step": dom_busy * 1e3, "overlap": dom_ms / dom_busy,
-                "timed_run_ms": max(b for _, _, b in intervals)}
+                "timed_run_ms": max(b for _, _, b in intervals),
+                # The timed run's place among the process's runs (0: the
+                # first run; then the warm-up and timed steps, and the
+                # write-run-read steps with their one warm-up run).
+                "timed_run_index": 1 + args.warmup + args.steps + 1 + args.steps}
 
     # The memory-bound kernels against HBM's published rate.
     n_out = len(rngs) if rngs else shape.batch

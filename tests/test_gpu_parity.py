@@ -1279,3 +1279,31 @@ def test_buffer_quantize_refuses_what_it_cannot_do(context):
             buf.quantize(mode, rows, dim, ranges)
         assert e.value.code == S.TURBO_E_INVALID_ARGUMENT
     buf.close()
+
+
+def test_a_timed_run_times_each_launch_by_its_kernels(context):
+    # A timed run binds each launch's event pair to its kernels' dispatch
+    # packets: the same bits as the untimed run (which replays the bin's
+    # graph), one interval a launch, each inside the run and as long as the
+    # launch's own time, and no graph replayed for it (bins to le4k, a split
+    # run of two parts at the top).
+    desc = MODELS["bert"](seed=83, hidden=128, inter=256, positions=320)
+    model = context.load(desc)
+    s = model.session(16, 320, S.TURBO_PRECISION_FASTEST)
+    for seed, (batch, seq) in enumerate([(3, 60), (16, 300)]):
+        ids, mask, types = small.ragged_rows(83 + seed, batch, seq, desc.vocab_size)
+        want = s.embed(ids, mask, types)
+        s.set_timing(True)
+        _, launched = s.graphs()
+        got = s.embed(ids, mask, types)
+        iv, times = s.intervals(), s.times()
+        assert s.graphs()[1] == launched
+        s.set_timing(False)
+        np.testing.assert_array_equal(got, want)
+        assert iv and all(0 <= a <= b for _, a, b in iv), iv[:4]
+        assert any(n.startswith("gemm") for n, _, _ in iv)
+        for name, ms in times.items():
+            spans = sum(b - a for n, a, b in iv if n == name)
+            assert abs(spans - ms) <= 1e-3 + 1e-2 * ms, (name, spans, ms)
+    s.close()
+    model.close()

@@ -8,6 +8,7 @@
 // are contiguous rows of d values; V follows transposed, [heads][d][tcap], so
 // one head's values of a run of keys are contiguous in each column.
 #include "kernels.h"
+#include "launch.h"
 #include "devmath.h"
 
 namespace rocm {
@@ -126,8 +127,8 @@ static hipError_t attention_t(hipStream_t s, const void *qkv, int tcap, int head
     const dim3 grid((max_len + 63) / 64, heads, max_rows);
 #define ATT_CASE(D)                                                                                             \
     case D:                                                                                                     \
-        hipLaunchKernelGGL((attention_simple_kernel<T, D>), grid, dim3(64 * SW), 0, s, (const T *)qkv, tcap,     \
-                           heads, p, mask, sp, window, (T *)ctx);                                               \
+        enqueue((attention_simple_kernel<T, D>), grid, dim3(64 * SW), 0, s, (const T *)qkv, tcap,     \
+                heads, p, mask, sp, window, (T *)ctx);                                               \
         break;
     switch (d) {
         ATT_CASE(8)
@@ -623,11 +624,11 @@ static hipError_t attention_mfma_t(hipStream_t s, const void *qkv, int tcap, int
     const int bytes = STAGES * 2 * 64 * 64 * 2 + ((max_len + 127) / 64) * 8;
     if (bytes > 160 * 1024) return hipErrorInvalidValue;
     if (window < INT32_MAX)
-        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, true, QB, STAGES, ATT_BPB>), dim3(blocks), dim3(THREADS), bytes,
-                           s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
+        enqueue((attention_mfma_kernel<T, 64, ATT_QT, true, QB, STAGES, ATT_BPB>), dim3(blocks), dim3(THREADS), bytes,
+                s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
     else
-        hipLaunchKernelGGL((attention_mfma_kernel<T, 64, ATT_QT, false, QB, STAGES, ATT_BPB>), dim3(blocks), dim3(THREADS), bytes,
-                           s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
+        enqueue((attention_mfma_kernel<T, 64, ATT_QT, false, QB, STAGES, ATT_BPB>), dim3(blocks), dim3(THREADS), bytes,
+                s, (const T *)qkv, tcap, heads, sp, nqb, p, mask, window, (T *)ctx);
     return hipGetLastError();
 }
 
@@ -940,15 +941,15 @@ static hipError_t deberta_t(hipStream_t s, const void *qkv, int tcap, int heads,
         if (pos_t && d == 64) {
             // A 1-D grid of groups of 8 (row, head) pairs times nqb query blocks.
             const int nqb = (max_len + 127) / 128, blocks = ((max_rows * heads + 7) / 8) * 8 * nqb;
-            hipLaunchKernelGGL((deberta_attention_mfma_kernel<T>), dim3(blocks), dim3(256), 0, s, (const T *)qkv, tcap, heads,
-                               sp, nqb, p, mask, (const T *)pos_t, buckets, positions, (T *)ctx);
+            enqueue((deberta_attention_mfma_kernel<T>), dim3(blocks), dim3(256), 0, s, (const T *)qkv, tcap, heads,
+                    sp, nqb, p, mask, (const T *)pos_t, buckets, positions, (T *)ctx);
             return hipGetLastError();
         }
     }
     const size_t lds = (size_t)4 * max_len * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((deberta_attention_kernel<T>), dim3(max_rows * heads), dim3(256), lds, s, (const T *)qkv, tcap,
-                       heads, d, p, mask, sp, pos, buckets, positions, (T *)ctx, max_len);
+    enqueue((deberta_attention_kernel<T>), dim3(max_rows * heads), dim3(256), lds, s, (const T *)qkv, tcap,
+            heads, d, p, mask, sp, pos, buckets, positions, (T *)ctx, max_len);
     return hipGetLastError();
 }
 

@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "kernels.h"
+#include "launch.h"
 #include "devmath.h"
 #include "rowmath.h"
 
@@ -295,8 +296,8 @@ template <typename T, int BM, int BN, int BK, Epi KIND>
 static hipError_t launch_k(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda,
                            const void *W, const EpiArgs &e) {
     const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM;
-    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, BK, KIND>), dim3(gn * gm), dim3(256), 0, s, gr.sp, gr.a_tok, N, K,
-                       (const T *)A, lda, (const T *)W, e, gn);
+    enqueue((gemm_kernel<T, BM, BN, BK, KIND>), dim3(gn * gm), dim3(256), 0, s, gr.sp, gr.a_tok, N, K,
+            (const T *)A, lda, (const T *)W, e, gn, 0, (size_t)0);
     return hipGetLastError();
 }
 
@@ -362,13 +363,13 @@ static hipError_t launch_split(hipStream_t s, const GemmRows &gr, int M, int N, 
     p.out = e.ws;
     p.ldo = N;
     const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM;
-    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, BK, Epi::Plain>), dim3(gn * gm, splits), dim3(256), 0, s, gr.sp,
-                       gr.a_tok, N, K, (const T *)A, lda, (const T *)W, p, gn, ks, stride);
+    enqueue((gemm_kernel<T, BM, BN, BK, Epi::Plain>), dim3(gn * gm, splits), dim3(256), 0, s, gr.sp,
+            gr.a_tok, N, K, (const T *)A, lda, (const T *)W, p, gn, ks, stride);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     const size_t quads = stride / 4;
-    hipLaunchKernelGGL((splitk_reduce_kernel<T>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, gr.sp, e.ws,
-                       splits, stride, N, e);
+    enqueue((splitk_reduce_kernel<T>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, gr.sp, e.ws,
+            splits, stride, N, e);
     return hipGetLastError();
 }
 
@@ -1158,8 +1159,8 @@ static hipError_t launch_lds_k(hipStream_t s, const GemmRows &gr, int M, int N, 
     constexpr int bytes = STAGES * (BM + BN) * BK * (int)sizeof(T);
     // Dynamic LDS up to the device's 160 KB per workgroup needs no attribute on gfx950.
     const int gn = (N + BN - 1) / BN, gm = (M + BM - 1) / BM;
-    hipLaunchKernelGGL((gemm_lds_kernel<T, OT, BM, BN, WM, WN, STAGES, BK, OCC, KIND>), dim3(gn * gm),
-                       dim3(64 * WM * WN), bytes, s, gr.sp, gr.a_tok, N, K, (const T *)A, lda, (const T *)W, e, gn);
+    enqueue((gemm_lds_kernel<T, OT, BM, BN, WM, WN, STAGES, BK, OCC, KIND>), dim3(gn * gm),
+            dim3(64 * WM * WN), bytes, s, gr.sp, gr.a_tok, N, K, (const T *)A, lda, (const T *)W, e, gn);
     return hipGetLastError();
 }
 
@@ -1315,8 +1316,8 @@ static hipError_t launch_ln(hipStream_t s, const GemmRows &gr, int M, int K, con
                             const LnArgs &e) {
     constexpr int BM = 128, BN = 768;
     constexpr int bytes = (BM + BN) * BK * (int)sizeof(T) * STAGES;
-    hipLaunchKernelGGL((gemm_ln_kernel<T, BM, BN, WM, WN, STAGES, BK>), dim3((M + BM - 1) / BM), dim3(64 * WM * WN),
-                       bytes, s, gr.sp, gr.a_tok, K, (const T *)A, lda, (const T *)W, e);
+    enqueue((gemm_ln_kernel<T, BM, BN, WM, WN, STAGES, BK>), dim3((M + BM - 1) / BM), dim3(64 * WM * WN),
+            bytes, s, gr.sp, gr.a_tok, K, (const T *)A, lda, (const T *)W, e);
     return hipGetLastError();
 }
 
@@ -1603,7 +1604,7 @@ __global__ void __launch_bounds__(256) mfma_probe_kernel(float *out, unsigned lo
 }
 
 hipError_t mfma_probe(hipStream_t s, int blocks, int iters, int random, float *out, unsigned long long *clk) {
-    hipLaunchKernelGGL(mfma_probe_kernel, dim3(blocks), dim3(256), 0, s, out, clk, iters, random);
+    enqueue(mfma_probe_kernel, dim3(blocks), dim3(256), 0, s, out, clk, iters, random);
     return hipGetLastError();
 }
 

@@ -7,6 +7,18 @@
 
 namespace rocm {
 
+// The timing hook of every launch. A timed run sets `stop` (and `start`)
+// before a launcher and clears them after it: the first kernel the launcher
+// enqueues on this thread takes the start event and each takes the stop
+// event, bound to the kernels' own dispatch packets, so the pair spans the
+// kernels' execution with no marker packet between launches. `bound` says
+// that a kernel took them.
+struct LaunchTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool bound = false;
+};
+LaunchTiming &launch_timing();
+
 // The arithmetic type of a session's GEMM operands and activations. I8 is
 // GEMM operands alone: int8 weights (per output channel) and activations (per
 // token), int32 sums; its activations are F16.

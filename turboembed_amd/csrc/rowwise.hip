@@ -6,6 +6,7 @@
 #include <mutex>
 
 #include "kernels.h"
+#include "launch.h"
 #include "devmath.h"
 #include "rowmath.h"
 
@@ -86,11 +87,11 @@ __global__ void __launch_bounds__(256) place_tokens_kernel(const RunDims *__rest
 }
 
 hipError_t pack_rows(hipStream_t s, const int32_t *mask, const RunDims *dims, int max_batch, int max_seq, Packing p) {
-    hipLaunchKernelGGL(pack_rows_kernel, dim3(1), dim3(1024), max_batch * sizeof(int32_t), s, mask, dims, p);
+    enqueue(pack_rows_kernel, dim3(1), dim3(1024), max_batch * sizeof(int32_t), s, mask, dims, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t blocks = std::min<size_t>(((size_t)max_batch * max_seq + 255) / 256, 1024);
-    hipLaunchKernelGGL(place_tokens_kernel, dim3(blocks), dim3(256), 0, s, dims, p);
+    enqueue(place_tokens_kernel, dim3(blocks), dim3(256), 0, s, dims, p);
     return hipGetLastError();
 }
 
@@ -429,18 +430,18 @@ static hipError_t add_ln_v(hipStream_t s, const Span &sp, int tokens, int hidden
     // must give the bits of the fused one.
     if constexpr (sizeof(Y) == 2 && sizeof(H) == 2) {
         if (res_h && hidden % 8 == 0) {
-            hipLaunchKernelGGL((add_ln_pair_kernel<G, Y, H, true, LN_ROWS, LN_WAVES>),
-                               (pair_blocks<LN_WAVES, LN_ROWS>(tokens)), dim3(64 * LN_WAVES), 0, s,
-                               sp, hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
+            enqueue((add_ln_pair_kernel<G, Y, H, true, LN_ROWS, LN_WAVES>),
+                    (pair_blocks<LN_WAVES, LN_ROWS>(tokens)), dim3(64 * LN_WAVES), 0, s,
+                    sp, hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
             return hipGetLastError();
         }
     }
     if (res_h && sizeof(H) == 2)
-        hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H, sizeof(H) == 2>), dim3((tokens + 3) / 4), dim3(256), 0, s,
-                           sp, hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
+        enqueue((add_layer_norm_kernel<G, Y, H, sizeof(H) == 2>), dim3((tokens + 3) / 4), dim3(256), 0, s,
+                sp, hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
     else
-        hipLaunchKernelGGL((add_layer_norm_kernel<G, Y, H, false>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp,
-                           hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
+        enqueue((add_layer_norm_kernel<G, Y, H, false>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp,
+                hidden, x, (const Y *)y, ln_w, ln_b, eps, pre_norm, (int)keep_f32, (H *)out_h, qo);
     return hipGetLastError();
 }
 
@@ -531,22 +532,22 @@ static hipError_t embed_ln_v(hipStream_t s, const Span &sp, int tokens, int hidd
                              const int32_t *zero_mask, const QuantOut &qo) {
     if constexpr (sizeof(H) == 2) {
         if (!x && xh && !qo.q && hidden % 8 == 0) {
-            hipLaunchKernelGGL((embed_ln_pair_kernel<G, H, LN_WAVES>), (pair_blocks<LN_WAVES, 1>(tokens)),
-                               dim3(64 * LN_WAVES), 0, s, sp, hidden, ids,
-                               types, p, offset, word, pos, type, ln_w, ln_b, eps, (H *)xh, zero_mask);
+            enqueue((embed_ln_pair_kernel<G, H, LN_WAVES>), (pair_blocks<LN_WAVES, 1>(tokens)),
+                    dim3(64 * LN_WAVES), 0, s, sp, hidden, ids,
+                    types, p, offset, word, pos, type, ln_w, ln_b, eps, (H *)xh, zero_mask);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((embed_ln_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp, hidden, ids, types, p,
-                       offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh, zero_mask, qo);
+    enqueue((embed_ln_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp, hidden, ids, types, p,
+            offset, word, pos, type, ln_w, ln_b, eps, x, (H *)xh, zero_mask, qo);
     return hipGetLastError();
 }
 
 template <typename H, int G>
 static hipError_t ln_v(hipStream_t s, const Span &sp, int tokens, int hidden, const float *in, const float *ln_w,
                        const float *ln_b, float eps, float *out_f32, void *out_h) {
-    hipLaunchKernelGGL((layer_norm_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp, hidden, in, ln_w,
-                       ln_b, eps, out_f32, (H *)out_h);
+    enqueue((layer_norm_kernel<G, H>), dim3((tokens + 3) / 4), dim3(256), 0, s, sp, hidden, in, ln_w,
+            ln_b, eps, out_f32, (H *)out_h);
     return hipGetLastError();
 }
 
@@ -845,10 +846,10 @@ hipError_t pool(hipStream_t s, const RunDims *dims, int max_items, const float *
     if (max_items <= 0) return hipSuccess;
     if (!ps.part || !ps.cnt || ps.chunks <= 0) return hipErrorInvalidValue;
     const int part_blocks = (int)std::min<long>((long)max_items * ps.chunks, POOL_GRID);
-    hipLaunchKernelGGL(pool_part_kernel, dim3(part_blocks), dim3(POOL_THREADS), 0, s, dims, x, hidden, p, mask, ranges,
-                       ps.part, ps.cnt, ps.chunks);
-    hipLaunchKernelGGL(pool_kernel, dim3(std::min(max_items, POOL_GRID)), dim3(POOL_THREADS), 0, s, dims, x, hidden, p,
-                       ranges, out, hw, hb, hout, ps.part, ps.cnt, ps.chunks);
+    enqueue(pool_part_kernel, dim3(part_blocks), dim3(POOL_THREADS), 0, s, dims, x, hidden, p, mask, ranges,
+            ps.part, ps.cnt, ps.chunks);
+    enqueue(pool_kernel, dim3(std::min(max_items, POOL_GRID)), dim3(POOL_THREADS), 0, s, dims, x, hidden, p,
+            ranges, out, hw, hb, hout, ps.part, ps.cnt, ps.chunks);
     return hipGetLastError();
 }
 
@@ -930,19 +931,19 @@ hipError_t quantize_rows(hipStream_t s, const void *src, Dt src_dt, int rows, in
     const dim3 grid((rows + 3) / 4);
     if (cols % 8 == 0 && ld % 8 == 0 && cols <= 8 * 64 * QMAXK && (src_dt == Dt::F32 || src_dt == Dt::F16)) {
         if (src_dt == Dt::F32)
-            hipLaunchKernelGGL(quantize_rows8_kernel<float>, grid, dim3(256), 0, s, (const float *)src, rows, cols, ld,
-                               dst, scale);
+            enqueue(quantize_rows8_kernel<float>, grid, dim3(256), 0, s, (const float *)src, rows, cols, ld,
+                    dst, scale);
         else
-            hipLaunchKernelGGL(quantize_rows8_kernel<_Float16>, grid, dim3(256), 0, s, (const _Float16 *)src, rows,
-                               cols, ld, dst, scale);
+            enqueue(quantize_rows8_kernel<_Float16>, grid, dim3(256), 0, s, (const _Float16 *)src, rows,
+                    cols, ld, dst, scale);
         return hipGetLastError();
     }
     if (src_dt == Dt::F32)
-        hipLaunchKernelGGL(quantize_rows_kernel<float>, grid, dim3(256), 0, s, (const float *)src, rows, cols, ld, dst,
-                           scale);
+        enqueue(quantize_rows_kernel<float>, grid, dim3(256), 0, s, (const float *)src, rows, cols, ld, dst,
+                scale);
     else if (src_dt == Dt::F16)
-        hipLaunchKernelGGL(quantize_rows_kernel<_Float16>, grid, dim3(256), 0, s, (const _Float16 *)src, rows, cols,
-                           ld, dst, scale);
+        enqueue(quantize_rows_kernel<_Float16>, grid, dim3(256), 0, s, (const _Float16 *)src, rows, cols,
+                ld, dst, scale);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1003,11 +1004,11 @@ hipError_t quantize_span(hipStream_t s, const Span &sp, int max_rows, const void
         return hipErrorInvalidValue;
     const dim3 grid((max_rows + 3) / 4);
     if (src_dt == Dt::F32)
-        hipLaunchKernelGGL(quantize_span_kernel<float>, grid, dim3(256), 0, s, sp, (const float *)src, cols, ld, dst,
-                           dst_tok, scale);
+        enqueue(quantize_span_kernel<float>, grid, dim3(256), 0, s, sp, (const float *)src, cols, ld, dst,
+                dst_tok, scale);
     else
-        hipLaunchKernelGGL(quantize_span_kernel<_Float16>, grid, dim3(256), 0, s, sp, (const _Float16 *)src, cols, ld,
-                           dst, dst_tok, scale);
+        enqueue(quantize_span_kernel<_Float16>, grid, dim3(256), 0, s, sp, (const _Float16 *)src, cols, ld,
+                dst, dst_tok, scale);
     return hipGetLastError();
 }
 
@@ -1031,7 +1032,7 @@ __global__ void __launch_bounds__(256) fill_uniform_kernel(float *__restrict__ d
 hipError_t fill_uniform(hipStream_t s, float *dst, size_t n, float amp, uint32_t seed) {
     if (n == 0) return hipSuccess;
     const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
-    hipLaunchKernelGGL(fill_uniform_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, n, amp, seed);
+    enqueue(fill_uniform_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, n, amp, seed);
     return hipGetLastError();
 }
 
@@ -1076,9 +1077,9 @@ hipError_t quantize_codes(hipStream_t s, const float *x, int rows, int dim, int 
     const size_t n = mode == 2 ? (size_t)rows * dim : (size_t)rows * ((dim + 7) / 8);
     const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
     if (mode == 2)
-        hipLaunchKernelGGL(int8_codes_kernel, dim3(blocks), dim3(256), 0, s, x, rows, dim, ranges, out);
+        enqueue(int8_codes_kernel, dim3(blocks), dim3(256), 0, s, x, rows, dim, ranges, out);
     else if (mode == 3)
-        hipLaunchKernelGGL(ubinary_codes_kernel, dim3(blocks), dim3(256), 0, s, x, rows, dim, out);
+        enqueue(ubinary_codes_kernel, dim3(blocks), dim3(256), 0, s, x, rows, dim, out);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1124,7 +1125,7 @@ hipError_t copy_bytes(hipStream_t s, const void *src, void *dst, size_t bytes) {
     const size_t n = bytes / 16;
     if (n == 0) return hipSuccess;
     const size_t blocks = std::min<size_t>((n + 255) / 256, 256 * 32);
-    hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const uint4 *)src, (uint4 *)dst, n);
+    enqueue(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const uint4 *)src, (uint4 *)dst, n);
     return hipGetLastError();
 }
 
@@ -1141,8 +1142,8 @@ hipError_t copy_rows(hipStream_t s, const Span &sp, int max_tokens, const void *
     const size_t n = (size_t)max_tokens * (row_bytes / 16);
     if (n == 0) return hipSuccess;
     const size_t blocks = std::min<size_t>((n + 255) / 256, 256 * 32);
-    hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, sp, (const uint4 *)src, (uint4 *)dst,
-                       (int)(row_bytes / 16));
+    enqueue(copy_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, sp, (const uint4 *)src, (uint4 *)dst,
+            (int)(row_bytes / 16));
     return hipGetLastError();
 }
 
@@ -1162,9 +1163,9 @@ hipError_t narrow(hipStream_t s, const float *src, void *dst, size_t n, Dt dt, i
     const int blocks = (int)std::min<size_t>((n + 255) / 256, 65536);
     if (n == 0) return hipSuccess;
     if (dt == Dt::F16)
-        hipLaunchKernelGGL(narrow_kernel<_Float16>, dim3(blocks), dim3(256), 0, s, src, (_Float16 *)dst, n, overflow);
+        enqueue(narrow_kernel<_Float16>, dim3(blocks), dim3(256), 0, s, src, (_Float16 *)dst, n, overflow);
     else if (dt == Dt::BF16)
-        hipLaunchKernelGGL(narrow_kernel<__bf16>, dim3(blocks), dim3(256), 0, s, src, (__bf16 *)dst, n, overflow);
+        enqueue(narrow_kernel<__bf16>, dim3(blocks), dim3(256), 0, s, src, (__bf16 *)dst, n, overflow);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -1031,20 +1031,36 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
 // the run starts and an event pair around each launch on the launch's own
 // stream, so a launch's interval is measured as the run executes it (a split
 // run's parts side by side).
+// The pair of a launch is bound to its kernels' dispatch packets (the
+// launch hook of the launchers): the start event to the first kernel's start,
+// the stop event to the last kernel's end, so the timed run executes as an
+// untimed one does, with no marker packet between its launches. A launch that
+// enqueued no kernel gets a marker pair of no length.
+LaunchTiming &launch_timing() {
+    static thread_local LaunchTiming t;
+    return t;
+}
+
 struct Timer {
     Session &s;
     explicit Timer(Session &ss) : s(ss) {
         s.ev_used = 0;
         if (s.timing && s.ev0) (void)hipEventRecord(s.ev0, s.ctx->stream);
     }
+    ~Timer() { launch_timing() = LaunchTiming{}; }
     void begin(const char *name, hipStream_t st) {
+        (void)st;
         if (!s.timing || s.ev_used + 2 > s.ev.size()) return;
         s.ev_name[s.ev_used / 2] = name;
-        (void)hipEventRecord(s.ev[s.ev_used], st);
+        launch_timing() = LaunchTiming{s.ev[s.ev_used], s.ev[s.ev_used + 1], false};
     }
     void end(hipStream_t st) {
         if (!s.timing || s.ev_used + 2 > s.ev.size()) return;
-        (void)hipEventRecord(s.ev[s.ev_used + 1], st);
+        if (!launch_timing().bound) {
+            (void)hipEventRecord(s.ev[s.ev_used], st);
+            (void)hipEventRecord(s.ev[s.ev_used + 1], st);
+        }
+        launch_timing() = LaunchTiming{};
         s.ev_used += 2;
     }
 };
