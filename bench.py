@@ -102,18 +102,27 @@ def traffic_file(workload):
     return os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
 
 
-def summarize_pmc(fetch_dir, write_dir, workload, command):
-    """HBM bytes per launch of the GEMM kernel (every instantiation in the
-    run) from two rocprofv3 --pmc runs of this script with --copy-probe
-    (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
-    same counter read for the plain copy of COPY_PROBE_BYTES; written to
-    profiles/traffic_<workload>.json and .md. Also per product: the run
-    launches each layer's products in the order QKV, out, FFN-in, FFN-out, so
-    its GEMM dispatches, in dispatch order, take those names in turn; each
-    product's algorithmic bytes (operands read once, output written once) are
-    for launches over tokens / parts rows (the default split)."""
+def summarize_pmc(fetch_dir, write_dir, workload, command, bench_log=None):
+    """HBM bytes per launch of the GEMM kernel from two rocprofv3 --pmc runs
+    of this script with --copy-probe (FETCH_SIZE, then WRITE_SIZE, KiB per
+    dispatch), each scaled by what the same counter read for the plain copy
+    of COPY_PROBE_BYTES; written to profiles/traffic_<workload>.json and .md.
+    With the profiled command's output (bench_log), the dispatches of the
+    roofline's whole-batch run alone (the run at its timed_run_index; each
+    run's first kernel is pack_rows_kernel), else every GEMM dispatch of the
+    command. Also per product: a run launches each layer's products in the
+    order QKV, out, FFN-in, FFN-out, so its GEMM dispatches, in dispatch
+    order, take those names in turn; each product's algorithmic bytes
+    (operands read once, output written once) are for launches over the
+    whole batch (or over half of it, the default split, without bench_log)."""
     import csv
     import glob
+
+    index = None
+    if bench_log:
+        for text in open(bench_log, errors="replace"):
+            if text.startswith('{"metric"'):
+                index = json.loads(text)["roofline"]["timed_run_index"]
 
     def per_dispatch(d, counter):
         rows = []
@@ -123,12 +132,19 @@ def summarize_pmc(fetch_dir, write_dir, workload, command):
                     rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
         return sorted(rows)
 
+    def run_only(v):
+        if index is None:
+            return v
+        starts = [i for i, (_, k, _) in enumerate(v) if "pack_rows_kernel" in k]
+        return v[starts[index]:starts[index + 1] if index + 1 < len(starts) else len(v)]
+
     shape = W.SHAPES[workload]
     H, I = shape.hidden, shape.intermediate
     gated = shape.family == S.TURBO_FAMILY_MODERNBERT
     el = 4 if shape.precision == S.TURBO_PRECISION_EXACT else 2
     # Whole-row batches of the embedding task only (every launch's rows known).
-    M = shape.batch * shape.seq // 2 if shape.lengths is None and shape.task == S.TURBO_TASK_EMBED else None
+    M = shape.batch * shape.seq // (1 if index is not None else 2) \
+        if shape.lengths is None and shape.task == S.TURBO_TASK_EMBED else None
     products = [("qkv", H, 3 * H), ("out", H, H), ("ffn_in", H, (2 if gated else 1) * I), ("ffn_out", I, H)]
     out = {"workload": workload, "command": command, "copy_probe_bytes": COPY_PROBE_BYTES}
     lines = [f"# HBM traffic per launch: {workload}", "", "Commands (from the repository root, one MI355X):", "",
@@ -139,7 +155,7 @@ def summarize_pmc(fetch_dir, write_dir, workload, command):
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         v = per_dispatch(d, counter)
         copy = [x for _, k, x in v if "copy_kernel" in k]
-        gemm = [x for _, k, x in v if "gemm_lds_kernel" in k]
+        gemm = [x for _, k, x in run_only(v) if "gemm_" in k and "splitk_reduce" not in k]
         expected = COPY_PROBE_BYTES / 1024.0
         factor = expected / (sum(copy) / len(copy))
         mean = sum(gemm) / len(gemm)
@@ -223,10 +239,11 @@ def unsplit_rooflines(rows, workload):
 
 
 def timed_run_from_trace(stats_dir, bench_log):
-    """The bench's timed run in the kernel trace of the profiled command: the
-    run at the JSON line's roofline.timed_run_index (each run's first kernel
-    is pack_rows_kernel), its GEMM launches' average duration and busy time
-    beside what the bench's HIP events gave for the same run."""
+    """The bench's timed runs in the kernel trace of the profiled command:
+    the roofline's whole-batch run and the split run (the runs at the JSON
+    line's timed_run_index; each run's first kernel is pack_rows_kernel),
+    their GEMM launches' average duration and busy time beside what the
+    bench's HIP events gave for the same runs."""
     import csv
     import glob
     line = None
@@ -242,26 +259,44 @@ def timed_run_from_trace(stats_dir, bench_log):
         rows += list(csv.DictReader(open(f)))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     starts = [i for i, r in enumerate(rows) if "pack_rows_kernel" in r["Kernel_Name"]]
-    k = rf["timed_run_index"]
-    if k >= len(starts):
-        return []
-    run = rows[starts[k]:starts[k + 1] if k + 1 < len(starts) else len(rows)]
-    spans = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in run if "gemm_" in r["Kernel_Name"])
-    if not spans:
-        return []
-    busy, end = 0, -1
-    for a, b in spans:
-        if b > end:
-            busy += b - max(a, end)
-            end = b
-    mean = sum(b - a for a, b in spans) / len(spans) / 1e3
-    streams = sorted({r["Stream_Id"] for r in run})
-    return ["", f"The bench's timed run (run {k} of the command, its kernels on stream(s) {', '.join(streams)}) in the "
-            f"kernel trace: {len(spans)} GEMM launches, average {mean:.1f} µs a launch, busy {busy / 1e3:.0f} µs "
-            f"(the union of their intervals). The bench's HIP events for the same run: "
-            f"{rf['launches_per_step']} launches, average {rf['avg_launch_us']:.1f} µs, busy "
-            f"{rf['busy_us_per_step']:.0f} µs; roofline {rf['achieved']:.0f} {rf['unit']}, "
-            f"{100 * rf['frac']:.1f}% of peak."]
+
+    def run_of(k):
+        if k >= len(starts):
+            return None
+        run = rows[starts[k]:starts[k + 1] if k + 1 < len(starts) else len(rows)]
+        spans = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in run
+                       if "gemm_" in r["Kernel_Name"])
+        busy, end = 0, -1
+        for a, b in spans:
+            if b > end:
+                busy += b - max(a, end)
+                end = b
+        length = (max(int(r["End_Timestamp"]) for r in run) - int(run[0]["Start_Timestamp"])) / 1e3
+        return spans, busy / 1e3, length, sorted({r["Stream_Id"] for r in run})
+
+    out = []
+    w = run_of(rf["timed_run_index"])
+    if w and w[0]:
+        spans, busy, length, streams = w
+        mean = sum(b - a for a, b in spans) / len(spans) / 1e3
+        out += ["", f"The roofline's whole-batch run (run {rf['timed_run_index']} of the command, stream(s) "
+                f"{', '.join(streams)}) in the kernel trace: {len(spans)} GEMM launches, average {mean:.1f} µs a "
+                f"launch, {sum(b - a for a, b in spans) / 1e6:.2f} ms in all within the run's {length / 1e3:.2f} ms. "
+                f"The bench's HIP events for the same run: {rf['launches_per_step']} launches, average "
+                f"{rf['avg_launch_us']:.1f} µs, {rf['launch_ms_per_step']:.2f} ms in all within "
+                f"{rf['timed_run_ms']:.2f} ms; roofline {rf['achieved']:.0f} {rf['unit']}, "
+                f"{100 * rf['frac']:.1f}% of peak."]
+    c = rf.get("concurrent")
+    s = run_of(c["timed_run_index"]) if c else None
+    if s and s[0]:
+        spans, busy, length, streams = s
+        mean = sum(b - a for a, b in spans) / len(spans) / 1e3
+        out += ["", f"The split run (run {c['timed_run_index']}, parts side by side on stream(s) "
+                f"{', '.join(streams)}) in the kernel trace: {len(spans)} GEMM launches, average {mean:.1f} µs a "
+                f"launch (overlapping), busy {busy:.0f} µs. The bench's events: {c['launches_per_step']} launches, "
+                f"average {c['avg_launch_us']:.1f} µs, busy {c['busy_us_per_step']:.0f} µs; "
+                f"{c['achieved']:.0f} {rf['unit']} over the busy time."]
+    return out
 
 
 def summarize_stats(stats_dir, workload, command, summary_tag="", bench_log=None):
@@ -498,7 +533,8 @@ def main():
     ap.add_argument("--summarize-stats", metavar="STATS_DIR",
                     help="write profiles/kernels_<workload>.md from a rocprofv3 --kernel-trace --stats run and exit")
     ap.add_argument("--bench-log", metavar="FILE",
-                    help="with --summarize-stats: the profiled command's output, whose JSON line names the timed run")
+                    help="with --summarize-stats or --summarize-pmc: the profiled command's output, whose JSON line "
+                         "names the timed runs")
     ap.add_argument("--summary-tag", default="", choices=["", "unsplit"],
                     help="with --summarize-stats: 'unsplit' for a run under TURBO_ROCM_SPLIT=1 of full-length rows "
                          "(per-kernel rates added; written to kernels_<workload>_unsplit.md)")
@@ -514,7 +550,7 @@ def main():
         sys.exit(2)
 
     if args.summarize_pmc:
-        summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.workload, args.pmc_command)
+        summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.workload, args.pmc_command, args.bench_log)
         return
     if args.summarize_counters:
         summarize_counters(args.summarize_counters, args.workload, args.pmc_command)
@@ -606,41 +642,76 @@ def main():
     # between launches): each launch's pair of events is bound to its
     # kernels' own dispatch packets (the start of the first, the end of the
     # last), the timestamps a kernel trace reads.
-    sess.set_timing(True)
-    sess.replay(1)
-    times = sess.times()
-    counts = sess.launches()
-    intervals = sess.intervals()
-    sess.set_timing(False)
+    def timed_run(s):
+        s.set_timing(True)
+        s.replay(1)
+        out = s.times(), s.launches(), s.intervals()
+        s.set_timing(False)
+        return out
+
+    times, counts, intervals = timed_run(sess)
+    # The process's runs so far (each begins with pack_rows_kernel, so a
+    # kernel trace finds them): the first run, the warm-up and timed steps,
+    # the write-run-read steps with their one warm-up run, the timed run.
+    runs_done = 1 + args.warmup + args.steps + 1 + args.steps + 1
     per = kernel_flops(shape, tokens, lens)
-    gemm_names = [k for k in times if k.startswith("gemm_")]
-    gemm_ms = sum(times[k] for k in gemm_names)
-    gemm_flops = sum(per[k] for k in gemm_names) * shape.layers
     total_flops = W.gemm_flops_per_token(shape) * tokens + W.attention_flops(shape, lens)
 
-    def busy_ms(names):
-        """The run's time with at least one launch of these kernels running:
-        the union of their launches' intervals over every stream."""
-        total, end = 0.0, float("-inf")
-        for a, b in sorted((a, b) for n, a, b in intervals if n in names):
-            if b > end:
-                total += b - max(a, end)
-                end = b
-        return total
+    def dominant(times, counts, intervals):
+        """The dominant kernel of a timed run, the GEMM kernel (every linear
+        layer's launches) or attention, whichever is busy longer: its name,
+        summed launch time, FLOPs, launches and busy time (the union of its
+        launches' intervals over every stream)."""
+        def busy_ms(names):
+            total, end = 0.0, float("-inf")
+            for a, b in sorted((a, b) for n, a, b in intervals if n in names):
+                if b > end:
+                    total += b - max(a, end)
+                    end = b
+            return total
 
-    # The dominant kernel: the GEMM kernel (every linear layer's launches),
-    # or attention when it is busy longer. Its rate is its FLOPs over the
-    # time it was running (the parts' launches overlap, so their own
-    # durations sum past that time).
-    gemm_busy = busy_ms(set(gemm_names))
-    if busy_ms({"attention"}) > gemm_busy:
-        dom, dom_ms, dom_flops, dom_launches = "attention", times["attention"], per["attention"] * shape.layers, \
-            counts["attention"]
-        dom_busy = busy_ms({"attention"})
+        gemm_names = [k for k in times if k.startswith("gemm_")]
+        gemm = ("gemm", sum(times[k] for k in gemm_names), sum(per[k] for k in gemm_names) * shape.layers,
+                sum(counts[k] for k in gemm_names), busy_ms(set(gemm_names)))
+        if "attention" in times and busy_ms({"attention"}) > gemm[4]:
+            return ("attention", times["attention"], per["attention"] * shape.layers, counts["attention"],
+                    busy_ms({"attention"}))
+        return gemm
+
+    # The split run's figures: its parts' launches overlap, so their own
+    # durations sum past the time the kernel was running; the rate there is
+    # over that busy time.
+    c_dom, c_ms, c_flops, c_launches, c_busy = dominant(times, counts, intervals)
+    concurrent = {"kernel": c_dom, "launches_per_step": c_launches, "avg_launch_us": c_ms / c_launches * 1e3,
+                  "busy_us_per_step": c_busy * 1e3, "achieved": c_flops / (c_busy / 1e3) / 1e12,
+                  "frac": c_flops / (c_busy / 1e3) / PEAK[dtype], "timed_run_ms": max(b for _, _, b in intervals),
+                  "timed_run_index": runs_done - 1}
+
+    # The roofline: the dominant kernel's launches over the whole batch (the
+    # same rows in a session whose runs do not split: one launch a layer per
+    # product, on one stream), so each launch's pair of events brackets that
+    # launch alone and the launches' summed time lies inside the run.
+    saved = os.environ.get("TURBO_ROCM_SPLIT")
+    os.environ["TURBO_ROCM_SPLIT"] = "1"
+    try:
+        whole = model.session(shape.batch, shape.seq, shape.precision, autotune=mode, budget_ms=args.budget_ms,
+                              max_ranges=len(rngs) if rngs else 0)
+    finally:
+        if saved is None:
+            del os.environ["TURBO_ROCM_SPLIT"]
+        else:
+            os.environ["TURBO_ROCM_SPLIT"] = saved
+    if rngs:
+        whole.write_ranges(ids, mask, rngs, types, normalize=shape.normalize)
     else:
-        dom, dom_ms, dom_flops, dom_launches = "gemm", gemm_ms, gemm_flops, sum(counts[k] for k in gemm_names)
-        dom_busy = gemm_busy
-    achieved = dom_flops / (dom_busy / 1e3)
+        whole.write_tokens(ids, mask, types, pooling=shape.pooling, normalize=shape.normalize)
+    whole.run()
+    whole.replay(2)
+    w_times, w_counts, w_intervals = timed_run(whole)
+    whole_index = runs_done + 3
+    whole.close()
+    dom, dom_ms, dom_flops, dom_launches, dom_busy = dominant(w_times, w_counts, w_intervals)
+    achieved = dom_flops / (dom_ms / 1e3)
     traffic = None
     if dom == "gemm" and os.path.exists(traffic_file(args.workload)):
         with open(traffic_file(args.workload)) as f:
@@ -659,16 +730,15 @@ def main():
         T.copy_probe(COPY_PROBE_BYTES, iters=3)
     roofline = {"kernel": dom, "bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK[dtype] / 1e12,
                 "unit": "TOP/s" if dtype == "i8" else "TFLOP/s", "frac": achieved / PEAK[dtype], "traffic": traffic,
+                "run": "whole batch: the same rows in a session whose runs do not split (one launch a layer per "
+                       "product, one stream)",
                 "launches_per_step": dom_launches, "avg_launch_us": dom_ms / dom_launches * 1e3,
                 "flops_per_launch": dom_flops / dom_launches,
-                # The kernel's busy time in the timed run (at most the step),
-                # and how many of its launches ran at once on average.
-                "busy_us_per_step": dom_busy * 1e3, "overlap": dom_ms / dom_busy,
-                "timed_run_ms": max(b for _, _, b in intervals),
+                "launch_ms_per_step": dom_ms, "timed_run_ms": max(b for _, _, b in w_intervals),
                 # The timed run's place among the process's runs (0: the
-                # first run; then the warm-up and timed steps, and the
-                # write-run-read steps with their one warm-up run).
-                "timed_run_index": 1 + args.warmup + args.steps + 1 + args.steps}
+                # first run), for finding it in a kernel trace.
+                "timed_run_index": whole_index,
+                "concurrent": concurrent}
 
     # The memory-bound kernels against HBM's published rate.
     n_out = len(rngs) if rngs else shape.batch

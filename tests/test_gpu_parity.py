@@ -410,7 +410,7 @@ def quantize_rows(x):
     return q, (mx / np.float32(127)).astype(np.float32)
 
 
-@pytest.mark.parametrize("tile", [0, 7, 9])
+@pytest.mark.parametrize("tile", [0, 7, 9, 15])
 @pytest.mark.parametrize("mnk", [(256, 256, 128), (300, 200, 64), (1000, 768, 768), (517, 2304, 3072), (33, 96, 192)])
 def test_int8_gemm_is_the_integer_product(runtime, tile, mnk):
     # The int32 sums are exact; the dequantized F32 result differs from
@@ -473,6 +473,32 @@ def test_int8_bert_base_meets_the_oracle(context):
     cos = small.cosine_rows(got, want)
     assert cos.min() >= I8_FLOOR, cos.min()
     s.close()
+    model.close()
+
+
+@pytest.mark.parametrize("split", ["0", "2"])
+def test_int8_block_shapes_give_the_same_bits(context, monkeypatch, split):
+    # The int32 sums are exact and each output is dequantized by the same
+    # steps in every block shape, so 256 x 384 tiles (their scales and
+    # biases read from LDS) and 256 x 256 tiles give the same states bit for
+    # bit: BERT-base width at 2 layers, ragged rows, the Q/K/V scatter, GELU
+    # and bias epilogues, split into two parts or not.
+    sh = W.SHAPES["bert-base"]
+    desc = int8_model(W.model(sh, layers=2))
+    ids, mask, types = W.rows(sh, batch=24, lengths=(64, 512))
+    model = context.load(desc)
+    out = {}
+    for tile in ("256x256", "256x384"):
+        monkeypatch.setenv("TURBO_ROCM_CHOICES", f"all:qkv={tile},out={tile},ffn1={tile},ffn2={tile}")
+        monkeypatch.setenv("TURBO_ROCM_SPLIT", split)
+        s = model.session(24, 512, S.TURBO_PRECISION_FASTEST)
+        assert s.compute_dtype == S.TURBO_DTYPE_I8 and f"qkv={tile}," in s.choices()
+        out[tile] = (s.embed(ids, mask, types, pooling=sh.pooling, normalize=sh.normalize), s.hidden())
+        s.close()
+    np.testing.assert_array_equal(out["256x256"][1], out["256x384"][1])
+    np.testing.assert_array_equal(out["256x256"][0], out["256x384"][0])
+    want = oracle.encode(desc, ids, mask, types, pooling=sh.pooling, normalize=sh.normalize)
+    assert small.cosine_rows(out["256x384"][0], want).min() >= I8_FLOOR
     model.close()
 
 

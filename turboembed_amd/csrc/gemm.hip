@@ -447,15 +447,17 @@ __device__ __forceinline__ u32x2_t pack4(const float (&v)[4]) {
 // so the epilogue reads nothing from global memory once its first store is
 // out. 16-bit operands: the bias of the lane's accumulator columns 32 j + ql,
 // added as the accumulators go to LDS (TN registers). int8 operands, whose
-// bias follows the scales: row-wise stores take 8 consecutive columns of each
-// of the lane's PH chunks, V^T stores the one column of each of its KV items.
+// bias follows the scales: the wave's COLS scales, then its COLS biases, NV
+// values a lane, go to the wave's LDS (stage_cols) once the stages are free,
+// and each store reads its columns' from there (registers for them all would
+// spill the wide block shapes' accumulators).
 template <int TN, int PASS, bool SCALED>
 struct EpiCols {
     static constexpr int COLS = TN * 32, CH = COLS / 8, PH = CH / gcd_c(64, CH);
-    static constexpr int KV = COLS * (PASS / 8) / 64;
+    static constexpr int NV = SCALED ? (2 * COLS + 63) / 64 : 1;
     float bl[TN];
-    float b[PH][8], w[PH][8];
-    float bv[KV], wv[KV];
+    float v[NV];
+    const float *lds = nullptr;
 };
 
 template <Epi KIND, int TN, int PASS, bool SCALED>
@@ -463,11 +465,7 @@ __device__ __forceinline__ void load_cols(EpiCols<TN, PASS, SCALED> &c, const Ep
     using C = EpiCols<TN, PASS, SCALED>;
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int p = 0; p < C::PH; ++p)
-#pragma unroll
-        for (int q = 0; q < 8; ++q) c.b[p][q] = 0.0f, c.w[p][q] = 1.0f;
-#pragma unroll
-    for (int k = 0; k < C::KV; ++k) c.bv[k] = 0.0f, c.wv[k] = 1.0f;
+    for (int k = 0; k < C::NV; ++k) c.v[k] = 0.0f;
 #if defined(__HIP_DEVICE_COMPILE__)
     // Buffer reads: columns at or past N read as 0 (their outputs are never stored).
     auto rsrc = [&](const float *p) {
@@ -476,35 +474,22 @@ __device__ __forceinline__ void load_cols(EpiCols<TN, PASS, SCALED> &c, const Ep
     auto at = [&](const __amdgpu_buffer_rsrc_t &r, int n) {
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, n * 4, 0, 0));
     };
-    const bool vt = (KIND == Epi::Qkv || KIND == Epi::QkvRope) && nw / e.hidden == 2;
 #pragma unroll
     for (int j = 0; j < TN; ++j) c.bl[j] = 0.0f;
     if (!SCALED && e.bias) {
         const __amdgpu_buffer_rsrc_t r = rsrc(e.bias);
 #pragma unroll
         for (int j = 0; j < TN; ++j) c.bl[j] = at(r, nw + j * 32 + (lane & 31));
-    } else if (e.bias) {
-        const __amdgpu_buffer_rsrc_t r = rsrc(e.bias);
-        if (vt) {
-#pragma unroll
-            for (int k = 0; k < C::KV; ++k) c.bv[k] = at(r, nw + (lane + 64 * k) / (PASS / 8));
-        } else {
-#pragma unroll
-            for (int p = 0; p < C::PH; ++p)
-#pragma unroll
-                for (int q = 0; q < 8; ++q) c.b[p][q] = at(r, nw + ((lane + 64 * p) % C::CH) * 8 + q);
-        }
     }
     if constexpr (SCALED) {
-        const __amdgpu_buffer_rsrc_t r = rsrc(e.w_scale);
-        if (vt) {
+        // Value i of the wave: scale i (i < COLS), bias i - COLS (0 with no bias).
+        const __amdgpu_buffer_rsrc_t rw = rsrc(e.w_scale);
+        const __amdgpu_buffer_rsrc_t rb = rsrc(e.bias);
 #pragma unroll
-            for (int k = 0; k < C::KV; ++k) c.wv[k] = at(r, nw + (lane + 64 * k) / (PASS / 8));
-        } else {
-#pragma unroll
-            for (int p = 0; p < C::PH; ++p)
-#pragma unroll
-                for (int q = 0; q < 8; ++q) c.w[p][q] = at(r, nw + ((lane + 64 * p) % C::CH) * 8 + q);
+        for (int k = 0; k < C::NV; ++k) {
+            const int i = lane + 64 * k;
+            if (i < C::COLS) c.v[k] = at(rw, nw + i);
+            else if (i < 2 * C::COLS && e.bias) c.v[k] = at(rb, nw + i - C::COLS);
         }
     }
 #else
@@ -513,6 +498,28 @@ __device__ __forceinline__ void load_cols(EpiCols<TN, PASS, SCALED> &c, const Ep
     (void)nw;
     (void)lane;
 #endif
+}
+
+// The int8 epilogue's constants into the wave's LDS (2 COLS floats, 16-byte
+// aligned), once the stages are free; the caller waits for the writes.
+template <int TN, int PASS, bool SCALED>
+__device__ __forceinline__ void stage_cols(EpiCols<TN, PASS, SCALED> &c, float *ccol) {
+    using C = EpiCols<TN, PASS, SCALED>;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < C::NV; ++k)
+        if (lane + 64 * k < 2 * C::COLS) ccol[lane + 64 * k] = c.v[k];
+    c.lds = ccol;
+}
+
+// The scales and biases of the 8 columns from cc, from the staged constants.
+template <int COLS>
+__device__ __forceinline__ void chunk_cols(const float *ccol, int cc, float (&wsc)[8], float (&bias)[8]) {
+    typedef float f4_t __attribute__((ext_vector_type(4)));
+    const f4_t w0 = *(const f4_t *)(ccol + cc), w1 = *(const f4_t *)(ccol + cc + 4);
+    const f4_t b0 = *(const f4_t *)(ccol + COLS + cc), b1 = *(const f4_t *)(ccol + COLS + cc + 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wsc[q] = w0[q], wsc[4 + q] = w1[q], bias[q] = b0[q], bias[4 + q] = b1[q];
 }
 
 // Head and column within the head of column `rem` of Q, K or V. (A lane's
@@ -636,10 +643,9 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
                         int head, c;
                         head_col(n - qkv_base, e.d, head, c);
                         float v[8];
-                        const float bias = cols.bv[k];
                         const int m = mt + g;
                         if constexpr (SCALED) {
-                            const float ws = cols.wv[k];
+                            const float ws = cols.lds[col], bias = cols.lds[COLS + col];
 #pragma unroll
                             for (int q = 0; q < 8; ++q) v[q] = dequant(scratch[(g + q) * SROW + col], ascale[m + q - mw], ws, bias);
                         } else {
@@ -674,8 +680,7 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
         }
         // Row-wise: 8 consecutive columns of one row a lane, item u = lane +
         // 64 k taking chunk u % CH of row u / CH. A lane's chunk repeats every
-        // PH items (64 PH is a multiple of CH), so its biases and scales are
-        // read once per phase.
+        // PH items (64 PH is a multiple of CH).
         constexpr int PH = EpiCols<TN, PASS, SCALED>::PH;
         static_assert((PASS * CH) % 64 == 0 && ((PASS * CH) / 64) % PH == 0, "whole items per lane");
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -743,8 +748,8 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
 #pragma unroll
                 for (int k = 0; k < NK; ++k) {
                     const int cc = ((lane + 64 * (k % PH)) % CH) * 8, n = nw + cc;
-                    const float(&bias)[8] = cols.b[k % PH];
-                    const float(&wsc)[8] = cols.w[k % PH];
+                    float bias[8], wsc[8];
+                    if constexpr (SCALED) chunk_cols<COLS>(cols.lds, cc, wsc, bias);
                     const int row = (lane + 64 * k) / CH, m = mt + row;
                     const bool ok = m < M && n < N;
                     const float4_t lo = *(const float4_t *)&scratch[row * SROW + cc];
@@ -838,8 +843,8 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
 #pragma unroll
         for (int k = 0; k < PASS * CH / 64; ++k) {
             const int cc = ((lane + 64 * (k % PH)) % CH) * 8, n = nw + cc;
-            const float(&bias)[8] = cols.b[k % PH];
-            const float(&wsc)[8] = cols.w[k % PH];
+            float bias[8], wsc[8];
+            if constexpr (SCALED) chunk_cols<COLS>(cols.lds, cc, wsc, bias);
             const int row = (lane + 64 * k) / CH;
             const int m = mt + row;
             if (m >= M || n >= N) continue;
@@ -1113,12 +1118,11 @@ gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int l
     // stores); 32 for the QKV scatter when they fit, so each V^T column
     // gets 64 contiguous bytes a store instead of 32.
     constexpr bool QKV_KIND = KIND == Epi::Qkv || KIND == Epi::QkvRope;
-    constexpr int PASS = QKV_KIND && WAVES * 32 * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <=
-                                         STAGES * TILE
-                             ? 32
-                             : 16;
-    static_assert(WAVES * PASS * (TN * 32 + 4) * 4 + (sizeof(T) == 1 ? WAVES * (BM / WM) * 4 : 0) <= STAGES * TILE,
-                  "epilogue staging fits the stages");
+    // (int8 operands: each wave's rows' activation scales, and its columns'
+    // weight scales and biases, beside the staging rows.)
+    constexpr int I8_LDS = sizeof(T) == 1 ? WAVES * (BM / WM + 2 * TN * 32) * 4 : 0;
+    constexpr int PASS = QKV_KIND && WAVES * 32 * (TN * 32 + 4) * 4 + I8_LDS <= STAGES * TILE ? 32 : 16;
+    static_assert(WAVES * PASS * (TN * 32 + 4) * 4 + I8_LDS <= STAGES * TILE, "epilogue staging fits the stages");
     const int mw = m0 + wm * (BM / WM), nw = n0 + wn * (BN / WN);
 
 
@@ -1141,6 +1145,8 @@ gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int l
     if constexpr (sizeof(T) == 1) {
 #pragma unroll
         for (int r = lane; r < BM / WM; r += 64) ascale[r] = mw + r < M ? e.a_scale[mw + r] : 0.0f;
+        stage_cols(cols, reinterpret_cast<float *>(smem + STAGES * TILE) - WAVES * (BM / WM) -
+                             (WAVES - wave) * 2 * TN * 32);
         __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's scales are in LDS
         __builtin_amdgcn_wave_barrier();
     }
@@ -1410,8 +1416,12 @@ int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap) 
         if (n < cap) out[n++] = t;
     };
     const bool qkv = e.kind == Epi::Qkv || e.kind == Epi::QkvRope;
+    // Q, K and V must each start on a wave's column boundary.
+    auto fits = [&](int t) { return !qkv || e.hidden % wave_cols(t) == 0; };
     if (dt == Dt::I8) {
         if (K % 128 == 0) add(7);
+        // (Not with the rotary epilogue, whose angles spill this shape's registers.)
+        if (K % 128 == 0 && fits(15) && e.kind != Epi::QkvRope) add(15);
         add(9);
         return n;
     }
@@ -1422,8 +1432,6 @@ int gemm_candidates(Dt dt, int K, int lda, const EpiArgs &e, int *out, int cap) 
         add(14);
         return n;
     }
-    // Q, K and V must each start on a wave's column boundary.
-    auto fits = [&](int t) { return !qkv || e.hidden % wave_cols(t) == 0; };
     for (int t : {7, 13, 15, 16, 4, 6, 5, 9, 10})
         if (fits(t)) add(t);
     return n;
@@ -1520,9 +1528,7 @@ static hipError_t gemm_t(hipStream_t s, const GemmRows &gr, int M, int N, int K,
 }
 
 // The int8 tier: the pipelined kernel alone, on 128-byte rows (K a multiple
-// of 128) or 64-byte rows (K a multiple of 64). (256 x 384 tiles of 128 x 96
-// waves spill their dequantizing epilogue's per-column scales and biases:
-// the rerank workload took 18.05 ms a step on them against 17.43 on 256 x 256.)
+// of 128: 256 x 256 or 256 x 384 tiles) or 64-byte rows (K a multiple of 64).
 static hipError_t gemm_i8(hipStream_t s, const GemmRows &gr, int M, int N, int K, const void *A, int lda, const void *W,
                           const EpiArgs &e,
                           int tile) {
@@ -1531,10 +1537,11 @@ static hipError_t gemm_i8(hipStream_t s, const GemmRows &gr, int M, int N, int K
         tile = K % 128 == 0 ? 7 : 9;
         if (gemm_made_to_fail(tile)) tile = tile == 7 ? 9 : 7;
     }
-    if (tile == 7 && K % 128 != 0) tile = 9;
+    if ((tile == 7 || tile == 15) && K % 128 != 0) tile = 9;
     if (gemm_made_to_fail(tile)) return hipErrorInvalidDeviceFunction;
     switch (tile) {
     case 7: return launch_lds<int8_t, 256, 256, 2, 4, 2, 128, 1>(s, gr, M, N, K, A, lda, W, e);
+    case 15: return launch_lds<int8_t, 256, 384, 2, 4, 2, 128, 1>(s, gr, M, N, K, A, lda, W, e);
     default: return launch_lds<int8_t, 256, 128, 2, 2, 2, 64, 2>(s, gr, M, N, K, A, lda, W, e);
     }
 }
