@@ -264,6 +264,10 @@ def timed_run_from_trace(stats_dir, bench_log):
         if k >= len(starts):
             return None
         run = rows[starts[k]:starts[k + 1] if k + 1 < len(starts) else len(rows)]
+        # (A run ends with its pooling; kernels after it, up to the next
+        # run, are the bench's own.)
+        ends = [i for i, r in enumerate(run) if "pool_kernel" in r["Kernel_Name"]]
+        run = run[:ends[-1] + 1] if ends else run
         spans = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in run
                        if "gemm_" in r["Kernel_Name"])
         busy, end = 0, -1
@@ -357,7 +361,7 @@ PMC_PASSES = (
 )
 
 
-def summarize_counters(dirs, workload, command):
+def summarize_counters(dirs, workload, command, bench_log=None):
     """profiles/counters_<workload>.md and .json from rocprofv3 --pmc runs of
     this script, one a counter set of PMC_PASSES (each dispatch counted on its
     own): per kernel instantiation, the matrix cores' busy share of the
@@ -440,6 +444,32 @@ def summarize_counters(dirs, workload, command):
             continue
         lines.append(f"| `{short(k)}` | {calls.get(k, 0)} | {100 * g / total:.1f}% | {100 * mf:.1f}% | {100 * cnt:.1f}% "
                      f"| {100 * valu:.1f}% | {100 * lds:.1f}% | {100 * conf:.1f}% | {100 * wait:.1f}% |")
+    # The command's runs as a whole (every kernel but the probe and the
+    # copy): the matrix cores' busy share of all their dispatches'
+    # SIMD-cycles, beside the bench line's algorithmic figure.
+    run = [v for k, v in rows if "mfma_probe" not in k and "copy_kernel" not in k]
+    sc = sum(simd_cycles(v) for v in run)
+    if sc > 0:
+        mf = sum(v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for v in run) / sc * factor
+        gm = [v for k, v in rows if "gemm_" in k]
+        at = [v for k, v in rows if "attention" in k]
+        share = lambda vs: (sum(v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for v in vs) /  # noqa: E731
+                            max(1.0, sum(simd_cycles(v) for v in vs)) * factor)
+        out["run_mfma_busy"] = mf
+        lines += ["", f"All the command's run kernels together (the probe and the copy left out): matrix cores busy "
+                  f"{100 * mf:.1f}% of their dispatches' SIMD-cycles; the GEMM kernel's dispatches {100 * share(gm):.1f}%, "
+                  f"attention's {100 * share(at):.1f}%. (The profiler runs each dispatch on its own, so these are "
+                  f"shares of each kernel's own time, not of the step's.)"]
+        if bench_log:
+            for text in open(bench_log, errors="replace"):
+                if text.startswith('{"metric"'):
+                    d = json.loads(text)
+                    out["bench_mfma_util_pct"] = d.get("mfma_util_pct")
+                    lines.append(f"The same command run without the profiler (its bench line): mfma_util_pct "
+                                 f"{d.get('mfma_util_pct'):.1f}% (the run's algorithmic FLOPs over its step time at "
+                                 f"the dense peak: the step's share, where the busy shares above are the kernels' "
+                                 f"own), roofline {d['roofline']['achieved']:.0f} {d['roofline']['unit']} for the "
+                                 f"{d['roofline']['kernel']} kernel ({100 * d['roofline']['frac']:.1f}% of peak).")
     base = os.path.join(ROOT, "profiles", f"counters_{workload}")
     with open(base + ".md", "w") as f:
         f.write("\n".join(lines) + "\n")
@@ -533,8 +563,8 @@ def main():
     ap.add_argument("--summarize-stats", metavar="STATS_DIR",
                     help="write profiles/kernels_<workload>.md from a rocprofv3 --kernel-trace --stats run and exit")
     ap.add_argument("--bench-log", metavar="FILE",
-                    help="with --summarize-stats or --summarize-pmc: the profiled command's output, whose JSON line "
-                         "names the timed runs")
+                    help="with --summarize-stats, --summarize-pmc or --summarize-counters: the profiled command's "
+                         "output, whose JSON line names the timed runs")
     ap.add_argument("--summary-tag", default="", choices=["", "unsplit"],
                     help="with --summarize-stats: 'unsplit' for a run under TURBO_ROCM_SPLIT=1 of full-length rows "
                          "(per-kernel rates added; written to kernels_<workload>_unsplit.md)")
@@ -553,7 +583,7 @@ def main():
         summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.workload, args.pmc_command, args.bench_log)
         return
     if args.summarize_counters:
-        summarize_counters(args.summarize_counters, args.workload, args.pmc_command)
+        summarize_counters(args.summarize_counters, args.workload, args.pmc_command, args.bench_log)
         return
     if args.summarize_stats:
         summarize_stats(args.summarize_stats, args.workload, args.pmc_command, args.summary_tag, args.bench_log)
