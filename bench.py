@@ -51,6 +51,30 @@ def kernel_flops(shape, tokens, lengths):
 HBM_PEAK = 8.0e12   # MI355X HBM3E, bytes/s (published)
 
 
+def busy_union(intervals, names):
+    """The time at least one of these kernels' launches was running: the
+    union of their (name, start, end) intervals, over every stream."""
+    total, end = 0.0, float("-inf")
+    for a, b in sorted((a, b) for n, a, b in intervals if n in names):
+        if b > end:
+            total += b - max(a, end)
+            end = b
+    return total
+
+
+def run_slice(items, index, name):
+    """The items (kernel dispatches, in order) of the process's run number
+    `index`: each run begins with pack_rows_kernel and ends with its pooling
+    (what follows, up to the next run, is the bench's own), or None when the
+    process ran fewer runs. `name` gives an item's kernel name."""
+    starts = [i for i, x in enumerate(items) if "pack_rows_kernel" in name(x)]
+    if index >= len(starts):
+        return None
+    run = items[starts[index]:starts[index + 1] if index + 1 < len(starts) else len(items)]
+    ends = [i for i, x in enumerate(run) if "pool_kernel" in name(x)]
+    return run[:ends[-1] + 1] if ends else run
+
+
 def tail_bytes(shape, dtype, tokens, rows, od):
     """Algorithmic HBM bytes of the memory-bound kernels' launches in one
     run, by the timing hook's names: each operand read once and each result
@@ -133,10 +157,7 @@ def summarize_pmc(fetch_dir, write_dir, workload, command, bench_log=None):
         return sorted(rows)
 
     def run_only(v):
-        if index is None:
-            return v
-        starts = [i for i, (_, k, _) in enumerate(v) if "pack_rows_kernel" in k]
-        return v[starts[index]:starts[index + 1] if index + 1 < len(starts) else len(v)]
+        return v if index is None else run_slice(v, index, lambda x: x[1]) or []
 
     shape = W.SHAPES[workload]
     H, I = shape.hidden, shape.intermediate
@@ -258,23 +279,13 @@ def timed_run_from_trace(stats_dir, bench_log):
     for f in traces:
         rows += list(csv.DictReader(open(f)))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    starts = [i for i, r in enumerate(rows) if "pack_rows_kernel" in r["Kernel_Name"]]
-
     def run_of(k):
-        if k >= len(starts):
+        run = run_slice(rows, k, lambda r: r["Kernel_Name"])
+        if not run:
             return None
-        run = rows[starts[k]:starts[k + 1] if k + 1 < len(starts) else len(rows)]
-        # (A run ends with its pooling; kernels after it, up to the next
-        # run, are the bench's own.)
-        ends = [i for i, r in enumerate(run) if "pool_kernel" in r["Kernel_Name"]]
-        run = run[:ends[-1] + 1] if ends else run
         spans = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in run
                        if "gemm_" in r["Kernel_Name"])
-        busy, end = 0, -1
-        for a, b in spans:
-            if b > end:
-                busy += b - max(a, end)
-                end = b
+        busy = busy_union([("g", a, b) for a, b in spans], {"g"})
         length = (max(int(r["End_Timestamp"]) for r in run) - int(run[0]["Start_Timestamp"])) / 1e3
         return spans, busy / 1e3, length, sorted({r["Stream_Id"] for r in run})
 
@@ -295,7 +306,8 @@ def timed_run_from_trace(stats_dir, bench_log):
     if s and s[0]:
         spans, busy, length, streams = s
         mean = sum(b - a for a, b in spans) / len(spans) / 1e3
-        out += ["", f"The split run (run {c['timed_run_index']}, parts side by side on stream(s) "
+        out += ["", f"The headline session's timed run (run {c['timed_run_index']}, its parts side by side when it "
+                f"splits; stream(s) "
                 f"{', '.join(streams)}) in the kernel trace: {len(spans)} GEMM launches, average {mean:.1f} µs a "
                 f"launch (overlapping), busy {busy:.0f} µs. The bench's events: {c['launches_per_step']} launches, "
                 f"average {c['avg_launch_us']:.1f} µs, busy {c['busy_us_per_step']:.0f} µs; "
@@ -693,12 +705,7 @@ def main():
         summed launch time, FLOPs, launches and busy time (the union of its
         launches' intervals over every stream)."""
         def busy_ms(names):
-            total, end = 0.0, float("-inf")
-            for a, b in sorted((a, b) for n, a, b in intervals if n in names):
-                if b > end:
-                    total += b - max(a, end)
-                    end = b
-            return total
+            return busy_union(intervals, names)
 
         gemm_names = [k for k in times if k.startswith("gemm_")]
         gemm = ("gemm", sum(times[k] for k in gemm_names), sum(per[k] for k in gemm_names) * shape.layers,
