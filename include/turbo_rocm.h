@@ -138,9 +138,11 @@ int32_t turbo_rocm_session_hidden(void *session, float *out, uint64_t floats, tu
 int32_t turbo_rocm_host_allocs(uint64_t *process, uint64_t *thread, turbo_error *err);
 
 /* Times every kernel of the session's later runs with HIP events, each
- * launch's pair on the stream it runs on (a split run's parts side by side,
- * as the run executes them; its runs launch their kernels directly rather
- * than replay a graph); turbo_rocm_session_times then writes
+ * launch's pair bound to its kernels' own dispatch packets (the first
+ * kernel's start, the last one's end: no marker packet between launches) on
+ * the stream it runs on (a split run's parts side by side, as the run
+ * executes them; timed runs launch their kernels directly rather than
+ * replay a graph, and take a replay's time); turbo_rocm_session_times then writes
  * "<kernel> <ms> <launches>" lines: the milliseconds summed over the last
  * run's launches of that kernel, and how many there were;
  * turbo_rocm_session_intervals writes "<kernel> <start> <end>" a launch, in
