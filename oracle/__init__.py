@@ -99,7 +99,7 @@ def encode(desc: ModelDesc, ids, mask, types=None, pooling=S.TURBO_POOLING_MEAN,
     hid = np.zeros((ids.shape[0] * ids.shape[1], desc.hidden), dtype=np.float32) if hidden else None
     why = C.create_string_buffer(512)
     if threads == 0:
-        # The cores this process may run on (a box's share, not its count).
+        # The cores this process may run on (its affinity, not the host's count).
         threads = len(os.sched_getaffinity(0))
     lib().oracle_set_gated_limit(gated_limit)
     try:
