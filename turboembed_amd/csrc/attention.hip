@@ -272,11 +272,15 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
     const int L = blockIdx.x;
     const int pair = (L / (8 * nqb)) * 8 + L % 8, qb = (L / 8) % nqb;
     const Live lv = live_of(sp);
-    if (pair >= heads * lv.rows) return;
+    // (The packing's pointers are tested too, never null, so their argument
+    // words are read beside the run's dimensions, not after them.)
+    if (pair >= heads * lv.rows || p.len == nullptr || p.start == nullptr) return;
     const int r = lv.row0 + pair / heads, head = pair % heads, q0 = qb * QB, seq = lv.seq;
-    const int len = p.len[r];
-    if (q0 >= len) return;
-    const int start = p.start[r];
+    // Both reads go out together: the test takes the start too (never
+    // negative), so the compiler cannot sink its read past the exit and
+    // wait for the two one after the other.
+    const int len = p.len[r], start = p.start[r];
+    if (q0 >= len || start < 0) return;
     // The wave's number as a scalar (readfirstlane): everything derived from
     // it (its queries, its window tests, its branches) stays uniform.
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, ql = lane & 31;
@@ -288,24 +292,6 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
     const int32_t *mk = mask + (size_t)r * seq;
     const bool wave_live = qw < len;   // a wave past the row's end loads and syncs but computes nothing
 
-    frag qf[QT][D / 16];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        const T *qrow = Q + (size_t)min(qw + 32 * qt + ql, len - 1) * D + h * 8;
-#pragma unroll
-        for (int s = 0; s < D / 16; ++s) {
-            const vec4 v = *(const vec4 *)(qrow + s * 16);
-            qf[qt][s] = *(const frag *)&v;
-        }
-    }
-    // Q times log2(e)/sqrt(d), rounded to the operand type.
-    const float scale = 1.4426950408889634f / sqrtf((float)D);
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int s = 0; s < D / 16; ++s)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qf[qt][s][e] = (T)((float)qf[qt][s][e] * scale);
     // o[qt]: the context of tile qt, transposed; lsum[qt]: its softmax sums
     // over this lane's 16 keys of each sub-block.
     constexpr int NO = D / 32;
@@ -393,14 +379,45 @@ __global__ void __launch_bounds__(64 * (QB / (32 * QT))) attention_mfma_kernel(c
 #pragma unroll
     for (int st = 0; st < AHEAD; ++st)
         if (st < nb) issue(st, k_lo + st * KB);
+    // Q goes out after the first blocks' loads, and the masks' reads after
+    // both, so one memory latency covers the three.
+    frag qf[QT][D / 16];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const T *qrow = Q + (size_t)min(qw + 32 * qt + ql, len - 1) * D + h * 8;
+#pragma unroll
+        for (int s = 0; s < D / 16; ++s) {
+            const vec4 v = *(const vec4 *)(qrow + s * 16);
+            qf[qt][s] = *(const frag *)&v;
+        }
+    }
     // Every block's live keys, once, before the loop (a mask read inside it
     // would make its wave wait on the prefetch loads too): block b's 64 keys
-    // as one 64-bit word, by wave b % WAVES.
-    for (int b = wave; b < nb; b += WAVES) {
-        const int key = k_lo + b * KB + lane;
-        const uint64_t bits = __ballot(key < len && mk[key] != 0);
-        if (lane == 0) live_bits[b] = bits;
+    // as one 64-bit word, by wave b % WAVES, eight blocks' reads in flight at
+    // once on long rows.
+    for (int b0 = wave; b0 < nb; b0 += 8 * WAVES) {
+        // Every lane reads, from a clamped block and key, and the empty asm
+        // takes all eight values: the reads cannot sink into the branches
+        // that use them, so they go out together and are waited for once.
+        int32_t mv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) mv[u] = mk[min(k_lo + min(b0 + u * WAVES, nb - 1) * KB + lane, len - 1)];
+        asm volatile("" ::"v"(mv[0]), "v"(mv[1]), "v"(mv[2]), "v"(mv[3]), "v"(mv[4]), "v"(mv[5]), "v"(mv[6]), "v"(mv[7]));
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int b = b0 + u * WAVES, key = k_lo + b * KB + lane;
+            const uint64_t bits = __ballot(b < nb && key < len && mv[u] != 0);
+            if (lane == 0 && b < nb) live_bits[b] = bits;
+        }
     }
+    // Q times log2(e)/sqrt(d), rounded to the operand type.
+    const float scale = 1.4426950408889634f / sqrtf((float)D);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int s = 0; s < D / 16; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[qt][s][e] = (T)((float)qf[qt][s][e] * scale);
 
     for (int bi = 0; bi < nb; ++bi) {
         const int kb = k_lo + bi * KB;

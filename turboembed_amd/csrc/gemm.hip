@@ -1038,13 +1038,16 @@ __device__ __forceinline__ void lds_mainloop(char *smem, const T *__restrict__ A
     auto fetch_a = [&](const char *base, int s, int set, int i) {
         fa[set][i] = *(const frag *)(base + off_a[i] + 16 * ((2 * s + h) ^ sw_a));
     };
+    // (In the order the first products use them: A's first row tile, then
+    // B's, then A's other row tiles.)
     auto fetch = [&](const char *base, int s, int set) {
         const int c = 2 * s + h;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-            if (!SINGLE_A || set == 0) fetch_a(base, s, SINGLE_A ? 0 : set, i);
+        if (!SINGLE_A || set == 0) fetch_a(base, s, SINGLE_A ? 0 : set, 0);
 #pragma unroll
         for (int j = 0; j < TN; ++j) fb[set][j] = *(const frag *)(base + off_b[j] + 16 * (c ^ sw_b));
+#pragma unroll
+        for (int i = 1; i < TM; ++i)
+            if (!SINGLE_A || set == 0) fetch_a(base, s, SINGLE_A ? 0 : set, i);
     };
     for (int kt = 0; kt < nk; ++kt) {
         // This wave's loads of stage kt have landed once at most the later
@@ -1054,12 +1057,16 @@ __device__ __forceinline__ void lds_mainloop(char *smem, const T *__restrict__ A
         else if (STAGES > 3 && later == 1) wait_vmcnt<L>();
         else wait_vmcnt<0>();
         __syncthreads();
-        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+        // The stage's first fragment reads go out before its successor's
+        // loads are issued, so the products restart as soon as they can
+        // after the barrier (FFN-out, K 3072: -2.5%).
         const char *base = smem + (kt % STAGES) * TILE;
+        fetch(base, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
         // The next k-step's fragments are read while this one's products run.
         // (sched_barrier keeps the compiler from sinking those reads back
         // under the products that do not need them.)
-        fetch(base, 0, 0);
 #pragma unroll
         for (int s = 0; s < ROWB / 32; ++s) {
             if constexpr (SINGLE_A) {
