@@ -440,22 +440,20 @@ __device__ __forceinline__ u32x2_t pack4(const float (&v)[4]) {
     return __builtin_bit_cast(u32x2_t, tmp);
 }
 
-// The per-column constants a lane's epilogue uses (the bias, and the int8
-// weight scales), read after the main loop and before the first store. A
-// global load issued among the stores would make the wait for its value wait
-// for every store before it too (the vector memory counter retires in order),
-// so the epilogue reads nothing from global memory once its first store is
-// out. 16-bit operands: the bias of the lane's accumulator columns 32 j + ql,
-// added as the accumulators go to LDS (TN registers). int8 operands, whose
-// bias follows the scales: the wave's COLS scales, then its COLS biases, NV
-// values a lane, go to the wave's LDS (stage_cols) once the stages are free,
-// and each store reads its columns' from there (registers for them all would
-// spill the wide block shapes' accumulators).
+// The per-column constants a lane's epilogue uses (the int8 weight scales
+// and biases; a 16-bit product's bias is in its accumulators from the
+// start), read after the main loop and before the first store. A global load
+// issued among the stores would make the wait for its value wait for every
+// store before it too (the vector memory counter retires in order), so the
+// epilogue reads nothing from global memory once its first store is out.
+// int8 operands, whose bias follows the scales: the wave's COLS scales, then
+// its COLS biases, NV values a lane, go to the wave's LDS (stage_cols) once
+// the stages are free, and each store reads its columns' from there
+// (registers for them all would spill the wide block shapes' accumulators).
 template <int TN, int PASS, bool SCALED>
 struct EpiCols {
     static constexpr int COLS = TN * 32, CH = COLS / 8, PH = CH / gcd_c(64, CH);
     static constexpr int NV = SCALED ? (2 * COLS + 63) / 64 : 1;
-    float bl[TN];
     float v[NV];
     const float *lds = nullptr;
 };
@@ -474,13 +472,6 @@ __device__ __forceinline__ void load_cols(EpiCols<TN, PASS, SCALED> &c, const Ep
     auto at = [&](const __amdgpu_buffer_rsrc_t &r, int n) {
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, n * 4, 0, 0));
     };
-#pragma unroll
-    for (int j = 0; j < TN; ++j) c.bl[j] = 0.0f;
-    if (!SCALED && e.bias) {
-        const __amdgpu_buffer_rsrc_t r = rsrc(e.bias);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) c.bl[j] = at(r, nw + j * 32 + (lane & 31));
-    }
     if constexpr (SCALED) {
         // Value i of the wave: scale i (i < COLS), bias i - COLS (0 with no bias).
         const __amdgpu_buffer_rsrc_t rw = rsrc(e.w_scale);
@@ -579,8 +570,8 @@ __device__ __forceinline__ void epilogue_lds(const EpiArgs &e, int M, int N, int
             for (int r = 0; r < 16; ++r) {
                 if (PASS == 16 && (r >> 3) != half) continue;
                 const int row = (r >> 2) * 8 + h * 4 + (r & 3) - (PASS == 16 ? half * 16 : 0);
-                // (16-bit operands: with the column's bias added.)
-                scratch[row * SROW + j * 32 + ql] = SCALED ? (float)acc[i][j][r] : (float)acc[i][j][r] + cols.bl[j];
+                // (16-bit operands: the bias is in the accumulators.)
+                scratch[row * SROW + j * 32 + ql] = (float)acc[i][j][r];
             }
         __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
         __builtin_amdgcn_wave_barrier();
@@ -958,12 +949,16 @@ struct LdsTile {
 // The pipelined main loop: acc[i][j] (this wave's MFMA tiles, zeroed by the
 // caller) takes the sums over all of K of the BM x BN tile whose first row
 // and column are m0 and n0 (rows of A past M and of W past N read as the
-// last ones). Leaves every wave's last fragment reads done but the stages
-// still in use: the caller syncs before it reuses the LDS.
+// last ones). With `bias` (16-bit operands), every accumulator starts from
+// its column's bias instead of 0 (columns past N from 0), so the epilogue
+// has no bias to add: y = b + sum, one F32 rounding per product as before.
+// Leaves every wave's last fragment reads done but the stages still in use:
+// the caller syncs before it reuses the LDS.
 template <typename T, int BM, int BN, int WM, int WN, int STAGES, int BK>
 __device__ __forceinline__ void lds_mainloop(char *smem, const T *__restrict__ A, int lda, const T *__restrict__ W,
                                              int M, int N, int K, int m0, int n0, int wave, int lane,
-                                             typename Mma<T>::acc (&acc)[BM / WM / 32][BN / WN / 32]) {
+                                             typename Mma<T>::acc (&acc)[BM / WM / 32][BN / WN / 32],
+                                             const float *__restrict__ bias = nullptr) {
     using P = LdsTile<T, BM, BN, WM, WN, STAGES, BK>;
     constexpr int EPC = P::EPC, ROWB = P::ROWB, CHUNKS = P::CHUNKS, RPI = P::RPI, TILE = P::TILE;
     constexpr int TM = P::TM, TN = P::TN, LA = P::LA, LB = P::LB, L = P::L;
@@ -1017,9 +1012,35 @@ __device__ __forceinline__ void lds_mainloop(char *smem, const T *__restrict__ A
     };
 
     const int nk = K / BK;
+    // The bias of this lane's columns n0 + wn (BN / WN) + 32 j + (lane & 31),
+    // read before the stages' loads so its wait leaves them in flight.
+    float binit[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) binit[j] = 0.0f;
+#if defined(__HIP_DEVICE_COMPILE__)
+    if constexpr (sizeof(T) == 2) {
+        if (bias) {
+            const __amdgpu_buffer_rsrc_t rbias = __builtin_amdgcn_make_buffer_rsrc((void *)bias, (short)0, N * 4, 0x00020000);
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                binit[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                         rbias, (n0 + wn * (BN / WN) + 32 * j + (lane & 31)) * 4, 0, 0));
+        }
+    }
+#endif
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
         if (st < nk) issue(st, st * BK);
+    if constexpr (sizeof(T) == 2) {
+        if (bias) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = binit[j];
+        }
+    }
     const int ra = wm * (BM / WM) + (lane & 31), rb = wn * (BN / WN) + (lane & 31);
     const int h = lane >> 5;
     // Each lane's fragment addresses within a stage, for chunk pair (h, s).
@@ -1140,7 +1161,8 @@ gemm_lds_kernel(Span sp, int a_tok, int N, int K, const T *__restrict__ A, int l
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{};
-    lds_mainloop<T, BM, BN, WM, WN, STAGES, BK>(smem, A, lda, W, M, N, K, m0, n0, wave, lane, acc);
+    lds_mainloop<T, BM, BN, WM, WN, STAGES, BK>(smem, A, lda, W, M, N, K, m0, n0, wave, lane, acc,
+                                                sizeof(T) == 2 ? e.bias : nullptr);
 
     // The epilogue's per-column constants, read now (not held through the
     // main loop) and before the first store, so no store waits behind them.
@@ -1243,14 +1265,10 @@ gemm_ln_kernel(Span sp, int a_tok, int K, const T *__restrict__ A, int lda, cons
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{};
-    lds_mainloop<T, BM, BN, WM, WN, STAGES, BK>(smem, A, lda, W, M, BN, K, m0, 0, wave, lane, acc);
+    // (The accumulators start from the bias, as the separate product's do.)
+    lds_mainloop<T, BM, BN, WM, WN, STAGES, BK>(smem, A, lda, W, M, BN, K, m0, 0, wave, lane, acc, e.bias);
 
     const int h = lane >> 5, ql = lane & 31;
-    // The bias of this lane's columns 32 j + ql of the wave's, added as the
-    // sums go to LDS.
-    float bl[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bl[j] = e.bias ? e.bias[wn * (BN / WN) + 32 * j + ql] : 0.0f;
     __syncthreads();   // every wave is done with the stages
     T *ys = reinterpret_cast<T *>(smem);
     float *lw = reinterpret_cast<float *>(smem + PR * YS * (int)sizeof(T));   // the norm's weight, then its bias
@@ -1287,7 +1305,7 @@ gemm_ln_kernel(Span sp, int a_tok, int K, const T *__restrict__ A, int lda, cons
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = wm * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                ys[row * YS + wn * (BN / WN) + 32 * j + ql] = from_f32<T>(acc[i][j][r] + bl[j]);
+                ys[row * YS + wn * (BN / WN) + 32 * j + ql] = from_f32<T>(acc[i][j][r]);
             }
         __syncthreads();
         if (i + 1 < TM) load_res(i + 1, res[(i + 1) & 1]);
