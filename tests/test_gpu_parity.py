@@ -354,6 +354,47 @@ def test_matrix_core_attention_meets_the_oracle(context, family, heads, monkeypa
     model.close()
 
 
+@pytest.mark.parametrize("family", ["bert", "modernbert"])
+def test_matrix_core_attention_on_long_rows_with_holes(context, family, monkeypatch):
+    # Rows past 64 key blocks, where each wave reads its blocks' mask words in
+    # more than one batch of eight (4,700 and 2,300 tokens, eight waves of the
+    # 256-query path and four of the 128-query one), with masked keys through
+    # them: on block edges (63, 64, 4095, 4096), in runs, and a whole 64-key
+    # block; ModernBERT's local layers on 16-key windows across those rows.
+    # Both query-block sizes against the oracle and against each other (the
+    # same per-wave arithmetic over the same blocks).
+    seq = 4800
+    if family == "bert":
+        desc = small.bert(seed=41, layers=2, hidden=128, heads=2, inter=256, positions=seq, std=0.2)
+    else:
+        desc = small.modernbert(seed=41, layers=2, hidden=128, heads=2, inter=192, positions=seq, window=16,
+                                global_every=2, std=0.2)
+    g = np.random.Generator(np.random.PCG64(41))
+    ids = g.integers(0, desc.vocab_size, size=(3, seq)).astype(np.int32)
+    mask = np.zeros((3, seq), np.int32)
+    mask[0, :4700] = 1
+    mask[0, g.choice(np.arange(1, 4699), size=40, replace=False)] = 0
+    mask[0, [63, 64, 4095, 4096]] = 0
+    mask[0, 1024:1088] = 0
+    mask[1, :2300] = 1
+    mask[1, 500:530] = 0
+    mask[1, [127, 128, 2047]] = 0
+    mask[2, :100] = 1
+    types = g.integers(0, 2, size=(3, seq)).astype(np.int32) if family == "bert" else None
+    want = oracle.encode(desc, ids, mask, types)
+    model = context.load(desc)
+    got = {}
+    for path in ("mfma", "mfma128"):
+        monkeypatch.setenv("TURBO_ROCM_CHOICES", f"attention={path}")
+        s = model.session(3, seq, S.TURBO_PRECISION_FASTEST)
+        assert f"attn={path}" in s.choices()
+        got[path] = s.embed(ids, mask, types)
+        assert_close(got[path], want, s.compute_dtype)
+        s.close()
+    model.close()
+    assert small.cosine_rows(got["mfma"], got["mfma128"]).min() >= 0.999999
+
+
 @pytest.mark.parametrize("tier", ["f16", "bf16"])
 @pytest.mark.parametrize("family", ["bert", "modernbert"])
 def test_matrix_core_attention_rescales_as_the_scalar_path_does(context, family, tier, monkeypatch):
