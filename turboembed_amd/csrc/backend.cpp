@@ -207,6 +207,10 @@ int32_t context_create(uint32_t ordinal, turbo_log_fn log, void *ud, void **out,
         // The device's fixed staging area (the no-allocation buffer_quantize):
         // its address on this device, looked up with the device current.
         check(static_scratch(c->ordinal, &c->scratch), "the device's staging area");
+        if (hipHostMalloc(&c->read_stage, Context::READ_STAGE, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            c->read_stage = nullptr;
+        }
         // Default priority on every stream: the one stream priority every run
         // uses. The side streams carry a split run's other parts of rows; the
         // events fork them from the first and join them back.
@@ -222,6 +226,7 @@ int32_t context_create(uint32_t ordinal, turbo_log_fn log, void *ud, void **out,
             }
             if (c->fork) (void)hipEventDestroy(c->fork);
             (void)hipStreamDestroy(c->stream);
+            if (c->read_stage) (void)hipHostFree(c->read_stage);
             fail(TURBO_E_RUNTIME, "rocm: the context's side streams and their events");
         }
         *out = c.release();
@@ -242,6 +247,7 @@ void context_release(void *ctx) {
         }
         (void)hipEventDestroy(c->fork);
         (void)hipStreamDestroy(c->stream);
+        if (c->read_stage) (void)hipHostFree(c->read_stage);
     }
     delete c;
 }
@@ -367,6 +373,18 @@ int32_t buffer_read(void *buf, void *dst, uint64_t bytes, turbo_error *err) {
                                                                  " bytes from a buffer of " + std::to_string(b->bytes));
         std::lock_guard<std::recursive_mutex> g(b->ctx->lock);
         OnDevice on(b->ctx->ordinal);
+        // A device buffer's bytes go to the context's pinned stage on the
+        // stream (a DMA that starts as soon as the run before it ends), then
+        // to dst on the host: a copy straight into pageable memory first
+        // waits for the stream and then stages through the runtime's buffers
+        // (BERT-base 64 x 512 write + run + read: 7.77 -> 7.6 ms).
+        if (b->placement == TURBO_PLACE_DEVICE && b->ctx->read_stage && bytes <= Context::READ_STAGE) {
+            check(hipMemcpyAsync(b->ctx->read_stage, b->dev, bytes, hipMemcpyDeviceToHost, b->ctx->stream),
+                  "buffer_read");
+            check(hipStreamSynchronize(b->ctx->stream), "buffer_read");
+            std::memcpy(dst, b->ctx->read_stage, bytes);
+            return TURBO_OK;
+        }
         check(hipMemcpyAsync(dst, b->dev ? b->dev : b->host, bytes, hipMemcpyDefault, b->ctx->stream), "buffer_read");
         check(hipStreamSynchronize(b->ctx->stream), "buffer_read");
         return TURBO_OK;

@@ -93,6 +93,11 @@ struct Context {
     // writes and runs rows under it).
     std::recursive_mutex lock;
     void *scratch = nullptr;         // the device's fixed staging area (static_scratch)
+    // Pinned host memory that buffer_read copies device buffers through (a
+    // copy into pageable memory waits for the stream, then stages through the
+    // runtime's own buffers): null if it could not be allocated.
+    static constexpr size_t READ_STAGE = (size_t)4 << 20;
+    void *read_stage = nullptr;
     void say(uint32_t level, const std::string &m) const;
 };
 
