@@ -1001,12 +1001,19 @@ void session_write(Session *s, const turbo_backend_embed_rows *r, const turbo_to
         }
     }
     // Planes are B*S long here but the device keeps them max_batch*max_seq
-    // apart: three copies, then the dimensions and the ranges in one.
+    // apart: three copies, then the dimensions and the ranges in one; rows
+    // that fill the planes go in one copy with them (the staging buffer and
+    // the device hold the same layout).
     const size_t n = (size_t)B * S * 4, tail = sizeof(RunDims) + (size_t)count * 12;
-    check(hipMemcpyAsync(s->ids, ids, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
-    check(hipMemcpyAsync(s->mask, mask, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
-    check(hipMemcpyAsync(s->types, types, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
-    check(hipMemcpyAsync(s->dims_dev, s->dims_host, tail, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+    if ((size_t)B * S == plane) {
+        const size_t at = (size_t)(reinterpret_cast<char *>(s->dims_host) - reinterpret_cast<char *>(s->staging));
+        check(hipMemcpyAsync(s->ids, s->staging, at + tail, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+    } else {
+        check(hipMemcpyAsync(s->ids, ids, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+        check(hipMemcpyAsync(s->mask, mask, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+        check(hipMemcpyAsync(s->types, types, n, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+        check(hipMemcpyAsync(s->dims_dev, s->dims_host, tail, hipMemcpyHostToDevice, s->ctx->stream), "embed_write");
+    }
     s->h2d = 3 * n + tail;
     s->batch = B;
     s->seq = S;
